@@ -1,0 +1,118 @@
+/*
+ * moex_attn.h -- C ABI of the MI355X (gfx950) attention hot path of moex (Qwen3.6-35B-A3B GQA layers:
+ * 16 query heads, 2 KV heads, head_dim 256).
+ *
+ * Every entry point replaces one function or kernel launch of the reference header src/kernels.cuh; the
+ * citation is on each declaration. Arguments keep the reference's order and meaning. Differences:
+ *   - the stream is an opaque hipStream_t passed as void* (NULL = the default stream);
+ *   - fp16 weight pointers (qn, kn) are raw binary16 bit patterns (uint16_t);
+ *   - raw kernel launches take their grid-defining sizes (T, ns) explicitly instead of a <<<grid>>>.
+ * All pointers are device pointers unless stated otherwise. Nothing allocates or synchronizes except
+ * moex_kv_alloc / moex_kv_free, so every attention call can be captured into a HIP graph.
+ *
+ * Errors (kernels.cuh:8-11, CK): a failing HIP call prints "HIP <error> at <file>:<line>" and exits(1),
+ * unless a soft-error slot is installed (moex_set_soft_error), in which case the first error code is
+ * stored there and the call returns. Argument errors (unsupported head_dim/group shapes) are reported
+ * the same way with code hipErrorInvalidValue (1).
+ */
+#ifndef MOEX_ATTN_H
+#define MOEX_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOEX_AHD 256   /* head dim (kernels.cuh:1111, AHD) */
+#define MOEX_TQ_KB 128 /* turbo K bytes per (kv head, position) (kernels.cuh:1122, TQ_KB) */
+#define MOEX_TQ_VB 96  /* turbo V bytes per (kv head, position) (kernels.cuh:1122, TQ_VB) */
+
+/* KV cache (kernels.cuh:1121, struct KVCache): same fields, same order, same layout.
+ * int8:  k, v int8 [KV][max_t][256]; ks, vs f32 [KV][max_t]          (520 B per kv head and position)
+ * turbo: k u8 [KV][max_t][128] (4-bit codes), v u8 [KV][max_t][96] (3-bit codes),
+ *        ks, vs f32 [KV][max_t][2] (one norm per 128-value half)      (240 B per kv head and position) */
+typedef struct moex_kv_cache {
+    int8_t* k;
+    int8_t* v;
+    float* ks;
+    float* vs;
+    int turbo;
+} moex_kv_cache;
+
+/* ---- cache storage (kernels.cuh:1867-1877) ---- */
+/* kv_alloc (kernels.cuh:1867): hipMalloc of the four arrays. */
+moex_kv_cache moex_kv_alloc(int KV, int max_t, int turbo);
+/* kv_bytes (kernels.cuh:1875): bytes kv_alloc takes, KV * max_t * (turbo ? 240 : 520). */
+size_t moex_kv_bytes(int KV, int max_t, int turbo);
+/* no counterpart (the reference never frees its cache): hipFree of the four arrays. */
+void moex_kv_free(moex_kv_cache kv);
+
+/* ---- full attention step (kernels.cuh:1846-1865, attn_decode) ----
+ * q: raw q_proj rows, token stride ld: query [h*512, +256), gate [h*512+256, +256). k, v: raw k/v rows, stride ld.
+ * Per token blockIdx-equivalent t at position *pos_d + t: q/k RMSNorm(1+w) and partial RoPE (rot dims, theta),
+ * all T K/V rows quantized into kv (int8, or turbo codes), the query written to qo [T][H][256] (turbo: rotated),
+ * then attention over keys [0, pos+t] written gated to out [T][H][256].
+ * Dispatch as the reference: T > 2 and ns == 1 -> prefill (FA; MOEX_FA=0 -> moex_attn_prefill for int8);
+ * ns > 1 -> split-K GQA decode + combine (part: T*H*ns*(256+2) floats); else the per-head kernel. */
+void moex_attn_decode(const float* q, const float* k, const float* v, const uint16_t* qn, const uint16_t* kn,
+                      float* qo, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d, int max_t,
+                      int rot, float theta, float eps, int T, int ld, void* stream, float* part, int ns);
+
+/* attn_fa (kernels.cuh:1713): FlashAttention-2 causal GQA prefill of T query tokens at *pos_d..*pos_d+T-1.
+ * qo [T][H][256] f32 (rotated for turbo); q_gate: the q rows (gate at [t*ld + h*512 + 256]); NULL = no gate
+ * (turbo, followed by moex_turbo_out). Needs H / KV == 8. */
+void moex_attn_fa(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
+                  const int* pos_d, int max_t, int ld, int T, void* stream);
+
+/* attn_prefill (kernels.cuh:1435): the int8-only prefill fallback (K7P), same arguments and result. */
+void moex_attn_prefill(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
+                       const int* pos_d, int max_t, int ld, int T, void* stream);
+
+/* ---- raw launches used by the reference's tests ---- */
+/* qk_norm_rope_k (kernels.cuh:1185), grid (H+KV, T): norm + RoPE + quantize-append. */
+void moex_qk_norm_rope(const float* q, const float* k, const float* v, const uint16_t* qn, const uint16_t* kn,
+                       float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, int rot,
+                       float theta, float eps, int ld, int T, void* stream);
+/* The quantize-append half of qk_norm_rope_k (kernels.cuh:1210-1235) alone: k rows are already normalized and
+ * rotated. Row kvh*max_t + *pos_d + t gets token t's k/v (token stride ld floats, kv head at kvh*256). */
+void moex_kv_append(const float* k, const float* v, moex_kv_cache kv, int KV, const int* pos_d, int max_t,
+                    int ld, int T, void* stream);
+/* attn_gqa_k (kernels.cuh:1745), grid (KV, T, ns): split-K GQA decode, writes partials {m, l, acc[256]} to
+ * part[((t*H + h)*ns + s)*(256+2)]. m is the running max in log2 units (the combine below reads it so). */
+void moex_attn_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part,
+                   int T, int ns, void* stream);
+/* attn_combine_k (kernels.cuh:1317), grid (H, T): merges ns partials, out = acc/l * sigmoid(gate) (no gate if
+ * q_gate is NULL). */
+void moex_attn_combine(const float* part, const float* q_gate, float* out, int H, int ns, int ld, int T,
+                       void* stream);
+/* attn_decode_k (kernels.cuh:1244), grid (H, T, ns): per-query-head decode (any H/KV). ns == 1 writes the gated
+ * output (no gate if q_gate is NULL), ns > 1 partials for moex_attn_combine. */
+void moex_attn_decode_heads(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
+                            const int* pos_d, int max_t, int ld, float* part, int T, int ns, void* stream);
+/* turbo_out_k (kernels.cuh:1731), grid (H, T): out = WHT_inverse(out) * sigmoid(gate), in place. */
+void moex_turbo_out(float* out, const float* q_gate, int H, int ld, int T, void* stream);
+/* set_int_k (kernels.cuh:1879): *p = v on the stream (graph-friendly position update). */
+void moex_set_int(int* p, int v, void* stream);
+
+/* ---- runtime switches ---- */
+/* g_soft_ck (kernels.cuh:8): while slot != NULL, errors are recorded in *slot (first one wins) instead of exit. */
+void moex_set_soft_error(int* slot);
+/* g_skip (kernels.cuh:46): while the device flag is nonzero, moex_qk_norm_rope and moex_turbo_out return at once
+ * (the graph fallback of the reference's decode step). Set on the stream. */
+void moex_set_skip(int value, void* stream);
+/* attn_fa_on (kernels.cuh:1699): 1 unless MOEX_FA=0 (read once). */
+int moex_fa_on(void);
+/* fa_supported (kernels.cuh:1705): 1 when the current device is gfx950. */
+int moex_fa_supported(void);
+/* Recommended ns for the split-K decode at n_ctx keys on the current device (the engine's ASPLIT). The part
+ * buffer must hold T*H*ns*(256+2) floats. No counterpart in the reference (ASPLIT is a constant there). */
+int moex_decode_splits(int n_ctx);
+/* Library build identifier. */
+const char* moex_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

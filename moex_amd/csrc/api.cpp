@@ -1,0 +1,185 @@
+// extern "C" entry points of libmoex_attn (include/moex_attn.h): argument checks, the reference's dispatch
+// (kernels.cuh:1846-1865) and error handling (kernels.cuh:8-11). Host code only; kernels are launched through the
+// internal launchers of the .hip files.
+#include <hip/hip_runtime.h>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include "common.hpp"
+
+namespace moex {
+
+static int* g_soft = nullptr;  // kernels.cuh:8 (g_soft_ck)
+
+void report(hipError_t e, const char* file, int line) {
+    if (g_soft) {
+        if (!*g_soft) *g_soft = (int)e;
+        return;
+    }
+    fprintf(stderr, "HIP %s at %s:%d\n", hipGetErrorString(e), file, line);
+    exit(1);
+}
+
+static bool arg_fail(const char* what) {
+    if (g_soft) {
+        if (!*g_soft) *g_soft = (int)hipErrorInvalidValue;
+        return true;
+    }
+    fprintf(stderr, "moex_attn: invalid argument: %s\n", what);
+    exit(1);
+}
+#define MOEX_REQUIRE(cond, what) do { if (!(cond)) { arg_fail(what); return; } } while (0)
+
+static inline hipStream_t S(void* st) { return reinterpret_cast<hipStream_t>(st); }
+
+}  // namespace moex
+
+using namespace moex;
+
+extern "C" {
+
+moex_kv_cache moex_kv_alloc(int KV, int max_t, int turbo) {
+    moex_kv_cache c;
+    memset(&c, 0, sizeof c);
+    c.turbo = turbo ? 1 : 0;
+    const size_t kb = turbo ? TQ_KB : AHD, vb = turbo ? TQ_VB : AHD, ns = turbo ? 2 : 1;
+    MOEX_CK(hipMalloc(&c.k, (size_t)KV * max_t * kb));
+    MOEX_CK(hipMalloc(&c.v, (size_t)KV * max_t * vb));
+    MOEX_CK(hipMalloc(&c.ks, (size_t)KV * max_t * ns * 4));
+    MOEX_CK(hipMalloc(&c.vs, (size_t)KV * max_t * ns * 4));
+    return c;
+}
+
+size_t moex_kv_bytes(int KV, int max_t, int turbo) {
+    return (size_t)KV * max_t * (turbo ? TQ_KB + TQ_VB + 16 : 2 * AHD + 8);
+}
+
+void moex_kv_free(moex_kv_cache kv) {
+    if (kv.k) MOEX_CK(hipFree(kv.k));
+    if (kv.v) MOEX_CK(hipFree(kv.v));
+    if (kv.ks) MOEX_CK(hipFree(kv.ks));
+    if (kv.vs) MOEX_CK(hipFree(kv.vs));
+}
+
+int moex_fa_on(void) {  // kernels.cuh:1699-1702
+    static const int on = !(getenv("MOEX_FA") && atoi(getenv("MOEX_FA")) == 0);
+    return on;
+}
+
+int moex_fa_supported(void) {  // kernels.cuh:1705-1712, asked per device
+    static int arch[64] = {};  // 0 = not asked, 1 = gfx950, 2 = other
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (!arch[dev]) {
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, dev) != hipSuccess) return 0;
+        arch[dev] = strncmp(p.gcnArchName, "gfx950", 6) == 0 ? 1 : 2;
+    }
+    return arch[dev] == 1;
+}
+
+int moex_decode_splits(int n_ctx) {
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
+    }
+    // two workgroups per CU over both kv heads, but at least ~256 keys per split
+    int ns = (n_ctx + 255) / 256;
+    if (ns > cus) ns = cus;
+    return ns < 1 ? 1 : ns;
+}
+
+const char* moex_version(void) { return "moex_attn gfx950 0.1"; }
+
+void moex_set_soft_error(int* slot) { g_soft = slot; }
+
+void moex_set_skip(int value, void* stream) { launch_set_skip(value, S(stream)); }
+
+void moex_set_int(int* p, int v, void* stream) { launch_set_int(p, v, S(stream)); }
+
+void moex_qk_norm_rope(const float* q, const float* k, const float* v, const uint16_t* qn, const uint16_t* kn,
+                       float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, int rot, float theta,
+                       float eps, int ld, int T, void* stream) {
+    MOEX_REQUIRE(H > 0 && KV > 0 && H % KV == 0 && T > 0, "H, KV, T");
+    MOEX_REQUIRE(rot >= 0 && rot <= AHD && rot % 2 == 0, "rot");
+    launch_qk_norm_rope(q, k, v, qn, kn, qo, kv, H, KV, pos_d, max_t, rot, theta, eps, ld, T, S(stream));
+}
+
+void moex_kv_append(const float* k, const float* v, moex_kv_cache kv, int KV, const int* pos_d, int max_t, int ld,
+                    int T, void* stream) {
+    MOEX_REQUIRE(KV > 0 && T > 0, "KV, T");
+    launch_kv_append(k, v, kv, KV, pos_d, max_t, ld, T, S(stream));
+}
+
+void moex_attn_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part, int T,
+                   int ns, void* stream) {
+    MOEX_REQUIRE(KV > 0 && H == KV * GQ, "the GQA kernel needs H / KV == 8");
+    MOEX_REQUIRE(T > 0 && ns > 0 && part, "T, ns, part");
+    launch_gqa(qo, kv, H, KV, pos_d, max_t, part, T, ns, S(stream));
+}
+
+void moex_attn_combine(const float* part, const float* q_gate, float* out, int H, int ns, int ld, int T, void* stream) {
+    MOEX_REQUIRE(H > 0 && T > 0 && ns > 0, "H, T, ns");
+    launch_combine(part, q_gate, out, H, ns, ld, T, 0, S(stream));
+}
+
+void moex_attn_decode_heads(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
+                            const int* pos_d, int max_t, int ld, float* part, int T, int ns, void* stream) {
+    MOEX_REQUIRE(H > 0 && KV > 0 && H % KV == 0 && T > 0 && ns > 0, "H, KV, T, ns");
+    MOEX_REQUIRE(ns == 1 || part, "part is needed when ns > 1");
+    launch_decode_heads(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, part, T, ns, S(stream));
+}
+
+void moex_turbo_out(float* out, const float* q_gate, int H, int ld, int T, void* stream) {
+    MOEX_REQUIRE(H > 0 && T > 0 && q_gate, "H, T, q_gate");
+    launch_turbo_out(out, q_gate, H, ld, T, S(stream));
+}
+
+void moex_attn_fa(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d,
+                  int max_t, int ld, int T, void* stream) {
+    MOEX_REQUIRE(KV > 0 && H == KV * GQ, "attn_fa needs H / KV == 8");
+    MOEX_REQUIRE(T > 0, "T");
+    if (!moex_fa_supported()) {  // kernels.cuh:1715-1719: outside gfx950 keep the simpler kernels
+        if (kv.turbo) launch_decode_heads(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, nullptr, T, 1, S(stream));
+        else launch_prefill_k7p(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, S(stream));
+        return;
+    }
+    launch_fa(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, S(stream));
+}
+
+void moex_attn_prefill(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
+                       const int* pos_d, int max_t, int ld, int T, void* stream) {
+    MOEX_REQUIRE(KV > 0 && H == KV * GQ, "attn_prefill needs H / KV == 8");
+    MOEX_REQUIRE(!kv.turbo, "attn_prefill reads int8 KV only");
+    MOEX_REQUIRE(T > 0, "T");
+    launch_prefill_k7p(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, S(stream));
+}
+
+void moex_attn_decode(const float* q, const float* k, const float* v, const uint16_t* qn, const uint16_t* kn, float* qo,
+                      moex_kv_cache kv, float* out, int H, int KV, const int* pos_d, int max_t, int rot, float theta,
+                      float eps, int T, int ld, void* stream, float* part, int ns) {
+    MOEX_REQUIRE(H > 0 && KV > 0 && H % KV == 0 && T > 0 && ns > 0, "H, KV, T, ns");
+    MOEX_REQUIRE(ns == 1 || part, "part is needed when ns > 1");
+    MOEX_REQUIRE(rot >= 0 && rot <= AHD && rot % 2 == 0, "rot");
+    hipStream_t st = S(stream);
+    launch_qk_norm_rope(q, k, v, qn, kn, qo, kv, H, KV, pos_d, max_t, rot, theta, eps, ld, T, st);
+    const int G = H / KV;
+    const float* gate = kv.turbo ? nullptr : q;  // turbo: gated after the inverse rotation
+    bool rotated = false;
+    if (T > 2 && ns == 1 && G == GQ && (moex_fa_on() || kv.turbo) && moex_fa_supported()) {
+        launch_fa(qo, gate, kv, out, H, KV, pos_d, max_t, ld, T, st);
+    } else if (T > 2 && ns == 1 && G == GQ && !kv.turbo) {
+        launch_prefill_k7p(qo, q, kv, out, H, KV, pos_d, max_t, ld, T, st);
+    } else if (ns > 1 && G == GQ) {
+        launch_gqa(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
+        launch_combine(part, q, out, H, ns, ld, T, kv.turbo, st);  // turbo: inverse WHT + gate fused in
+        rotated = true;
+    } else {
+        launch_decode_heads(qo, gate, kv, out, H, KV, pos_d, max_t, ld, part, T, ns, st);
+        if (ns > 1) launch_combine(part, gate, out, H, ns, ld, T, 0, st);
+    }
+    if (kv.turbo && !rotated) launch_turbo_out(out, q, H, ld, T, st);
+}
+
+}  // extern "C"

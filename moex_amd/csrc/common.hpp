@@ -1,0 +1,73 @@
+// Shared constants, device helpers and internal launcher declarations of libmoex_attn (gfx950 only).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "../../include/moex_attn.h"
+
+namespace moex {
+
+constexpr int AHD = 256;                  // head dim (kernels.cuh:1111)
+constexpr int TQ_KB = 128, TQ_VB = 96;    // turbo bytes per row (kernels.cuh:1122)
+constexpr int GQ = 8;                     // query heads per KV head on the GQA paths
+
+// error plumbing (api.cpp): HIP errors abort like the reference's CK, or go to the soft slot
+void report(hipError_t e, const char* file, int line);
+#define MOEX_CK(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) ::moex::report(e_, __FILE__, __LINE__); } while (0)
+#define MOEX_LAUNCHED() MOEX_CK(hipGetLastError())
+
+// ---- int8 -> fp16 widening (exact) ----
+// fp16 0x64XX = 1024 + XX. A signed byte b stored as (b ^ 0x80) = b + 128, so 0x64(b+128) - 1152 = b.
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ half2_t u2h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ __forceinline__ uint32_t h22u(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// Biased bytes (b + 128) in w -> two fp16 pairs: lo = bytes 0,1, hi = bytes 2,3.
+__device__ __forceinline__ void biased4_to_h4(uint32_t u, uint32_t& lo, uint32_t& hi) {
+    const half2_t off = u2h2(0x64806480u);  // {1152, 1152}
+    const uint32_t l = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t h = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    lo = h22u(u2h2(l) - off);
+    hi = h22u(u2h2(h) - off);
+}
+__device__ __forceinline__ void i8x4_to_h4(uint32_t w, uint32_t& lo, uint32_t& hi) { biased4_to_h4(w ^ 0x80808080u, lo, hi); }
+
+// 8 int8 (two dwords) -> one MFMA operand of 8 fp16
+__device__ __forceinline__ half8_t i8x8_to_h8(uint32_t a, uint32_t b) {
+    uint32_t r0, r1, r2, r3;
+    i8x4_to_h4(a, r0, r1);
+    i8x4_to_h4(b, r2, r3);
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 u = {r0, r1, r2, r3};
+    return __builtin_bit_cast(half8_t, u);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace moex
+
+// ---- internal launchers (each defined in its .hip file; argument checks happen in api.cpp) ----
+namespace moex {
+void launch_qk_norm_rope(const float* q, const float* k, const float* v, const uint16_t* qn, const uint16_t* kn,
+                         float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, int rot,
+                         float theta, float eps, int ld, int T, hipStream_t st);
+void launch_kv_append(const float* k, const float* v, moex_kv_cache kv, int KV, const int* pos_d, int max_t, int ld,
+                      int T, hipStream_t st);
+void launch_turbo_out(float* out, const float* q_gate, int H, int ld, int T, hipStream_t st);
+void launch_combine(const float* part, const float* q_gate, float* out, int H, int ns, int ld, int T, int turbo_rot,
+                    hipStream_t st);
+void launch_decode_heads(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
+                         const int* pos_d, int max_t, int ld, float* part, int T, int ns, hipStream_t st);
+void launch_set_int(int* p, int v, hipStream_t st);
+void launch_set_skip(int v, hipStream_t st);
+void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part, int T,
+                int ns, hipStream_t st);
+void launch_fa(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d,
+               int max_t, int ld, int T, hipStream_t st);
+void launch_prefill_k7p(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
+                        const int* pos_d, int max_t, int ld, int T, hipStream_t st);
+}  // namespace moex

@@ -1,0 +1,376 @@
+// Small kernels of the attention step: q/k RMSNorm + partial RoPE + KV quantize-append (int8 and TurboQuant),
+// the per-query-head decode kernel, the split combine (+ gate, + turbo inverse rotation) and turbo_out.
+//
+// The quantizer arithmetic must reproduce the reference's bits (kernels.cuh:1141-1236): no FMA contraction,
+// correctly rounded divide and square root, the 32-lane butterfly order of warp_sum and the in-order sum of the
+// four 32-lane partials of each 128-value half (tq_half_sum). A 256-thread block holds one head row, thread d
+// owns dim d; on a 64-wide wavefront an xor-shuffle with offset <= 16 never leaves its 32-lane half, so the
+// reference's warp tree is reproduced exactly. The WHT's stage 32 is a shuffle too (dims d and d^32 share a
+// wavefront); only stage 64 crosses wavefronts and goes through LDS.
+#pragma clang fp contract(off)
+#include "common.hpp"
+
+namespace moex {
+
+// TurboQuant constants (kernels.cuh:1123-1139): sign tables, centroid codes, decision thresholds.
+__constant__ float c_S1[128] = {
+    -1, 1, 1,-1,-1, 1,-1, 1,-1,-1, 1, 1, 1, 1, 1, 1, 1,-1, 1,-1, 1,-1,-1, 1, 1, 1,-1, 1, 1,-1,-1,-1,
+    -1, 1, 1,-1, 1, 1,-1, 1,-1, 1, 1,-1,-1, 1,-1, 1, 1, 1, 1,-1,-1,-1,-1,-1, 1,-1, 1, 1, 1, 1,-1, 1,
+    -1,-1, 1,-1,-1,-1, 1,-1,-1,-1, 1,-1,-1,-1, 1, 1, 1,-1,-1, 1, 1, 1,-1,-1, 1, 1,-1, 1, 1,-1, 1,-1,
+    -1, 1, 1,-1, 1,-1, 1,-1, 1, 1, 1, 1,-1, 1,-1, 1, 1,-1, 1, 1,-1,-1,-1,-1,-1, 1, 1,-1, 1, 1,-1, 1};
+__constant__ float c_S2[128] = {
+     1, 1, 1, 1,-1, 1, 1,-1, 1,-1,-1,-1, 1,-1,-1,-1, 1, 1,-1,-1, 1,-1, 1,-1, 1,-1,-1, 1,-1, 1, 1, 1,
+     1, 1,-1,-1,-1, 1,-1,-1,-1,-1,-1,-1, 1, 1, 1,-1, 1,-1, 1, 1, 1,-1,-1, 1,-1,-1,-1,-1,-1,-1, 1, 1,
+     1,-1, 1,-1,-1,-1,-1, 1,-1, 1,-1, 1,-1,-1, 1, 1,-1, 1,-1, 1, 1,-1, 1,-1,-1,-1,-1, 1,-1,-1, 1,-1,
+     1,-1, 1, 1, 1,-1,-1, 1,-1, 1,-1, 1, 1,-1,-1, 1,-1, 1,-1, 1, 1,-1, 1,-1, 1,-1,-1,-1,-1,-1, 1,-1};
+__constant__ int8_t c_I4[16] = {-127, -96, -75, -58, -44, -31, -18, -6, 6, 18, 31, 44, 58, 75, 96, 127};
+__constant__ int8_t c_I3[8] = {-127, -79, -45, -14, 14, 45, 79, 127};
+__constant__ float c_M4[15] = {-0.212203f, -0.162947f, -0.127026f, -0.097164f, -0.070671f, -0.046174f, -0.022824f, 0.f,
+                               0.022824f, 0.046174f, 0.070671f, 0.097164f, 0.127026f, 0.162947f, 0.212203f};
+__constant__ float c_M3[7] = {-0.154496f, -0.092804f, -0.044243f, 0.f, 0.044243f, 0.092804f, 0.154496f};
+constexpr float K4 = 0.241529f / 127.f, K3 = 0.190207f / 127.f;  // code scales (kernels.cuh:1135)
+
+// graph-fallback flag (kernels.cuh:46, g_skip): nonzero -> qk_norm_rope / turbo_out return at once
+__device__ int g_skip;
+
+// ---- block reductions over a 256-thread block (4 wavefronts of 64) ----
+__device__ __forceinline__ float sum32(float v) {  // 32-lane xor tree (kernels.cuh:13-16)
+#pragma unroll
+    for (int o = 16; o; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float max32(float v) {
+#pragma unroll
+    for (int o = 16; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+// sum over the thread's 128-value half: 32-lane trees, then ((s0 + s1) + s2) + s3 (kernels.cuh:1161-1169)
+__device__ __forceinline__ float half_sum(float v, float* sh8) {
+    v = sum32(v);
+    const int g = threadIdx.x >> 5;
+    __syncthreads();
+    if ((threadIdx.x & 31) == 0) sh8[g] = v;
+    __syncthreads();
+    const int b = g & ~3;
+    return ((sh8[b] + sh8[b + 1]) + sh8[b + 2]) + sh8[b + 3];
+}
+__device__ __forceinline__ float block_sum(float v, float* sh8) {
+    v = sum32(v);
+    const int g = threadIdx.x >> 5;
+    __syncthreads();
+    if ((threadIdx.x & 31) == 0) sh8[g] = v;
+    __syncthreads();
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) s += sh8[i];
+    return s;
+}
+__device__ __forceinline__ float block_max(float v, float* sh8) {
+    v = max32(v);
+    const int g = threadIdx.x >> 5;
+    __syncthreads();
+    if ((threadIdx.x & 31) == 0) sh8[g] = v;
+    __syncthreads();
+    float m = sh8[0];
+#pragma unroll
+    for (int i = 1; i < 8; i++) m = fmaxf(m, sh8[i]);
+    return m;
+}
+
+// WHT of both 128-value halves of the block's row (kernels.cuh:1143-1159); dir 0 forward, 1 inverse.
+__device__ __forceinline__ float wht(float x, float* sh, int dir) {
+    const int d = threadIdx.x, j = d & 127;
+    float v = x * (dir ? c_S2[j] : c_S1[j]);
+#pragma unroll
+    for (int h = 1; h < 64; h <<= 1) {  // stages 1..32: within the wavefront
+        const float o = __shfl_xor(v, h);
+        v = (d & h) ? o - v : v + o;
+    }
+    __syncthreads();
+    sh[d] = v;
+    __syncthreads();
+    const float a = sh[d & ~64], b = sh[d | 64];  // stage 64: dims j and j ^ 64 (different wavefronts)
+    v = (j & 64) ? a - b : a + b;
+    return v * 0.08838834764831845f * (dir ? c_S1[j] : c_S2[j]);
+}
+
+// TurboQuant code of x (thread d of the row); norm_out = the half's corrected norm (kernels.cuh:1172-1183)
+template <int BITS>
+__device__ __forceinline__ int tq_quant(float x, float* sh, float* sh8, float& norm_out) {
+    const float n = sqrtf(half_sum(x * x, sh8));
+    const float r = wht(n > 1e-20f ? x / n : 0.f, sh, 0);
+    int idx = 0;
+    if (BITS == 4) {
+#pragma unroll
+        for (int i = 0; i < 15; i++) idx += r >= c_M4[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 7; i++) idx += r >= c_M3[i];
+    }
+    const float c = BITS == 4 ? (float)c_I4[idx] * K4 : (float)c_I3[idx] * K3;
+    const float rn = sqrtf(half_sum(c * c, sh8));
+    norm_out = rn > 1e-20f ? n / rn : n;
+    return idx;
+}
+
+// Quantize-append of one (kv head, position) row: x = post-RoPE k of dim d, vv = raw v of dim d.
+__device__ __forceinline__ void append_row(float x, float vv, moex_kv_cache kv, size_t row, float* sh, float* sh8) {
+    const int d = threadIdx.x;
+    if (kv.turbo) {  // K 4-bit, V 3-bit (kernels.cuh:1210-1226)
+        const int j = d & 127, b = d >> 7;
+        float nk, nv;
+        const int ik = tq_quant<4>(x, sh, sh8, nk);
+        const int iv = tq_quant<3>(vv, sh, sh8, nv);
+        uint8_t* K = reinterpret_cast<uint8_t*>(kv.k) + row * TQ_KB;
+        uint8_t* V = reinterpret_cast<uint8_t*>(kv.v) + row * TQ_VB;
+        const int ik1 = __shfl_down(ik, 1);
+        if (!(j & 1)) K[b * 64 + j / 2] = (uint8_t)(ik | (ik1 << 4));
+        const int lo = iv & 3;
+        const int q4 = lo | (__shfl_down(lo, 1) << 2) | (__shfl_down(lo, 2) << 4) | (__shfl_down(lo, 3) << 6);
+        if (!(j & 3)) V[b * 32 + j / 4] = (uint8_t)q4;
+        const unsigned long long hb = __ballot(iv & 4);
+        if (!(j & 7)) V[64 + b * 16 + j / 8] = (uint8_t)(hb >> (d & 63));
+        if (j == 0) { kv.ks[row * 2 + b] = nk; kv.vs[row * 2 + b] = nv; }
+    } else {  // int8 per row (kernels.cuh:1227-1235)
+        const float mk = block_max(fabsf(x), sh8), mv = block_max(fabsf(vv), sh8 + 8);
+        const float sk = mk > 0.f ? mk / 127.f : 1.f, sv = mv > 0.f ? mv / 127.f : 1.f;
+        const size_t o = row * AHD + d;
+        kv.k[o] = (int8_t)__builtin_rintf(x / sk);
+        kv.v[o] = (int8_t)__builtin_rintf(vv / sv);
+        if (d == 0) { kv.ks[row] = sk; kv.vs[row] = sv; }
+    }
+}
+
+// qk_norm_rope_k (kernels.cuh:1185-1236): grid (H + KV, T), 256 threads. Blocks [0, H): query heads -> qo;
+// [H, H+KV): key heads -> quantize-append of k and v at position *pos_d + token.
+__global__ void __launch_bounds__(256) qk_norm_rope_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const uint16_t* __restrict__ qn, const uint16_t* __restrict__ kn, float* __restrict__ qo, moex_kv_cache kv,
+    int H, int KV, const int* __restrict__ pos_d, int max_t, int rot, float theta, float eps, int ld) {
+    if (g_skip) return;
+    __shared__ float t[AHD];
+    __shared__ float sh[AHD];
+    __shared__ float sh8[16];
+    const int tok = blockIdx.y, pos = *pos_d + tok, hh = blockIdx.x, d = threadIdx.x;
+    q += (size_t)tok * ld; k += (size_t)tok * ld; v += (size_t)tok * ld; qo += (size_t)tok * H * AHD;
+    const bool isq = hh < H;
+    float x = isq ? q[hh * 2 * AHD + d] : k[(hh - H) * AHD + d];
+    const float r = rsqrtf(block_sum(x * x, sh8) / AHD + eps);
+    const float w = (float)__builtin_bit_cast(_Float16, (isq ? qn : kn)[d]);
+    x = x * r * (1.f + w);
+    t[d] = x;
+    __syncthreads();
+    const int h2 = rot / 2;
+    if (d < rot) {
+        const int j = d < h2 ? d : d - h2;
+        const float ang = (float)pos * powf(theta, -2.f * j / rot);
+        const float cs = cosf(ang), sn = sinf(ang);
+        x = d < h2 ? t[d] * cs - t[d + h2] * sn : t[d] * cs + t[d - h2] * sn;
+    }
+    if (isq) {
+        const float y = kv.turbo ? wht(x, sh, 0) : x;  // turbo: the keys' rotation (the block is uniform)
+        qo[hh * AHD + d] = y;
+    } else {
+        append_row(x, v[(hh - H) * AHD + d], kv, (size_t)(hh - H) * max_t + pos, sh, sh8);
+    }
+}
+
+// Quantize-append only: grid (KV, T); k already normalized and rotated.
+__global__ void __launch_bounds__(256) kv_append_kernel(const float* __restrict__ k, const float* __restrict__ v,
+                                                        moex_kv_cache kv, const int* __restrict__ pos_d, int max_t,
+                                                        int ld) {
+    __shared__ float sh[AHD];
+    __shared__ float sh8[16];
+    const int tok = blockIdx.y, kvh = blockIdx.x, d = threadIdx.x;
+    const size_t o = (size_t)tok * ld + kvh * AHD + d;
+    append_row(k[o], v[o], kv, (size_t)kvh * max_t + *pos_d + tok, sh, sh8);
+}
+
+// turbo_out_k (kernels.cuh:1730-1738): out = WHT_inv(out) / (1 + e^-g), in place. Grid (H, T).
+__global__ void __launch_bounds__(256) turbo_out_kernel(float* __restrict__ out, const float* __restrict__ q_gate,
+                                                        int H, int ld) {
+    if (g_skip) return;
+    __shared__ float sh[AHD];
+    const int h = blockIdx.x, tok = blockIdx.y, d = threadIdx.x;
+    float* o = out + ((size_t)tok * H + h) * AHD;
+    const float x = wht(o[d], sh, 1);
+    o[d] = x / (1.f + __expf(-q_gate[(size_t)tok * ld + h * 2 * AHD + AHD + d]));
+}
+
+// attn_combine_k (kernels.cuh:1317-1329): merge ns partials {m (log2 units), l, acc[256]}. Grid (H, T), 256
+// threads. turbo_rot: the merged row is rotated back (inverse WHT) before the gate, i.e. turbo_out fused in.
+__global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ part, const float* __restrict__ q_gate,
+                                                      float* __restrict__ out, int H, int ns, int ld, int turbo_rot) {
+    __shared__ float w[1024];
+    __shared__ float sh[AHD];
+    __shared__ float sh8[16];
+    const int tok = blockIdx.y, h = blockIdx.x, d = threadIdx.x;
+    const float* p = part + ((size_t)tok * H + h) * ns * (AHD + 2);
+    float M = -INFINITY;
+    for (int s = d; s < ns; s += 256) M = fmaxf(M, p[(size_t)s * (AHD + 2)]);
+    M = block_max(M, sh8);  // split 0 is never empty, so M is finite
+    float l = 0.f;
+    for (int s0 = 0; s0 < ns; s0 += 1024) {  // weights of up to 1024 splits at a time
+        const int n = min(1024, ns - s0);
+        __syncthreads();
+        for (int s = d; s < n; s += 256) {
+            const float* q = p + (size_t)(s0 + s) * (AHD + 2);
+            const float ws = q[1] > 0.f ? fast_exp2(q[0] - M) : 0.f;
+            w[s] = ws;
+            l += q[1] * ws;
+        }
+        __syncthreads();
+    }
+    l = block_sum(l, sh8);
+    float acc = 0.f;
+    for (int s0 = 0; s0 < ns; s0 += 1024) {
+        const int n = min(1024, ns - s0);
+        __syncthreads();
+        for (int s = d; s < n; s += 256) {
+            const float* q = p + (size_t)(s0 + s) * (AHD + 2);
+            w[s] = q[1] > 0.f ? fast_exp2(q[0] - M) : 0.f;
+        }
+        __syncthreads();
+        int s = 0;
+        for (; s + 4 <= n; s += 4) {
+            const float* q = p + (size_t)(s0 + s) * (AHD + 2) + 2 + d;
+            const float a0 = q[0], a1 = q[AHD + 2], a2 = q[2 * (AHD + 2)], a3 = q[3 * (AHD + 2)];
+            acc += w[s] * a0; acc += w[s + 1] * a1; acc += w[s + 2] * a2; acc += w[s + 3] * a3;
+        }
+        for (; s < n; s++) acc += w[s] * p[(size_t)(s0 + s) * (AHD + 2) + 2 + d];
+    }
+    float x = acc / l;
+    if (turbo_rot) x = wht(x, sh, 1);
+    if (q_gate) x = x / (1.f + __expf(-q_gate[(size_t)tok * ld + h * 2 * AHD + AHD + d]));
+    out[((size_t)tok * H + h) * AHD + d] = x;
+}
+
+// attn_decode_k (kernels.cuh:1238-1315): one block per (query head, token, split), 256 threads, any H / KV.
+// Keys in tiles of 1024 scores; one wavefront scores 4 keys at a time (16 lanes per key, 16 dims per lane);
+// base-2 online softmax; thread d accumulates dim d. ns == 1: gated output; else partials.
+constexpr int DT = 1024;
+__global__ void __launch_bounds__(256) decode_heads_kernel(const float* __restrict__ qo, const float* __restrict__ q_gate,
+                                                           moex_kv_cache kv, float* __restrict__ out, int H, int KV,
+                                                           const int* __restrict__ pos_d, int max_t, int ld,
+                                                           float* __restrict__ part) {
+    __shared__ float sc[DT];
+    __shared__ __align__(16) float qs[AHD];
+    __shared__ float c4[16], c3[8], sh8[16];
+    const int tok = blockIdx.y, Tk = *pos_d + tok + 1;
+    const int ns = gridDim.z, L = (Tk + ns - 1) / ns, lo = blockIdx.z * L, hi = min(Tk, lo + L);
+    const int h = blockIdx.x, kvh = h / (H / KV), tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    qo += (size_t)tok * H * AHD;
+    if (q_gate) q_gate += (size_t)tok * ld;
+    out += (size_t)tok * H * AHD;
+    qs[tid] = qo[h * AHD + tid];
+    if (tid < 16) c4[tid] = (float)c_I4[tid] * K4;
+    if (tid < 8) c3[tid] = (float)c_I3[tid] * K3;
+    __syncthreads();
+    const bool tb = kv.turbo;
+    const float sl2 = 0.0625f * 1.4426950408889634f;  // 1/sqrt(256) * log2(e)
+    const size_t rbase = (size_t)kvh * max_t;
+    // turbo V of dim tid: low 2 bits at byte vq (shift vsh), high bit at byte vg (bit vgb)
+    const int vq = (tid >> 7) * 32 + ((tid & 127) >> 2), vsh = 2 * (tid & 3), vg = 64 + (tid >> 7) * 16 + ((tid & 127) >> 3), vgb = tid & 7;
+    const int sub = lane >> 4, l16 = lane & 15;  // key slot within the wavefront, lane within the key
+    float m = -INFINITY, l = 0.f, acc = 0.f;
+    for (int t0 = lo; t0 < hi; t0 += DT) {
+        const int n = min(DT, hi - t0);
+        for (int i = wv * 4 + sub; i < n; i += 16) {  // 16 lanes per key, dims l16*16 .. +15
+            const size_t row = rbase + t0 + i;
+            float s = 0.f;
+            if (tb) {  // 8 bytes of nibbles = 16 dims of half l16 / 8
+                const uint2 u = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(kv.k) + row * TQ_KB + (l16 >> 3) * 64 + (l16 & 7) * 8);
+                const uint32_t w2[2] = {u.x, u.y};
+#pragma unroll
+                for (int a = 0; a < 2; a++)
+#pragma unroll
+                    for (int b = 0; b < 8; b++) s += c4[(w2[a] >> (4 * b)) & 15] * qs[l16 * 16 + a * 8 + b];
+                s *= kv.ks[row * 2 + (l16 >> 3)];
+            } else {
+                const uint4 u = *reinterpret_cast<const uint4*>(kv.k + row * AHD + l16 * 16);
+                const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int a = 0; a < 4; a++)
+#pragma unroll
+                    for (int b = 0; b < 4; b++) s += (float)(int8_t)(w4[a] >> (8 * b)) * qs[l16 * 16 + a * 4 + b];
+            }
+#pragma unroll
+            for (int o = 8; o; o >>= 1) s += __shfl_xor(s, o);
+            if (l16 == 0) sc[i] = s * (tb ? 1.f : kv.ks[row]) * sl2;
+        }
+        __syncthreads();
+        float mt = -INFINITY;
+        for (int i = tid; i < n; i += 256) mt = fmaxf(mt, sc[i]);
+        const float mn = fmaxf(m, block_max(mt, sh8)), c = fast_exp2(m - mn);  // m = -inf on the first tile: c = 0
+        float s = 0.f;
+        for (int i = tid; i < n; i += 256) {
+            const float e = fast_exp2(sc[i] - mn);
+            s += e;
+            sc[i] = tb ? e : e * kv.vs[rbase + t0 + i];  // V's scale folded in
+        }
+        l = l * c + block_sum(s, sh8 + 8);  // syncs: sc[] complete after it
+        acc *= c;
+        if (tb) {
+            const uint8_t* Vt = reinterpret_cast<const uint8_t*>(kv.v) + (rbase + t0) * TQ_VB;
+            const float* vn = kv.vs + (rbase + t0) * 2 + (tid >> 7);
+            for (int i = 0; i < n; i++) {
+                const uint8_t* r = Vt + (size_t)i * TQ_VB;
+                acc += sc[i] * (c3[((r[vq] >> vsh) & 3) | (((r[vg] >> vgb) & 1) << 2)] * vn[(size_t)i * 2]);
+            }
+        } else {
+            const int8_t* V = kv.v + (rbase + t0) * AHD + tid;
+            for (int i = 0; i < n; i++) acc += sc[i] * (float)V[(size_t)i * AHD];
+        }
+        m = mn;
+        __syncthreads();  // sc[] is overwritten by the next tile
+    }
+    if (ns == 1) {
+        out[h * AHD + tid] = q_gate ? acc / l / (1.f + __expf(-q_gate[h * 2 * AHD + AHD + tid])) : acc / l;
+        return;
+    }
+    float* p = part + (((size_t)tok * H + h) * ns + blockIdx.z) * (AHD + 2);
+    p[2 + tid] = acc;
+    if (tid == 0) { p[0] = m; p[1] = l; }  // an empty split leaves m = -inf, l = 0, acc = 0
+}
+
+__global__ void set_int_kernel(int* p, int v) { *p = v; }
+__global__ void set_skip_kernel(int v) { g_skip = v; }
+
+// ---- launchers ----
+void launch_qk_norm_rope(const float* q, const float* k, const float* v, const uint16_t* qn, const uint16_t* kn,
+                         float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, int rot,
+                         float theta, float eps, int ld, int T, hipStream_t st) {
+    hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(H + KV, T), dim3(256), 0, st, q, k, v, qn, kn, qo, kv, H, KV, pos_d,
+                       max_t, rot, theta, eps, ld);
+    MOEX_LAUNCHED();
+}
+void launch_kv_append(const float* k, const float* v, moex_kv_cache kv, int KV, const int* pos_d, int max_t, int ld,
+                      int T, hipStream_t st) {
+    hipLaunchKernelGGL(kv_append_kernel, dim3(KV, T), dim3(256), 0, st, k, v, kv, pos_d, max_t, ld);
+    MOEX_LAUNCHED();
+}
+void launch_turbo_out(float* out, const float* q_gate, int H, int ld, int T, hipStream_t st) {
+    hipLaunchKernelGGL(turbo_out_kernel, dim3(H, T), dim3(256), 0, st, out, q_gate, H, ld);
+    MOEX_LAUNCHED();
+}
+void launch_combine(const float* part, const float* q_gate, float* out, int H, int ns, int ld, int T, int turbo_rot,
+                    hipStream_t st) {
+    hipLaunchKernelGGL(combine_kernel, dim3(H, T), dim3(256), 0, st, part, q_gate, out, H, ns, ld, turbo_rot);
+    MOEX_LAUNCHED();
+}
+void launch_decode_heads(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
+                         const int* pos_d, int max_t, int ld, float* part, int T, int ns, hipStream_t st) {
+    hipLaunchKernelGGL(decode_heads_kernel, dim3(H, T, ns), dim3(256), 0, st, qo, q_gate, kv, out, H, KV, pos_d, max_t,
+                       ld, part);
+    MOEX_LAUNCHED();
+}
+void launch_set_int(int* p, int v, hipStream_t st) {
+    hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, st, p, v);
+    MOEX_LAUNCHED();
+}
+void launch_set_skip(int v, hipStream_t st) {
+    hipLaunchKernelGGL(set_skip_kernel, dim3(1), dim3(1), 0, st, v);
+    MOEX_LAUNCHED();
+}
+
+}  // namespace moex

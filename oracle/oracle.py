@@ -1,0 +1,156 @@
+"""ctypes/numpy face of the CPU oracle (oracle/moex_oracle.c). TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as the
+checker (or the timed CPU baseline). The product path never imports it.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = os.path.join(_HERE, "liboracle.so")
+AHD = 256
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB):
+            build()
+        L = ctypes.CDLL(_LIB)
+        c = ctypes
+        L.orc_tq_tables.argtypes = [_f32p, _f32p, _i8p, _i8p, _f32p, _f32p, _f32p]
+        L.orc_round_f16_array.argtypes = [_f32p, _f32p, c.c_long]
+        L.orc_int8_quant_row.argtypes = [_f32p, _i8p, _f32p]
+        L.orc_tq_half_sum.argtypes = [_f32p]
+        L.orc_tq_half_sum.restype = c.c_float
+        L.orc_tq_wht.argtypes = [_f32p, _f32p, c.c_int]
+        L.orc_tq_quant.argtypes = [_f32p, c.c_int, _i32p, _f32p]
+        L.orc_turbo_pack.argtypes = [_i32p, _i32p, _u8p, _u8p]
+        L.orc_turbo_unpack.argtypes = [_u8p, _u8p, _i32p, _i32p]
+        L.orc_kv_append.argtypes = [_f32p, _f32p, c.c_long, c.c_int, c.c_int, c.c_int, c.c_int, c.c_int,
+                                    c.c_void_p, c.c_void_p, _f32p, _f32p]
+        rows_args = [_f32p, c.c_void_p, c.c_long, c.c_int, c.c_int, c.c_void_p, c.c_void_p, _f32p, _f32p,
+                     c.c_int, c.c_int, c.c_int, _i32p, c.c_int, _f64p]
+        L.orc_attn_rows_f64.argtypes = rows_args
+        L.orc_attn_rows_fa_emul.argtypes = rows_args
+        L.orc_qk_norm_rope_row.argtypes = [_f32p, _u16p, c.c_int, c.c_int, c.c_float, c.c_float, c.c_int, _f32p]
+        _lib = L
+    return _lib
+
+
+def tables():
+    s1 = np.zeros(128, np.float32); s2 = np.zeros(128, np.float32)
+    i4 = np.zeros(16, np.int8); i3 = np.zeros(8, np.int8)
+    k = np.zeros(2, np.float32); m4 = np.zeros(15, np.float32); m3 = np.zeros(7, np.float32)
+    lib().orc_tq_tables(s1, s2, i4, i3, k, m4, m3)
+    return dict(S1=s1, S2=s2, I4=i4, I3=i3, K4=k[0], K3=k[1], M4=m4, M3=m3)
+
+
+def round_f16(x):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_round_f16_array(x.reshape(-1), y.reshape(-1), x.size)
+    return y
+
+
+def int8_quant_row(x):
+    x = np.ascontiguousarray(x, np.float32)
+    q = np.zeros(AHD, np.int8); s = np.zeros(1, np.float32)
+    lib().orc_int8_quant_row(x, q, s)
+    return q, s[0]
+
+
+def half_sum(v128):
+    return np.float32(lib().orc_tq_half_sum(np.ascontiguousarray(v128, np.float32)))
+
+
+def wht(x, inverse=False):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.zeros(AHD, np.float32)
+    lib().orc_tq_wht(x, y, 1 if inverse else 0)
+    return y
+
+
+def tq_quant(x, bits):
+    idx = np.zeros(AHD, np.int32); n = np.zeros(2, np.float32)
+    lib().orc_tq_quant(np.ascontiguousarray(x, np.float32), bits, idx, n)
+    return idx, n
+
+
+def turbo_pack(ik, iv):
+    kb = np.zeros(128, np.uint8); vb = np.zeros(96, np.uint8)
+    lib().orc_turbo_pack(np.ascontiguousarray(ik, np.int32), np.ascontiguousarray(iv, np.int32), kb, vb)
+    return kb, vb
+
+
+def turbo_unpack(kb, vb):
+    ik = np.zeros(AHD, np.int32); iv = np.zeros(AHD, np.int32)
+    lib().orc_turbo_unpack(np.ascontiguousarray(kb, np.uint8), np.ascontiguousarray(vb, np.uint8), ik, iv)
+    return ik, iv
+
+
+class HostCache:
+    """Host copy of a KVCache (kernels.cuh:1121): int8 k,v [KV][max_t][256] + ks,vs [KV][max_t], or turbo
+    k [KV][max_t][128], v [KV][max_t][96] (uint8) + ks,vs [KV][max_t][2]."""
+
+    def __init__(self, KV, max_t, turbo):
+        self.KV, self.max_t, self.turbo = KV, max_t, int(turbo)
+        kb, vb, ns = (128, 96, 2) if turbo else (AHD, AHD, 1)
+        self.k = np.zeros((KV, max_t, kb), np.int8)
+        self.v = np.zeros((KV, max_t, vb), np.int8)
+        self.ks = np.zeros((KV, max_t, ns), np.float32) if turbo else np.zeros((KV, max_t), np.float32)
+        self.vs = np.zeros_like(self.ks)
+
+
+def kv_append(cache, k, v, ld, T, pos0):
+    """Quantize-append T tokens (k, v: float32 arrays, token stride ld)."""
+    k = np.ascontiguousarray(k, np.float32).reshape(-1)
+    v = np.ascontiguousarray(v, np.float32).reshape(-1)
+    lib().orc_kv_append(k, v, ld, T, cache.KV, pos0, cache.max_t, cache.turbo,
+                        cache.k.ctypes.data, cache.v.ctypes.data, cache.ks.reshape(-1), cache.vs.reshape(-1))
+
+
+def _rows(fn, qo, gate, ld, H, cache, pos0, rows):
+    qo = np.ascontiguousarray(qo, np.float32).reshape(-1)
+    rows = np.ascontiguousarray(np.asarray(rows, np.int32).reshape(-1))
+    out = np.zeros((len(rows) // 2, AHD), np.float64)
+    g = None
+    if gate is not None:
+        g = np.ascontiguousarray(gate, np.float32).reshape(-1)
+    fn(qo, None if g is None else g.ctypes.data, ld, H, cache.KV, cache.k.ctypes.data, cache.v.ctypes.data,
+       cache.ks.reshape(-1), cache.vs.reshape(-1), cache.max_t, cache.turbo, pos0, rows, len(rows) // 2, out.reshape(-1))
+    return out
+
+
+def attn_rows_f64(qo, gate, ld, H, cache, pos0, rows):
+    """fp64 reference attention for (token, head) rows (tests/test_fa.cu:59-80; turbo: + inverse WHT)."""
+    return _rows(lib().orc_attn_rows_f64, qo, gate, ld, H, cache, pos0, rows)
+
+
+def attn_rows_fa_emul(qo, gate, ld, H, cache, pos0, rows):
+    """Precision model of the reference attn_fa_k (fp16 Q, fp16 P*vscale, fp32 softmax): its error estimate."""
+    return _rows(lib().orc_attn_rows_fa_emul, qo, gate, ld, H, cache, pos0, rows)
+
+
+def qk_norm_rope_row(x, w_f16_bits, pos, rot, theta, eps, wht_fwd=False):
+    out = np.zeros(AHD, np.float32)
+    lib().orc_qk_norm_rope_row(np.ascontiguousarray(x, np.float32), np.ascontiguousarray(w_f16_bits, np.uint16),
+                               pos, rot, theta, eps, 1 if wht_fwd else 0, out)
+    return out

@@ -1,0 +1,60 @@
+"""CPU checks of the C ABI: the library loads and exports every entry point include/moex_attn.h declares, the host
+mirror keeps the reference's names, and the product path never touches the oracle."""
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    txt = open(os.path.join(ROOT, "include", "moex_attn.h")).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(moex_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_header_declares_the_reference_entry_points():
+    names = _declared()
+    for n in ("moex_attn_decode", "moex_attn_fa", "moex_attn_prefill", "moex_kv_alloc", "moex_kv_bytes",
+              "moex_attn_gqa", "moex_attn_combine", "moex_attn_decode_heads", "moex_turbo_out", "moex_qk_norm_rope"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    import ctypes
+    import moex_amd
+    if not os.path.exists(moex_amd.LIB_PATH):
+        pytest.skip("libmoex_attn.so not built (run __graft_entry__.build())")
+    L = ctypes.CDLL(moex_amd.LIB_PATH)
+    missing = [n for n in _declared() if not hasattr(L, n)]
+    assert not missing, missing
+    assert sorted(moex_amd.EXPORTS) == _declared()
+
+
+def test_kv_bytes_formula():
+    import moex_amd
+    if not os.path.exists(moex_amd.LIB_PATH):
+        pytest.skip("libmoex_attn.so not built")
+    # kernels.cuh:1875: int8 520 B, turbo 240 B per (kv head, position)
+    assert moex_amd.kv_bytes(2, 90000, 0) == 2 * 90000 * 520
+    assert moex_amd.kv_bytes(2, 262144, 1) == 2 * 262144 * 240
+
+
+def test_python_mirror_keeps_reference_names():
+    import moex_amd
+    for n in ("attn_decode", "attn_fa", "attn_prefill", "kv_alloc", "kv_bytes", "attn_gqa", "attn_combine",
+              "attn_decode_heads", "turbo_out", "qk_norm_rope", "kv_append", "set_int"):
+        assert callable(getattr(moex_amd, n))
+
+
+def test_product_never_uses_the_oracle():
+    for dirpath, _, files in os.walk(os.path.join(ROOT, "moex_amd")):
+        for f in files:
+            if f.endswith((".py", ".hip", ".cpp", ".hpp", ".h")) or f == "Makefile":
+                txt = open(os.path.join(dirpath, f)).read()
+                assert "oracle" not in txt.replace("oracle/", ""), f
+    # the built library links nothing from oracle/
+    import moex_amd
+    if os.path.exists(moex_amd.LIB_PATH):
+        assert b"liboracle" not in open(moex_amd.LIB_PATH, "rb").read()

@@ -1,0 +1,109 @@
+"""The full attention step attn_decode (kernels.cuh:1846-1865): front + append + dispatch, int8 and turbo caches
+written from the same N(0,1) q/k/v (tests/test_fa.cu:141-200):
+  - turbo vs int8 outputs of the prefill chunk: cosine >= 0.97 (test_fa.cu:181);
+  - the last token again through the split GQA decode and the per-head decode: within 2% of max |FA output|
+    (test_fa.cu:198);
+  - int8 chunk output against the fp64 oracle fed with the kernel's own qo and cache (test_fa.cu:114 rule).
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests.gpu_util import AHD, H, KV, dev, download, pos_tensor, report, sample_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def test_attn_decode_paths():
+    import torch
+    import moex_amd as M
+    LQ = H * 2 * AHD + 2 * KV * AHD
+    T, pos0 = 512, 1500
+    ctx = pos0 + T + 8
+    c8, ct = M.DeviceKVCache(KV, ctx, 0), M.DeviceKVCache(KV, ctx, 1)
+    qn = torch.zeros(AHD, dtype=torch.int16, device="cuda")
+    kn = torch.zeros(AHD, dtype=torch.int16, device="cuda")
+    ns = 4
+    qo = torch.empty((T, H, AHD), dtype=torch.float32, device="cuda")
+    oa = torch.empty((T, H, AHD), dtype=torch.float32, device="cuda")
+    ob = torch.empty_like(oa)
+    part = torch.empty(T * H * ns * (AHD + 2), dtype=torch.float32, device="cuda")
+    g = torch.Generator(device="cuda").manual_seed(1)
+    qkv = torch.empty((T, LQ), dtype=torch.float32, device="cuda")
+    pos_d = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+    def run(c, out, p0, n, nsplit, pt, qov=qo):
+        M.set_int(pos_d, p0)
+        M.attn_decode(qkv, qkv[:, H * 2 * AHD:], qkv[:, H * 2 * AHD + KV * AHD:], qn, kn, qov, c, out, H, KV, pos_d,
+                      ctx, 64, 1e7, 1e-6, n, LQ, None, pt, nsplit)
+        torch.cuda.synchronize()
+
+    for p in range(0, pos0, T):  # context before the chunk, the same rows in both caches
+        n = min(T, pos0 - p)
+        qkv.normal_(generator=g)
+        run(c8, oa, p, n, 1, None)
+        run(ct, ob, p, n, 1, None)
+    qkv.normal_(generator=g)
+    run(c8, oa, pos0, T, 1, None)
+    qo8 = qo.clone()
+    run(ct, ob, pos0, T, 1, None)
+    a, b = oa.cpu().numpy().astype(np.float64), ob.cpu().numpy().astype(np.float64)
+    cs = float((a * b).sum() / np.sqrt((a * a).sum() * (b * b).sum()))
+    report("turbo vs int8 (FA path)", cosine=cs)
+    assert np.all(np.isfinite(b)) and cs >= 0.97
+
+    # int8 chunk vs the oracle on the kernel's own inputs
+    hc = download(c8)
+    q_host = qkv.cpu().numpy()
+    rows = sample_rows(T)
+    ref = orc.attn_rows_f64(qo8.cpu().numpy(), q_host, LQ, H, hc, pos0, rows)
+    emu = orc.attn_rows_fa_emul(qo8.cpu().numpy(), q_host, LQ, H, hc, pos0, rows)
+    got = np.stack([a[t, h] for t, h in rows])
+    mag = float(np.abs(ref).max())
+    e_new, e_ref = float(np.abs(got - ref).max()), float(np.abs(emu - ref).max())
+    report("attn_decode int8 chunk vs fp64", e_new=e_new, e_ref=e_ref, mag=mag)
+    assert e_new <= 2 * e_ref + 1e-3 * mag
+
+    # the last token again through the decode paths (its K/V rows are rewritten with the same values)
+    last = qkv[T - 1:T].clone()
+    qkv[:1].copy_(last)
+    d1 = torch.empty((1, H, AHD), dtype=torch.float32, device="cuda")
+    d2 = torch.empty_like(d1)
+    q1 = torch.empty((1, H, AHD), dtype=torch.float32, device="cuda")
+    for cache, full in ((ct, b), (c8, a)):
+        run(cache, d1, pos0 + T - 1, 1, ns, part, q1)   # GQA split + combine
+        run(cache, d2, pos0 + T - 1, 1, 1, None, q1)    # per-head kernel
+        f = full[T - 1]
+        e1 = float(np.abs(d1.cpu().numpy()[0] - f).max())
+        e2 = float(np.abs(d2.cpu().numpy()[0] - f).max())
+        mg = float(np.abs(f).max())
+        report("last token decode vs FA", turbo=cache.turbo, e_gqa=e1, e_heads=e2, mag=mg)
+        assert e1 < 0.02 * mg and e2 < 0.02 * mg
+
+
+def test_skip_flag_and_soft_errors():
+    """g_skip makes the append/front and turbo_out return at once (kernels.cuh:1189,1732); argument errors go to the
+    soft slot instead of exiting while it is installed (kernels.cuh:8-11)."""
+    import ctypes
+    import torch
+    import moex_amd as M
+    T, max_t = 4, 16
+    cache = M.DeviceKVCache(KV, max_t, 0)
+    cache.k.zero_(); cache.ks.zero_()
+    LQ = H * 2 * AHD + 2 * KV * AHD
+    k = torch.ones((T, LQ), dtype=torch.float32, device="cuda")
+    M.set_skip(1)
+    M.qk_norm_rope(k, k[:, H * 2 * AHD:], k[:, H * 2 * AHD + KV * AHD:], torch.zeros(AHD, dtype=torch.int16, device="cuda"),
+                   torch.zeros(AHD, dtype=torch.int16, device="cuda"), torch.empty((T, H, AHD), device="cuda"),
+                   cache, H, KV, pos_tensor(0), max_t, 64, 1e7, 1e-6, LQ, T)
+    torch.cuda.synchronize()
+    assert cache.ks.abs().sum().item() == 0
+    M.set_skip(0)
+    torch.cuda.synchronize()
+    slot = ctypes.c_int(0)
+    M.lib().moex_set_soft_error(ctypes.byref(slot))
+    try:
+        M.attn_fa(k, None, cache, k, 12, KV, pos_tensor(0), max_t, 0, T)  # H / KV == 6: unsupported
+    finally:
+        M.lib().moex_set_soft_error(None)
+    assert slot.value == 1  # hipErrorInvalidValue

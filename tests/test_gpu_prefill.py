@@ -1,0 +1,107 @@
+"""Chunked causal GQA prefill: attn_fa (kernels.cuh:1443-1728) and the int8 fallback attn_prefill (:1331-1441)
+against the fp64 oracle, with the acceptance rule of tests/test_fa.cu:114:
+
+    e_new <= 2 * e_ref + 1e-3 * mag
+
+where e_ref is the error of the reference kernel's arithmetic (the oracle's precision model of attn_fa_k: fp16 Q,
+fp16 P * vscale, fp32 softmax) on the same rows, mag = max |ref|. Cases and row sample follow test_fa.cu:82,95.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests.gpu_util import AHD, H, KV, LD, dev, download, pos_tensor, random_int8_cache, report, sample_rows, upload
+
+pytestmark = pytest.mark.gpu
+
+CASES = [(0, 37), (0, 1024), (5, 3), (1000, 100), (4093, 2048), (30000, 2048), (32768, 2048)]
+
+
+@pytest.fixture(scope="module")
+def setup():
+    max_t = 34816 + 64
+    hc = random_int8_cache(max_t, seed=1)
+    dc = upload(hc)
+    rng = np.random.default_rng(2)
+    qo = rng.uniform(-2, 2, (2048, H, AHD)).astype(np.float32)
+    qg = rng.uniform(-2, 2, (2048, LD)).astype(np.float32)
+    return hc, dc, qo, qg, dev(qo), dev(qg)
+
+
+def _gate(name, out, qo, qg, hc, pos0, T):
+    rows = sample_rows(T)
+    ref = orc.attn_rows_f64(qo, qg, LD, H, hc, pos0, rows)
+    emu = orc.attn_rows_fa_emul(qo, qg, LD, H, hc, pos0, rows)
+    got = np.stack([out[t, h] for t, h in rows])
+    mag = float(np.abs(ref).max())
+    e_new, e_ref = float(np.abs(got - ref).max()), float(np.abs(emu - ref).max())
+    report(name, pos0=pos0, T=T, e_new=e_new, e_ref=e_ref, mag=mag)
+    assert np.all(np.isfinite(got))
+    assert e_new <= 2.0 * e_ref + 1e-3 * mag
+    return e_new
+
+
+@pytest.mark.parametrize("pos0,T", CASES)
+def test_fa_int8(setup, pos0, T):
+    import torch
+    import moex_amd as M
+    hc, dc, qo, qg, qo_d, qg_d = setup
+    out = torch.zeros((T, H, AHD), dtype=torch.float32, device="cuda")
+    M.attn_fa(qo_d, qg_d, dc, out, H, KV, pos_tensor(pos0), dc.max_t, LD, T)
+    torch.cuda.synchronize()
+    o = out.cpu().numpy()
+    _gate("fa int8", o, qo, qg, hc, pos0, T)
+    # every row of the chunk is finite and written
+    assert np.all(np.isfinite(o)) and np.all(np.abs(o).max(axis=-1) > 0)
+
+
+@pytest.mark.parametrize("pos0,T", CASES[:5])
+def test_prefill_fallback_int8(setup, pos0, T):
+    import torch
+    import moex_amd as M
+    hc, dc, qo, qg, qo_d, qg_d = setup
+    out = torch.zeros((T, H, AHD), dtype=torch.float32, device="cuda")
+    M.attn_prefill(qo_d, qg_d, dc, out, H, KV, pos_tensor(pos0), dc.max_t, LD, T)
+    torch.cuda.synchronize()
+    o = out.cpu().numpy()
+    _gate("prefill(K7P) int8", o, qo, qg, hc, pos0, T)
+    # FA vs the fallback over every row (test_fa.cu:107 prints it; K7P vs per-row decode is 5e-3, test_kernels.cu:809)
+    o2 = torch.zeros_like(out)
+    M.attn_fa(qo_d, qg_d, dc, o2, H, KV, pos_tensor(pos0), dc.max_t, LD, T)
+    torch.cuda.synchronize()
+    e_ab = float(np.abs(o2.cpu().numpy() - o).max())
+    report("fa vs fallback", pos0=pos0, T=T, e_ab=e_ab)
+    assert e_ab <= 5e-3 * float(np.abs(o).max())
+
+
+@pytest.fixture(scope="module")
+def turbo_setup():
+    import torch
+    import moex_amd as M
+    max_t, n = 6208, 6144
+    dc = M.DeviceKVCache(KV, max_t, 1)
+    g = torch.Generator(device="cuda").manual_seed(9)
+    k = torch.randn((n, KV * AHD), generator=g, device="cuda")
+    v = torch.randn((n, KV * AHD), generator=g, device="cuda")
+    M.kv_append(k, v, dc, KV, pos_tensor(0), max_t, KV * AHD, n)
+    torch.cuda.synchronize()
+    hc = download(dc)
+    rng = np.random.default_rng(3)
+    qo = rng.standard_normal((2048, H, AHD)).astype(np.float32)
+    qg = rng.standard_normal((2048, LD)).astype(np.float32)
+    return hc, dc, qo, qg, dev(qo), dev(qg)
+
+
+@pytest.mark.parametrize("pos0,T", [(0, 37), (5, 3), (1000, 100), (4096, 2048)])
+def test_fa_turbo(turbo_setup, pos0, T):
+    """No gate (turbo: attn_fa writes the rotated-domain output), then turbo_out -> the full turbo reference."""
+    import torch
+    import moex_amd as M
+    hc, dc, qo, qg, qo_d, qg_d = turbo_setup
+    out = torch.zeros((T, H, AHD), dtype=torch.float32, device="cuda")
+    M.attn_fa(qo_d, None, dc, out, H, KV, pos_tensor(pos0), dc.max_t, LD, T)
+    torch.cuda.synchronize()
+    _gate("fa turbo (rotated)", out.cpu().numpy(), qo, None, hc, pos0, T)
+    M.turbo_out(out, qg_d, H, LD, T)
+    torch.cuda.synchronize()
+    _gate("fa turbo + turbo_out", out.cpu().numpy(), qo, qg, hc, pos0, T)

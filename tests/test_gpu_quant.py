@@ -1,0 +1,94 @@
+"""KV quantize-append parity (kernels.cuh:1185-1236): codes and scales/norms bit-exact against the oracle; the
+query/key front (RMSNorm(1+w) + partial RoPE) within 1e-5 relative (tests/test_kernels.cu:773)."""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests.gpu_util import AHD, H, KV, dev, download, pos_tensor, report
+
+pytestmark = pytest.mark.gpu
+
+
+def _rows(T, seed):
+    rng = np.random.default_rng(seed)
+    k = rng.standard_normal((T, KV * AHD)).astype(np.float32)
+    v = rng.standard_normal((T, KV * AHD)).astype(np.float32)
+    scales = np.geomspace(1e-4, 1e4, T).astype(np.float32)
+    k *= scales[:, None]
+    v *= scales[::-1, None]
+    k[3] = 0.0                    # zero row: scale 1 / norm 0
+    v[4, :AHD] = 0.0
+    k[5, :AHD] = 1.0              # constant row
+    k[6, :AHD] = np.linspace(-127, 127, AHD, dtype=np.float32)  # exact quotients: ties to even
+    k[6, 7] = 2.5
+    k[7, AHD:] = 1e-30            # tiny half norms (turbo: the 1e-20 guard)
+    v[8, 128:AHD] = 0.0           # one zero half (turbo)
+    return k, v
+
+
+@pytest.mark.parametrize("turbo", [0, 1])
+def test_append_bitexact(turbo):
+    import torch
+    import moex_amd as M
+    T, pos0, max_t = 96, 7, 128
+    k, v = _rows(T, 11 + turbo)
+    cache = M.DeviceKVCache(KV, max_t, turbo)
+    M.kv_append(dev(k), dev(v), cache, KV, pos_tensor(pos0), max_t, KV * AHD, T)
+    torch.cuda.synchronize()
+    got = download(cache)
+    ref = orc.HostCache(KV, max_t, turbo)
+    orc.kv_append(ref, k, v, KV * AHD, T, pos0)
+    sl = slice(pos0, pos0 + T)
+    for name in ("k", "v"):
+        a, b = getattr(got, name)[:, sl], getattr(ref, name)[:, sl]
+        bad = np.argwhere(a != b)
+        assert bad.size == 0, f"{name} codes differ at {bad[:5].tolist()}"
+    for name in ("ks", "vs"):
+        a, b = getattr(got, name)[:, sl], getattr(ref, name)[:, sl]
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), name
+    report("append", turbo=turbo, rows=T * KV)
+
+
+@pytest.mark.parametrize("turbo,pos0", [(0, 0), (1, 0), (0, 1000), (1, 1000)])
+def test_qk_norm_rope_front(turbo, pos0):
+    """1e-5 relative at positions 0..23 (the golden positions of test_kernels.cu:742-785 are 0..11). At position
+    ~1000 the fp32 angle pos * powf(theta, -2j/rot) itself (kernels.cuh:1203, the reference's own arithmetic) is
+    off by up to ~pos * 2^-23 rad from the exact angle, so the bound there is 2e-4."""
+    import torch
+    import moex_amd as M
+    T, max_t, rot, theta, eps = 24, 1100, 64, 1e7, 1e-6
+    tol = 1e-5 if pos0 == 0 else 2e-4
+    rng = np.random.default_rng(20 + turbo)
+    LQ = H * 2 * AHD + 2 * KV * AHD
+    qkv = (rng.standard_normal((T, LQ)) * 2).astype(np.float32)
+    qn = (rng.standard_normal(AHD) * 0.1).astype(np.float16)
+    kn = (rng.standard_normal(AHD) * 0.1).astype(np.float16)
+    d = dev(qkv)
+    qo = torch.zeros((T, H, AHD), dtype=torch.float32, device="cuda")
+    cache = M.DeviceKVCache(KV, max_t, turbo)
+    M.qk_norm_rope(d, d[:, H * 2 * AHD:], d[:, H * 2 * AHD + KV * AHD:], dev(qn.view(np.uint16)),
+                   dev(kn.view(np.uint16)), qo, cache, H, KV, pos_tensor(pos0), max_t, rot, theta, eps, LQ, T)
+    torch.cuda.synchronize()
+    qg = qo.cpu().numpy()
+    err = 0.0
+    for t in range(T):
+        for h in range(H):
+            ref = orc.qk_norm_rope_row(qkv[t, h * 2 * AHD: h * 2 * AHD + AHD], qn.view(np.uint16), pos0 + t, rot,
+                                       theta, eps, wht_fwd=bool(turbo))
+            err = max(err, float(np.abs(qg[t, h] - ref).max() / np.abs(ref).max()))
+    report("qk_norm_rope query", turbo=turbo, pos0=pos0, rel=err)
+    assert err < tol
+    # keys: the oracle quantizes its own (fp64-front) post-RoPE rows; codes agree except at rounding boundaries
+    got = download(cache)
+    kpost = np.stack([np.concatenate([orc.qk_norm_rope_row(qkv[t, H * 2 * AHD + h * AHD: H * 2 * AHD + (h + 1) * AHD],
+                                                           kn.view(np.uint16), pos0 + t, rot, theta, eps)
+                                      for h in range(KV)]) for t in range(T)])
+    vraw = qkv[:, H * 2 * AHD + KV * AHD:]
+    ref = orc.HostCache(KV, max_t, turbo)
+    orc.kv_append(ref, kpost, vraw, KV * AHD, T, pos0)
+    sl = slice(pos0, pos0 + T)
+    same = np.mean(got.k[:, sl] == ref.k[:, sl])
+    assert same > 0.97, same
+    assert np.array_equal(got.v[:, sl], ref.v[:, sl])  # V is not normalized: bit-exact
+    assert np.allclose(got.ks[:, sl], ref.ks[:, sl], rtol=1e-5)
+    assert np.array_equal(got.vs[:, sl].view(np.uint32), ref.vs[:, sl].view(np.uint32))

@@ -1,0 +1,270 @@
+"""Pins the CPU oracle (oracle/moex_oracle.c) against closed forms, invariants and independent formulations.
+
+The reference holds no golden vectors for the attention path (its tests generate data at run time from seeded
+std::mt19937: tests/test_fa.cu:18, tests/test_kernels.cu:787,820), so each oracle function is pinned here by
+mathematics chosen so that a plausible mistake (wrong sign, dropped term, transposed index, wrong reduction order)
+fails a check.
+"""
+import numpy as np
+import pytest
+from scipy.linalg import hadamard
+from scipy.special import softmax
+from scipy.stats import norm
+
+AHD = 256
+
+
+# ---------------- int8 quantizer (kernels.cuh:1227-1235) ----------------
+def test_int8_closed_form(orc):
+    rng = np.random.default_rng(0)
+    for scale in (1.0, 1e-3, 37.0):
+        x = (rng.standard_normal(AHD) * scale).astype(np.float32)
+        q, s = orc.int8_quant_row(x)
+        mk = np.max(np.abs(x))
+        sk = np.float32(mk) / np.float32(127.0)
+        assert np.float32(s) == sk
+        expect = np.rint(x / sk).astype(np.int8)  # float32 divide, round half to even
+        assert np.array_equal(q, expect)
+        assert np.abs(q).max() == 127
+
+
+def test_int8_ties_and_zero(orc):
+    x = np.zeros(AHD, np.float32)
+    x[:6] = [127.0, 2.5, 3.5, -2.5, 0.5, 1.5]  # sk = 1: quotients are the values themselves
+    q, s = orc.int8_quant_row(x)
+    assert s == 1.0
+    assert list(q[:6]) == [127, 2, 4, -2, 0, 2]
+    q, s = orc.int8_quant_row(np.zeros(AHD, np.float32))
+    assert s == 1.0 and not q.any()
+
+
+# ---------------- reductions (kernels.cuh:13-16, 1161-1169) ----------------
+def test_half_sum_butterfly_tree(orc):
+    # within a 32-lane group the xor tree adds lanes i and i^16 first: 2^24 + (-2^24) = 0, then + 1 -> 1.
+    # A left-to-right sum would absorb the 1 into 2^24 and return 0.
+    v = np.zeros(128, np.float32)
+    v[0], v[1], v[16] = 2.0 ** 24, 1.0, -(2.0 ** 24)
+    assert orc.half_sum(v) == 1.0
+    # across groups the four partials are added in order: ((2^24 + 1) + 1) + (-2^24) = 0 (pairwise would give 1)
+    v = np.zeros(128, np.float32)
+    v[0], v[32], v[64], v[96] = 2.0 ** 24, 1.0, 1.0, -(2.0 ** 24)
+    assert orc.half_sum(v) == 0.0
+
+
+def test_half_sum_value(orc):
+    rng = np.random.default_rng(1)
+    v = rng.standard_normal(128).astype(np.float32)
+    assert abs(float(orc.half_sum(v)) - float(np.sum(v.astype(np.float64)))) < 1e-5
+
+
+# ---------------- WHT (kernels.cuh:1143-1159) ----------------
+def _wht_matrix(orc, inverse=False):
+    W = np.zeros((AHD, AHD), np.float64)
+    for i in range(AHD):
+        e = np.zeros(AHD, np.float32)
+        e[i] = 1.0
+        W[:, i] = orc.wht(e, inverse)
+    return W
+
+
+def test_wht_is_signed_sylvester(orc):
+    t = orc.tables()
+    Hs = hadamard(128).astype(np.float64)  # natural (Sylvester) order
+    assert set(np.unique(t["S1"])) == {-1.0, 1.0} and set(np.unique(t["S2"])) == {-1.0, 1.0}
+    fwd = np.diag(t["S2"].astype(np.float64)) @ Hs @ np.diag(t["S1"].astype(np.float64)) / np.sqrt(128.0)
+    inv = np.diag(t["S1"].astype(np.float64)) @ Hs @ np.diag(t["S2"].astype(np.float64)) / np.sqrt(128.0)
+    W, Wi = _wht_matrix(orc), _wht_matrix(orc, True)
+    for b in range(2):
+        sl = slice(128 * b, 128 * (b + 1))
+        assert np.abs(W[sl, sl] - fwd).max() < 1e-7
+        assert np.abs(Wi[sl, sl] - inv).max() < 1e-7
+    assert np.abs(W[:128, 128:]).max() == 0 and np.abs(W[128:, :128]).max() == 0
+    assert np.abs(Hs @ Hs - 128 * np.eye(128)).max() == 0
+    assert np.abs(W @ W.T - np.eye(AHD)).max() < 1e-6
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal(AHD).astype(np.float32)
+    assert np.abs(orc.wht(orc.wht(x), True) - x).max() < 1e-5
+
+
+# ---------------- TurboQuant tables and quantizer (kernels.cuh:1112-1139, 1172-1183) ----------------
+def _lloyd_max(levels, sigma, iters=2000):
+    c = np.linspace(-2.5, 2.5, levels) * sigma
+    for _ in range(iters):
+        t = np.concatenate([[-np.inf], (c[:-1] + c[1:]) / 2, [np.inf]])
+        a, b = t[:-1] / sigma, t[1:] / sigma
+        c = sigma * (norm.pdf(a) - norm.pdf(b)) / (norm.cdf(b) - norm.cdf(a))
+    return c, (c[:-1] + c[1:]) / 2
+
+
+def test_tq_tables_are_lloyd_max(orc):
+    t = orc.tables()
+    sigma = 1.0 / np.sqrt(128.0)
+    for levels, codes, k, m in ((16, t["I4"], t["K4"], t["M4"]), (8, t["I3"], t["K3"], t["M3"])):
+        c, thr = _lloyd_max(levels, sigma)
+        cmax = c[-1]
+        assert abs(float(k) * 127 - cmax) < 2e-6
+        assert np.array_equal(codes.astype(int), np.rint(127 * c / cmax).astype(int))
+        assert np.abs(m.astype(np.float64) - thr).max() < 2e-6
+
+
+def test_tq_quant_nearest_centroid_and_norm(orc):
+    t = orc.tables()
+    sigma = 1.0 / np.sqrt(128.0)
+    W = _wht_matrix(orc)
+    rng = np.random.default_rng(3)
+    for bits, codes, k in ((4, t["I4"], t["K4"]), (3, t["I3"], t["K3"])):
+        c, thr = _lloyd_max(2 ** bits, sigma)
+        for trial in range(20):
+            x = (rng.standard_normal(AHD) * (0.1 + trial)).astype(np.float32)
+            idx, nrm = orc.tq_quant(x, bits)
+            for b in range(2):
+                sl = slice(128 * b, 128 * (b + 1))
+                n = np.sqrt(np.sum(x[sl].astype(np.float64) ** 2))
+                r = W[sl, sl] @ (x[sl] / n)
+                near = np.argmin(np.abs(r[:, None] - c[None, :]), axis=1)
+                clear = np.min(np.abs(r[:, None] - thr[None, :]), axis=1) > 1e-5
+                assert np.array_equal(idx[sl][clear], near[clear])
+                deq = codes[idx[sl]].astype(np.float64) * float(k) * float(nrm[b])
+                assert abs(np.linalg.norm(deq) - n) < 1e-5 * n
+
+
+def test_tq_quant_zero_row(orc):
+    for bits, zidx in ((4, 8), (3, 4)):  # r = 0 >= every threshold up to and including the 0 one
+        idx, nrm = orc.tq_quant(np.zeros(AHD, np.float32), bits)
+        assert np.all(idx == zidx) and np.all(nrm == 0)
+
+
+def test_turbo_packing(orc):
+    ik = np.zeros(AHD, np.int32)
+    iv = np.zeros(AHD, np.int32)
+    ik[0], ik[1], ik[130], ik[131] = 1, 2, 15, 4
+    iv[0], iv[5], iv[130], iv[255] = 5, 7, 2, 4
+    kb, vb = orc.turbo_pack(ik, iv)
+    assert kb[0] == 0x21 and kb[64 + 1] == 0x4F and kb.sum() == 0x21 + 0x4F
+    assert vb[0] == 0x01 and vb[64] & 1 == 1          # dim 0: code 5 = low 01, high 1
+    assert (vb[1] >> 2) & 3 == 3 and (vb[64] >> 5) & 1  # dim 5: code 7
+    assert (vb[32] >> 4) & 3 == 2 and not (vb[80] >> 2) & 1  # dim 130 = half 1, j 2: code 2
+    assert vb[32 + 31] == 0 and (vb[64 + 16 + 15] >> 7) & 1  # dim 255: code 4 = low 00, high 1
+    rng = np.random.default_rng(4)
+    for _ in range(10):
+        ik = rng.integers(0, 16, AHD).astype(np.int32)
+        iv = rng.integers(0, 8, AHD).astype(np.int32)
+        a, b = orc.turbo_unpack(*orc.turbo_pack(ik, iv))
+        assert np.array_equal(a, ik) and np.array_equal(b, iv)
+
+
+# ---------------- fp64 attention (tests/test_fa.cu:59-80) ----------------
+def _dense_reference(orc, qo, gate, ld, H, cache, pos0, t, h):
+    """Independent formulation: dequantize the whole key range, scipy softmax, matrix products."""
+    kvh = h // (H // cache.KV)
+    n = pos0 + t + 1
+    tb = orc.tables()
+    if cache.turbo:
+        K = np.zeros((n, AHD)); V = np.zeros((n, AHD))
+        for j in range(n):
+            ik, iv = orc.turbo_unpack(cache.k[kvh, j].view(np.uint8), cache.v[kvh, j].view(np.uint8))
+            K[j] = tb["I4"][ik] * float(tb["K4"]) * np.repeat(cache.ks[kvh, j].astype(np.float64), 128)
+            V[j] = tb["I3"][iv] * float(tb["K3"]) * np.repeat(cache.vs[kvh, j].astype(np.float64), 128)
+    else:
+        K = cache.k[kvh, :n].astype(np.float64) * cache.ks[kvh, :n, None]
+        V = cache.v[kvh, :n].astype(np.float64) * cache.vs[kvh, :n, None]
+    q = qo[t, h].astype(np.float64)
+    o = softmax(K @ q / 16.0) @ V
+    if gate is None:
+        return o
+    if cache.turbo:  # exact inverse rotation per half: S1 . H . S2 / sqrt(128)
+        Wi = np.diag(tb["S1"].astype(np.float64)) @ hadamard(128) @ np.diag(tb["S2"].astype(np.float64)) / np.sqrt(128)
+        o = np.concatenate([Wi @ o[:128], Wi @ o[128:]])
+    g = gate.reshape(-1)[t * ld + h * 2 * AHD + AHD: t * ld + h * 2 * AHD + 2 * AHD].astype(np.float64)
+    return o / (1 + np.exp(-g))
+
+
+@pytest.mark.parametrize("turbo", [0, 1])
+def test_attn_f64_against_dense(orc, turbo):
+    rng = np.random.default_rng(5 + turbo)
+    H, KV, max_t, T, pos0 = 16, 2, 48, 5, 30
+    ld = H * 2 * AHD
+    cache = orc.HostCache(KV, max_t, turbo)
+    k = rng.standard_normal((T + pos0, KV * AHD)).astype(np.float32)
+    v = rng.standard_normal((T + pos0, KV * AHD)).astype(np.float32)
+    orc.kv_append(cache, k, v, KV * AHD, T + pos0, 0)
+    qo = rng.standard_normal((T, H, AHD)).astype(np.float32)
+    gate = rng.standard_normal((T, ld)).astype(np.float32)
+    rows = [(t, h) for t in range(T) for h in (0, 7, 8, 15)]
+    got = orc.attn_rows_f64(qo, gate, ld, H, cache, pos0, rows)
+    for (t, h), g in zip(rows, got):
+        ref = _dense_reference(orc, qo, gate, ld, H, cache, pos0, t, h)
+        assert np.abs(g - ref).max() < 1e-12 * max(1.0, np.abs(ref).max())
+    # no gate: the raw (for turbo: rotated-domain) attention output
+    got = orc.attn_rows_f64(qo, None, ld, H, cache, pos0, rows[:3])
+    for (t, h), g in zip(rows[:3], got):
+        assert np.abs(g - _dense_reference(orc, qo, None, ld, H, cache, pos0, t, h)).max() < 1e-12
+
+
+def test_attn_f64_closed_forms(orc):
+    H, KV, max_t = 16, 2, 8
+    ld = H * 2 * AHD
+    rng = np.random.default_rng(7)
+    cache = orc.HostCache(KV, max_t, 0)
+    cache.k[:] = rng.integers(-127, 128, cache.k.shape)
+    cache.v[:] = rng.integers(-127, 128, cache.v.shape)
+    cache.ks[:] = 0.01
+    cache.vs[:] = rng.uniform(0.005, 0.05, cache.vs.shape)
+    qo = rng.standard_normal((1, H, AHD)).astype(np.float32)
+    gate = rng.standard_normal((1, ld)).astype(np.float32)
+    # a single visible key: out = v0 * vs0 * sigmoid(g)
+    out = orc.attn_rows_f64(qo, gate, ld, H, cache, 0, [(0, 3)])[0]
+    g = gate[0, 3 * 512 + 256: 3 * 512 + 512].astype(np.float64)
+    assert np.allclose(out, cache.v[0, 0] * float(cache.vs[0, 0]) / (1 + np.exp(-g)), rtol=1e-13, atol=0)
+    # identical keys: uniform weights, out = mean of v_j vs_j
+    cache.k[1, :6] = cache.k[1, 0]
+    out = orc.attn_rows_f64(qo, None, ld, H, cache, 5, [(0, 12)])[0]
+    ref = np.mean(cache.v[1, :6].astype(np.float64) * cache.vs[1, :6, None], axis=0)
+    assert np.allclose(out, ref, rtol=1e-12, atol=1e-15)
+
+
+def test_fa_precision_model_close(orc):
+    rng = np.random.default_rng(8)
+    H, KV, max_t, T, pos0 = 16, 2, 300, 9, 200
+    ld = H * 2 * AHD
+    for turbo in (0, 1):
+        cache = orc.HostCache(KV, max_t, turbo)
+        k = rng.standard_normal((pos0 + T, KV * AHD)).astype(np.float32)
+        v = rng.standard_normal((pos0 + T, KV * AHD)).astype(np.float32)
+        orc.kv_append(cache, k, v, KV * AHD, pos0 + T, 0)
+        qo = rng.standard_normal((T, H, AHD)).astype(np.float32)
+        gate = rng.standard_normal((T, ld)).astype(np.float32)
+        rows = [(0, 0), (4, 9), (8, 15)]
+        a = orc.attn_rows_f64(qo, gate, ld, H, cache, pos0, rows)
+        b = orc.attn_rows_fa_emul(qo, gate, ld, H, cache, pos0, rows)
+        err = np.abs(a - b).max()
+        assert 0 < err < 2e-3 * np.abs(a).max()
+
+
+def test_round_f16(orc):
+    x = np.array([1.0, 1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11, 65504.0, 65520.0, 2 ** -24, 2 ** -25, 3 * 2 ** -25,
+                  -0.1, 1e-7], np.float32)
+    assert np.array_equal(orc.round_f16(x), x.astype(np.float16).astype(np.float32))
+    y = np.random.default_rng(9).standard_normal(10000).astype(np.float32) * 100
+    assert np.array_equal(orc.round_f16(y), y.astype(np.float16).astype(np.float32))
+
+
+# ---------------- query/key front (ref/qwen36_ref.py:62-76) ----------------
+def test_qk_norm_rope_front(orc):
+    rng = np.random.default_rng(10)
+    x = rng.standard_normal(AHD).astype(np.float32) * 3
+    w = (rng.standard_normal(AHD) * 0.1).astype(np.float16)
+    wb = w.view(np.uint16)
+    eps, rot, theta = 1e-6, 64, 1e7
+    # pos 0: no rotation; weight 0: unit RMS
+    y0 = orc.qk_norm_rope_row(x, np.zeros(AHD, np.uint16), 0, rot, theta, eps)
+    assert abs(np.sqrt(np.mean(y0.astype(np.float64) ** 2)) - 1) < 1e-5
+    # rotation of the first 64 dims preserves the pair norms and leaves the rest unchanged
+    y = orc.qk_norm_rope_row(x, wb, 12345, rot, theta, eps)
+    yn = orc.qk_norm_rope_row(x, wb, 0, rot, theta, eps)
+    assert np.allclose(y[rot:], yn[rot:], rtol=0, atol=0)
+    pn = lambda z: z[:32].astype(np.float64) ** 2 + z[32:64].astype(np.float64) ** 2
+    assert np.allclose(pn(y), pn(yn), rtol=1e-5)
+    # angle of pair j = pos * theta^(-2j/rot): the first pair rotates by exactly pos radians
+    a0 = np.arctan2(yn[32], yn[0]); a1 = np.arctan2(y[32], y[0])
+    assert abs(((a1 - a0 - 12345) + np.pi) % (2 * np.pi) - np.pi) < 1e-3
