@@ -1,0 +1,257 @@
+"""Benchmark of the moex attention hot path on one MI355X.
+
+Headline (BASELINE.json metric, configs[1]): one FA-2 prefill chunk of T=2048 query tokens at positions
+32768..34815 over an int8 KV cache of 34816 keys (16 q heads, 2 KV heads, head_dim 256, gated), in TFLOPS with the
+reference's flop count 4*H*D*T*(pos0 + T/2) (tests/test_fa.cu:137). A step = one attn_fa call; inputs (Q, gate,
+cache) are resident in HBM before the timed region.
+
+Also reported (other configs of BASELINE.json, same JSON line): decode / MTP verify at 90k context (T=1, T=4;
+HBM GB/s over the 520 B/row KV, MALL flushed before every step), TurboQuant decode at 262144, TurboQuant prefill at
+260096..262143 and the int8 chunk at the same depth, and config 0 (pos0 = 0).
+
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+H, KV, AHD = 16, 2, 256
+LD = H * 2 * AHD
+PEAK_F16 = 2500.0   # TFLOP/s, MI355X dense fp16 MFMA
+PEAK_HBM = 8000.0   # GB/s
+METRIC = "prefill attn TFLOPS @2048-chunk/32k ctx; decode attn HBM GB/s @90k ctx"
+
+
+def flops_prefill(T, pos0):
+    return 4.0 * H * AHD * T * (pos0 + T / 2.0)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--quick", action="store_true", help="headline only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (the attention path of a batch-1 engine); "
+              "--gpus must be 1", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import moex_amd as M
+    torch.cuda.set_device(0)
+    dev = "cuda"
+    st = torch.cuda.current_stream()
+    gen = torch.Generator(device=dev).manual_seed(1)
+
+    def ev():
+        return torch.cuda.Event(enable_timing=True)
+
+    def fill_cache(cache, n, seed):
+        """K, V ~ N(0,1) fp32 quantized by the product's own append kernel (int8 per row or TurboQuant)."""
+        g = torch.Generator(device=dev).manual_seed(seed)
+        zero = torch.zeros(1, dtype=torch.int32, device=dev)
+        chunk = 32768
+        for p in range(0, n, chunk):
+            m = min(chunk, n - p)
+            k = torch.randn((m, KV * AHD), generator=g, device=dev)
+            v = torch.randn((m, KV * AHD), generator=g, device=dev)
+            zero.fill_(p)
+            M.kv_append(k, v, cache, KV, zero, cache.max_t, KV * AHD, m)
+        torch.cuda.synchronize()
+
+    def q_and_gate(T, seed):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        qo = torch.randn((T, H, AHD), generator=g, device=dev).half().float()  # fp16-representable (BASELINE: fp16 Q)
+        qg = torch.randn((T, LD), generator=g, device=dev).half().float()
+        return qo, qg
+
+    def time_steps(fn, steps, warmup):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = ev(), ev()
+        t0 = time.perf_counter()
+        e0.record(st)
+        for _ in range(steps):
+            fn()
+        e1.record(st)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3
+        return e0.elapsed_time(e1) / steps, wall / steps
+
+    flush = torch.empty(768 << 20, dtype=torch.uint8, device=dev)  # > 256 MB MALL + L2
+
+    def time_flushed(fn, reps):
+        ts = []
+        for i in range(reps + 3):
+            flush.fill_(i & 0xff)
+            e0, e1 = ev(), ev()
+            e0.record(st)
+            fn()
+            e1.record(st)
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        return float(np.median(ts[3:]))
+
+    res = {}
+    # ---------------- headline: config 1, int8 prefill chunk at 32k ----------------
+    T, pos0 = 2048, 32768
+    n = pos0 + T
+    c8 = M.DeviceKVCache(KV, 262144 + 64, 0)
+    fill_cache(c8, 262144, seed=10)
+    qo, qg = q_and_gate(T, seed=11)
+    out = torch.empty((T, H, AHD), device=dev)
+    pos_d = torch.tensor([pos0], dtype=torch.int32, device=dev)
+
+    def prefill():
+        M.attn_fa(qo, qg, c8, out, H, KV, pos_d, c8.max_t, LD, T, st)
+
+    ms, wall_ms = time_steps(prefill, a.steps, a.warmup)
+    tflops = flops_prefill(T, pos0) / (ms * 1e-3) / 1e12
+    print(f"[bench] config1 int8 prefill T={T} pos0={pos0}: {ms:.3f} ms/step, {tflops:.1f} TFLOPS "
+          f"({100 * tflops / PEAK_F16:.1f}% of {PEAK_F16:.0f})", flush=True)
+
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", "fa_prefill_int8_c1_traffic.json")
+    if os.path.exists(tf):
+        traffic = json.load(open(tf)).get("bytes_per_launch")
+
+    extra = {}
+    if not a.quick:
+        # ---------------- config 0: pos0 = 0 ----------------
+        pz = torch.tensor([0], dtype=torch.int32, device=dev)
+        ms0, _ = time_steps(lambda: M.attn_fa(qo, qg, c8, out, H, KV, pz, c8.max_t, LD, T, st), 10, 3)
+        extra["config0_prefill_int8"] = {"ms": round(ms0, 4), "tflops": round(flops_prefill(T, 0) / ms0 / 1e9, 1)}
+        print(f"[bench] config0 int8 prefill pos0=0: {ms0:.3f} ms, {extra['config0_prefill_int8']['tflops']} TFLOPS",
+              flush=True)
+        # ---------------- config 2: decode + MTP verify at 90k (int8) ----------------
+        dec = {}
+        ctx = 90000
+        for Tq in (1, 4):
+            ns = M.decode_splits(ctx)
+            part = torch.empty(Tq * H * ns * (AHD + 2), device=dev)
+            o1 = torch.empty((Tq, H, AHD), device=dev)
+            pd = torch.tensor([ctx - Tq], dtype=torch.int32, device=dev)
+
+            def gqa():
+                M.attn_gqa(qo[:Tq], c8, H, KV, pd, c8.max_t, part, Tq, ns, st)
+
+            def full():
+                gqa()
+                M.attn_combine(part, qg[:Tq], o1, H, ns, LD, Tq, st)
+
+            t_k = time_flushed(gqa, 20)
+            t_f = time_flushed(full, 20)
+            kv_bytes = 2.0 * ctx * 520
+            dec[f"T{Tq}"] = {"ns": ns, "split_kernel_us": round(t_k * 1e3, 2), "with_combine_us": round(t_f * 1e3, 2),
+                             "GBps": round(kv_bytes / (t_f * 1e-3) / 1e9, 1),
+                             "split_kernel_GBps": round(kv_bytes / (t_k * 1e-3) / 1e9, 1)}
+            print(f"[bench] config2 decode T={Tq} ctx={ctx} ns={ns}: {t_f * 1e3:.1f} us "
+                  f"({dec[f'T{Tq}']['GBps']} GB/s; split kernel alone {t_k * 1e3:.1f} us)", flush=True)
+        extra["config2_decode_int8_90k"] = dec
+        # ---------------- config 1 depth comparison / config 4: turbo at 262k ----------------
+        ct = M.DeviceKVCache(KV, 262144 + 64, 1)
+        fill_cache(ct, 262144, seed=12)
+        ctx = 262144
+        ns = M.decode_splits(ctx)
+        part = torch.empty(H * ns * (AHD + 2), device=dev)
+        o1 = torch.empty((1, H, AHD), device=dev)
+        pd = torch.tensor([ctx - 1], dtype=torch.int32, device=dev)
+
+        def tdec():
+            M.attn_gqa(qo[:1], ct, H, KV, pd, ct.max_t, part, 1, ns, st)
+            M.attn_combine(part, None, o1, H, ns, LD, 1, st)
+            M.turbo_out(o1, qg[:1], H, LD, 1, st)
+
+        t_td = time_flushed(tdec, 10)
+        tb = 2.0 * ctx * 240
+        extra["config3_decode_turbo_262k"] = {"ns": ns, "us": round(t_td * 1e3, 2),
+                                              "GBps": round(tb / (t_td * 1e-3) / 1e9, 1)}
+        print(f"[bench] config3 turbo decode ctx={ctx}: {t_td * 1e3:.1f} us ({tb / t_td / 1e6:.0f} GB/s)", flush=True)
+        p4 = torch.tensor([260096], dtype=torch.int32, device=dev)
+        ms_t, _ = time_steps(lambda: M.attn_fa(qo, None, ct, out, H, KV, p4, ct.max_t, LD, T, st), 3, 1)
+        ms_i, _ = time_steps(lambda: M.attn_fa(qo, qg, c8, out, H, KV, p4, c8.max_t, LD, T, st), 3, 1)
+        f4 = flops_prefill(T, 260096)
+        extra["config4_prefill_260k"] = {"turbo_ms": round(ms_t, 3), "turbo_tflops": round(f4 / ms_t / 1e9, 1),
+                                         "int8_ms": round(ms_i, 3), "int8_tflops": round(f4 / ms_i / 1e9, 1)}
+        print(f"[bench] config4 prefill at 260096: turbo {ms_t:.2f} ms ({f4 / ms_t / 1e9:.0f} TFLOPS), "
+              f"int8 {ms_i:.2f} ms ({f4 / ms_i / 1e9:.0f} TFLOPS)", flush=True)
+        del ct
+
+    cpu = None
+    if not a.no_cpu:
+        cpu = cpu_baseline(c8, qo, qg, pos0, T, a.cpu_seconds)
+        print(f"[bench] cpu fp64 baseline: {cpu['value']:.4f} {cpu['unit']} on {cpu['cores']} threads "
+              f"({cpu['sample']})", flush=True)
+
+    line = {
+        "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOPS", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16", "data": "synthetic (seeded N(0,1) Q/gate/K/V; K/V int8-quantized by the "
+                                                   "product's append kernel)",
+        "config": {"workload": "configs[1]: int8-KV causal GQA FA-2 prefill chunk, T=2048 at pos0=32768 (34816 "
+                               "keys), H=16, KV=2, head_dim=256, sigmoid-gated", "global_batch": 1, "seq_len": n,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_F16, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_F16, 4), "traffic": traffic},
+        "cpu_baseline": cpu,
+        "wall_ms_per_step": round(wall_ms, 4),
+    }
+    line.update(extra)
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(c8, qo, qg, pos0, T, seconds):
+    """The fp64 reference attention (tests/test_fa.cu:59-80 semantics, oracle/moex_oracle.c) on the host cores,
+    threaded over (token, head) rows, on a time-bounded sample of the headline chunk's rows; reported as TFLOPS with
+    the same per-row flop count (4 * D * keys)."""
+    import concurrent.futures as cf
+    import numpy as np
+    from oracle import oracle as orc
+    n = pos0 + T
+    hc = orc.HostCache(KV, n, 0)
+    hc.k[:] = c8.k[:, :n].cpu().numpy()
+    hc.v[:] = c8.v[:, :n].cpu().numpy()
+    hc.ks[:] = c8.ks[:, :n].cpu().numpy()
+    hc.vs[:] = c8.vs[:, :n].cpu().numpy()
+    q = qo.cpu().numpy()
+    g = qg.cpu().numpy()
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    # rows in an order that spreads over the chunk: tokens by bit-reversed stride, all heads
+    toks = list(range(0, T, 37)) + list(range(18, T, 37))
+    rows = [(t, h) for t in toks for h in range(H)]
+    deadline = time.perf_counter() + seconds
+    done, flops = 0, 0.0
+
+    def work(chunk):
+        orc.attn_rows_f64(q, g, LD, H, hc, pos0, chunk)
+        return sum(4.0 * AHD * (pos0 + t + 1) for t, _ in chunk)
+
+    t0 = time.perf_counter()
+    with cf.ThreadPoolExecutor(threads) as ex:
+        i = 0
+        while time.perf_counter() < deadline and i < len(rows):
+            batch = [rows[i + j * 4: i + j * 4 + 4] for j in range(threads)]
+            batch = [b for b in batch if b]
+            i += 4 * threads
+            for f in ex.map(work, batch):
+                flops += f
+            done += sum(len(b) for b in batch)
+    el = time.perf_counter() - t0
+    return {"value": round(flops / el / 1e12, 6), "unit": "TFLOPS", "cores": threads, "kind": "port",
+            "sample": f"{done} of the {T * H} (token, head) rows of the configs[1] chunk (each over its "
+                      f"{pos0 + 1}..{n} causal keys), fp64, {el:.1f} s; nproc={os.cpu_count()}"}
+
+
+if __name__ == "__main__":
+    main()

@@ -79,14 +79,15 @@ int moex_fa_supported(void) {  // kernels.cuh:1705-1712, asked per device
 }
 
 int moex_decode_splits(int n_ctx) {
-    int dev = 0, cus = 256;
+    int dev = 0, cus = 256;  // MI355X
     if (hipGetDevice(&dev) == hipSuccess) {
         int v = 0;
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
     }
-    // two workgroups per CU over both kv heads, but at least ~256 keys per split
-    int ns = (n_ctx + 255) / 256;
-    if (ns > cus) ns = cus;
+    // two streaming workgroups per CU over both kv heads (each walks its split in 128-key chunks), but no split
+    // shorter than 256 keys
+    int ns = cus;
+    if (ns > (n_ctx + 255) / 256) ns = (n_ctx + 255) / 256;
     return ns < 1 ? 1 : ns;
 }
 

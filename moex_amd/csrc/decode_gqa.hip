@@ -325,13 +325,327 @@ __global__ void __launch_bounds__(256, 2) gqa_decode_kernel(const float* __restr
     }
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// int8 KV: the same split-K decode on v_mfma_i32_16x16x64_i8, with the raw int8 K and V bytes as MFMA operands (no
+// widening at all). The fp32 query and the probabilities enter as 24-bit fixed point written in three signed base-256
+// digits (x = d2*2^16 + d1*2^8 + d0, each digit in [-128, 127]); every digit product is accumulated exactly in int32
+// and the digits are recombined in fp32, so both products keep fp32-level precision (the reference decode is fp32).
+// Two passes over each chunk of keys make the int32 accumulation possible: pass 1 computes all scores of the chunk
+// and their exact maximum (no online rescaling), pass 2 forms P = 2^(s - max) and accumulates P.V.
+//   Q.K:  16 keys x 16 columns per MFMA; column m < 8 = digit 2 of head m, m >= 8 = digit 1 of head m-8, a second
+//         MFMA holds digit 0 of the 8 heads. Lane (g = lane/16, m = lane%16) receives keys 4g + i of the group for
+//         column m; the digits of a head are brought together with two row_ror:8 DPP moves.
+//   P.V:  rows = the same digit/head layout for P; the four wavefronts split the 256 dims (64 each) and all of them
+//         walk every key of the chunk, reading the P operands that pass 1 left in LDS. Each lane loads 4 bytes (dims
+//         64w + 4m .. +3) of 16 key rows and a 4x4 byte transpose turns them into the B operands.
+constexpr int ICH = 128;                           // keys per chunk: 32 keys (two 16-key groups) per wavefront
+typedef int int4_t_ __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int dpp_ror8(int x) { return __builtin_amdgcn_update_dpp(0, x, 0x128, 0xf, 0xf, false); }
+
+// three signed base-256 digits of n, |n| <= 2^22 + 2^15: n = d2*65536 + d1*256 + d0
+__device__ __forceinline__ void digits3(int n, int& d2, int& d1, int& d0) {
+    d2 = (n + 32896) >> 16;
+    const int r = n - (d2 << 16);
+    d1 = (r + 128) >> 8;
+    d0 = r - (d1 << 8);
+}
+__device__ __forceinline__ uint32_t pack_bytes(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) | ((uint32_t)d << 24);
+}
+__device__ __forceinline__ void tr4x4_(const uint32_t r0, const uint32_t r1, const uint32_t r2, const uint32_t r3, uint32_t c[4]) {
+    const uint32_t t0 = __builtin_amdgcn_perm(r1, r0, 0x05010400u), t1 = __builtin_amdgcn_perm(r1, r0, 0x07030602u);
+    const uint32_t t2 = __builtin_amdgcn_perm(r3, r2, 0x05010400u), t3 = __builtin_amdgcn_perm(r3, r2, 0x07030602u);
+    c[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u); c[1] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+    c[2] = __builtin_amdgcn_perm(t3, t1, 0x05040100u); c[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+}
+typedef __attribute__((address_space(1))) const void* gptr_t;
+typedef __attribute__((address_space(3))) void* lptr_t;
+
+// One workgroup per split, walking it in chunks of 256 keys with the loads of chunk c+1 in flight while chunk c is
+// computed: the V rows go straight to LDS (global_load_lds_dwordx4, double buffered, 64-byte blocks XOR-swizzled by
+// key/4 so the pass-2 reads of the four lane groups hit disjoint banks), the K rows and the scales to registers.
+// The query digits are computed once per workgroup and shared through LDS.
+constexpr int I8_VBUF = ICH * AHD;                                       // 64 KB per V buffer
+constexpr int I8_LDS_ALL = 2 * I8_VBUF + 2 * (ICH / 64) * 64 * 16 + 2 * 4 * 64 * 16;  // + P operands + Q operands
+
+__device__ __forceinline__ void issue_v_chunk(const int8_t* Vg, unsigned char* buf, int c0, int nk, int hi, int tid,
+                                              int wv) {
+    const int nit = (nk + 15) >> 4;  // 16 keys (256 16-byte pieces) per workgroup-wide instruction
+    for (int it = 0; it < nit; it++) {
+        const int q = it * 256 + tid, key = q >> 4, pc = (q & 15) ^ (4 * ((key >> 2) & 3));
+        const int t = min(c0 + key, hi - 1);
+        __builtin_amdgcn_global_load_lds((gptr_t)(Vg + (size_t)t * AHD + 16 * pc),
+                                         (lptr_t)(buf + (size_t)(it * 256 + 64 * wv) * 16), 16, 0, 0);
+    }
+}
+
+__global__ void __launch_bounds__(256, 2) gqa_i8_kernel(const float* __restrict__ qo, moex_kv_cache kv, int H,
+                                                        const int* __restrict__ pos_d, int max_t,
+                                                        float* __restrict__ part, int T, int ns) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    int4_t_* Pl = reinterpret_cast<int4_t_*>(smem + 2 * I8_VBUF);             // [ICH/64][2][64]
+    int4_t_* Ql = Pl + (ICH / 64) * 2 * 64;                                   // [2][4][64]
+    __shared__ float mxw[4][GQ], lsum[4][GQ], vmw[4], qsc[GQ];
+    const int nb = gridDim.x, w_id = xcd_work_id(blockIdx.x, nb);
+    const int tok = w_id % T, s = (w_id / T) % ns, kvh = w_id / (T * ns);
+    const int pos0 = *pos_d, Tk = pos0 + tok + 1, Tmax = pos0 + T;
+    const int L = (Tmax + ns - 1) / ns, lo = s * L, hi = min(Tk, lo + L);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 4, m16 = lane & 15, hq = m16 & 7;
+    const bool lo8 = m16 < 8;
+    const size_t rbase = (size_t)kvh * max_t;
+    const int8_t* Kg = kv.k + rbase * AHD;
+    const int8_t* Vg = kv.v + rbase * AHD;
+    const float* ksg = kv.ks + rbase;
+    const float* vsg = kv.vs + rbase;
+    const int nch = hi > lo ? (hi - lo + ICH - 1) / ICH : 0;
+
+    // ---- loads of chunk 0 (registers: this wavefront's K step and scales; LDS: all V rows) ----
+    int4_t_ kr[2][4];
+    float ksn[8], vvn[8];  // scales of the next chunk to compute
+    const int stw = wv >> 1, gq0 = 2 * (wv & 1);  // this wavefront's Q.K step and first 16-key group
+    int4_t_ krn[2][4];  // K rows of the next chunk (double buffer)
+    auto issue_kr = [&](int k0) {
+#pragma unroll
+        for (int grp = 0; grp < 2; grp++) {
+            const int4_t_* kp = reinterpret_cast<const int4_t_*>(Kg + (size_t)min(k0 + 16 * grp + m16, hi - 1) * AHD + 16 * g);
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) krn[grp][ks] = kp[4 * ks];
+        }
+    };
+    auto issue_scales = [&](int k0) {
+        if (k0 + 32 <= hi) {
+#pragma unroll
+            for (int grp = 0; grp < 2; grp++) {
+                const float4 a = *reinterpret_cast<const float4*>(ksg + k0 + 16 * grp + 4 * g);
+                const float4 b = *reinterpret_cast<const float4*>(vsg + k0 + 16 * grp + 4 * g);
+                ksn[4 * grp] = a.x; ksn[4 * grp + 1] = a.y; ksn[4 * grp + 2] = a.z; ksn[4 * grp + 3] = a.w;
+                vvn[4 * grp] = b.x; vvn[4 * grp + 1] = b.y; vvn[4 * grp + 2] = b.z; vvn[4 * grp + 3] = b.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int t = min(k0 + 16 * (j >> 2) + 4 * g + (j & 3), hi - 1);
+                ksn[j] = ksg[t]; vvn[j] = vsg[t];
+            }
+        }
+    };
+    if (nch > 0) {
+        const int k0 = lo + 64 * stw + 16 * gq0;
+        if (k0 < hi) { issue_kr(k0); issue_scales(k0); }
+        issue_v_chunk(Vg, smem, lo, min(ICH, hi - lo), hi, tid, wv);
+    }
+
+    // ---- query digits, once per workgroup: thread = (head tid/32, dims 8*(tid%32) .. +7) ----
+    {
+        const int h = tid >> 5, d0 = (tid & 31) * 8;
+        const float* qrow = qo + ((size_t)tok * H + kvh * GQ + h) * AHD + d0;
+        const float4 x0 = reinterpret_cast<const float4*>(qrow)[0], x1 = reinterpret_cast<const float4*>(qrow)[1];
+        const float qv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        float qm = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) qm = fmaxf(qm, fabsf(qv[j]));
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) qm = fmaxf(qm, __shfl_xor(qm, o));
+        int e = 0;
+        if (qm > 0.f) (void)frexpf(qm, &e);  // qm < 2^e
+        const float up = ldexpf(1.f, 22 - e);
+        if ((tid & 31) == 0) qsc[h] = ldexpf(1.f, e - 22);
+        int d2[8], d1[8], dz[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) digits3((int)__builtin_rintf(qv[j] * up), d2[j], d1[j], dz[j]);
+        // B operand of Q.K: MFMA ks, lane 16g + m holds dims 64ks + 16g + 0..15 of column m
+        const int ks = d0 >> 6, gg = (d0 >> 4) & 3, jb = d0 & 15;
+        unsigned char* qa_b = reinterpret_cast<unsigned char*>(Ql + (0 * 4 + ks) * 64);
+        unsigned char* qb_b = reinterpret_cast<unsigned char*>(Ql + (1 * 4 + ks) * 64);
+        *reinterpret_cast<uint2*>(qa_b + (16 * gg + h) * 16 + jb) =
+            make_uint2(pack_bytes(d2[0], d2[1], d2[2], d2[3]), pack_bytes(d2[4], d2[5], d2[6], d2[7]));
+        *reinterpret_cast<uint2*>(qa_b + (16 * gg + h + 8) * 16 + jb) =
+            make_uint2(pack_bytes(d1[0], d1[1], d1[2], d1[3]), pack_bytes(d1[4], d1[5], d1[6], d1[7]));
+        *reinterpret_cast<uint2*>(qb_b + (16 * gg + h) * 16 + jb) =
+            make_uint2(pack_bytes(dz[0], dz[1], dz[2], dz[3]), pack_bytes(dz[4], dz[5], dz[6], dz[7]));
+        *reinterpret_cast<uint2*>(qb_b + (16 * gg + h + 8) * 16 + jb) = make_uint2(0u, 0u);
+    }
+    __syncthreads();
+    int4_t_ qa[4], qb[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) { qa[ks] = Ql[ks * 64 + lane]; qb[ks] = Ql[(4 + ks) * 64 + lane]; }
+    const float qscale = qsc[hq];
+
+    float of[4][4];                 // fp32 result: [MFMA c][row i]; lanes g < 2: head 4g + i, dim 64*wv + 4*m16 + c
+    float m_run[4];                 // running max of heads 4*(g&1) + i
+    float lw_acc = 0.f, mh_run = -INFINITY;  // this lane's share of head hq's sum, head hq's running max
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) of[c][i] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) m_run[i] = -INFINITY;
+    const int rd = 16 * ((4 * wv + (m16 >> 2)) ^ (4 * g)) + 4 * (m16 & 3);  // swizzled byte offset of my V dims
+
+    for (int c = 0; c < nch; c++) {
+        const int c0 = lo + c * ICH, nk = min(ICH, hi - c0), nsteps = (nk + 63) >> 6;
+        const int k0 = c0 + 64 * stw + 16 * gq0;
+        const bool has = k0 < hi;
+        unsigned char* Vs = smem + (c & 1) * I8_VBUF;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // chunk c's K, scales and V rows have landed
+        __syncthreads();                                   // ... for every wavefront; chunk c-1 is done with LDS
+        float ksv[8], vv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) { ksv[j] = ksn[j]; vv[j] = vvn[j]; }
+#pragma unroll
+        for (int grp = 0; grp < 2; grp++)
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) kr[grp][ks] = krn[grp][ks];
+        const int c1 = c0 + ICH;  // the next chunk: all its loads go out now
+        if (c + 1 < nch) {
+            const int k1 = c1 + 64 * stw + 16 * gq0;
+            if (k1 < hi) { issue_kr(k1); issue_scales(k1); }
+            issue_v_chunk(Vg, smem + ((c + 1) & 1) * I8_VBUF, c1, min(ICH, hi - c1), hi, tid, wv);
+        }
+        // ---- pass 1: scores of this wavefront's 32 keys ----
+        float sc[8];
+        float mx = -INFINITY, vm = 0.f;
+        if (has) {
+#pragma unroll
+            for (int grp = 0; grp < 2; grp++) {
+                int4_t_ da = {0, 0, 0, 0}, db = {0, 0, 0, 0};
+#pragma unroll
+                for (int ks = 0; ks < 4; ks++) {
+                    da = __builtin_amdgcn_mfma_i32_16x16x64_i8(kr[grp][ks], qa[ks], da, 0, 0, 0);
+                    db = __builtin_amdgcn_mfma_i32_16x16x64_i8(kr[grp][ks], qb[ks], db, 0, 0, 0);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int x = dpp_ror8(da[i]), y = dpp_ror8(db[i]);
+                    const int a2 = lo8 ? da[i] : x, a1 = lo8 ? x : da[i], a0 = lo8 ? db[i] : y;
+                    const float raw = ((float)a2 * 65536.f + (float)a1 * 256.f) + (float)a0;
+                    const int j = 4 * grp + i, key = k0 + 16 * grp + 4 * g + i;
+                    const float v = key < hi ? raw * (ksv[j] * (SL2 * qscale)) : -INFINITY;
+                    sc[j] = v;
+                    mx = fmaxf(mx, v);
+                    if (key < hi) vm = fmaxf(vm, vv[j]);
+                }
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16)); mx = fmaxf(mx, __shfl_xor(mx, 32));
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) vm = fmaxf(vm, __shfl_xor(vm, o));
+        if (g == 0 && lo8) mxw[wv][m16] = mx;
+        if (lane == 0) vmw[wv] = vm;
+        __syncthreads();
+        const float M = fmaxf(fmaxf(mxw[0][hq], mxw[1][hq]), fmaxf(mxw[2][hq], mxw[3][hq]));  // head hq, this chunk
+        float VM = fmaxf(fmaxf(vmw[0], vmw[1]), fmaxf(vmw[2], vmw[3]));
+        VM = VM > 0.f ? VM : 1.f;
+        const float iv = 4194304.f / VM;  // P' = p * vs / VM in 22-bit fixed point
+        // ---- pass 1.5: P digits of this wavefront's 32 keys -> LDS (dwords gq0, gq0+1 of the step's operands) ----
+        float lc = 0.f;
+        if (has) {
+            uint32_t wa[2], wb[2];
+#pragma unroll
+            for (int q4 = 0; q4 < 2; q4++) {
+                int da[4], db[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int j = 4 * q4 + u;
+                    const float p = fast_exp2(sc[j] - M);  // 0 for masked keys
+                    lc += p;
+                    int d2, d1, d0;
+                    digits3((int)(p * (vv[j] * iv) + 0.5f), d2, d1, d0);
+                    da[u] = lo8 ? d2 : d1;
+                    db[u] = lo8 ? d0 : 0;
+                }
+                wa[q4] = pack_bytes(da[0], da[1], da[2], da[3]);
+                wb[q4] = pack_bytes(db[0], db[1], db[2], db[3]);
+            }
+            *(reinterpret_cast<uint2*>(Pl + (stw * 2 + 0) * 64 + lane) + (wv & 1)) = make_uint2(wa[0], wa[1]);
+            *(reinterpret_cast<uint2*>(Pl + (stw * 2 + 1) * 64 + lane) + (wv & 1)) = make_uint2(wb[0], wb[1]);
+        } else if (stw < nsteps) {  // the step exists but none of its keys is mine: zero probabilities
+            *(reinterpret_cast<uint2*>(Pl + (stw * 2 + 0) * 64 + lane) + (wv & 1)) = make_uint2(0u, 0u);
+            *(reinterpret_cast<uint2*>(Pl + (stw * 2 + 1) * 64 + lane) + (wv & 1)) = make_uint2(0u, 0u);
+        }
+        {   // chunk bookkeeping of head hq (identical in every wavefront)
+            const float mh_new = fmaxf(mh_run, M);
+            lw_acc = lw_acc * fast_exp2(mh_run - mh_new) + (lo8 ? lc : 0.f) * fast_exp2(M - mh_new);
+            mh_run = mh_new;
+        }
+        __syncthreads();
+        // ---- pass 2: P.V for this wavefront's 64 dims over every step of the chunk ----
+        int4_t_ oa[4], ob[4];
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) { oa[cc] = int4_t_{0, 0, 0, 0}; ob[cc] = int4_t_{0, 0, 0, 0}; }
+        for (int st = 0; st < nsteps; st++) {
+            uint32_t r[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const int key = 64 * st + 16 * (j >> 2) + 4 * g + (j & 3);
+                r[j] = *reinterpret_cast<const uint32_t*>(Vs + key * AHD + rd);
+            }
+            const int4_t_ pa = Pl[(st * 2 + 0) * 64 + lane], pb = Pl[(st * 2 + 1) * 64 + lane];
+            uint32_t tq[4][4];
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++) tr4x4_(r[4 * q4], r[4 * q4 + 1], r[4 * q4 + 2], r[4 * q4 + 3], tq[q4]);
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                const int4_t_ vb = {(int)tq[0][cc], (int)tq[1][cc], (int)tq[2][cc], (int)tq[3][cc]};
+                oa[cc] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, vb, oa[cc], 0, 0, 0);
+                ob[cc] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pb, vb, ob[cc], 0, 0, 0);
+            }
+        }
+        // ---- fold the chunk into fp32: rows 4g+i (g < 2) = digit 2 of head 4g+i, its digit 1 in lane + 32 ----
+        const float vs_scale = VM * (1.f / 4194304.f);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int h = 4 * (g & 1) + i;
+            const float Mh = fmaxf(fmaxf(mxw[0][h], mxw[1][h]), fmaxf(mxw[2][h], mxw[3][h]));
+            const float mn = fmaxf(m_run[i], Mh);
+            const float f_old = fast_exp2(m_run[i] - mn), f_new = fast_exp2(Mh - mn) * vs_scale;
+            m_run[i] = mn;
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                const int d1 = __shfl_xor(oa[cc][i], 32);
+                const float x = ((float)oa[cc][i] * 65536.f + (float)d1 * 256.f) + (float)ob[cc][i];
+                of[cc][i] = of[cc][i] * f_old + x * f_new;
+            }
+        }
+    }
+    // ---- head sums: lanes m16 < 8 of every group and wavefront hold parts of head m16's sum ----
+    float l_run = lw_acc;
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+    __syncthreads();  // the last chunk's readers of mxw are done
+    if (g == 0 && lo8) lsum[wv][m16] = l_run;
+    __syncthreads();
+    if (g < 2) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int h = 4 * g + i;
+            float* p = part + (((size_t)tok * H + kvh * GQ + h) * ns + s) * (AHD + 2);
+            float2* dst = reinterpret_cast<float2*>(p + 2 + 64 * wv + 4 * m16);  // rows are 8-byte aligned
+            dst[0] = make_float2(of[0][i], of[1][i]);
+            dst[1] = make_float2(of[2][i], of[3][i]);
+            if (wv == 0 && m16 == 0) {
+                p[0] = nch ? m_run[i] : -INFINITY;
+                p[1] = nch ? lsum[0][h] + lsum[1][h] + lsum[2][h] + lsum[3][h] : 0.f;
+            }
+        }
+    }
+}
+
 void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part, int T,
                 int ns, hipStream_t st) {
     const int nb = KV * ns * T;
     if (kv.turbo)
         hipLaunchKernelGGL(gqa_decode_kernel<true>, dim3(nb), dim3(256), 0, st, qo, kv, H, pos_d, max_t, part, T, ns);
-    else
-        hipLaunchKernelGGL(gqa_decode_kernel<false>, dim3(nb), dim3(256), 0, st, qo, kv, H, pos_d, max_t, part, T, ns);
+    else {
+        static bool once = [] {
+            MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_i8_kernel),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, I8_LDS_ALL));
+            return true;
+        }();
+        (void)once;
+        hipLaunchKernelGGL(gqa_i8_kernel, dim3(nb), dim3(256), I8_LDS_ALL, st, qo, kv, H, pos_d, max_t, part, T, ns);
+    }
     MOEX_LAUNCHED();
 }
 

@@ -197,52 +197,63 @@ __global__ void __launch_bounds__(256) turbo_out_kernel(float* __restrict__ out,
     o[d] = x / (1.f + __expf(-q_gate[(size_t)tok * ld + h * 2 * AHD + AHD + d]));
 }
 
-// attn_combine_k (kernels.cuh:1317-1329): merge ns partials {m (log2 units), l, acc[256]}. Grid (H, T), 256
-// threads. turbo_rot: the merged row is rotated back (inverse WHT) before the gate, i.e. turbo_out fused in.
+// attn_combine_k (kernels.cuh:1317-1329): merge ns partials {m (log2 units), l, acc[256]}.
+// Grid (H, T, DC): block (h, t, c) owns dims [c*256/DC, (c+1)*256/DC); its 256 threads are DW = 256/DC dims x DC
+// split groups, so every thread walks ns/DC partials with 8 loads in flight, then the groups are summed in LDS.
+// turbo_rot (DC = 1): the merged row is rotated back (inverse WHT) before the gate, i.e. turbo_out fused in.
+template <int DC>
 __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ part, const float* __restrict__ q_gate,
                                                       float* __restrict__ out, int H, int ns, int ld, int turbo_rot) {
-    __shared__ float w[1024];
+    constexpr int DW = AHD / DC;  // dims per block
+    constexpr int NG = 256 / DW;  // split groups
+    __shared__ float w[2048];
+    __shared__ float red[NG][DW];
     __shared__ float sh[AHD];
     __shared__ float sh8[16];
-    const int tok = blockIdx.y, h = blockIdx.x, d = threadIdx.x;
+    const int tok = blockIdx.y, h = blockIdx.x, tid = threadIdx.x;
     const float* p = part + ((size_t)tok * H + h) * ns * (AHD + 2);
     float M = -INFINITY;
-    for (int s = d; s < ns; s += 256) M = fmaxf(M, p[(size_t)s * (AHD + 2)]);
+    for (int s = tid; s < ns; s += 256) M = fmaxf(M, p[(size_t)s * (AHD + 2)]);
     M = block_max(M, sh8);  // split 0 is never empty, so M is finite
-    float l = 0.f;
-    for (int s0 = 0; s0 < ns; s0 += 1024) {  // weights of up to 1024 splits at a time
-        const int n = min(1024, ns - s0);
+    const int dl = tid % DW, gi = tid / DW, d = blockIdx.z * DW + dl;
+    float l = 0.f, acc = 0.f;
+    for (int s0 = 0; s0 < ns; s0 += 2048) {
+        const int n = min(2048, ns - s0);
         __syncthreads();
-        for (int s = d; s < n; s += 256) {
+        for (int s = tid; s < n; s += 256) {
             const float* q = p + (size_t)(s0 + s) * (AHD + 2);
-            const float ws = q[1] > 0.f ? fast_exp2(q[0] - M) : 0.f;
+            const float ls = q[1], ws = ls > 0.f ? fast_exp2(q[0] - M) : 0.f;
             w[s] = ws;
-            l += q[1] * ws;
+            l += ls * ws;
         }
         __syncthreads();
+        int s = gi;
+        for (; s + 7 * NG < n; s += 8 * NG) {
+            float a[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) a[u] = p[(size_t)(s0 + s + u * NG) * (AHD + 2) + 2 + d];
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc += w[s + u * NG] * a[u];
+        }
+        for (; s < n; s += NG) acc += w[s] * p[(size_t)(s0 + s) * (AHD + 2) + 2 + d];
     }
-    l = block_sum(l, sh8);
-    float acc = 0.f;
-    for (int s0 = 0; s0 < ns; s0 += 1024) {
-        const int n = min(1024, ns - s0);
-        __syncthreads();
-        for (int s = d; s < n; s += 256) {
-            const float* q = p + (size_t)(s0 + s) * (AHD + 2);
-            w[s] = q[1] > 0.f ? fast_exp2(q[0] - M) : 0.f;
-        }
-        __syncthreads();
-        int s = 0;
-        for (; s + 4 <= n; s += 4) {
-            const float* q = p + (size_t)(s0 + s) * (AHD + 2) + 2 + d;
-            const float a0 = q[0], a1 = q[AHD + 2], a2 = q[2 * (AHD + 2)], a3 = q[3 * (AHD + 2)];
-            acc += w[s] * a0; acc += w[s + 1] * a1; acc += w[s + 2] * a2; acc += w[s + 3] * a3;
-        }
-        for (; s < n; s++) acc += w[s] * p[(size_t)(s0 + s) * (AHD + 2) + 2 + d];
+    l = block_sum(l, sh8 + 8);
+    red[gi][dl] = acc;
+    __syncthreads();
+    if (tid >= DW) {
+        if (!turbo_rot) return;
     }
-    float x = acc / l;
-    if (turbo_rot) x = wht(x, sh, 1);
-    if (q_gate) x = x / (1.f + __expf(-q_gate[(size_t)tok * ld + h * 2 * AHD + AHD + d]));
-    out[((size_t)tok * H + h) * AHD + d] = x;
+    float x = 0.f;
+    if (tid < DW) {
+#pragma unroll
+        for (int g = 0; g < NG; g++) x += red[g][tid];
+        x /= l;
+    }
+    if (turbo_rot) x = wht(x, sh, 1);  // DC == 1: every thread holds one dim
+    if (tid < DW) {
+        if (q_gate) x = x / (1.f + __expf(-q_gate[(size_t)tok * ld + h * 2 * AHD + AHD + d]));
+        out[((size_t)tok * H + h) * AHD + d] = x;
+    }
 }
 
 // attn_decode_k (kernels.cuh:1238-1315): one block per (query head, token, split), 256 threads, any H / KV.
@@ -355,7 +366,10 @@ void launch_turbo_out(float* out, const float* q_gate, int H, int ld, int T, hip
 }
 void launch_combine(const float* part, const float* q_gate, float* out, int H, int ns, int ld, int T, int turbo_rot,
                     hipStream_t st) {
-    hipLaunchKernelGGL(combine_kernel, dim3(H, T), dim3(256), 0, st, part, q_gate, out, H, ns, ld, turbo_rot);
+    if (turbo_rot)
+        hipLaunchKernelGGL(combine_kernel<1>, dim3(H, T, 1), dim3(256), 0, st, part, q_gate, out, H, ns, ld, 1);
+    else
+        hipLaunchKernelGGL(combine_kernel<8>, dim3(H, T, 8), dim3(256), 0, st, part, q_gate, out, H, ns, ld, 0);
     MOEX_LAUNCHED();
 }
 void launch_decode_heads(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
