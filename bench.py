@@ -6,7 +6,7 @@ reference's flop count 4*H*D*T*(pos0 + T/2) (tests/test_fa.cu:137). A step = one
 cache) are resident in HBM before the timed region.
 
 Also reported (other configs of BASELINE.json, same JSON line): decode / MTP verify at 90k context (T=1, T=4;
-HBM GB/s over the 520 B/row KV, MALL flushed before every step), TurboQuant decode at 262144, TurboQuant prefill at
+HBM GB/s over the 520 B/row KV, rotating over 4 caches that together exceed the MALL), TurboQuant decode at 262144, TurboQuant prefill at
 260096..262143 and the int8 chunk at the same depth, and config 0 (pos0 = 0).
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
@@ -39,6 +39,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="only run a plain 256 MiB device copy 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (the attention path of a batch-1 engine); "
@@ -51,7 +53,14 @@ def main():
     torch.cuda.set_device(0)
     dev = "cuda"
     st = torch.cuda.current_stream()
-    gen = torch.Generator(device=dev).manual_seed(1)
+    if a.copy_calib:
+        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calib_bytes_each_way": src.numel() * 4, "launches": 5}))
+        return
 
     def ev():
         return torch.cuda.Event(enable_timing=True)
@@ -89,19 +98,20 @@ def main():
         wall = (time.perf_counter() - t0) * 1e3
         return e0.elapsed_time(e1) / steps, wall / steps
 
-    flush = torch.empty(768 << 20, dtype=torch.uint8, device=dev)  # > 256 MB MALL + L2
-
-    def time_flushed(fn, reps):
-        ts = []
-        for i in range(reps + 3):
-            flush.fill_(i & 0xff)
-            e0, e1 = ev(), ev()
-            e0.record(st)
-            fn()
-            e1.record(st)
-            e1.synchronize()
-            ts.append(e0.elapsed_time(e1))
-        return float(np.median(ts[3:]))
+    def time_rotating(fns, steps):
+        """Average time per call of fns[i % len(fns)] over `steps` back-to-back calls. Each fn reads its own KV
+        cache and together they exceed the 256 MB MALL, so every call streams its cache from HBM; timing a loop
+        avoids the event overhead that dominates a single ~20 us launch."""
+        for f in fns:
+            f()
+        torch.cuda.synchronize()
+        e0, e1 = ev(), ev()
+        e0.record(st)
+        for i in range(steps):
+            fns[i % len(fns)]()
+        e1.record(st)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
 
     res = {}
     # ---------------- headline: config 1, int8 prefill chunk at 32k ----------------
@@ -137,29 +147,41 @@ def main():
         # ---------------- config 2: decode + MTP verify at 90k (int8) ----------------
         dec = {}
         ctx = 90000
+        NROT = 4  # 4 x 93.6 MB of KV > MALL
+        rot = []
+        for i in range(NROT):
+            c = M.DeviceKVCache(KV, ctx + 64, 0)
+            fill_cache(c, ctx, seed=20 + i)
+            rot.append(c)
         for Tq in (1, 4):
             ns = M.decode_splits(ctx)
             part = torch.empty(Tq * H * ns * (AHD + 2), device=dev)
             o1 = torch.empty((Tq, H, AHD), device=dev)
             pd = torch.tensor([ctx - Tq], dtype=torch.int32, device=dev)
 
-            def gqa():
-                M.attn_gqa(qo[:Tq], c8, H, KV, pd, c8.max_t, part, Tq, ns, st)
+            def gqa(c):
+                return lambda: M.attn_gqa(qo[:Tq], c, H, KV, pd, c.max_t, part, Tq, ns, st)
 
-            def full():
-                gqa()
-                M.attn_combine(part, qg[:Tq], o1, H, ns, LD, Tq, st)
+            def full(c):
+                def f():
+                    M.attn_gqa(qo[:Tq], c, H, KV, pd, c.max_t, part, Tq, ns, st)
+                    M.attn_combine(part, qg[:Tq], o1, H, ns, LD, Tq, st)
+                return f
 
-            t_k = time_flushed(gqa, 20)
-            t_f = time_flushed(full, 20)
+            t_k = time_rotating([gqa(c) for c in rot], 200)
+            t_f = time_rotating([full(c) for c in rot], 200)
             kv_bytes = 2.0 * ctx * 520
             dec[f"T{Tq}"] = {"ns": ns, "split_kernel_us": round(t_k * 1e3, 2), "with_combine_us": round(t_f * 1e3, 2),
                              "GBps": round(kv_bytes / (t_f * 1e-3) / 1e9, 1),
-                             "split_kernel_GBps": round(kv_bytes / (t_k * 1e-3) / 1e9, 1)}
+                             "split_kernel_GBps": round(kv_bytes / (t_k * 1e-3) / 1e9, 1),
+                             "hbm_frac": round(kv_bytes / (t_f * 1e-3) / 1e9 / PEAK_HBM, 4)}
             print(f"[bench] config2 decode T={Tq} ctx={ctx} ns={ns}: {t_f * 1e3:.1f} us "
                   f"({dec[f'T{Tq}']['GBps']} GB/s; split kernel alone {t_k * 1e3:.1f} us)", flush=True)
+        del rot
         extra["config2_decode_int8_90k"] = dec
         # ---------------- config 1 depth comparison / config 4: turbo at 262k ----------------
+        flush_read = torch.ones(192 << 20, dtype=torch.float32, device=dev)  # 768 MB read between calls
+        t_flush = time_rotating([lambda: flush_read.sum()], 20)
         ct = M.DeviceKVCache(KV, 262144 + 64, 1)
         fill_cache(ct, 262144, seed=12)
         ctx = 262144
@@ -173,7 +195,7 @@ def main():
             M.attn_combine(part, None, o1, H, ns, LD, 1, st)
             M.turbo_out(o1, qg[:1], H, LD, 1, st)
 
-        t_td = time_flushed(tdec, 10)
+        t_td = time_rotating([tdec, lambda: flush_read.sum()], 20) * 2 - t_flush
         tb = 2.0 * ctx * 240
         extra["config3_decode_turbo_262k"] = {"ns": ns, "us": round(t_td * 1e3, 2),
                                               "GBps": round(tb / (t_td * 1e-3) / 1e9, 1)}
@@ -228,7 +250,7 @@ def cpu_baseline(c8, qo, qg, pos0, T, seconds):
     g = qg.cpu().numpy()
     threads = max(1, min(16, len(os.sched_getaffinity(0))))
     # rows in an order that spreads over the chunk: tokens by bit-reversed stride, all heads
-    toks = list(range(0, T, 37)) + list(range(18, T, 37))
+    toks = [t for s0 in range(37) for t in range((s0 * 19) % 37, T, 37)]
     rows = [(t, h) for t in toks for h in range(H)]
     deadline = time.perf_counter() + seconds
     done, flops = 0, 0.0
