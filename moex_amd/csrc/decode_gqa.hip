@@ -326,18 +326,15 @@ __global__ void __launch_bounds__(256, 2) gqa_decode_kernel(const float* __restr
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// int8 KV: the same split-K decode on v_mfma_i32_16x16x64_i8, with the raw int8 K and V bytes as MFMA operands (no
-// widening at all). The fp32 query and the probabilities enter as 24-bit fixed point written in three signed base-256
-// digits (x = d2*2^16 + d1*2^8 + d0, each digit in [-128, 127]); every digit product is accumulated exactly in int32
-// and the digits are recombined in fp32, so both products keep fp32-level precision (the reference decode is fp32).
-// Two passes over each chunk of keys make the int32 accumulation possible: pass 1 computes all scores of the chunk
-// and their exact maximum (no online rescaling), pass 2 forms P = 2^(s - max) and accumulates P.V.
+// int8 KV (gqa_x_kernel below). Q.K runs on v_mfma_i32_16x16x64_i8 with the raw int8 K bytes as operands: the fp32
+// query enters as 24-bit fixed point in three signed base-256 digits (x = d2*2^16 + d1*2^8 + d0, each digit in
+// [-128, 127]), every digit product is accumulated exactly in int32 and the digits are recombined in fp32, so the
+// scores keep fp32-level precision (the reference decode is fp32).
 //   Q.K:  16 keys x 16 columns per MFMA; column m < 8 = digit 2 of head m, m >= 8 = digit 1 of head m-8, a second
 //         MFMA holds digit 0 of the 8 heads. Lane (g = lane/16, m = lane%16) receives keys 4g + i of the group for
 //         column m; the digits of a head are brought together with two row_ror:8 DPP moves.
-//   P.V:  rows = the same digit/head layout for P; the four wavefronts split the 256 dims (64 each) and all of them
-//         walk every key of the chunk, reading the P operands that pass 1 left in LDS. Each lane loads 4 bytes (dims
-//         64w + 4m .. +3) of 16 key rows and a 4x4 byte transpose turns them into the B operands.
+// P.V runs on fp16 MFMA (see gqa_x_kernel). Each chunk first computes all its scores and their maximum (pass 1), then
+// forms P (pass 1.5) and accumulates P.V (pass 2).
 constexpr int ICH = 128;                           // keys per chunk: 32 keys (two 16-key groups) per wavefront
 typedef int int4_t_ __attribute__((ext_vector_type(4)));
 
@@ -362,35 +359,50 @@ __device__ __forceinline__ void tr4x4_(const uint32_t r0, const uint32_t r1, con
 typedef __attribute__((address_space(1))) const void* gptr_t;
 typedef __attribute__((address_space(3))) void* lptr_t;
 
-// One workgroup per split, walking it in chunks of 256 keys with the loads of chunk c+1 in flight while chunk c is
-// computed: the V rows go straight to LDS (global_load_lds_dwordx4, double buffered, 64-byte blocks XOR-swizzled by
-// key/4 so the pass-2 reads of the four lane groups hit disjoint banks), the K rows and the scales to registers.
-// The query digits are computed once per workgroup and shared through LDS.
-constexpr int I8_VBUF = ICH * AHD;                                       // 64 KB per V buffer
-constexpr int I8_LDS_ALL = 2 * I8_VBUF + 2 * (ICH / 64) * 64 * 16 + 2 * 4 * 64 * 16;  // + P operands + Q operands
+// One workgroup per (kv head, split, group of TT query tokens), walking the split in chunks of ICH keys with the
+// loads of chunk c+1 in flight while chunk c is computed: the V rows go straight to LDS (global_load_lds_dwordx4,
+// double buffered, 16-byte pieces XOR-swizzled by key/4 so the pass-2 reads of the four lane groups hit disjoint
+// banks), the K rows and the scales to registers (two buffers that swap roles every chunk). Every K/V byte of the
+// chunk serves all TT tokens of the group (MTP verify windows): per token only the MFMAs, the scores and P are
+// repeated. TT = 1 runs two workgroups per CU; TT > 1 holds TT tokens' scores and accumulators (and reads the query
+// digits from LDS) and runs one workgroup per CU.
+constexpr int I8_VBUF = ICH * AHD;                 // 32 KB per V buffer
+constexpr int I8_QL = 2 * 4 * 64 * 16;             // Q digit operands of one token
+static_assert(I8_QL <= I8_VBUF, "query digits of one token stage in V buffer 1");
+// 2^(a - b) with 2^(-inf - -inf) = 1 (a running maximum that has not moved, also while it is still -inf)
+__device__ __forceinline__ float ex2d(float a, float b) { return a == b ? 1.f : fast_exp2(a - b); }
 
-__device__ __forceinline__ void issue_v_chunk(const int8_t* Vg, unsigned char* buf, int c0, int nk, int hi, int tid,
-                                              int wv) {
-    const int nit = (nk + 15) >> 4;  // 16 keys (256 16-byte pieces) per workgroup-wide instruction
-    for (int it = 0; it < nit; it++) {
-        const int q = it * 256 + tid, key = q >> 4, pc = (q & 15) ^ (4 * ((key >> 2) & 3));
-        const int t = min(c0 + key, hi - 1);
-        __builtin_amdgcn_global_load_lds((gptr_t)(Vg + (size_t)t * AHD + 16 * pc),
-                                         (lptr_t)(buf + (size_t)(it * 256 + 64 * wv) * 16), 16, 0, 0);
-    }
-}
+// ---- gqa_x_kernel: Q.K on the int8 MFMA (as gqa_i8_kernel: exact int32 products of the int8 K rows with the
+// query's three base-256 digits), P.V on v_mfma_f32_16x16x32_f16 with fp32 accumulation:
+//   P.V:  A = P, 16 rows (hi parts of the 8 heads, then lo parts: p * vs * 2^sig = hi + lo in fp16, ~22 bits) x 32
+//         keys (a wavefront's keys; lane group g takes keys 4g..4g+3 of both 16-key groups, which is where the Q.K
+//         output layout left them); B = V widened exactly to fp16; output column n of tile j is dim 64*wv + 4n + j,
+//         so each lane reads one dword (4 dims) per key.
+// O stays in the MFMA accumulators across chunks (rescaled by 2^(m_old - m_new) times the change of the per-chunk power
+// of two 2^sig), so a chunk costs no int32 -> fp32 fold and the per-token work is only the MFMAs, the scores and P.
+constexpr int X_PL = 4 * 64 * 16;  // P operands of one token per chunk: [step = wavefront][lane] half8
+template <int TT>
+constexpr int x_lds() { return 2 * I8_VBUF + TT * X_PL + (TT > 1 ? TT * I8_QL : 0); }
 
-__global__ void __launch_bounds__(256, 2) gqa_i8_kernel(const float* __restrict__ qo, moex_kv_cache kv, int H,
-                                                        const int* __restrict__ pos_d, int max_t,
-                                                        float* __restrict__ part, int T, int ns) {
+template <int TT>
+__global__ void __launch_bounds__(256, TT == 1 ? 2 : 1) gqa_x_kernel(const float* __restrict__ qo, moex_kv_cache kv,
+                                                                     int H, const int* __restrict__ pos_d, int max_t,
+                                                                     float* __restrict__ part, int T, int ns) {
     extern __shared__ __align__(16) unsigned char smem[];
-    int4_t_* Pl = reinterpret_cast<int4_t_*>(smem + 2 * I8_VBUF);             // [ICH/64][2][64]
-    int4_t_* Ql = Pl + (ICH / 64) * 2 * 64;                                   // [2][4][64]
-    __shared__ float mxw[4][GQ], lsum[4][GQ], vmw[4], qsc[GQ];
+    half8_t* Pl = reinterpret_cast<half8_t*>(smem + 2 * I8_VBUF);  // [TT][4][64]
+    // query digits: [TT][2][4][64]; TT = 1 holds them in registers and only stages them in V buffer 1
+    int4_t_* Ql = reinterpret_cast<int4_t_*>(TT == 1 ? smem + I8_VBUF : smem + 2 * I8_VBUF + TT * X_PL);
+    __shared__ float mxw[TT][4][GQ], lsum[TT][4][GQ], vmw[4], qsc_s[TT][GQ];
     const int nb = gridDim.x, w_id = xcd_work_id(blockIdx.x, nb);
-    const int tok = w_id % T, s = (w_id / T) % ns, kvh = w_id / (T * ns);
-    const int pos0 = *pos_d, Tk = pos0 + tok + 1, Tmax = pos0 + T;
-    const int L = (Tmax + ns - 1) / ns, lo = s * L, hi = min(Tk, lo + L);
+    const int ngr = (T + TT - 1) / TT;
+    const int tg = w_id % ngr, s = (w_id / ngr) % ns, kvh = w_id / (ngr * ns);
+    const int tb = tg * TT, ntok = min(TT, T - tb);
+    const int pos0 = *pos_d, Tmax = pos0 + T;
+    const int L = (Tmax + ns - 1) / ns, lo = s * L;
+    const int hi = min(pos0 + tb + ntok, lo + L);  // keys of the group's last token; token t sees [lo, hit[t])
+    int hit[TT];
+#pragma unroll
+    for (int t = 0; t < TT; t++) hit[t] = min(pos0 + tb + min(t, ntok - 1) + 1, lo + L);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 4, m16 = lane & 15, hq = m16 & 7;
     const bool lo8 = m16 < 8;
     const size_t rbase = (size_t)kvh * max_t;
@@ -400,46 +412,67 @@ __global__ void __launch_bounds__(256, 2) gqa_i8_kernel(const float* __restrict_
     const float* vsg = kv.vs + rbase;
     const int nch = hi > lo ? (hi - lo + ICH - 1) / ICH : 0;
 
-    // ---- loads of chunk 0 (registers: this wavefront's K step and scales; LDS: all V rows) ----
-    int4_t_ kr[2][4];
-    float ksn[8], vvn[8];  // scales of the next chunk to compute
-    const int stw = wv >> 1, gq0 = 2 * (wv & 1);  // this wavefront's Q.K step and first 16-key group
-    int4_t_ krn[2][4];  // K rows of the next chunk (double buffer)
-    auto issue_kr = [&](int k0) {
+    // ---- loaders. V: thread tid moves 16-byte piece (tid%16) ^ (4*wv) of key 16*it + tid/16 into LDS slot tid%16
+    // (the swizzle depends on (key/4)%4 = wv only). K: this wavefront's keys c0 + 32*wv + 16*grp + m16, dims
+    // 64*ks + 16g + 0..15; scales of the keys 16*grp + 4g + i its lane scores. ----
+    const int8_t* vsrc = Vg + 16 * ((tid & 15) ^ (4 * wv));
+    auto issue_v = [&](unsigned char* buf, int c0) {
+        const int nk = min(ICH, hi - c0);
+        if (nk == ICH) {
+            const int8_t* p = vsrc + (size_t)(c0 + (tid >> 4)) * AHD;
 #pragma unroll
-        for (int grp = 0; grp < 2; grp++) {
-            const int4_t_* kp = reinterpret_cast<const int4_t_*>(Kg + (size_t)min(k0 + 16 * grp + m16, hi - 1) * AHD + 16 * g);
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) krn[grp][ks] = kp[4 * ks];
+            for (int it = 0; it < ICH / 16; it++)
+                __builtin_amdgcn_global_load_lds((gptr_t)(p + it * 16 * AHD), (lptr_t)(buf + (it * 256 + 64 * wv) * 16), 16, 0, 0);
+        } else {
+            const int nit = (nk + 15) >> 4;
+            for (int it = 0; it < nit; it++) {
+                const int t = min(c0 + 16 * it + (tid >> 4), hi - 1);
+                __builtin_amdgcn_global_load_lds((gptr_t)(vsrc + (size_t)t * AHD), (lptr_t)(buf + (it * 256 + 64 * wv) * 16), 16, 0, 0);
+            }
         }
     };
-    auto issue_scales = [&](int k0) {
+    auto issue_k = [&](int4_t_ (&kd)[2][4], float (&ksd)[8], float (&vsd)[8], int c0) {
+        const int k0 = c0 + 32 * wv;
+        if (k0 >= hi) return;
         if (k0 + 32 <= hi) {
+            const int8_t* kp = Kg + (size_t)(k0 + m16) * AHD + 16 * g;
+#pragma unroll
+            for (int grp = 0; grp < 2; grp++)
+#pragma unroll
+                for (int ks = 0; ks < 4; ks++) kd[grp][ks] = *reinterpret_cast<const int4_t_*>(kp + grp * 16 * AHD + 64 * ks);
 #pragma unroll
             for (int grp = 0; grp < 2; grp++) {
                 const float4 a = *reinterpret_cast<const float4*>(ksg + k0 + 16 * grp + 4 * g);
                 const float4 b = *reinterpret_cast<const float4*>(vsg + k0 + 16 * grp + 4 * g);
-                ksn[4 * grp] = a.x; ksn[4 * grp + 1] = a.y; ksn[4 * grp + 2] = a.z; ksn[4 * grp + 3] = a.w;
-                vvn[4 * grp] = b.x; vvn[4 * grp + 1] = b.y; vvn[4 * grp + 2] = b.z; vvn[4 * grp + 3] = b.w;
+                ksd[4 * grp] = a.x; ksd[4 * grp + 1] = a.y; ksd[4 * grp + 2] = a.z; ksd[4 * grp + 3] = a.w;
+                vsd[4 * grp] = b.x; vsd[4 * grp + 1] = b.y; vsd[4 * grp + 2] = b.z; vsd[4 * grp + 3] = b.w;
             }
         } else {
 #pragma unroll
+            for (int grp = 0; grp < 2; grp++) {
+                const int8_t* kp = Kg + (size_t)min(k0 + 16 * grp + m16, hi - 1) * AHD + 16 * g;
+#pragma unroll
+                for (int ks = 0; ks < 4; ks++) kd[grp][ks] = *reinterpret_cast<const int4_t_*>(kp + 64 * ks);
+            }
+#pragma unroll
             for (int j = 0; j < 8; j++) {
                 const int t = min(k0 + 16 * (j >> 2) + 4 * g + (j & 3), hi - 1);
-                ksn[j] = ksg[t]; vvn[j] = vsg[t];
+                ksd[j] = ksg[t]; vsd[j] = vsg[t];
             }
         }
     };
+    int4_t_ kA[2][4], kB[2][4];
+    float ksA[8], vsA[8], ksB[8], vsB[8];
     if (nch > 0) {
-        const int k0 = lo + 64 * stw + 16 * gq0;
-        if (k0 < hi) { issue_kr(k0); issue_scales(k0); }
-        issue_v_chunk(Vg, smem, lo, min(ICH, hi - lo), hi, tid, wv);
+        issue_k(kA, ksA, vsA, lo);
+        issue_v(smem, lo);
     }
 
-    // ---- query digits, once per workgroup: thread = (head tid/32, dims 8*(tid%32) .. +7) ----
-    {
+    // ---- query digits, once per workgroup: thread = (head tid/32, dims 8*(tid%32) .. +7), per token ----
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
         const int h = tid >> 5, d0 = (tid & 31) * 8;
-        const float* qrow = qo + ((size_t)tok * H + kvh * GQ + h) * AHD + d0;
+        const float* qrow = qo + ((size_t)(tb + min(t, ntok - 1)) * H + kvh * GQ + h) * AHD + d0;
         const float4 x0 = reinterpret_cast<const float4*>(qrow)[0], x1 = reinterpret_cast<const float4*>(qrow)[1];
         const float qv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
         float qm = 0.f;
@@ -450,14 +483,14 @@ __global__ void __launch_bounds__(256, 2) gqa_i8_kernel(const float* __restrict_
         int e = 0;
         if (qm > 0.f) (void)frexpf(qm, &e);  // qm < 2^e
         const float up = ldexpf(1.f, 22 - e);
-        if ((tid & 31) == 0) qsc[h] = ldexpf(1.f, e - 22);
+        if ((tid & 31) == 0) qsc_s[t][h] = ldexpf(1.f, e - 22) * SL2;
         int d2[8], d1[8], dz[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) digits3((int)__builtin_rintf(qv[j] * up), d2[j], d1[j], dz[j]);
         // B operand of Q.K: MFMA ks, lane 16g + m holds dims 64ks + 16g + 0..15 of column m
         const int ks = d0 >> 6, gg = (d0 >> 4) & 3, jb = d0 & 15;
-        unsigned char* qa_b = reinterpret_cast<unsigned char*>(Ql + (0 * 4 + ks) * 64);
-        unsigned char* qb_b = reinterpret_cast<unsigned char*>(Ql + (1 * 4 + ks) * 64);
+        unsigned char* qa_b = reinterpret_cast<unsigned char*>(Ql + ((t * 2 + 0) * 4 + ks) * 64);
+        unsigned char* qb_b = reinterpret_cast<unsigned char*>(Ql + ((t * 2 + 1) * 4 + ks) * 64);
         *reinterpret_cast<uint2*>(qa_b + (16 * gg + h) * 16 + jb) =
             make_uint2(pack_bytes(d2[0], d2[1], d2[2], d2[3]), pack_bytes(d2[4], d2[5], d2[6], d2[7]));
         *reinterpret_cast<uint2*>(qa_b + (16 * gg + h + 8) * 16 + jb) =
@@ -467,184 +500,205 @@ __global__ void __launch_bounds__(256, 2) gqa_i8_kernel(const float* __restrict_
         *reinterpret_cast<uint2*>(qb_b + (16 * gg + h + 8) * 16 + jb) = make_uint2(0u, 0u);
     }
     __syncthreads();
-    int4_t_ qa[4], qb[4];
+    int4_t_ qa[4], qb[4];  // TT = 1 only
+    float qs[TT];
 #pragma unroll
-    for (int ks = 0; ks < 4; ks++) { qa[ks] = Ql[ks * 64 + lane]; qb[ks] = Ql[(4 + ks) * 64 + lane]; }
-    const float qscale = qsc[hq];
+    for (int t = 0; t < TT; t++) qs[t] = qsc_s[t][hq];
+    if (TT == 1) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) { qa[ks] = Ql[ks * 64 + lane]; qb[ks] = Ql[(4 + ks) * 64 + lane]; }
+    }
 
-    float of[4][4];                 // fp32 result: [MFMA c][row i]; lanes g < 2: head 4g + i, dim 64*wv + 4*m16 + c
-    float m_run[4];                 // running max of heads 4*(g&1) + i
-    float lw_acc = 0.f, mh_run = -INFINITY;  // this lane's share of head hq's sum, head hq's running max
+    float4_t o[TT][4];                    // O^T tiles j: lane (g, m16) holds rows 4g + i, column m16
+    float m4[TT][4], mo[TT], lacc[TT];    // running max of heads 4(g&1)+i and of head hq; head hq's partial sum
 #pragma unroll
-    for (int c = 0; c < 4; c++)
+    for (int t = 0; t < TT; t++) {
+        mo[t] = -INFINITY; lacc[t] = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; i++) of[c][i] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) m_run[i] = -INFINITY;
+        for (int i = 0; i < 4; i++) { m4[t][i] = -INFINITY; o[t][i] = float4_t{0.f, 0.f, 0.f, 0.f}; }
+    }
+    int sig_ref = 0;  // O is held times 2^sig_ref
     const int rd = 16 * ((4 * wv + (m16 >> 2)) ^ (4 * g)) + 4 * (m16 & 3);  // swizzled byte offset of my V dims
 
-    for (int c = 0; c < nch; c++) {
-        const int c0 = lo + c * ICH, nk = min(ICH, hi - c0), nsteps = (nk + 63) >> 6;
-        const int k0 = c0 + 64 * stw + 16 * gq0;
+    auto chunk = [&](int c, const int4_t_ (&kr)[2][4], const float (&ksv)[8], const float (&vv)[8],
+                     int4_t_ (&kn)[2][4], float (&ksn)[8], float (&vn)[8]) __attribute__((always_inline)) {
+        const int c0 = lo + c * ICH, nk = min(ICH, hi - c0), nsteps = (nk + 31) >> 5;
+        const int k0 = c0 + 32 * wv;
         const bool has = k0 < hi;
-        unsigned char* Vs = smem + (c & 1) * I8_VBUF;
+        const unsigned char* Vs = smem + (c & 1) * I8_VBUF;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // chunk c's K, scales and V rows have landed
         __syncthreads();                                   // ... for every wavefront; chunk c-1 is done with LDS
-        float ksv[8], vv[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) { ksv[j] = ksn[j]; vv[j] = vvn[j]; }
-#pragma unroll
-        for (int grp = 0; grp < 2; grp++)
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) kr[grp][ks] = krn[grp][ks];
-        const int c1 = c0 + ICH;  // the next chunk: all its loads go out now
-        if (c + 1 < nch) {
-            const int k1 = c1 + 64 * stw + 16 * gq0;
-            if (k1 < hi) { issue_kr(k1); issue_scales(k1); }
-            issue_v_chunk(Vg, smem + ((c + 1) & 1) * I8_VBUF, c1, min(ICH, hi - c1), hi, tid, wv);
+        if (c + 1 < nch) {                                 // all loads of chunk c+1 go out now
+            issue_k(kn, ksn, vn, c0 + ICH);
+            issue_v(smem + ((c + 1) & 1) * I8_VBUF, c0 + ICH);
         }
-        // ---- pass 1: scores of this wavefront's 32 keys ----
-        float sc[8];
-        float mx = -INFINITY, vm = 0.f;
+        // ---- pass 1: scores of this wavefront's 32 keys (int8 MFMA on the query digits) ----
+        float sc[TT][8];
+        float vm = 0.f;
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) sc[t][j] = -INFINITY;
         if (has) {
 #pragma unroll
-            for (int grp = 0; grp < 2; grp++) {
-                int4_t_ da = {0, 0, 0, 0}, db = {0, 0, 0, 0};
+            for (int j = 0; j < 8; j++)
+                if (k0 + 16 * (j >> 2) + 4 * g + (j & 3) < hi) vm = fmaxf(vm, vv[j]);
 #pragma unroll
-                for (int ks = 0; ks < 4; ks++) {
-                    da = __builtin_amdgcn_mfma_i32_16x16x64_i8(kr[grp][ks], qa[ks], da, 0, 0, 0);
-                    db = __builtin_amdgcn_mfma_i32_16x16x64_i8(kr[grp][ks], qb[ks], db, 0, 0, 0);
-                }
+            for (int t = 0; t < TT; t++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int x = dpp_ror8(da[i]), y = dpp_ror8(db[i]);
-                    const int a2 = lo8 ? da[i] : x, a1 = lo8 ? x : da[i], a0 = lo8 ? db[i] : y;
-                    const float raw = ((float)a2 * 65536.f + (float)a1 * 256.f) + (float)a0;
-                    const int j = 4 * grp + i, key = k0 + 16 * grp + 4 * g + i;
-                    const float v = key < hi ? raw * (ksv[j] * (SL2 * qscale)) : -INFINITY;
-                    sc[j] = v;
-                    mx = fmaxf(mx, v);
-                    if (key < hi) vm = fmaxf(vm, vv[j]);
+                for (int grp = 0; grp < 2; grp++) {
+                    int4_t_ da = {0, 0, 0, 0}, db = {0, 0, 0, 0};
+#pragma unroll
+                    for (int ks = 0; ks < 4; ks++) {
+                        const int4_t_ a = TT == 1 ? qa[ks] : Ql[(t * 8 + ks) * 64 + lane];
+                        const int4_t_ b = TT == 1 ? qb[ks] : Ql[(t * 8 + 4 + ks) * 64 + lane];
+                        da = __builtin_amdgcn_mfma_i32_16x16x64_i8(kr[grp][ks], a, da, 0, 0, 0);
+                        db = __builtin_amdgcn_mfma_i32_16x16x64_i8(kr[grp][ks], b, db, 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int x = dpp_ror8(da[i]), y = dpp_ror8(db[i]);
+                        const int a2 = lo8 ? da[i] : x, a1 = lo8 ? x : da[i], a0 = lo8 ? db[i] : y;
+                        const float raw = ((float)a2 * 65536.f + (float)a1 * 256.f) + (float)a0;
+                        const int j = 4 * grp + i, key = k0 + 16 * grp + 4 * g + i;
+                        sc[t][j] = key < hit[t] ? raw * (ksv[j] * qs[t]) : -INFINITY;
+                    }
                 }
-            }
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16)); mx = fmaxf(mx, __shfl_xor(mx, 32));
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) vm = fmaxf(vm, __shfl_xor(vm, o));
-        if (g == 0 && lo8) mxw[wv][m16] = mx;
+        for (int t = 0; t < TT; t++) {
+            float mx = sc[t][0];
+#pragma unroll
+            for (int j = 1; j < 8; j++) mx = fmaxf(mx, sc[t][j]);
+            mx = fmaxf(mx, __shfl_xor(mx, 16)); mx = fmaxf(mx, __shfl_xor(mx, 32));
+            if (g == 0 && lo8) mxw[t][wv][m16] = mx;
+        }
+#pragma unroll
+        for (int o2 = 1; o2 < 64; o2 <<= 1) vm = fmaxf(vm, __shfl_xor(vm, o2));
         if (lane == 0) vmw[wv] = vm;
         __syncthreads();
-        const float M = fmaxf(fmaxf(mxw[0][hq], mxw[1][hq]), fmaxf(mxw[2][hq], mxw[3][hq]));  // head hq, this chunk
-        float VM = fmaxf(fmaxf(vmw[0], vmw[1]), fmaxf(vmw[2], vmw[3]));
-        VM = VM > 0.f ? VM : 1.f;
-        const float iv = 4194304.f / VM;  // P' = p * vs / VM in 22-bit fixed point
-        // ---- pass 1.5: P digits of this wavefront's 32 keys -> LDS (dwords gq0, gq0+1 of the step's operands) ----
-        float lc = 0.f;
-        if (has) {
-            uint32_t wa[2], wb[2];
+        const float VM = fmaxf(fmaxf(vmw[0], vmw[1]), fmaxf(vmw[2], vmw[3]));
+        int ev = 0;
+        if (VM > 0.f) (void)frexpf(VM, &ev);  // VM < 2^ev: p * vs * 2^(10 - ev) < 2^10
+        const int sig = 10 - ev;
+        const float vsc = ldexpf(1.f, sig);
+        const float sfac = c == 0 ? 1.f : ldexpf(1.f, sig - sig_ref);  // O re-expressed at the new power of two
+        sig_ref = sig;
+        // ---- pass 1.5: probabilities (hi/lo fp16 operands to LDS), running maxima, O rescale ----
 #pragma unroll
-            for (int q4 = 0; q4 < 2; q4++) {
-                int da[4], db[4];
+        for (int t = 0; t < TT; t++) {
+            const float M = fmaxf(fmaxf(mxw[t][0][hq], mxw[t][1][hq]), fmaxf(mxw[t][2][hq], mxw[t][3][hq]));
+            const float mn = fmaxf(mo[t], M);
+            float ls = 0.f;
+            if (has) {
+                half8_t pv;
 #pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    const int j = 4 * q4 + u;
-                    const float p = fast_exp2(sc[j] - M);  // 0 for masked keys
-                    lc += p;
-                    int d2, d1, d0;
-                    digits3((int)(p * (vv[j] * iv) + 0.5f), d2, d1, d0);
-                    da[u] = lo8 ? d2 : d1;
-                    db[u] = lo8 ? d0 : 0;
+                for (int j = 0; j < 8; j++) {
+                    const float p = mn == -INFINITY ? 0.f : fast_exp2(sc[t][j] - mn);  // 0 for masked keys
+                    ls += p;
+                    const float x = p * (vv[j] * vsc);
+                    const _Float16 h = (_Float16)x;
+                    pv[j] = lo8 ? h : (_Float16)(x - (float)h);
                 }
-                wa[q4] = pack_bytes(da[0], da[1], da[2], da[3]);
-                wb[q4] = pack_bytes(db[0], db[1], db[2], db[3]);
+                Pl[(t * 4 + wv) * 64 + lane] = pv;
             }
-            *(reinterpret_cast<uint2*>(Pl + (stw * 2 + 0) * 64 + lane) + (wv & 1)) = make_uint2(wa[0], wa[1]);
-            *(reinterpret_cast<uint2*>(Pl + (stw * 2 + 1) * 64 + lane) + (wv & 1)) = make_uint2(wb[0], wb[1]);
-        } else if (stw < nsteps) {  // the step exists but none of its keys is mine: zero probabilities
-            *(reinterpret_cast<uint2*>(Pl + (stw * 2 + 0) * 64 + lane) + (wv & 1)) = make_uint2(0u, 0u);
-            *(reinterpret_cast<uint2*>(Pl + (stw * 2 + 1) * 64 + lane) + (wv & 1)) = make_uint2(0u, 0u);
-        }
-        {   // chunk bookkeeping of head hq (identical in every wavefront)
-            const float mh_new = fmaxf(mh_run, M);
-            lw_acc = lw_acc * fast_exp2(mh_run - mh_new) + (lo8 ? lc : 0.f) * fast_exp2(M - mh_new);
-            mh_run = mh_new;
+            lacc[t] = lacc[t] * ex2d(mo[t], mn) + ls;
+            mo[t] = mn;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int h = 4 * (g & 1) + i;
+                const float Mh = fmaxf(fmaxf(mxw[t][0][h], mxw[t][1][h]), fmaxf(mxw[t][2][h], mxw[t][3][h]));
+                const float mnh = fmaxf(m4[t][i], Mh);
+                const float f = ex2d(m4[t][i], mnh) * sfac;
+                m4[t][i] = mnh;
+#pragma unroll
+                for (int jt = 0; jt < 4; jt++) o[t][jt][i] *= f;
+            }
         }
         __syncthreads();
-        // ---- pass 2: P.V for this wavefront's 64 dims over every step of the chunk ----
-        int4_t_ oa[4], ob[4];
-#pragma unroll
-        for (int cc = 0; cc < 4; cc++) { oa[cc] = int4_t_{0, 0, 0, 0}; ob[cc] = int4_t_{0, 0, 0, 0}; }
+        // ---- pass 2: O^T += P . V over the chunk's steps (one per wavefront that had keys), this wavefront's dims ----
         for (int st = 0; st < nsteps; st++) {
-            uint32_t r[16];
+            uint32_t r[8];
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const int key = 64 * st + 16 * (j >> 2) + 4 * g + (j & 3);
+            for (int j = 0; j < 8; j++) {
+                const int key = 32 * st + 16 * (j >> 2) + 4 * g + (j & 3);
                 r[j] = *reinterpret_cast<const uint32_t*>(Vs + key * AHD + rd);
             }
-            const int4_t_ pa = Pl[(st * 2 + 0) * 64 + lane], pb = Pl[(st * 2 + 1) * 64 + lane];
-            uint32_t tq[4][4];
+            uint32_t c0v[4], c1v[4];
+            tr4x4_(r[0], r[1], r[2], r[3], c0v);
+            tr4x4_(r[4], r[5], r[6], r[7], c1v);
+            half8_t vb[4];
 #pragma unroll
-            for (int q4 = 0; q4 < 4; q4++) tr4x4_(r[4 * q4], r[4 * q4 + 1], r[4 * q4 + 2], r[4 * q4 + 3], tq[q4]);
+            for (int jt = 0; jt < 4; jt++) vb[jt] = i8x8_to_h8(c0v[jt], c1v[jt]);
 #pragma unroll
-            for (int cc = 0; cc < 4; cc++) {
-                const int4_t_ vb = {(int)tq[0][cc], (int)tq[1][cc], (int)tq[2][cc], (int)tq[3][cc]};
-                oa[cc] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, vb, oa[cc], 0, 0, 0);
-                ob[cc] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pb, vb, ob[cc], 0, 0, 0);
+            for (int t = 0; t < TT; t++) {
+                const half8_t pa = Pl[(t * 4 + st) * 64 + lane];
+#pragma unroll
+                for (int jt = 0; jt < 4; jt++) o[t][jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb[jt], o[t][jt], 0, 0, 0);
             }
         }
-        // ---- fold the chunk into fp32: rows 4g+i (g < 2) = digit 2 of head 4g+i, its digit 1 in lane + 32 ----
-        const float vs_scale = VM * (1.f / 4194304.f);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int h = 4 * (g & 1) + i;
-            const float Mh = fmaxf(fmaxf(mxw[0][h], mxw[1][h]), fmaxf(mxw[2][h], mxw[3][h]));
-            const float mn = fmaxf(m_run[i], Mh);
-            const float f_old = fast_exp2(m_run[i] - mn), f_new = fast_exp2(Mh - mn) * vs_scale;
-            m_run[i] = mn;
-#pragma unroll
-            for (int cc = 0; cc < 4; cc++) {
-                const int d1 = __shfl_xor(oa[cc][i], 32);
-                const float x = ((float)oa[cc][i] * 65536.f + (float)d1 * 256.f) + (float)ob[cc][i];
-                of[cc][i] = of[cc][i] * f_old + x * f_new;
-            }
-        }
+    };
+    for (int c = 0; c < nch; c += 2) {  // two chunks per trip: the K/scale register buffers swap roles
+        chunk(c, kA, ksA, vsA, kB, ksB, vsB);
+        if (c + 1 < nch) chunk(c + 1, kB, ksB, vsB, kA, ksA, vsA);
     }
-    // ---- head sums: lanes m16 < 8 of every group and wavefront hold parts of head m16's sum ----
-    float l_run = lw_acc;
-    l_run += __shfl_xor(l_run, 16);
-    l_run += __shfl_xor(l_run, 32);
-    __syncthreads();  // the last chunk's readers of mxw are done
-    if (g == 0 && lo8) lsum[wv][m16] = l_run;
+    // ---- partials: rows 4g+i of the O^T tiles are the hi parts (g < 2) of head 4(g&1)+i, the lo parts (g >= 2) ----
     __syncthreads();
-    if (g < 2) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int h = 4 * g + i;
-            float* p = part + (((size_t)tok * H + kvh * GQ + h) * ns + s) * (AHD + 2);
-            float2* dst = reinterpret_cast<float2*>(p + 2 + 64 * wv + 4 * m16);  // rows are 8-byte aligned
-            dst[0] = make_float2(of[0][i], of[1][i]);
-            dst[1] = make_float2(of[2][i], of[3][i]);
-            if (wv == 0 && m16 == 0) {
-                p[0] = nch ? m_run[i] : -INFINITY;
-                p[1] = nch ? lsum[0][h] + lsum[1][h] + lsum[2][h] + lsum[3][h] : 0.f;
+    for (int t = 0; t < TT; t++) {
+        float l = lo8 ? lacc[t] : 0.f;
+        l += __shfl_xor(l, 16);
+        l += __shfl_xor(l, 32);
+        if (g == 0 && lo8) lsum[t][wv][m16] = l;
+    }
+    __syncthreads();
+    const float unscale = ldexpf(1.f, -sig_ref);
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+        float ov[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int jt = 0; jt < 4; jt++) ov[i][jt] = (o[t][jt][i] + __shfl_xor(o[t][jt][i], 32)) * unscale;
+        if (g < 2 && t < ntok) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int h = 4 * g + i;
+                float* p = part + (((size_t)(tb + t) * H + kvh * GQ + h) * ns + s) * (AHD + 2);
+                float2* dst = reinterpret_cast<float2*>(p + 2 + 64 * wv + 4 * m16);  // rows are 8-byte aligned
+                dst[0] = make_float2(ov[i][0], ov[i][1]);
+                dst[1] = make_float2(ov[i][2], ov[i][3]);
+                if (wv == 0 && m16 == 0) {
+                    p[0] = m4[t][i];  // -inf when the token has no key in this split
+                    p[1] = lsum[t][0][h] + lsum[t][1][h] + lsum[t][2][h] + lsum[t][3][h];
+                }
             }
         }
     }
 }
 
+template <int TT>
+static void launch_x(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part,
+                     int T, int ns, hipStream_t st) {
+    static bool once = [] {
+        MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_x_kernel<TT>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, x_lds<TT>()));
+        return true;
+    }();
+    (void)once;
+    const int nb = KV * ns * ((T + TT - 1) / TT);
+    hipLaunchKernelGGL(gqa_x_kernel<TT>, dim3(nb), dim3(256), x_lds<TT>(), st, qo, kv, H, pos_d, max_t, part, T, ns);
+}
+
 void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part, int T,
                 int ns, hipStream_t st) {
-    const int nb = KV * ns * T;
-    if (kv.turbo)
+    if (kv.turbo) {
+        const int nb = KV * ns * T;
         hipLaunchKernelGGL(gqa_decode_kernel<true>, dim3(nb), dim3(256), 0, st, qo, kv, H, pos_d, max_t, part, T, ns);
-    else {
-        static bool once = [] {
-            MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_i8_kernel),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, I8_LDS_ALL));
-            return true;
-        }();
-        (void)once;
-        hipLaunchKernelGGL(gqa_i8_kernel, dim3(nb), dim3(256), I8_LDS_ALL, st, qo, kv, H, pos_d, max_t, part, T, ns);
+    } else {
+        if (T == 1) launch_x<1>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
+        else if (T == 2) launch_x<2>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
+        else launch_x<4>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
     }
     MOEX_LAUNCHED();
 }
