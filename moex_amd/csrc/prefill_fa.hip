@@ -1,31 +1,37 @@
 // FlashAttention-2 chunked causal GQA prefill on gfx950 (replaces attn_fa_k<TB>, kernels.cuh:1443-1728).
 //
 // Workgroup = (kv head, 16 query tokens) = 128 query rows (8 heads x 16 tokens), 4 wavefronts of 32 rows;
-// wavefront w owns tokens 4w .. 4w+3, row r = (token 4w + r/8, head r%8). Keys in tiles of 32:
-//   - the block stages each K/V tile once: int8 (or turbo codes) from HBM -> fp16 in LDS, K as [key][dim]
-//     (16-byte chunks XOR-swizzled by key), V transposed as [dim][key] (row stride 72 B: conflict-free reads);
-//     the next tile's global loads are in flight while the current one is computed (double-buffered LDS);
-//   - S^T = K . Q^T on v_mfma_f32_32x32x16_f16 (Q fp16 in registers): the 32x32 D layout gives every lane ONE
-//     query row (lane % 32) and 16 keys, so the row max / row sum are in-lane plus one cross-half exchange;
-//   - P^T (fp16, times V's row scale) stays in registers and is directly the B operand of O^T += V^T . P^T;
-//     O^T (256 dims x 32 rows per wavefront, 128 fp32 per lane) lives in registers for the whole key loop.
-// Softmax in base 2 with the K scale, 1/sqrt(256) and log2(e) folded into one factor per key (kernels.cuh:1513).
-// Rounding points follow the reference kernel: Q and P * vscale rounded to fp16, fp32 accumulate (:1508,:1656).
-// Turbo: K codes decoded to the centroids' int8 codes, S accumulated per 128-half and combined with the half norms;
-// V's two half norms give two P operands (dims < 128 / >= 128). No gate when q_gate is null.
+// wavefront w owns tokens 4w .. 4w+3, row r = (token 4w + r/8, head r%8). Keys in tiles of 64.
+//   - The block stages every K/V tile once, widening int8 (or turbo codes) to fp16 in LDS: K as [key][dim] with
+//     16-byte chunks XOR-swizzled by key, V transposed as [dim][key] and already multiplied by its row scale
+//     (int8: vs; turbo: half norm * K3), so P enters the P.V product as plain fp16 probabilities. Turbo K is
+//     likewise multiplied by its half norm * K4; int8 K stays exact and its scale is applied to the fp32 score.
+//   - K and V have separate double buffers with staggered lifetimes: while tile j is computed, K of tile j+2 and V
+//     of tile j+1 are written, so one barrier per tile suffices.
+//   - Software pipeline per wavefront: S^T of tile j+1 (v_mfma_f32_32x32x16_f16, Q fp16 in registers) is computed
+//     while the softmax of tile j runs on the VALU, then O^T += V^T . P^T for tile j. The 32x32 D layout gives each
+//     lane one query row (lane % 32) and 16 keys per S tile: row max / row sum are in-lane plus one cross-half swap.
+//   - Lazy rescale: O and l are only rescaled when a row's maximum grows by more than 8 (log2 units) over the value
+//     the probabilities are referenced to, so p <= 2^8; O (256 fp32 per row, 128 accumulators per lane in AGPRs)
+//     is touched by the VALU only then.
+// Softmax in base 2 (scale 1/sqrt(256) * log2(e), kernels.cuh:1513). Rounding: Q, P and the scaled K/V values are
+// fp16 MFMA operands with fp32 accumulation; the reference rounds Q and P * vscale (kernels.cuh:1508,1656).
+#include <type_traits>
 #include "common.hpp"
 
 namespace moex {
 
 namespace {
-constexpr int FT = 16;               // tokens per workgroup
-constexpr int BK = 32;               // keys per tile
-constexpr int VST = BK + 4;          // V^T row stride in halves (72 B)
-constexpr int KT_BYTES = BK * AHD * 2;      // 16 KB
-constexpr int VT_BYTES = AHD * VST * 2;     // 18 KB
-constexpr int BUF_BYTES = KT_BYTES + VT_BYTES + 4 * BK * 4;  // + ks, vs (turbo: kn0, kn1 / vs0, vs1)
+constexpr int FT = 16;                      // tokens per workgroup
+constexpr int BK = 32;                      // keys per tile
+constexpr int VST = BK + 8;                 // V^T row stride in halves (80 B: conflict-free A-operand reads)
+constexpr int KT_BYTES = BK * AHD * 2;      // 32 KB
+constexpr int VT_BYTES = AHD * VST * 2;     // 36 KB
+constexpr int SC_BYTES = BK * 4;            // per-key score scale
+constexpr int LDS_BYTES = 2 * KT_BYTES + 2 * VT_BYTES + 3 * SC_BYTES;  // 2 score-scale slots + a spare
 constexpr float SL2 = 0.0625f * 1.4426950408889634f;
 constexpr float TK4 = 0.241529f / 127.f, TK3 = 0.190207f / 127.f;
+constexpr float RESCALE_SLACK = 8.f;        // p <= 2^8 between rescales
 
 constexpr uint32_t pack4(int a, int b, int c, int d) {
     return (uint32_t)(a + 128) | ((uint32_t)(b + 128) << 8) | ((uint32_t)(c + 128) << 16) | ((uint32_t)(d + 128) << 24);
@@ -34,142 +40,162 @@ constexpr uint32_t K4T0 = pack4(-127, -96, -75, -58), K4T1 = pack4(-44, -31, -18
 constexpr uint32_t K4T2 = pack4(6, 18, 31, 44), K4T3 = pack4(58, 75, 96, 127);
 constexpr uint32_t V3T0 = pack4(-127, -79, -45, -14), V3T1 = pack4(14, 45, 79, 127);
 
-__device__ __forceinline__ uint32_t lut16(uint32_t idx) {
+__device__ __forceinline__ uint32_t lut16(uint32_t idx) {  // 4 nibble indices (one per byte) -> 4 biased K codes
     const uint32_t s = idx & 0x07070707u;
     const uint32_t lo = __builtin_amdgcn_perm(K4T1, K4T0, s), hi = __builtin_amdgcn_perm(K4T3, K4T2, s);
     const uint32_t mask = ((idx >> 3) & 0x01010101u) * 0xffu;
     return (hi & mask) | (lo & ~mask);
 }
-
 // 4x4 byte transpose: r[k] = 4 bytes (dims) of key k -> c[d] = 4 bytes (keys) of dim d
-__device__ __forceinline__ void tr4x4(const uint32_t r[4], uint32_t c[4]) {
-    const uint32_t t0 = __builtin_amdgcn_perm(r[1], r[0], 0x05010400u), t1 = __builtin_amdgcn_perm(r[1], r[0], 0x07030602u);
-    const uint32_t t2 = __builtin_amdgcn_perm(r[3], r[2], 0x05010400u), t3 = __builtin_amdgcn_perm(r[3], r[2], 0x07030602u);
+__device__ __forceinline__ void tr4x4(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3, uint32_t c[4]) {
+    const uint32_t t0 = __builtin_amdgcn_perm(r1, r0, 0x05010400u), t1 = __builtin_amdgcn_perm(r1, r0, 0x07030602u);
+    const uint32_t t2 = __builtin_amdgcn_perm(r3, r2, 0x05010400u), t3 = __builtin_amdgcn_perm(r3, r2, 0x07030602u);
     c[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u); c[1] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
     c[2] = __builtin_amdgcn_perm(t3, t1, 0x05040100u); c[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
 }
-
-__device__ __forceinline__ int kchunk(int key, int c) { return c ^ (key & 15); }  // swizzled 16-byte chunk
+__device__ __forceinline__ int kchunk(int key, int c) { return c ^ (key & 15); }  // swizzled 16-byte chunk of a K row
+// V^T key positions within each 16-key group are [0..3, 8..11, 4..7, 12..15]: a P.V A operand (keys 16m + 4h + 0..3
+// and 16m + 8 + 4h + 0..3) is the 8 contiguous halves at position 16m + 8h, and one staging thread writes them.
 
 // raw global data of one tile held by a thread between the load and the LDS write
-struct Stage {
-    uint4 k[2];      // int8: 32 bytes of key t/8 (dims 32*(t%8) ..); turbo: k[0] = 16 nibble bytes
-    uint32_t v[8];   // int8: 4 bytes (dims 4*(t%64) ..) of keys 8*(t/64) .. +7; turbo: (low byte | high byte << 8)
-    float sa, sb, sc, sd;  // thread < BK: scales of key t
+constexpr int TPK = 256 / BK;               // threads per K row; each owns BK dims (BK bytes of int8)
+struct StageK {
+    uint4 k[BK / 16];  // int8: BK bytes of key t/TPK (dims BK*(t%TPK) ..); turbo: the first BK/32 hold its nibbles
+    float kn;          // turbo: the half norm of those dims
+    float ks;          // thread < BK: score scale of key t (int8: ks * sl2, turbo: sl2)
 };
+// V: thread t stages dims 4*(t%64) .. +3 of the 8 keys 16m + 4h + {0..3, 8..11} with m = t/128, h = (t/64)%2
+struct StageV {
+    uint32_t v[8];     // int8: 4 bytes of each key; turbo: low byte | high byte << 8
+    float vs[8];       // scales of those keys (turbo: half norm * K3 of the thread's dims)
+};
+__device__ __forceinline__ int vkey(int tid, int i) { return 16 * (tid >> 7) + 4 * ((tid >> 6) & 1) + (i & 3) + 8 * (i >> 2); }
 
-template <bool TB>
-__device__ __forceinline__ void stage_load(Stage& S, moex_kv_cache kv, size_t rbase, int k0, int hi, int tid) {
-    {
-        const int key = tid >> 3, c = tid & 7, t = k0 + key;
-        const size_t row = rbase + (t < hi ? t : hi - 1);
-        if (TB) {
-            S.k[0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(kv.k) + row * TQ_KB + c * 16);
-        } else {
-            const uint4* p = reinterpret_cast<const uint4*>(kv.k + row * AHD + c * 32);
-            S.k[0] = p[0]; S.k[1] = p[1];
-        }
-    }
-    {
-        const int dg = tid & 63, kb = (tid >> 6) * 8;
+// FULL: every key of the tile exists (no clamping / masking)
+template <bool TB, bool FULL = false>
+__device__ __forceinline__ void load_k(StageK& S, moex_kv_cache kv, size_t rbase, int k0, int hi, int tid) {
+    const int key = tid / TPK, c = tid % TPK, t = k0 + key;
+    const size_t row = rbase + (FULL || t < hi ? t : hi - 1);
+    if (TB) {  // dims BK*c .. +BK-1 are nibble bytes (BK/2)*c .. of the row (halves are contiguous in the layout)
+        const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(kv.k) + row * TQ_KB + c * (BK / 2));
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int t = k0 + kb + i;
-            const size_t row = rbase + (t < hi ? t : hi - 1);
-            if (TB) {
-                const uint8_t* vp = reinterpret_cast<const uint8_t*>(kv.v) + row * TQ_VB;
-                const int b = dg >> 5;
-                S.v[i] = (uint32_t)vp[b * 32 + (dg & 31)] | ((uint32_t)vp[64 + b * 16 + ((dg & 31) >> 1)] << 8);
-            } else {
-                S.v[i] = *reinterpret_cast<const uint32_t*>(kv.v + row * AHD + dg * 4);
-            }
-        }
+        for (int i = 0; i < BK / 32; i++) S.k[i] = p[i];
+        S.kn = kv.ks[row * 2 + (BK * c) / 128];
+    } else {
+        const uint4* p = reinterpret_cast<const uint4*>(kv.k + row * AHD + c * BK);
+#pragma unroll
+        for (int i = 0; i < BK / 16; i++) S.k[i] = p[i];
     }
-    if (tid < BK) {
-        const int t = k0 + tid;
-        const size_t row = rbase + (t < hi ? t : hi - 1);
+    {   // every thread loads a scale (branch-free); threads < BK own key tid's
+        const int tt = k0 + (tid & (BK - 1));
+        S.ks = TB ? SL2 : kv.ks[rbase + (FULL || tt < hi ? tt : hi - 1)] * SL2;
+    }
+}
+
+template <bool TB, bool FULL = false>
+__device__ __forceinline__ void load_v(StageV& S, moex_kv_cache kv, size_t rbase, int k0, int hi, int tid) {
+    const int dg = tid & 63;
+    if (FULL && !TB) {  // rows k0 + vkey(tid, 0) + {0..3, 8..11}: one base address, constant offsets
+        const size_t row0 = rbase + k0 + vkey(tid, 0);
+        const int8_t* vp = kv.v + row0 * AHD + dg * 4;
+#pragma unroll
+        for (int i = 0; i < 8; i++) S.v[i] = *reinterpret_cast<const uint32_t*>(vp + ((i & 3) + 8 * (i >> 2)) * AHD);
+        const float4 a = *reinterpret_cast<const float4*>(kv.vs + row0), b = *reinterpret_cast<const float4*>(kv.vs + row0 + 8);
+        S.vs[0] = a.x; S.vs[1] = a.y; S.vs[2] = a.z; S.vs[3] = a.w;
+        S.vs[4] = b.x; S.vs[5] = b.y; S.vs[6] = b.z; S.vs[7] = b.w;
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int t = k0 + vkey(tid, i);
+        const size_t row = rbase + (FULL || t < hi ? t : hi - 1);
         if (TB) {
-            const float2 kn = *reinterpret_cast<const float2*>(kv.ks + row * 2);
-            const float2 vn = *reinterpret_cast<const float2*>(kv.vs + row * 2);
-            S.sa = kn.x; S.sb = kn.y; S.sc = vn.x; S.sd = vn.y;
+            const uint8_t* vp = reinterpret_cast<const uint8_t*>(kv.v) + row * TQ_VB;
+            const int b = dg >> 5;
+            S.v[i] = (uint32_t)vp[b * 32 + (dg & 31)] | ((uint32_t)vp[64 + b * 16 + ((dg & 31) >> 1)] << 8);
+            S.vs[i] = kv.vs[row * 2 + b] * TK3;
         } else {
-            S.sa = kv.ks[row]; S.sc = kv.vs[row];
+            S.v[i] = *reinterpret_cast<const uint32_t*>(kv.v + row * AHD + dg * 4);
+            S.vs[i] = kv.vs[row];
         }
     }
 }
 
-template <bool TB>
-__device__ __forceinline__ void stage_store(const Stage& S, unsigned char* buf, int k0, int hi, int tid) {
-    _Float16* Kt = reinterpret_cast<_Float16*>(buf);
-    _Float16* Vt = reinterpret_cast<_Float16*>(buf + KT_BYTES);
-    float* sc = reinterpret_cast<float*>(buf + KT_BYTES + VT_BYTES);
-    {
-        const int key = tid >> 3, c = tid & 7;
-        const bool ok = k0 + key < hi;
-        uint32_t w[16];
-        if (TB) {
-            const uint32_t in[4] = {S.k[0].x, S.k[0].y, S.k[0].z, S.k[0].w};
+template <bool TB, bool FULL = false>
+__device__ __forceinline__ void store_k(const StageK& S, unsigned char* kbuf, float* sbuf, float* spare, int k0, int hi,
+                                        int tid) {
+    _Float16* Kt = reinterpret_cast<_Float16*>(kbuf);
+    const int key = tid / TPK, c = tid % TPK;
+    const bool ok = k0 + key < hi;
+    uint32_t w[BK / 2];  // BK halves
+    if (TB) {  // BK nibbles -> biased codes -> fp16, times the half norm * K4
+        const half2_t sc = half2_t{(_Float16)(S.kn * TK4), (_Float16)(S.kn * TK4)};
 #pragma unroll
-            for (int i = 0; i < 4; i++) {  // 8 nibbles -> dims 8i .. 8i+7 (biased codes), widened
-                const uint32_t e = lut16(in[i] & 0x0f0f0f0fu), o = lut16((in[i] >> 4) & 0x0f0f0f0fu);
-                const uint32_t d01 = __builtin_amdgcn_perm(o, e, 0x05010400u), d23 = __builtin_amdgcn_perm(o, e, 0x07030602u);
-                biased4_to_h4(d01, w[4 * i], w[4 * i + 1]);
-                biased4_to_h4(d23, w[4 * i + 2], w[4 * i + 3]);
-            }
-        } else {
-            const uint32_t in[8] = {S.k[0].x, S.k[0].y, S.k[0].z, S.k[0].w, S.k[1].x, S.k[1].y, S.k[1].z, S.k[1].w};
-#pragma unroll
-            for (int i = 0; i < 8; i++) i8x4_to_h4(in[i], w[2 * i], w[2 * i + 1]);
+        for (int i = 0; i < BK / 8; i++) {
+            const uint4 u = S.k[i >> 2];
+            const uint32_t x = (i & 3) == 0 ? u.x : (i & 3) == 1 ? u.y : (i & 3) == 2 ? u.z : u.w;
+            const uint32_t e = lut16(x & 0x0f0f0f0fu), o = lut16((x >> 4) & 0x0f0f0f0fu);
+            const uint32_t d01 = __builtin_amdgcn_perm(o, e, 0x05010400u), d23 = __builtin_amdgcn_perm(o, e, 0x07030602u);
+            uint32_t a0, a1, a2, a3;
+            biased4_to_h4(d01, a0, a1);
+            biased4_to_h4(d23, a2, a3);
+            w[4 * i] = h22u(u2h2(a0) * sc); w[4 * i + 1] = h22u(u2h2(a1) * sc);
+            w[4 * i + 2] = h22u(u2h2(a2) * sc); w[4 * i + 3] = h22u(u2h2(a3) * sc);
         }
-        if (!ok) {
+    } else {
 #pragma unroll
-            for (int i = 0; i < 16; i++) w[i] = 0u;
-        }
-#pragma unroll
-        for (int q = 0; q < 4; q++)  // 4 chunks of 8 halves: dims 32c + 8q
-            *reinterpret_cast<uint4*>(Kt + key * AHD + kchunk(key, 4 * c + q) * 8) = make_uint4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
-    }
-    {
-        const int dg = tid & 63, kb = (tid >> 6) * 8;
-        uint32_t r[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            uint32_t x;
-            if (TB) {  // 4 dims: 3-bit codes from the low-bit byte and a nibble of the high-bit byte -> biased codes
-                const uint32_t lo8 = S.v[i] & 0xffu, hb4 = (S.v[i] >> (8 + 4 * (dg & 1))) & 15u;
-                uint32_t idx = 0;
-#pragma unroll
-                for (int e = 0; e < 4; e++) idx |= (((lo8 >> (2 * e)) & 3u) | (((hb4 >> e) & 1u) << 2)) << (8 * e);
-                x = __builtin_amdgcn_perm(V3T1, V3T0, idx);
-            } else {
-                x = S.v[i] ^ 0x80808080u;  // biased
-            }
-            r[i] = k0 + kb + i < hi ? x : 0x80808080u;  // zero codes past the end
-        }
-        uint32_t ca[4], cb[4];
-        tr4x4(r, ca);
-        tr4x4(r + 4, cb);
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            uint32_t h0, h1, h2, h3;
-            biased4_to_h4(ca[e], h0, h1);
-            biased4_to_h4(cb[e], h2, h3);
-            _Float16* dst = Vt + (4 * dg + e) * VST + kb;
-            *reinterpret_cast<uint2*>(dst) = make_uint2(h0, h1);
-            *reinterpret_cast<uint2*>(dst + 4) = make_uint2(h2, h3);
+        for (int i = 0; i < BK / 4; i++) {
+            const uint4 u = S.k[i >> 2];
+            const uint32_t x = (i & 3) == 0 ? u.x : (i & 3) == 1 ? u.y : (i & 3) == 2 ? u.z : u.w;
+            i8x4_to_h4(x, w[2 * i], w[2 * i + 1]);
         }
     }
-    if (tid < BK) {
-        const bool ok = k0 + tid < hi;
-        if (TB) {
-            sc[tid] = ok ? S.sa : 0.f;
-            sc[BK + tid] = ok ? S.sb : 0.f;
-            sc[2 * BK + tid] = ok ? S.sc * TK3 : 0.f;
-            sc[3 * BK + tid] = ok ? S.sd * TK3 : 0.f;
+    if (!FULL && !ok) {
+#pragma unroll
+        for (int i = 0; i < BK / 2; i++) w[i] = 0u;
+    }
+#pragma unroll
+    for (int q = 0; q < BK / 8; q++)  // chunks of 8 halves: dims BK*c + 8q
+        *reinterpret_cast<uint4*>(Kt + key * AHD + kchunk(key, (BK / 8) * c + q) * 8) = make_uint4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
+    // threads >= BK write their copy to the spare slot (branch-free)
+    float* dst = tid < BK ? sbuf + tid : spare + (tid & (BK - 1));
+    *dst = FULL || k0 + (tid & (BK - 1)) < hi ? S.ks : 0.f;
+}
+
+template <bool TB, bool FULL = false>
+__device__ __forceinline__ void store_v(const StageV& S, unsigned char* vbuf, int k0, int hi, int tid) {
+    _Float16* Vt = reinterpret_cast<_Float16*>(vbuf);
+    const int dg = tid & 63;
+    uint32_t r[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        uint32_t x;
+        if (TB) {  // 4 dims: 3-bit codes from the low-bit byte and a nibble of the high-bit byte -> biased codes
+            const uint32_t lo8 = S.v[i] & 0xffu, hb4 = (S.v[i] >> (8 + 4 * (dg & 1))) & 15u;
+            uint32_t idx = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) idx |= (((lo8 >> (2 * e)) & 3u) | (((hb4 >> e) & 1u) << 2)) << (8 * e);
+            x = __builtin_amdgcn_perm(V3T1, V3T0, idx);
         } else {
-            sc[tid] = ok ? S.sa * SL2 : 0.f;
-            sc[2 * BK + tid] = ok ? S.sc : 0.f;
+            x = S.v[i] ^ 0x80808080u;  // biased
         }
+        r[i] = FULL || k0 + vkey(tid, i) < hi ? x : 0x80808080u;  // zero past the end
+    }
+    // per dim e: the 8 keys -> fp16 times the key's scale, one 16-byte write at V^T position 16m + 8h
+    half2_t vsc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) vsc[i] = half2_t{(_Float16)S.vs[2 * i], (_Float16)S.vs[2 * i + 1]};
+    uint32_t ca[4], cb[4];
+    tr4x4(r[0], r[1], r[2], r[3], ca);
+    tr4x4(r[4], r[5], r[6], r[7], cb);
+    _Float16* base = Vt + (4 * dg) * VST + 16 * (tid >> 7) + 8 * ((tid >> 6) & 1);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        uint32_t h0, h1, h2, h3;
+        biased4_to_h4(ca[e], h0, h1);
+        biased4_to_h4(cb[e], h2, h3);
+        *reinterpret_cast<uint4*>(base + e * VST) = make_uint4(h22u(u2h2(h0) * vsc[0]), h22u(u2h2(h1) * vsc[1]),
+                                                               h22u(u2h2(h2) * vsc[2]), h22u(u2h2(h3) * vsc[3]));
     }
 }
 
@@ -187,28 +213,79 @@ __device__ __forceinline__ bool map_block(int b, int KV, int NT, int& kvh, int& 
     kvh = b / NT; tile = NT - 1 - b % NT;
     return kvh < KV;
 }
-}  // namespace
-
 int fa_grid(int KV, int T) {
     const int NT = (T + FT - 1) / FT;
     if (8 % KV == 0) { const int xpk = 8 / KV; return 8 * ((NT + xpk - 1) / xpk); }
     return KV * NT;
 }
+}  // namespace
 
+// Warp-specialised workgroup of 8 wavefronts. Wavefronts 0-3 compute (32 query rows each); wavefronts 4-7 stage: they
+// load the next tiles' int8/turbo K and V, widen them and write them to the LDS buffers. Each SIMD holds one wavefront of
+// each kind, so the staging VALU work runs beside the other wavefront's MFMAs. One barrier per key tile: during tile j
+// the computing wavefronts read buffers j%2 while the staging wavefronts fill buffers (j+1)%2.
 template <bool TB>
-__global__ void __launch_bounds__(256, 1) fa_prefill_kernel(const float* __restrict__ qo, const float* __restrict__ q_gate,
+__global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restrict__ qo, const float* __restrict__ q_gate,
                                                             moex_kv_cache kv, float* __restrict__ out, int H, int KV,
                                                             const int* __restrict__ pos_d, int max_t, int ld, int T) {
     extern __shared__ __align__(16) unsigned char smem[];
+#define KBUF(i) (smem + (i) * KT_BYTES)
+#define VBUF(i) (smem + 2 * KT_BYTES + (i) * VT_BYTES)
+#define SBUF(i) (reinterpret_cast<float*>(smem + 2 * KT_BYTES + 2 * VT_BYTES) + (i) * BK)
     const int NT = (T + FT - 1) / FT;
     int kvh, tile;
     if (!map_block(blockIdx.x, KV, NT, kvh, tile)) return;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h32 = lane >> 5, r = lane & 31;
     const int t0 = tile * FT, pos0 = *pos_d, nt = min(FT, T - t0), hi = pos0 + t0 + nt;  // keys [0, hi)
+    const size_t rbase = (size_t)kvh * max_t;
+    const int ntiles = (hi + BK - 1) / BK;
+
+    if (threadIdx.x >= 256) {
+        // ---------------- staging wavefronts ----------------
+        const int tid = threadIdx.x - 256;
+        StageK sk;
+        StageV sv;
+        load_k<TB>(sk, kv, rbase, 0, hi, tid);
+        load_v<TB>(sv, kv, rbase, 0, hi, tid);
+        store_k<TB>(sk, KBUF(0), SBUF(0), SBUF(2), 0, hi, tid);
+        store_v<TB>(sv, VBUF(0), 0, hi, tid);
+        if (ntiles > 1) {
+            load_k<TB>(sk, kv, rbase, BK, hi, tid);
+            load_v<TB>(sv, kv, rbase, BK, hi, tid);
+        }
+        __syncthreads();
+        for (int j = 0; j < ntiles; j++) {
+            const int k1 = (j + 1) * BK;
+            if (j + 1 < ntiles) {
+                if (k1 + BK <= hi) {
+                    store_k<TB, true>(sk, KBUF((j + 1) & 1), SBUF((j + 1) & 1), SBUF(2), k1, hi, tid);
+                    store_v<TB, true>(sv, VBUF((j + 1) & 1), k1, hi, tid);
+                } else {
+                    store_k<TB>(sk, KBUF((j + 1) & 1), SBUF((j + 1) & 1), SBUF(2), k1, hi, tid);
+                    store_v<TB>(sv, VBUF((j + 1) & 1), k1, hi, tid);
+                }
+            }
+            if (j + 2 < ntiles) {
+                const int k2 = k1 + BK;
+                if (k2 + BK <= hi) {
+                    load_k<TB, true>(sk, kv, rbase, k2, hi, tid);
+                    load_v<TB, true>(sv, kv, rbase, k2, hi, tid);
+                } else {
+                    load_k<TB>(sk, kv, rbase, k2, hi, tid);
+                    load_v<TB>(sv, kv, rbase, k2, hi, tid);
+                }
+            }
+            __syncthreads();
+        }
+        return;
+    }
+
+    // ---------------- computing wavefronts ----------------
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h32 = lane >> 5, r = lane & 31;
     const int tokw = 4 * w + (r >> 3), head = kvh * GQ + (r & 7);                     // this lane's row
     const int prow = min(pos0 + t0 + tokw, hi - 1);                                     // its last visible key
-    const int wmax = min(pos0 + t0 + 4 * w + 3, hi - 1);                                // the wavefront's last key
-    const size_t rbase = (size_t)kvh * max_t;
+    const int wmin = min(pos0 + t0 + 4 * w, hi - 1);                                    // the wavefront's first row
+    const int wmax = min(pos0 + t0 + 4 * w + 3, hi - 1);                                // ... and its last key
+    const int wtiles = wmax / BK + 1;  // tiles this wavefront computes
 
     // Q row (fp16) as B operands: MFMA s covers dims 16s + 8*h32 + 0..7
     half8_t qf[16];
@@ -227,98 +304,81 @@ __global__ void __launch_bounds__(256, 1) fa_prefill_kernel(const float* __restr
     for (int db = 0; db < 8; db++)
 #pragma unroll
         for (int i = 0; i < 16; i++) o[db][i] = 0.f;
-    float m_run = -INFINITY, l_run = 0.f;
+    float m_ref = -INFINITY, l_run = 0.f;
+    const half2_t ones = half2_t{(_Float16)1.f, (_Float16)1.f};
+    __syncthreads();
 
-    const int ntiles = (hi + BK - 1) / BK;
-    Stage S;
-    stage_load<TB>(S, kv, rbase, 0, hi, tid);
-    for (int kt = 0; kt < ntiles; kt++) {
-        const int k0 = kt * BK;
-        unsigned char* buf = smem + (kt & 1) * BUF_BYTES;
-        stage_store<TB>(S, buf, k0, hi, tid);
+    for (int j = 0; j < ntiles; j++) {
+        if (j < wtiles) {
+            const _Float16* Kt = reinterpret_cast<const _Float16*>(KBUF(j & 1));
+            const _Float16* Vt = reinterpret_cast<const _Float16*>(VBUF(j & 1));
+            const float* scl = SBUF(j & 1);
+            const int k0 = j * BK;
+            // ---- S^T = K . Q^T: lane = (row r, key half h32), element i: key 8*(i/4) + 4*h32 + i%4 ----
+            float16_t sc;
+#pragma unroll
+            for (int i = 0; i < 16; i++) sc[i] = 0.f;
+#pragma unroll
+            for (int s = 0; s < 16; s++) {
+                const half8_t a = *reinterpret_cast<const half8_t*>(Kt + r * AHD + kchunk(r, 2 * s + h32) * 8);
+                sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], sc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int a4 = 0; a4 < 4; a4++) {
+                const float4 kq = *reinterpret_cast<const float4*>(scl + 8 * a4 + 4 * h32);
+                sc[4 * a4] *= kq.x; sc[4 * a4 + 1] *= kq.y; sc[4 * a4 + 2] *= kq.z; sc[4 * a4 + 3] *= kq.w;
+            }
+            if (k0 + BK - 1 > wmin) {  // a diagonal tile: causal mask per row
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    if (k0 + 8 * (i >> 2) + 4 * h32 + (i & 3) > prow) sc[i] = -INFINITY;
+            }
+            float mt = sc[0];
+#pragma unroll
+            for (int i = 1; i < 16; i++) mt = fmaxf(mt, sc[i]);
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            // lazy rescale: O and l are referenced to m_ref, moved only when a row's maximum passes it by the slack
+            if (__ballot(mt > m_ref + RESCALE_SLACK)) {
+                const float m_new = fmaxf(m_ref, mt);
+                const float cf = fast_exp2(m_ref - m_new);  // 0 on the first tile
+                if (__ballot(m_ref != -INFINITY)) {
+#pragma unroll
+                    for (int db = 0; db < 8; db++)
+#pragma unroll
+                        for (int i = 0; i < 16; i++) o[db][i] *= cf;
+                }
+                l_run *= cf;
+                m_ref = m_new;
+            }
+            // ---- P^T (fp16) as B operands: MFMA m (keys 16m ..) takes S elements 8m .. 8m+7 ----
+            half8_t pf[2];
+            float ls = 0.f;
+#pragma unroll
+            for (int m = 0; m < 2; m++)
+#pragma unroll
+                for (int jj = 0; jj < 8; jj += 2) {
+                    const float p0 = fast_exp2(sc[8 * m + jj] - m_ref), p1 = fast_exp2(sc[8 * m + jj + 1] - m_ref);
+                    const half2_t ph = half2_t{(_Float16)p0, (_Float16)p1};
+                    pf[m][jj] = ph[0]; pf[m][jj + 1] = ph[1];
+                    ls = __builtin_amdgcn_fdot2(ph, ones, ls, false);
+                }
+            l_run += ls;
+            // ---- O^T += V^T . P^T ----
+#pragma unroll
+            for (int db = 0; db < 8; db++) {
+                const _Float16* vrow = Vt + (32 * db + r) * VST + 8 * h32;
+#pragma unroll
+                for (int m = 0; m < 2; m++) {
+                    const half8_t a = *reinterpret_cast<const half8_t*>(vrow + 16 * m);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[m], o[db], 0, 0, 0);
+                }
+            }
+        }
         __syncthreads();
-        if (kt + 1 < ntiles) stage_load<TB>(S, kv, rbase, k0 + BK, hi, tid);
-        if (k0 > wmax) continue;  // every row of this wavefront is before the tile (causal)
-        const _Float16* Kt = reinterpret_cast<const _Float16*>(buf);
-        const _Float16* Vt = reinterpret_cast<const _Float16*>(buf + KT_BYTES);
-        const float* scl = reinterpret_cast<const float*>(buf + KT_BYTES + VT_BYTES);
-        // ---- S^T = K . Q^T ----
-        float16_t s0, s1;
-#pragma unroll
-        for (int i = 0; i < 16; i++) { s0[i] = 0.f; s1[i] = 0.f; }
-#pragma unroll
-        for (int s = 0; s < 16; s++) {
-            const half8_t a = *reinterpret_cast<const half8_t*>(Kt + r * AHD + kchunk(r, 2 * s + h32) * 8);
-            if (TB && s >= 8) s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], s1, 0, 0, 0);
-            else s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], s0, 0, 0, 0);
-        }
-        // lane: row r, keys kk(i) = 8*(i/4) + 4*h32 + i%4
-        float sv[16], mt = -INFINITY;
-#pragma unroll
-        for (int a4 = 0; a4 < 4; a4++) {
-            const int kb = 8 * a4 + 4 * h32;
-            const float4 ksc = *reinterpret_cast<const float4*>(scl + kb);
-            const float kv4[4] = {ksc.x, ksc.y, ksc.z, ksc.w};
-            float kv4b[4] = {0.f, 0.f, 0.f, 0.f};
-            if (TB) {
-                const float4 k1 = *reinterpret_cast<const float4*>(scl + BK + kb);
-                kv4b[0] = k1.x; kv4b[1] = k1.y; kv4b[2] = k1.z; kv4b[3] = k1.w;
-            }
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int i = 4 * a4 + e;
-                float x = TB ? (s0[i] * kv4[e] + s1[i] * kv4b[e]) * (TK4 * SL2) : s0[i] * kv4[e];
-                if (k0 + kb + e > prow) x = -INFINITY;
-                sv[i] = x;
-                mt = fmaxf(mt, x);
-            }
-        }
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
-        const float m_new = fmaxf(m_run, mt);  // key 0 is visible to every row: finite from the first tile
-        const float cf = fast_exp2(m_run - m_new);
-        m_run = m_new;
-        if (__ballot(cf != 1.f)) {
-#pragma unroll
-            for (int db = 0; db < 8; db++)
-#pragma unroll
-                for (int i = 0; i < 16; i++) o[db][i] *= cf;
-        }
-        // ---- P^T (times V's scale) as B operands: MFMA m uses i = 8m .. 8m+7 ----
-        half8_t pb0[2], pb1[2];
-        float psum = 0.f;
-#pragma unroll
-        for (int a4 = 0; a4 < 4; a4++) {
-            const int kb = 8 * a4 + 4 * h32;
-            const float4 v4 = *reinterpret_cast<const float4*>(scl + 2 * BK + kb);
-            const float va[4] = {v4.x, v4.y, v4.z, v4.w};
-            float vb[4] = {0.f, 0.f, 0.f, 0.f};
-            if (TB) {
-                const float4 v5 = *reinterpret_cast<const float4*>(scl + 3 * BK + kb);
-                vb[0] = v5.x; vb[1] = v5.y; vb[2] = v5.z; vb[3] = v5.w;
-            }
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int i = 4 * a4 + e;
-                const float p = fast_exp2(sv[i] - m_new);
-                psum += p;
-                pb0[i >> 3][i & 7] = (_Float16)(p * va[e]);
-                if (TB) pb1[i >> 3][i & 7] = (_Float16)(p * vb[e]);
-            }
-        }
-        l_run = l_run * cf + psum;
-        // ---- O^T += V^T . P^T: A = V^T rows dim 32db + r, keys 16m + 4*h32 + {0..3} and 16m + 8 + 4*h32 + {0..3}
-#pragma unroll
-        for (int db = 0; db < 8; db++) {
-            const _Float16* vrow = Vt + (32 * db + r) * VST + 4 * h32;
-#pragma unroll
-            for (int m = 0; m < 2; m++) {
-                const half4_t x0 = *reinterpret_cast<const half4_t*>(vrow + 16 * m);
-                const half4_t x1 = *reinterpret_cast<const half4_t*>(vrow + 16 * m + 8);
-                const half8_t a = half8_t{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, (TB && db >= 4) ? pb1[m] : pb0[m], o[db], 0, 0, 0);
-            }
-        }
     }
+#undef KBUF
+#undef VBUF
+#undef SBUF
     // ---- epilogue: O / l * sigmoid(gate) ----
     l_run += __shfl_xor(l_run, 32);
     if (tokw >= nt) return;
@@ -345,17 +405,17 @@ void launch_fa(const float* qo, const float* q_gate, moex_kv_cache kv, float* ou
                int max_t, int ld, int T, hipStream_t st) {
     static bool once = [] {
         MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(fa_prefill_kernel<false>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, 2 * BUF_BYTES));
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES));
         MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(fa_prefill_kernel<true>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, 2 * BUF_BYTES));
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES));
         return true;
     }();
     (void)once;
     const int nb = fa_grid(KV, T);
     if (kv.turbo)
-        hipLaunchKernelGGL(fa_prefill_kernel<true>, dim3(nb), dim3(256), 2 * BUF_BYTES, st, qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T);
+        hipLaunchKernelGGL(fa_prefill_kernel<true>, dim3(nb), dim3(512), LDS_BYTES, st, qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T);
     else
-        hipLaunchKernelGGL(fa_prefill_kernel<false>, dim3(nb), dim3(256), 2 * BUF_BYTES, st, qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T);
+        hipLaunchKernelGGL(fa_prefill_kernel<false>, dim3(nb), dim3(512), LDS_BYTES, st, qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T);
     MOEX_LAUNCHED();
 }
 
