@@ -25,12 +25,14 @@ namespace {
 constexpr int FT = 16;                      // tokens per workgroup
 constexpr int BK = 32;                      // keys per tile
 constexpr int VST = BK + 8;                 // V^T row stride in halves (80 B: conflict-free A-operand reads)
-constexpr int KT_BYTES = BK * AHD * 2;      // 32 KB
+constexpr int KST = AHD + 8;                // K row stride in halves (528 B: rows shift by 4 banks, conflict-free reads)
+constexpr int KT_BYTES = BK * KST * 2;      // 16.5 KB
 constexpr int VT_BYTES = AHD * VST * 2;     // 36 KB
 constexpr int SC_BYTES = BK * 4;            // per-key score scale
 constexpr int LDS_BYTES = 2 * KT_BYTES + 2 * VT_BYTES + 3 * SC_BYTES;  // 2 score-scale slots + a spare
 constexpr float SL2 = 0.0625f * 1.4426950408889634f;
 constexpr float TK4 = 0.241529f / 127.f, TK3 = 0.190207f / 127.f;
+constexpr int FA_KPF = 2;                   // LDS operand reads in flight ahead of the MFMAs
 constexpr float RESCALE_SLACK = 8.f;        // p <= 2^8 between rescales
 
 constexpr uint32_t pack4(int a, int b, int c, int d) {
@@ -53,7 +55,6 @@ __device__ __forceinline__ void tr4x4(uint32_t r0, uint32_t r1, uint32_t r2, uin
     c[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u); c[1] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
     c[2] = __builtin_amdgcn_perm(t3, t1, 0x05040100u); c[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
 }
-__device__ __forceinline__ int kchunk(int key, int c) { return c ^ (key & 15); }  // swizzled 16-byte chunk of a K row
 // V^T key positions within each 16-key group are [0..3, 8..11, 4..7, 12..15]: a P.V A operand (keys 16m + 4h + 0..3
 // and 16m + 8 + 4h + 0..3) is the 8 contiguous halves at position 16m + 8h, and one staging thread writes them.
 
@@ -156,7 +157,7 @@ __device__ __forceinline__ void store_k(const StageK& S, unsigned char* kbuf, fl
     }
 #pragma unroll
     for (int q = 0; q < BK / 8; q++)  // chunks of 8 halves: dims BK*c + 8q
-        *reinterpret_cast<uint4*>(Kt + key * AHD + kchunk(key, (BK / 8) * c + q) * 8) = make_uint4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
+        *reinterpret_cast<uint4*>(Kt + key * KST + ((BK / 8) * c + q) * 8) = make_uint4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
     // threads >= BK write their copy to the spare slot (branch-free)
     float* dst = tid < BK ? sbuf + tid : spare + (tid & (BK - 1));
     *dst = FULL || k0 + (tid & (BK - 1)) < hi ? S.ks : 0.f;
@@ -318,10 +319,19 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
             float16_t sc;
 #pragma unroll
             for (int i = 0; i < 16; i++) sc[i] = 0.f;
+            {   // K operands read FA_KPF MFMAs ahead of their use (LDS latency)
+                const _Float16* krow = Kt + r * KST + 8 * h32;
+                half8_t ka[FA_KPF];
 #pragma unroll
-            for (int s = 0; s < 16; s++) {
-                const half8_t a = *reinterpret_cast<const half8_t*>(Kt + r * AHD + kchunk(r, 2 * s + h32) * 8);
-                sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], sc, 0, 0, 0);
+                for (int s = 0; s < FA_KPF; s++) ka[s] = *reinterpret_cast<const half8_t*>(krow + 16 * s);
+#pragma unroll
+                for (int s = 0; s < 16; s++) {
+                    const half8_t a = ka[s % FA_KPF];
+                    if (s + FA_KPF < 16)
+                        ka[s % FA_KPF] = *reinterpret_cast<const half8_t*>(krow + 16 * (s + FA_KPF));
+                    __builtin_amdgcn_sched_barrier(0);  // keep each read FA_KPF MFMAs ahead of its use
+                    sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], sc, 0, 0, 0);
+                }
             }
 #pragma unroll
             for (int a4 = 0; a4 < 4; a4++) {
@@ -364,13 +374,20 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
                 }
             l_run += ls;
             // ---- O^T += V^T . P^T ----
+            {   // V^T operands read FA_KPF MFMAs ahead (MFMA q: dims 32*(q/2) + r, keys 16*(q%2) ..)
+                const _Float16* vrow = Vt + r * VST + 8 * h32;
+                half8_t va[FA_KPF];
 #pragma unroll
-            for (int db = 0; db < 8; db++) {
-                const _Float16* vrow = Vt + (32 * db + r) * VST + 8 * h32;
+                for (int q = 0; q < FA_KPF; q++) va[q] = *reinterpret_cast<const half8_t*>(vrow + 32 * (q >> 1) * VST + 16 * (q & 1));
 #pragma unroll
-                for (int m = 0; m < 2; m++) {
-                    const half8_t a = *reinterpret_cast<const half8_t*>(vrow + 16 * m);
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[m], o[db], 0, 0, 0);
+                for (int q = 0; q < 16; q++) {
+                    const half8_t a = va[q % FA_KPF];
+                    if (q + FA_KPF < 16) {
+                        const int qn = q + FA_KPF;
+                        va[q % FA_KPF] = *reinterpret_cast<const half8_t*>(vrow + 32 * (qn >> 1) * VST + 16 * (qn & 1));
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    o[q >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[q & 1], o[q >> 1], 0, 0, 0);
                 }
             }
         }
