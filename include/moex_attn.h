@@ -79,8 +79,10 @@ void moex_qk_norm_rope(const float* q, const float* k, const float* v, const uin
  * rotated. Row kvh*max_t + *pos_d + t gets token t's k/v (token stride ld floats, kv head at kvh*256). */
 void moex_kv_append(const float* k, const float* v, moex_kv_cache kv, int KV, const int* pos_d, int max_t,
                     int ld, int T, void* stream);
-/* attn_gqa_k (kernels.cuh:1745), grid (KV, T, ns): split-K GQA decode, writes partials {m, l, acc[256]} to
- * part[((t*H + h)*ns + s)*(256+2)]. m is the running max in log2 units (the combine below reads it so). */
+/* attn_gqa_k (kernels.cuh:1745), grid (KV, T, ns): split-K GQA decode, writes partials {m, l, acc[256]} into part
+ * (T*H*ns*(256+2) floats, the reference's size): acc rows at part[((t*H + h)*ns + s)*256], then the {m, l} pairs at
+ * part[T*H*ns*256 + ((t*H + h)*ns + s)*2]. m is the running max in log2 units (the combine below reads it so).
+ * part must be 16-byte aligned (any hipMalloc / cudaMalloc pointer is). */
 void moex_attn_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part,
                    int T, int ns, void* stream);
 /* attn_combine_k (kernels.cuh:1317), grid (H, T): merges ns partials, out = acc/l * sigmoid(gate) (no gate if

@@ -117,12 +117,13 @@ void moex_attn_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* 
                    int ns, void* stream) {
     MOEX_REQUIRE(KV > 0 && H == KV * GQ, "the GQA kernel needs H / KV == 8");
     MOEX_REQUIRE(T > 0 && ns > 0 && part, "T, ns, part");
+    MOEX_REQUIRE(((uintptr_t)part & 15) == 0, "part must be 16-byte aligned");
     launch_gqa(qo, kv, H, KV, pos_d, max_t, part, T, ns, S(stream));
 }
 
 void moex_attn_combine(const float* part, const float* q_gate, float* out, int H, int ns, int ld, int T, void* stream) {
     MOEX_REQUIRE(H > 0 && T > 0 && ns > 0, "H, T, ns");
-    launch_combine(part, q_gate, out, H, ns, ld, T, 0, S(stream));
+    launch_combine(part, q_gate, out, H, ns, ld, T, S(stream));
 }
 
 void moex_attn_decode_heads(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
@@ -162,25 +163,24 @@ void moex_attn_decode(const float* q, const float* k, const float* v, const uint
                       float eps, int T, int ld, void* stream, float* part, int ns) {
     MOEX_REQUIRE(H > 0 && KV > 0 && H % KV == 0 && T > 0 && ns > 0, "H, KV, T, ns");
     MOEX_REQUIRE(ns == 1 || part, "part is needed when ns > 1");
+    MOEX_REQUIRE(((uintptr_t)part & 15) == 0, "part must be 16-byte aligned");
     MOEX_REQUIRE(rot >= 0 && rot <= AHD && rot % 2 == 0, "rot");
     hipStream_t st = S(stream);
     launch_qk_norm_rope(q, k, v, qn, kn, qo, kv, H, KV, pos_d, max_t, rot, theta, eps, ld, T, st);
     const int G = H / KV;
     const float* gate = kv.turbo ? nullptr : q;  // turbo: gated after the inverse rotation
-    bool rotated = false;
     if (T > 2 && ns == 1 && G == GQ && (moex_fa_on() || kv.turbo) && moex_fa_supported()) {
         launch_fa(qo, gate, kv, out, H, KV, pos_d, max_t, ld, T, st);
     } else if (T > 2 && ns == 1 && G == GQ && !kv.turbo) {
         launch_prefill_k7p(qo, q, kv, out, H, KV, pos_d, max_t, ld, T, st);
     } else if (ns > 1 && G == GQ) {
         launch_gqa(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
-        launch_combine(part, q, out, H, ns, ld, T, kv.turbo, st);  // turbo: inverse WHT + gate fused in
-        rotated = true;
+        launch_combine(part, gate, out, H, ns, ld, T, st);
     } else {
         launch_decode_heads(qo, gate, kv, out, H, KV, pos_d, max_t, ld, part, T, ns, st);
-        if (ns > 1) launch_combine(part, gate, out, H, ns, ld, T, 0, st);
+        if (ns > 1) launch_combine(part, gate, out, H, ns, ld, T, st);
     }
-    if (kv.turbo && !rotated) launch_turbo_out(out, q, H, ld, T, st);
+    if (kv.turbo) launch_turbo_out(out, q, H, ld, T, st);
 }
 
 }  // extern "C"

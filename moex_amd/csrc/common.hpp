@@ -48,6 +48,16 @@ __device__ __forceinline__ half8_t i8x8_to_h8(uint32_t a, uint32_t b) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Split-K partials in the caller's part buffer (T*H*ns*(AHD+2) floats, the reference's size): the acc rows
+// [T][H][ns][AHD] first, then {m (log2 units), l} pairs [T][H][ns][2], so the combine reads every split's m and l
+// contiguously and each acc row is 16-byte aligned.
+__device__ __forceinline__ float* part_acc(float* part, int t, int h, int s, int H, int ns) {
+    return part + (((size_t)t * H + h) * ns + s) * AHD;
+}
+__device__ __forceinline__ float* part_ml(float* part, int t, int h, int s, int H, int ns, int T) {
+    return part + (size_t)T * H * ns * AHD + (((size_t)t * H + h) * ns + s) * 2;
+}
+
 }  // namespace moex
 
 // ---- internal launchers (each defined in its .hip file; argument checks happen in api.cpp) ----
@@ -58,8 +68,7 @@ void launch_qk_norm_rope(const float* q, const float* k, const float* v, const u
 void launch_kv_append(const float* k, const float* v, moex_kv_cache kv, int KV, const int* pos_d, int max_t, int ld,
                       int T, hipStream_t st);
 void launch_turbo_out(float* out, const float* q_gate, int H, int ld, int T, hipStream_t st);
-void launch_combine(const float* part, const float* q_gate, float* out, int H, int ns, int ld, int T, int turbo_rot,
-                    hipStream_t st);
+void launch_combine(const float* part, const float* q_gate, float* out, int H, int ns, int ld, int T, hipStream_t st);
 void launch_decode_heads(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
                          const int* pos_d, int max_t, int ld, float* part, int T, int ns, hipStream_t st);
 void launch_set_int(int* p, int v, hipStream_t st);

@@ -319,9 +319,11 @@ __global__ void __launch_bounds__(256, 2) gqa_decode_kernel(const float* __restr
             l += lw[w][h] * f;
             acc += ow[w][h][d] * f;
         }
-        float* p = part + (((size_t)tok * H + kvh * GQ + h) * ns + s) * (AHD + 2);
-        p[2 + d] = acc * vdenorm;
-        if (d == 0) { p[0] = M; p[1] = l; }  // empty split: m = -inf, l = 0, acc = 0
+        part_acc(part, tok, kvh * GQ + h, s, H, ns)[d] = acc * vdenorm;
+        if (d == 0) {  // empty split: m = -inf, l = 0, acc = 0
+            float* ml = part_ml(part, tok, kvh * GQ + h, s, H, ns, T);
+            ml[0] = M; ml[1] = l;
+        }
     }
 }
 
@@ -664,13 +666,12 @@ __global__ void __launch_bounds__(256, TT == 1 ? 2 : 1) gqa_x_kernel(const float
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int h = 4 * g + i;
-                float* p = part + (((size_t)(tb + t) * H + kvh * GQ + h) * ns + s) * (AHD + 2);
-                float2* dst = reinterpret_cast<float2*>(p + 2 + 64 * wv + 4 * m16);  // rows are 8-byte aligned
-                dst[0] = make_float2(ov[i][0], ov[i][1]);
-                dst[1] = make_float2(ov[i][2], ov[i][3]);
+                float* p = part_acc(part, tb + t, kvh * GQ + h, s, H, ns);
+                *reinterpret_cast<float4*>(p + 64 * wv + 4 * m16) = make_float4(ov[i][0], ov[i][1], ov[i][2], ov[i][3]);
                 if (wv == 0 && m16 == 0) {
-                    p[0] = m4[t][i];  // -inf when the token has no key in this split
-                    p[1] = lsum[t][0][h] + lsum[t][1][h] + lsum[t][2][h] + lsum[t][3][h];
+                    float* ml = part_ml(part, tb + t, kvh * GQ + h, s, H, ns, T);
+                    ml[0] = m4[t][i];  // -inf when the token has no key in this split
+                    ml[1] = lsum[t][0][h] + lsum[t][1][h] + lsum[t][2][h] + lsum[t][3][h];
                 }
             }
         }

@@ -198,62 +198,60 @@ __global__ void __launch_bounds__(256) turbo_out_kernel(float* __restrict__ out,
 }
 
 // attn_combine_k (kernels.cuh:1317-1329): merge ns partials {m (log2 units), l, acc[256]}.
-// Grid (H, T, DC): block (h, t, c) owns dims [c*256/DC, (c+1)*256/DC); its 256 threads are DW = 256/DC dims x DC
-// split groups, so every thread walks ns/DC partials with 8 loads in flight, then the groups are summed in LDS.
-// turbo_rot (DC = 1): the merged row is rotated back (inverse WHT) before the gate, i.e. turbo_out fused in.
-template <int DC>
+// Grid (H, T, DC): block (h, t, c) owns dims [c*DW, (c+1)*DW), DW = 256/DC; its 256 threads are DW dims x NG split
+// groups. Every thread merges its splits online (running max, no separate max pass) with 16 loads in flight, then the
+// NG groups are merged through LDS. One pass over the partials.
+constexpr int CDC = 16, CDW = AHD / CDC, CNG = 256 / CDW;
 __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ part, const float* __restrict__ q_gate,
-                                                      float* __restrict__ out, int H, int ns, int ld, int turbo_rot) {
-    constexpr int DW = AHD / DC;  // dims per block
-    constexpr int NG = 256 / DW;  // split groups
-    __shared__ float w[2048];
-    __shared__ float red[NG][DW];
-    __shared__ float sh[AHD];
-    __shared__ float sh8[16];
-    const int tok = blockIdx.y, h = blockIdx.x, tid = threadIdx.x;
-    const float* p = part + ((size_t)tok * H + h) * ns * (AHD + 2);
-    float M = -INFINITY;
-    for (int s = tid; s < ns; s += 256) M = fmaxf(M, p[(size_t)s * (AHD + 2)]);
-    M = block_max(M, sh8);  // split 0 is never empty, so M is finite
-    const int dl = tid % DW, gi = tid / DW, d = blockIdx.z * DW + dl;
-    float l = 0.f, acc = 0.f;
-    for (int s0 = 0; s0 < ns; s0 += 2048) {
-        const int n = min(2048, ns - s0);
-        __syncthreads();
-        for (int s = tid; s < n; s += 256) {
-            const float* q = p + (size_t)(s0 + s) * (AHD + 2);
-            const float ls = q[1], ws = ls > 0.f ? fast_exp2(q[0] - M) : 0.f;
-            w[s] = ws;
-            l += ls * ws;
-        }
-        __syncthreads();
-        int s = gi;
-        for (; s + 7 * NG < n; s += 8 * NG) {
-            float a[8];
+                                                      float* __restrict__ out, int H, int ns, int ld) {
+    __shared__ float sm[CNG][CDW], sl[CNG][CDW], sa[CNG][CDW];
+    const int tok = blockIdx.y, h = blockIdx.x, tid = threadIdx.x, T = gridDim.y;
+    float* pp = const_cast<float*>(part);
+    const float* acc_rows = part_acc(pp, tok, h, 0, H, ns);
+    const float2* ml = reinterpret_cast<const float2*>(part_ml(pp, tok, h, 0, H, ns, T));
+    const int dl = tid % CDW, gi = tid / CDW, d = blockIdx.z * CDW + dl;
+    float mt = -INFINITY, lt = 0.f, at = 0.f;
+    for (int s0 = gi; s0 < ns; s0 += 16 * CNG) {
+        float2 q[16];
+        float a[16];
 #pragma unroll
-            for (int u = 0; u < 8; u++) a[u] = p[(size_t)(s0 + s + u * NG) * (AHD + 2) + 2 + d];
-#pragma unroll
-            for (int u = 0; u < 8; u++) acc += w[s + u * NG] * a[u];
+        for (int u = 0; u < 16; u++) {
+            const int s = s0 + u * CNG;
+            if (s < ns) {
+                q[u] = ml[s];
+                a[u] = acc_rows[(size_t)s * AHD + d];
+            } else {
+                q[u] = make_float2(-INFINITY, 0.f);
+                a[u] = 0.f;
+            }
         }
-        for (; s < n; s += NG) acc += w[s] * p[(size_t)(s0 + s) * (AHD + 2) + 2 + d];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            if (q[u].y > 0.f) {  // empty splits (l = 0, m = -inf) contribute nothing
+                const float mn = fmaxf(mt, q[u].x);
+                const float f = fast_exp2(mt - mn), g = fast_exp2(q[u].x - mn);  // f = 0 while mt = -inf
+                lt = lt * f + q[u].y * g;
+                at = at * f + a[u] * g;
+                mt = mn;
+            }
+        }
     }
-    l = block_sum(l, sh8 + 8);
-    red[gi][dl] = acc;
+    sm[gi][dl] = mt; sl[gi][dl] = lt; sa[gi][dl] = at;
     __syncthreads();
-    if (tid >= DW) {
-        if (!turbo_rot) return;
-    }
-    float x = 0.f;
-    if (tid < DW) {
+    if (tid >= CDW) return;
+    float M = -INFINITY;
 #pragma unroll
-        for (int g = 0; g < NG; g++) x += red[g][tid];
-        x /= l;
+    for (int g = 0; g < CNG; g++) M = fmaxf(M, sm[g][tid]);  // split 0 is never empty: M is finite
+    float l = 0.f, acc = 0.f;
+#pragma unroll
+    for (int g = 0; g < CNG; g++) {
+        const float f = fast_exp2(sm[g][tid] - M);
+        l += sl[g][tid] * f;
+        acc += sa[g][tid] * f;
     }
-    if (turbo_rot) x = wht(x, sh, 1);  // DC == 1: every thread holds one dim
-    if (tid < DW) {
-        if (q_gate) x = x / (1.f + __expf(-q_gate[(size_t)tok * ld + h * 2 * AHD + AHD + d]));
-        out[((size_t)tok * H + h) * AHD + d] = x;
-    }
+    float x = acc / l;
+    if (q_gate) x = x / (1.f + __expf(-q_gate[(size_t)tok * ld + h * 2 * AHD + AHD + d]));
+    out[((size_t)tok * H + h) * AHD + d] = x;
 }
 
 // attn_decode_k (kernels.cuh:1238-1315): one block per (query head, token, split), 256 threads, any H / KV.
@@ -339,9 +337,11 @@ __global__ void __launch_bounds__(256) decode_heads_kernel(const float* __restri
         out[h * AHD + tid] = q_gate ? acc / l / (1.f + __expf(-q_gate[h * 2 * AHD + AHD + tid])) : acc / l;
         return;
     }
-    float* p = part + (((size_t)tok * H + h) * ns + blockIdx.z) * (AHD + 2);
-    p[2 + tid] = acc;
-    if (tid == 0) { p[0] = m; p[1] = l; }  // an empty split leaves m = -inf, l = 0, acc = 0
+    part_acc(part, tok, h, blockIdx.z, H, ns)[tid] = acc;
+    if (tid == 0) {  // an empty split leaves m = -inf, l = 0, acc = 0
+        float* ml = part_ml(part, tok, h, blockIdx.z, H, ns, gridDim.y);
+        ml[0] = m; ml[1] = l;
+    }
 }
 
 __global__ void set_int_kernel(int* p, int v) { *p = v; }
@@ -364,12 +364,8 @@ void launch_turbo_out(float* out, const float* q_gate, int H, int ld, int T, hip
     hipLaunchKernelGGL(turbo_out_kernel, dim3(H, T), dim3(256), 0, st, out, q_gate, H, ld);
     MOEX_LAUNCHED();
 }
-void launch_combine(const float* part, const float* q_gate, float* out, int H, int ns, int ld, int T, int turbo_rot,
-                    hipStream_t st) {
-    if (turbo_rot)
-        hipLaunchKernelGGL(combine_kernel<1>, dim3(H, T, 1), dim3(256), 0, st, part, q_gate, out, H, ns, ld, 1);
-    else
-        hipLaunchKernelGGL(combine_kernel<8>, dim3(H, T, 8), dim3(256), 0, st, part, q_gate, out, H, ns, ld, 0);
+void launch_combine(const float* part, const float* q_gate, float* out, int H, int ns, int ld, int T, hipStream_t st) {
+    hipLaunchKernelGGL(combine_kernel, dim3(H, T, CDC), dim3(256), 0, st, part, q_gate, out, H, ns, ld);
     MOEX_LAUNCHED();
 }
 void launch_decode_heads(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
