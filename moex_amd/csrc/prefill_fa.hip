@@ -29,10 +29,7 @@ constexpr int KST = AHD + 8;                // K row stride in halves (528 B: ro
 constexpr int KT_BYTES = BK * KST * 2;      // 16.5 KB
 constexpr int VT_BYTES = AHD * VST * 2;     // 36 KB
 constexpr int SC_BYTES = BK * 4;            // per-key score scale
-constexpr int NST = 4;                      // ring of staged key tiles
-constexpr int STAGE_BYTES = KT_BYTES + VT_BYTES + SC_BYTES;
-constexpr int LDS_BYTES = NST * STAGE_BYTES + SC_BYTES + 2 * NST * 4;  // stages, a spare scale slot, ring counters
-constexpr int SPIN_MAX = 1 << 22;           // bound of every ring wait (the waits always end well before it)
+constexpr int LDS_BYTES = 2 * KT_BYTES + 2 * VT_BYTES + 3 * SC_BYTES;  // 2 score-scale slots + a spare
 constexpr float SL2 = 0.0625f * 1.4426950408889634f;
 constexpr float TK4 = 0.241529f / 127.f, TK3 = 0.190207f / 127.f;
 constexpr int FA_KPF = 2;                   // LDS operand reads in flight ahead of the MFMAs
@@ -225,67 +222,60 @@ int fa_grid(int KV, int T) {
 }  // namespace
 
 // Warp-specialised workgroup of 8 wavefronts. Wavefronts 0-3 compute (32 query rows each); wavefronts 4-7 stage: they
-// load the next tiles' int8/turbo K and V, widen them and write them into a ring of NST LDS stages. Each SIMD holds
-// one wavefront of each kind, so the staging VALU work runs beside the other wavefront's MFMAs. The two kinds meet
-// only through two LDS counters per stage: full[s] counts staging wavefronts that finished writing a tile into stage
-// s, empty[s] counts computing wavefronts that finished reading it, so staging runs up to NST tiles ahead.
-__device__ __forceinline__ void ring_wait(int* cnt, int target) {
-    int it = 0;
-    while (__hip_atomic_load(cnt, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target && ++it < SPIN_MAX)
-        __builtin_amdgcn_s_sleep(1);
-}
-__device__ __forceinline__ void ring_arrive(int* cnt) {
-    __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-
+// load the next tiles' int8/turbo K and V, widen them and write them to the LDS buffers. Each SIMD holds one wavefront of
+// each kind, so the staging VALU work runs beside the other wavefront's MFMAs. One barrier per key tile: during tile j
+// the computing wavefronts read buffers j%2 while the staging wavefronts fill buffers (j+1)%2.
 template <bool TB>
 __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restrict__ qo, const float* __restrict__ q_gate,
                                                             moex_kv_cache kv, float* __restrict__ out, int H, int KV,
                                                             const int* __restrict__ pos_d, int max_t, int ld, int T) {
     extern __shared__ __align__(16) unsigned char smem[];
-#define KBUF(i) (smem + (i) * STAGE_BYTES)
-#define VBUF(i) (smem + (i) * STAGE_BYTES + KT_BYTES)
-#define SBUF(i) (reinterpret_cast<float*>(smem + (i) * STAGE_BYTES + KT_BYTES + VT_BYTES))
-    float* spare = reinterpret_cast<float*>(smem + NST * STAGE_BYTES);
-    int* full = reinterpret_cast<int*>(smem + NST * STAGE_BYTES + SC_BYTES);
-    int* empty = full + NST;
+#define KBUF(i) (smem + (i) * KT_BYTES)
+#define VBUF(i) (smem + 2 * KT_BYTES + (i) * VT_BYTES)
+#define SBUF(i) (reinterpret_cast<float*>(smem + 2 * KT_BYTES + 2 * VT_BYTES) + (i) * BK)
     const int NT = (T + FT - 1) / FT;
     int kvh, tile;
     if (!map_block(blockIdx.x, KV, NT, kvh, tile)) return;
     const int t0 = tile * FT, pos0 = *pos_d, nt = min(FT, T - t0), hi = pos0 + t0 + nt;  // keys [0, hi)
     const size_t rbase = (size_t)kvh * max_t;
     const int ntiles = (hi + BK - 1) / BK;
-    if (threadIdx.x < 2 * NST) full[threadIdx.x] = 0;  // full[] and empty[] are contiguous
-    __syncthreads();
 
     if (threadIdx.x >= 256) {
-        // ---------------- staging wavefronts: tile j into stage j % NST; loads two tiles ahead ----------------
-        const int tid = threadIdx.x - 256, lane = tid & 63;
-        StageK sk[2];
-        StageV sv[2];
-        auto load = [&](int jt, int b) {
-            const int k0 = jt * BK;
-            if (k0 + BK <= hi) { load_k<TB, true>(sk[b], kv, rbase, k0, hi, tid); load_v<TB, true>(sv[b], kv, rbase, k0, hi, tid); }
-            else { load_k<TB>(sk[b], kv, rbase, k0, hi, tid); load_v<TB>(sv[b], kv, rbase, k0, hi, tid); }
-        };
-        auto stage = [&](int jt, int b) {
-            const int st = jt % NST, k0 = jt * BK;
-            ring_wait(empty + st, 4 * (jt / NST));  // the computing wavefronts are done with tile jt - NST
-            if (k0 + BK <= hi) {
-                store_k<TB, true>(sk[b], KBUF(st), SBUF(st), spare, k0, hi, tid);
-                store_v<TB, true>(sv[b], VBUF(st), k0, hi, tid);
-            } else {
-                store_k<TB>(sk[b], KBUF(st), SBUF(st), spare, k0, hi, tid);
-                store_v<TB>(sv[b], VBUF(st), k0, hi, tid);
+        // ---------------- staging wavefronts ----------------
+        const int tid = threadIdx.x - 256;
+        StageK sk;
+        StageV sv;
+        load_k<TB>(sk, kv, rbase, 0, hi, tid);
+        load_v<TB>(sv, kv, rbase, 0, hi, tid);
+        store_k<TB>(sk, KBUF(0), SBUF(0), SBUF(2), 0, hi, tid);
+        store_v<TB>(sv, VBUF(0), 0, hi, tid);
+        if (ntiles > 1) {
+            load_k<TB>(sk, kv, rbase, BK, hi, tid);
+            load_v<TB>(sv, kv, rbase, BK, hi, tid);
+        }
+        __syncthreads();
+        for (int j = 0; j < ntiles; j++) {
+            const int k1 = (j + 1) * BK;
+            if (j + 1 < ntiles) {
+                if (k1 + BK <= hi) {
+                    store_k<TB, true>(sk, KBUF((j + 1) & 1), SBUF((j + 1) & 1), SBUF(2), k1, hi, tid);
+                    store_v<TB, true>(sv, VBUF((j + 1) & 1), k1, hi, tid);
+                } else {
+                    store_k<TB>(sk, KBUF((j + 1) & 1), SBUF((j + 1) & 1), SBUF(2), k1, hi, tid);
+                    store_v<TB>(sv, VBUF((j + 1) & 1), k1, hi, tid);
+                }
             }
-            if (jt + 2 < ntiles) load(jt + 2, b);
-            if (lane == 0) ring_arrive(full + st);
-        };
-        load(0, 0);
-        if (ntiles > 1) load(1, 1);
-        for (int j = 0; j < ntiles; j += 2) {  // two tiles per trip: the register buffers alternate
-            stage(j, 0);
-            if (j + 1 < ntiles) stage(j + 1, 1);
+            if (j + 2 < ntiles) {
+                const int k2 = k1 + BK;
+                if (k2 + BK <= hi) {
+                    load_k<TB, true>(sk, kv, rbase, k2, hi, tid);
+                    load_v<TB, true>(sv, kv, rbase, k2, hi, tid);
+                } else {
+                    load_k<TB>(sk, kv, rbase, k2, hi, tid);
+                    load_v<TB>(sv, kv, rbase, k2, hi, tid);
+                }
+            }
+            __syncthreads();
         }
         return;
     }
@@ -317,14 +307,13 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
         for (int i = 0; i < 16; i++) o[db][i] = 0.f;
     float m_ref = -INFINITY, l_run = 0.f;
     const half2_t ones = half2_t{(_Float16)1.f, (_Float16)1.f};
+    __syncthreads();
 
     for (int j = 0; j < ntiles; j++) {
-        const int st = j % NST;
-        ring_wait(full + st, 4 * (j / NST + 1));
         if (j < wtiles) {
-            const _Float16* Kt = reinterpret_cast<const _Float16*>(KBUF(st));
-            const _Float16* Vt = reinterpret_cast<const _Float16*>(VBUF(st));
-            const float* scl = SBUF(st);
+            const _Float16* Kt = reinterpret_cast<const _Float16*>(KBUF(j & 1));
+            const _Float16* Vt = reinterpret_cast<const _Float16*>(VBUF(j & 1));
+            const float* scl = SBUF(j & 1);
             const int k0 = j * BK;
             // ---- S^T = K . Q^T: lane = (row r, key half h32), element i: key 8*(i/4) + 4*h32 + i%4 ----
             float16_t sc;
@@ -402,7 +391,7 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
                 }
             }
         }
-        if (lane == 0) ring_arrive(empty + st);  // release: this wavefront's reads of the stage have completed
+        __syncthreads();
     }
 #undef KBUF
 #undef VBUF
