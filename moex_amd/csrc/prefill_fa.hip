@@ -1,20 +1,20 @@
 // FlashAttention-2 chunked causal GQA prefill on gfx950 (replaces attn_fa_k<TB>, kernels.cuh:1443-1728).
 //
-// Workgroup = (kv head, 16 query tokens) = 128 query rows (8 heads x 16 tokens), 4 wavefronts of 32 rows;
-// wavefront w owns tokens 4w .. 4w+3, row r = (token 4w + r/8, head r%8). Keys in tiles of 64.
-//   - The block stages every K/V tile once, widening int8 (or turbo codes) to fp16 in LDS: K as [key][dim] with
-//     16-byte chunks XOR-swizzled by key, V transposed as [dim][key] and already multiplied by its row scale
-//     (int8: vs; turbo: half norm * K3), so P enters the P.V product as plain fp16 probabilities. Turbo K is
-//     likewise multiplied by its half norm * K4; int8 K stays exact and its scale is applied to the fp32 score.
-//   - K and V have separate double buffers with staggered lifetimes: while tile j is computed, K of tile j+2 and V
-//     of tile j+1 are written, so one barrier per tile suffices.
-//   - Software pipeline per wavefront: S^T of tile j+1 (v_mfma_f32_32x32x16_f16, Q fp16 in registers) is computed
-//     while the softmax of tile j runs on the VALU, then O^T += V^T . P^T for tile j. The 32x32 D layout gives each
-//     lane one query row (lane % 32) and 16 keys per S tile: row max / row sum are in-lane plus one cross-half swap.
-//   - Lazy rescale: O and l are only rescaled when a row's maximum grows by more than 8 (log2 units) over the value
-//     the probabilities are referenced to, so p <= 2^8; O (256 fp32 per row, 128 accumulators per lane in AGPRs)
-//     is touched by the VALU only then.
-// Softmax in base 2 (scale 1/sqrt(256) * log2(e), kernels.cuh:1513). Rounding: Q, P and the scaled K/V values are
+// Workgroup = (kv head, 16 query tokens) = 128 query rows (8 heads x 16 tokens) and 8 wavefronts:
+//   - wavefronts 4-7 stage key tiles of 32: they load int8 (or turbo codes) K and V one tile ahead, widen them to
+//     fp16 and write them to LDS - K as [key][dim] (row stride padded to 528 B: conflict-free reads with immediate
+//     offsets), V transposed as [dim][key] and already multiplied by its row scale (int8: vs; turbo: half norm * K3),
+//     so P enters the P.V product as plain fp16 probabilities. Turbo K is likewise multiplied by its half norm * K4;
+//     int8 K stays exact and its scale is applied to the fp32 score;
+//   - wavefronts 0-3 compute, 32 query rows each (wavefront w: tokens 4w .. 4w+3, row r = (token 4w + r/8,
+//     head r%8)): S^T = K . Q^T and O^T += V^T . P^T on v_mfma_f32_32x32x16_f16 with Q fp16 in registers. The 32x32
+//     D layout gives each lane one query row (lane % 32) and 16 keys: row max / row sum are in-lane plus one
+//     cross-half swap. LDS operand reads are issued two MFMAs ahead of their use.
+// A SIMD holds one wavefront of each kind, so the staging VALU work runs beside the other's MFMAs; one barrier per
+// tile (double-buffered LDS).
+// Lazy rescale: O and l are only rescaled when a row's maximum grows by more than 8 (log2 units) over the value the
+// probabilities are referenced to, so p <= 2^8 and the VALU touches O only then.
+// Softmax in base 2 (scale 1/sqrt(256) * log2(e), kernels.cuh:1513). Rounding: Q, P and the scaled V values are
 // fp16 MFMA operands with fp32 accumulation; the reference rounds Q and P * vscale (kernels.cuh:1508,1656).
 #include <type_traits>
 #include "common.hpp"
