@@ -154,7 +154,7 @@ def main():
             fill_cache(c, ctx, seed=20 + i)
             rot.append(c)
         for Tq in (1, 4):
-            ns = M.decode_splits(ctx)
+            ns = M.gqa_splits(Tq, KV, M.decode_splits(ctx))
             part = torch.empty(Tq * H * ns * (AHD + 2), device=dev)
             o1 = torch.empty((Tq, H, AHD), device=dev)
             pd = torch.tensor([ctx - Tq], dtype=torch.int32, device=dev)

@@ -111,6 +111,10 @@ int moex_fa_supported(void);
 /* Recommended ns for the split-K decode at n_ctx keys on the current device (the engine's ASPLIT). The part
  * buffer must hold T*H*ns*(256+2) floats. No counterpart in the reference (ASPLIT is a constant there). */
 int moex_decode_splits(int n_ctx);
+/* The split count moex_attn_decode runs its GQA kernel with when it is given ns splits for T query tokens of a
+ * cache with KV heads (turbo != 0 for a turbo cache): at most ns. A caller that launches moex_attn_gqa and
+ * moex_attn_combine itself passes this value to both. No counterpart in the reference. */
+int moex_gqa_splits(int T, int KV, int ns, int turbo);
 /* Library build identifier. */
 const char* moex_version(void);
 

@@ -60,6 +60,8 @@ def lib():
     L.moex_fa_supported.restype = i
     L.moex_decode_splits.argtypes = [i]
     L.moex_decode_splits.restype = i
+    L.moex_gqa_splits.argtypes = [i, i, i, i]
+    L.moex_gqa_splits.restype = i
     L.moex_version.restype = ctypes.c_char_p
     _lib = L
     return L
@@ -68,7 +70,7 @@ def lib():
 EXPORTS = ["moex_kv_alloc", "moex_kv_bytes", "moex_kv_free", "moex_attn_decode", "moex_attn_fa", "moex_attn_prefill",
            "moex_qk_norm_rope", "moex_kv_append", "moex_attn_gqa", "moex_attn_combine", "moex_attn_decode_heads",
            "moex_turbo_out", "moex_set_int", "moex_set_soft_error", "moex_set_skip", "moex_fa_on",
-           "moex_fa_supported", "moex_decode_splits", "moex_version"]
+           "moex_fa_supported", "moex_decode_splits", "moex_gqa_splits", "moex_version"]
 
 
 def _p(x):
@@ -186,6 +188,11 @@ def set_skip(v, st=None):
 
 def decode_splits(n_ctx):
     return lib().moex_decode_splits(n_ctx)
+
+
+def gqa_splits(T, KV, ns, turbo=0):
+    """split count moex_attn_decode uses for the GQA kernel when allowed ns (pass it to attn_gqa and attn_combine)"""
+    return lib().moex_gqa_splits(T, KV, ns, int(turbo))
 
 
 def fa_on():

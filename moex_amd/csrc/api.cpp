@@ -91,6 +91,14 @@ int moex_decode_splits(int n_ctx) {
     return ns < 1 ? 1 : ns;
 }
 
+int moex_gqa_splits(int T, int KV, int ns, int turbo) {
+    if (!(T > 0 && KV > 0 && ns > 0)) {
+        arg_fail("T, KV, ns");
+        return 1;
+    }
+    return gqa_splits(T, KV, ns, turbo != 0);
+}
+
 const char* moex_version(void) { return "moex_attn gfx950 0.1"; }
 
 void moex_set_soft_error(int* slot) { g_soft = slot; }
@@ -174,6 +182,7 @@ void moex_attn_decode(const float* q, const float* k, const float* v, const uint
     } else if (T > 2 && ns == 1 && G == GQ && !kv.turbo) {
         launch_prefill_k7p(qo, q, kv, out, H, KV, pos_d, max_t, ld, T, st);
     } else if (ns > 1 && G == GQ) {
+        ns = gqa_splits(T, KV, ns, kv.turbo != 0);
         launch_gqa(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
         launch_combine(part, gate, out, H, ns, ld, T, st);
     } else {

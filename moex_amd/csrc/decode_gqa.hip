@@ -77,18 +77,25 @@ __device__ __forceinline__ float ex2d(float a, float b) { return a == b ? 1.f : 
 // O stays in the MFMA accumulators across chunks (rescaled by 2^(m_old - m_new) times the change of the per-chunk power
 // of two 2^sig), so a chunk costs no int32 -> fp32 fold and the per-token work is only the MFMAs, the scores and P.
 constexpr int X_PL = 4 * 64 * 16;  // P operands of one token per chunk: [step = wavefront][lane] half8
+// Query-token pairs share the Q.K MFMAs: column m of the B operand is (token 2pp + m/8, head m%8) of pair pp, and
+// the three base-256 digits of the query are three MFMAs, so a lane recombines the score of its own (token, head)
+// from three accumulators without lane exchanges (TT = 1 leaves columns 8..15 as a copy of token 0).
 template <int TT>
-constexpr int x_lds() { return 2 * I8_VBUF + TT * X_PL + (TT > 1 ? TT * I8_QL : 0); }
+constexpr int x_np() { return (TT + 1) / 2; }
+template <int TT>
+constexpr int x_lds() { return 2 * I8_VBUF + TT * X_PL + (TT > 2 ? x_np<TT>() * 3 * 4 * 64 * 16 : 0); }
+static_assert(3 * 4 * 64 * 16 <= I8_VBUF, "one token pair's query digits stage in V buffer 1");
 
 template <int TT>
-__global__ void __launch_bounds__(256, TT == 1 ? 2 : 1) gqa_x_kernel(const float* __restrict__ qo, moex_kv_cache kv,
+__global__ void __launch_bounds__(256, TT <= 2 ? 2 : 1) gqa_x_kernel(const float* __restrict__ qo, moex_kv_cache kv,
                                                                      int H, const int* __restrict__ pos_d, int max_t,
                                                                      float* __restrict__ part, int T, int ns) {
+    constexpr int NP = x_np<TT>(), TE = 2 * NP;  // token pairs, token slots (TT = 1: slot 1 copies token 0)
+    constexpr bool QREG = TT <= 2;               // query digits in registers (else re-read from LDS)
     extern __shared__ __align__(16) unsigned char smem[];
     half8_t* Pl = reinterpret_cast<half8_t*>(smem + 2 * I8_VBUF);  // [TT][4][64]
-    // query digits: [TT][2][4][64]; TT = 1 holds them in registers and only stages them in V buffer 1
-    int4_t_* Ql = reinterpret_cast<int4_t_*>(TT == 1 ? smem + I8_VBUF : smem + 2 * I8_VBUF + TT * X_PL);
-    __shared__ float mxw[TT][4][GQ], lsum[TT][4][GQ], vmw[4], qsc_s[TT][GQ];
+    int4_t_* Ql = reinterpret_cast<int4_t_*>(QREG ? smem + I8_VBUF : smem + 2 * I8_VBUF + TT * X_PL);  // [NP][3][4][64]
+    __shared__ float mxw[TE][4][GQ], lsum[TE][4][GQ], vmw[4], qsc_s[TE][GQ];
     const int nb = gridDim.x, w_id = xcd_work_id(blockIdx.x, nb);
     const int ngr = (T + TT - 1) / TT;
     const int tg = w_id % ngr, s = (w_id / ngr) % ns, kvh = w_id / (ngr * ns);
@@ -96,11 +103,11 @@ __global__ void __launch_bounds__(256, TT == 1 ? 2 : 1) gqa_x_kernel(const float
     const int pos0 = *pos_d, Tmax = pos0 + T;
     const int L = (Tmax + ns - 1) / ns, lo = s * L;
     const int hi = min(pos0 + tb + ntok, lo + L);  // keys of the group's last token; token t sees [lo, hit[t])
-    int hit[TT];
-#pragma unroll
-    for (int t = 0; t < TT; t++) hit[t] = min(pos0 + tb + min(t, ntok - 1) + 1, lo + L);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 4, m16 = lane & 15, hq = m16 & 7;
-    const bool lo8 = m16 < 8;
+    const int tp = m16 >> 3;                       // this lane's token within each pair
+    int hitl[NP];                                  // key bound of this lane's token of each pair
+#pragma unroll
+    for (int pp = 0; pp < NP; pp++) hitl[pp] = min(pos0 + tb + min(2 * pp + tp, ntok - 1) + 1, lo + L);
     const size_t rbase = (size_t)kvh * max_t;
     const int8_t* Kg = kv.k + rbase * AHD;
     const int8_t* Vg = kv.v + rbase * AHD;
@@ -164,9 +171,10 @@ __global__ void __launch_bounds__(256, TT == 1 ? 2 : 1) gqa_x_kernel(const float
         issue_v(smem, lo);
     }
 
-    // ---- query digits, once per workgroup: thread = (head tid/32, dims 8*(tid%32) .. +7), per token ----
+    // ---- query digits, once per workgroup: thread = (head tid/32, dims 8*(tid%32) .. +7), per token slot; slot t
+    // goes to pair t/2, column 8*(t%2) + head ----
 #pragma unroll
-    for (int t = 0; t < TT; t++) {
+    for (int t = 0; t < TE; t++) {
         const int h = tid >> 5, d0 = (tid & 31) * 8;
         const float* qrow = qo + ((size_t)(tb + min(t, ntok - 1)) * H + kvh * GQ + h) * AHD + d0;
         const float4 x0 = reinterpret_cast<const float4*>(qrow)[0], x1 = reinterpret_cast<const float4*>(qrow)[1];
@@ -180,39 +188,40 @@ __global__ void __launch_bounds__(256, TT == 1 ? 2 : 1) gqa_x_kernel(const float
         if (qm > 0.f) (void)frexpf(qm, &e);  // qm < 2^e
         const float up = ldexpf(1.f, 22 - e);
         if ((tid & 31) == 0) qsc_s[t][h] = ldexpf(1.f, e - 22) * SL2;
-        int d2[8], d1[8], dz[8];
+        int dg[3][8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) digits3((int)__builtin_rintf(qv[j] * up), d2[j], d1[j], dz[j]);
-        // B operand of Q.K: MFMA ks, lane 16g + m holds dims 64ks + 16g + 0..15 of column m
-        const int ks = d0 >> 6, gg = (d0 >> 4) & 3, jb = d0 & 15;
-        unsigned char* qa_b = reinterpret_cast<unsigned char*>(Ql + ((t * 2 + 0) * 4 + ks) * 64);
-        unsigned char* qb_b = reinterpret_cast<unsigned char*>(Ql + ((t * 2 + 1) * 4 + ks) * 64);
-        *reinterpret_cast<uint2*>(qa_b + (16 * gg + h) * 16 + jb) =
-            make_uint2(pack_bytes(d2[0], d2[1], d2[2], d2[3]), pack_bytes(d2[4], d2[5], d2[6], d2[7]));
-        *reinterpret_cast<uint2*>(qa_b + (16 * gg + h + 8) * 16 + jb) =
-            make_uint2(pack_bytes(d1[0], d1[1], d1[2], d1[3]), pack_bytes(d1[4], d1[5], d1[6], d1[7]));
-        *reinterpret_cast<uint2*>(qb_b + (16 * gg + h) * 16 + jb) =
-            make_uint2(pack_bytes(dz[0], dz[1], dz[2], dz[3]), pack_bytes(dz[4], dz[5], dz[6], dz[7]));
-        *reinterpret_cast<uint2*>(qb_b + (16 * gg + h + 8) * 16 + jb) = make_uint2(0u, 0u);
+        for (int j = 0; j < 8; j++) digits3((int)__builtin_rintf(qv[j] * up), dg[2][j], dg[1][j], dg[0][j]);
+        // B operand: MFMA (digit, ks), lane 16g + m holds dims 64ks + 16g + 0..15 of column m
+        const int ks = d0 >> 6, gg = (d0 >> 4) & 3, jb = d0 & 15, col = 8 * (t & 1) + h;
+#pragma unroll
+        for (int dig = 0; dig < 3; dig++) {
+            unsigned char* qd = reinterpret_cast<unsigned char*>(Ql + (((t >> 1) * 3 + dig) * 4 + ks) * 64);
+            *reinterpret_cast<uint2*>(qd + (16 * gg + col) * 16 + jb) =
+                make_uint2(pack_bytes(dg[dig][0], dg[dig][1], dg[dig][2], dg[dig][3]),
+                           pack_bytes(dg[dig][4], dg[dig][5], dg[dig][6], dg[dig][7]));
+        }
     }
     __syncthreads();
-    int4_t_ qa[4], qb[4];  // TT = 1 only
-    float qs[TT];
+    int4_t_ qd[QREG ? 3 : 1][4];  // pair 0's digits (TT <= 2)
+    float qs[NP];
 #pragma unroll
-    for (int t = 0; t < TT; t++) qs[t] = qsc_s[t][hq];
-    if (TT == 1) {
+    for (int pp = 0; pp < NP; pp++) qs[pp] = qsc_s[2 * pp + tp][hq];
+    if (QREG) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) { qa[ks] = Ql[ks * 64 + lane]; qb[ks] = Ql[(4 + ks) * 64 + lane]; }
+        for (int dig = 0; dig < 3; dig++)
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) qd[dig][ks] = Ql[(dig * 4 + ks) * 64 + lane];
     }
 
-    float4_t o[TT][4];                    // O^T tiles j: lane (g, m16) holds rows 4g + i, column m16
-    float m4[TT][4], mo[TT], lacc[TT];    // running max of heads 4(g&1)+i and of head hq; head hq's partial sum
+    float4_t o[TT][4];              // O^T tiles j: lane (g, m16) holds rows 4g + i, column m16
+    float m4[TT][4];                // running max of heads 4(g&1)+i, per token
+    float mo[NP], lacc[NP];         // running max and partial sum of this lane's (token, head) of each pair
 #pragma unroll
-    for (int t = 0; t < TT; t++) {
-        mo[t] = -INFINITY; lacc[t] = 0.f;
+    for (int t = 0; t < TT; t++)
 #pragma unroll
         for (int i = 0; i < 4; i++) { m4[t][i] = -INFINITY; o[t][i] = float4_t{0.f, 0.f, 0.f, 0.f}; }
-    }
+#pragma unroll
+    for (int pp = 0; pp < NP; pp++) { mo[pp] = -INFINITY; lacc[pp] = 0.f; }
     int sig_ref = 0;  // O is held times 2^sig_ref
     const int rd = 16 * ((4 * wv + (m16 >> 2)) ^ (4 * g)) + 4 * (m16 & 3);  // swizzled byte offset of my V dims
 
@@ -228,46 +237,44 @@ __global__ void __launch_bounds__(256, TT == 1 ? 2 : 1) gqa_x_kernel(const float
             issue_k(kn, ksn, vn, c0 + ICH);
             issue_v(smem + ((c + 1) & 1) * I8_VBUF, c0 + ICH);
         }
-        // ---- pass 1: scores of this wavefront's 32 keys (int8 MFMA on the query digits) ----
-        float sc[TT][8];
+        // ---- pass 1: scores of this wavefront's 32 keys, one (token, head) per lane and pair ----
+        float sc[NP][8];
         float vm = 0.f;
 #pragma unroll
-        for (int t = 0; t < TT; t++)
+        for (int pp = 0; pp < NP; pp++)
 #pragma unroll
-            for (int j = 0; j < 8; j++) sc[t][j] = -INFINITY;
+            for (int j = 0; j < 8; j++) sc[pp][j] = -INFINITY;
         if (has) {
 #pragma unroll
             for (int j = 0; j < 8; j++)
                 if (k0 + 16 * (j >> 2) + 4 * g + (j & 3) < hi) vm = fmaxf(vm, vv[j]);
 #pragma unroll
-            for (int t = 0; t < TT; t++)
+            for (int pp = 0; pp < NP; pp++)
 #pragma unroll
                 for (int grp = 0; grp < 2; grp++) {
-                    int4_t_ da = {0, 0, 0, 0}, db = {0, 0, 0, 0};
+                    int4_t_ acc[3] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
-                    for (int ks = 0; ks < 4; ks++) {
-                        const int4_t_ a = TT == 1 ? qa[ks] : Ql[(t * 8 + ks) * 64 + lane];
-                        const int4_t_ b = TT == 1 ? qb[ks] : Ql[(t * 8 + 4 + ks) * 64 + lane];
-                        da = __builtin_amdgcn_mfma_i32_16x16x64_i8(kr[grp][ks], a, da, 0, 0, 0);
-                        db = __builtin_amdgcn_mfma_i32_16x16x64_i8(kr[grp][ks], b, db, 0, 0, 0);
-                    }
+                    for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+                        for (int dig = 0; dig < 3; dig++) {
+                            const int4_t_ b = QREG ? qd[dig][ks] : Ql[((pp * 3 + dig) * 4 + ks) * 64 + lane];
+                            acc[dig] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kr[grp][ks], b, acc[dig], 0, 0, 0);
+                        }
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        const int x = dpp_ror8(da[i]), y = dpp_ror8(db[i]);
-                        const int a2 = lo8 ? da[i] : x, a1 = lo8 ? x : da[i], a0 = lo8 ? db[i] : y;
-                        const float raw = ((float)a2 * 65536.f + (float)a1 * 256.f) + (float)a0;
+                        const float raw = ((float)acc[2][i] * 65536.f + (float)acc[1][i] * 256.f) + (float)acc[0][i];
                         const int j = 4 * grp + i, key = k0 + 16 * grp + 4 * g + i;
-                        sc[t][j] = key < hit[t] ? raw * (ksv[j] * qs[t]) : -INFINITY;
+                        sc[pp][j] = key < hitl[pp] ? raw * (ksv[j] * qs[pp]) : -INFINITY;
                     }
                 }
         }
 #pragma unroll
-        for (int t = 0; t < TT; t++) {
-            float mx = sc[t][0];
+        for (int pp = 0; pp < NP; pp++) {
+            float mx = sc[pp][0];
 #pragma unroll
-            for (int j = 1; j < 8; j++) mx = fmaxf(mx, sc[t][j]);
+            for (int j = 1; j < 8; j++) mx = fmaxf(mx, sc[pp][j]);
             mx = fmaxf(mx, __shfl_xor(mx, 16)); mx = fmaxf(mx, __shfl_xor(mx, 32));
-            if (g == 0 && lo8) mxw[t][wv][m16] = mx;
+            if (g == 0) mxw[2 * pp + tp][wv][hq] = mx;
         }
 #pragma unroll
         for (int o2 = 1; o2 < 64; o2 <<= 1) vm = fmaxf(vm, __shfl_xor(vm, o2));
@@ -280,26 +287,34 @@ __global__ void __launch_bounds__(256, TT == 1 ? 2 : 1) gqa_x_kernel(const float
         const float vsc = ldexpf(1.f, sig);
         const float sfac = c == 0 ? 1.f : ldexpf(1.f, sig - sig_ref);  // O re-expressed at the new power of two
         sig_ref = sig;
-        // ---- pass 1.5: probabilities (hi/lo fp16 operands to LDS), running maxima, O rescale ----
+        // ---- pass 1.5: P of this lane's (token, head) as hi/lo fp16 rows head / 8 + head of its token's operand ----
 #pragma unroll
-        for (int t = 0; t < TT; t++) {
-            const float M = fmaxf(fmaxf(mxw[t][0][hq], mxw[t][1][hq]), fmaxf(mxw[t][2][hq], mxw[t][3][hq]));
-            const float mn = fmaxf(mo[t], M);
+        for (int pp = 0; pp < NP; pp++) {
+            const int tl = 2 * pp + tp;
+            const float M = fmaxf(fmaxf(mxw[tl][0][hq], mxw[tl][1][hq]), fmaxf(mxw[tl][2][hq], mxw[tl][3][hq]));
+            const float mn = fmaxf(mo[pp], M);
             float ls = 0.f;
             if (has) {
-                half8_t pv;
+                half8_t ph, pl;
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    const float p = mn == -INFINITY ? 0.f : fast_exp2(sc[t][j] - mn);  // 0 for masked keys
+                    const float p = mn == -INFINITY ? 0.f : fast_exp2(sc[pp][j] - mn);  // 0 for masked keys
                     ls += p;
                     const float x = p * (vv[j] * vsc);
                     const _Float16 h = (_Float16)x;
-                    pv[j] = lo8 ? h : (_Float16)(x - (float)h);
+                    ph[j] = h;
+                    pl[j] = (_Float16)(x - (float)h);
                 }
-                Pl[(t * 4 + wv) * 64 + lane] = pv;
+                if (tl < TT) {
+                    Pl[(tl * 4 + wv) * 64 + 16 * g + hq] = ph;
+                    Pl[(tl * 4 + wv) * 64 + 16 * g + 8 + hq] = pl;
+                }
             }
-            lacc[t] = lacc[t] * ex2d(mo[t], mn) + ls;
-            mo[t] = mn;
+            lacc[pp] = lacc[pp] * ex2d(mo[pp], mn) + ls;
+            mo[pp] = mn;
+        }
+#pragma unroll
+        for (int t = 0; t < TT; t++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int h = 4 * (g & 1) + i;
@@ -310,7 +325,6 @@ __global__ void __launch_bounds__(256, TT == 1 ? 2 : 1) gqa_x_kernel(const float
 #pragma unroll
                 for (int jt = 0; jt < 4; jt++) o[t][jt][i] *= f;
             }
-        }
         __syncthreads();
         // ---- pass 2: O^T += P . V over the chunk's steps (one per wavefront that had keys), this wavefront's dims ----
         for (int st = 0; st < nsteps; st++) {
@@ -341,11 +355,11 @@ __global__ void __launch_bounds__(256, TT == 1 ? 2 : 1) gqa_x_kernel(const float
     // ---- partials: rows 4g+i of the O^T tiles are the hi parts (g < 2) of head 4(g&1)+i, the lo parts (g >= 2) ----
     __syncthreads();
 #pragma unroll
-    for (int t = 0; t < TT; t++) {
-        float l = lo8 ? lacc[t] : 0.f;
+    for (int pp = 0; pp < NP; pp++) {
+        float l = lacc[pp];
         l += __shfl_xor(l, 16);
         l += __shfl_xor(l, 32);
-        if (g == 0 && lo8) lsum[t][wv][m16] = l;
+        if (g == 0) lsum[2 * pp + tp][wv][hq] = l;
     }
     __syncthreads();
     const float unscale = ldexpf(1.f, -sig_ref);
@@ -687,6 +701,21 @@ __global__ void __launch_bounds__(256, 2) gqa_xt_kernel(const float* __restrict_
             }
         }
     }
+}
+
+int gqa_splits(int T, int KV, int ns, bool turbo) {
+    // T <= 2 (and turbo) run two workgroups per CU; the four-token kernel runs one, so beyond one workgroup per CU
+    // extra splits only add per-workgroup set-up and partials
+    if (turbo || T <= 2) return ns;
+    static const int cus = [] {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            return v;
+        return 256;
+    }();
+    const int fill = cus / (KV * ((T + 3) / 4));
+    return fill < 1 ? 1 : (fill < ns ? fill : ns);
 }
 
 void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part, int T,

@@ -58,3 +58,16 @@ def test_product_never_uses_the_oracle():
     import moex_amd
     if os.path.exists(moex_amd.LIB_PATH):
         assert b"liboracle" not in open(moex_amd.LIB_PATH, "rb").read()
+
+
+def test_gqa_splits_policy():
+    """moex_attn_decode keeps ns for one or two query tokens and fills one workgroup per CU (256 on MI355X, the
+    fallback without a device) per four-token group beyond that, never above the caller's ns"""
+    import moex_amd as M
+    assert M.gqa_splits(1, 2, 256) == 256
+    assert M.gqa_splits(2, 2, 256) == 256
+    assert M.gqa_splits(4, 2, 256) == 128
+    assert M.gqa_splits(8, 2, 256) == 64
+    assert M.gqa_splits(4, 2, 32) == 32
+    assert M.gqa_splits(4, 2, 256, turbo=1) == 256
+    assert M.gqa_splits(64, 2, 256) == 8
