@@ -1,8 +1,10 @@
 // Split-K GQA decode / MTP-verify attention on gfx950 (replaces attn_gqa_k, kernels.cuh:1740-1844).
 //
-// One workgroup = (kv head, key split, group of query tokens), 4 wavefronts; the 8 query heads of the group share
-// every K/V byte. gqa_x_kernel serves the int8 cache, gqa_xt_kernel the TurboQuant cache (the same design with the
-// codes unpacked on the way). The partial written per (token, head, split) is {m (log2 units), l, acc[256]}.
+// One workgroup = (kv head, key split, group of query tokens); the 8 query heads of the group share every K/V byte.
+// int8 cache: gqa_ws_kernel for a single query token (warp-specialised: producer wavefronts stream K/V into LDS,
+// consumer wavefronts compute), gqa_x_kernel for MTP-verify windows (2 or 4 tokens per workgroup). gqa_xt_kernel serves
+// the TurboQuant cache (gqa_x_kernel's design with the codes unpacked on the way). The partial written per (token,
+// head, split) is {m (log2 units), l, acc[256]}.
 #include "common.hpp"
 
 namespace moex {
@@ -386,6 +388,313 @@ __global__ void __launch_bounds__(256, TT <= 2 ? 2 : 1) gqa_x_kernel(const float
     }
 }
 
+// x combined with its partner lane l ^ 16 / l ^ 32 (v_permlane16/32_swap: both lanes of a pair receive both values)
+__device__ __forceinline__ float max_x16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_x32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_x16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_x32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// ---- gqa_ws_kernel: one query token (plain decode), warp-specialised. A vector-memory instruction waits at issue
+// while the CU's request queue is full, which under the chip-wide K/V stream is most of the time; a wavefront that
+// both loads and computes therefore cannot compute while its next chunk goes out. Here waves 4..7 only move rows
+// (global_load_lds: K, V and the scales of a chunk into one of two LDS stages) and waves 0..3 only compute, one per
+// SIMD. Each consumer owns 32 keys of every chunk and keeps its own running maximum, sum and O over all 256 dims, so
+// the chunk loop needs no exchange between consumers: one barrier per chunk hands a landed stage to the consumers
+// and the other stage back to the producers. The four consumer states merge once at the end.
+//   K stage: row r holds its 16-byte piece p in slot p ^ (r % 16), so the 16 lanes of a ds_read_b128 (16 rows, one
+//            piece) hit 16 different slots.
+//   V stage: as gqa_x_kernel (slot p ^ 4 * ((r / 4) % 4)).
+//   O:       16 tiles; column n of tile 4 pc + j is dim 64 pc + 4 n + j, row 2h (2h + 1) is the hi (lo) part of
+//            head h, so lane group g holds heads 2g and 2g + 1 whole. It is rescaled only when the reference maximum of a head moves by more
+//            than WS_SLACK (log2 units; P then stays below 2^WS_SLACK) or the V scale exponent grows.
+constexpr int WS_NC = 4;                              // consumer wavefronts (waves 0 .. WS_NC-1)
+constexpr int WS_NP = 4;                              // producer wavefronts (the next WS_NP waves)
+constexpr int WS_CH = 32 * WS_NC;                     // keys per chunk: 32 per consumer
+constexpr int WS_NS = 2;                              // LDS stages: one chunk streams while one is computed
+constexpr int WS_KB = WS_CH * AHD;                    // K rows of a stage; the V rows follow, then ks[128], vs[128]
+constexpr int WS_STAGE = 2 * WS_CH * AHD + 2 * 128 * 4;
+constexpr int WS_LDS = WS_NS * WS_STAGE + WS_NC * 64 * 16;  // stages + one P operand per consumer
+constexpr float WS_SLACK = 8.f;
+static_assert(WS_CH % 8 == 0 && WS_CH <= 128, "chunk shape");
+static_assert(WS_NC * GQ * AHD * 4 <= WS_STAGE, "the consumer merge fits in stage 0");
+static_assert(WS_LDS <= 160 * 1024, "LDS");
+// s_waitcnt with only vmcnt = n (expcnt, lgkmcnt left at their no-wait maxima)
+template <int n>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(n >= 0 && n < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+__global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws_kernel(const float* __restrict__ qo, moex_kv_cache kv,
+                                                                        int H, const int* __restrict__ pos_d,
+                                                                        int max_t, float* __restrict__ part, int T,
+                                                                        int ns) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ float cm[WS_NC][GQ], cl[WS_NC][GQ];
+    const int nb = gridDim.x, w_id = xcd_work_id(blockIdx.x, nb);
+    const int tok = w_id % T, s = (w_id / T) % ns, kvh = w_id / (T * ns);
+    const int pos0 = *pos_d, Tmax = pos0 + T;
+    const int L = (Tmax + ns - 1) / ns, lo = s * L;
+    const int hi = min(pos0 + tok + 1, lo + L);  // keys [lo, hi) of this split that the token sees
+    const int nch = hi > lo ? (hi - lo + WS_CH - 1) / WS_CH : 0;
+    // chunk 0 is the short one (the remainder of the split over WS_CH), so the first chunk lands soonest
+    const int first = hi > lo ? hi - lo - (nch - 1) * WS_CH : 0;
+    auto clo = [&](int c) { return c == 0 ? lo : lo + first + (c - 1) * WS_CH; };  // chunk c is keys [clo, chi)
+    auto chi = [&](int c) { return c == 0 ? lo + first : lo + first + c * WS_CH; };
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 4, m16 = lane & 15;
+    const size_t rbase = (size_t)kvh * max_t;
+
+    if (wv >= WS_NC) {
+        // ---- producers: chunk c -> stage c % WS_NS. Producers 0, 1 move the K rows, 2, 3 the V rows (WS_CH/8
+        // instructions of 4 rows each); producer j also moves 64 scales (ks for j < 2, else vs; 4 bytes a lane).
+        // Rows past the chunk repeat its last row: their P is 0. ----
+        const int pw = wv - WS_NC;
+        const int8_t* src = (pw < 2 ? kv.k : kv.v) + rbase * AHD;
+        const float* ssrc = (pw < 2 ? kv.ks : kv.vs) + rbase;
+        const int r4 = lane >> 4, sl = lane & 15;
+        auto issue = [&](int c) {
+            const int c0 = clo(c), ce = chi(c);
+            unsigned char* st = smem + (c % WS_NS) * WS_STAGE;
+            unsigned char* sb = st + (pw < 2 ? 0 : WS_KB);
+#pragma unroll
+            for (int u = 0; u < WS_CH / 8; u++) {
+                const int i = (WS_CH / 8) * (pw & 1) + u, r = 4 * i + r4;  // instruction i covers rows 4i .. 4i+3
+                const int piece = pw < 2 ? sl ^ (r & 15) : sl ^ (4 * (i & 3));
+                const int key = min(c0 + r, ce - 1);
+                __builtin_amdgcn_global_load_lds((gptr_t)(src + (size_t)key * AHD + 16 * piece), (lptr_t)(sb + i * 1024),
+                                                 16, 0, 0);
+            }
+            const int key = min(c0 + 64 * (pw & 1) + lane, ce - 1);
+            __builtin_amdgcn_global_load_lds((gptr_t)(ssrc + key),
+                                             (lptr_t)(st + 2 * WS_KB + (pw < 2 ? 0 : 512) + 256 * (pw & 1)), 4, 0, 0);
+        };
+        // One chunk in flight at a time, issued the moment a stage frees: chunks issued together are served
+        // interleaved, so a deeper queue only delays each of them (and the query the consumers wait for).
+        if (nch > 0) issue(0);
+        for (int c = 0; c < nch; c++) {
+            wait_vm<0>();     // chunk c has landed
+            __syncthreads();  // ... and the consumers are done with chunk c - 1: its stage takes chunk c + 1
+            if (c + 1 < nch) issue(c + 1);
+        }
+        __syncthreads();
+        __syncthreads();
+    } else {
+        // ---- consumers. Query digits in registers: column m16 of the Q.K MFMA is head m16 / 2 (every head twice);
+        // lane (g, m16) holds dims 64 ks + 16 g .. +15 of it, the 4 lanes of a column together hold its 256 dims ----
+        int4_t_ qd[3][4];
+        float qs;
+        {
+            const float* qrow = qo + ((size_t)tok * H + kvh * GQ + (m16 >> 1)) * AHD + 16 * g;
+            float4 qv4[16];
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+                for (int u = 0; u < 4; u++) qv4[4 * ks + u] = *reinterpret_cast<const float4*>(qrow + 64 * ks + 4 * u);
+            float qm = 0.f;
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                qm = fmaxf(fmaxf(qm, fmaxf(fabsf(qv4[u].x), fabsf(qv4[u].y))), fmaxf(fabsf(qv4[u].z), fabsf(qv4[u].w)));
+            qm = fmaxf(qm, __shfl_xor(qm, 16));
+            qm = fmaxf(qm, __shfl_xor(qm, 32));
+            int e = 0;
+            if (qm > 0.f) (void)frexpf(qm, &e);  // qm < 2^e
+            const float up = ldexpf(1.f, 22 - e);
+            qs = ldexpf(1.f, e - 22) * SL2;
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const float4 x = qv4[4 * ks + u];
+                    int d[3][4];
+                    digits3((int)__builtin_rintf(x.x * up), d[2][0], d[1][0], d[0][0]);
+                    digits3((int)__builtin_rintf(x.y * up), d[2][1], d[1][1], d[0][1]);
+                    digits3((int)__builtin_rintf(x.z * up), d[2][2], d[1][2], d[0][2]);
+                    digits3((int)__builtin_rintf(x.w * up), d[2][3], d[1][3], d[0][3]);
+#pragma unroll
+                    for (int dig = 0; dig < 3; dig++)
+                        qd[dig][ks][u] = (int)pack_bytes(d[dig][0], d[dig][1], d[dig][2], d[dig][3]);
+                }
+        }
+        half8_t* Plw = reinterpret_cast<half8_t*>(smem + WS_NS * WS_STAGE) + 64 * wv;
+        float4_t o[16];
+#pragma unroll
+        for (int J = 0; J < 16; J++) o[J] = float4_t{0.f, 0.f, 0.f, 0.f};
+        float mref = -INFINITY, lacc = 0.f, vmax = 0.f;  // reference maximum and sum of column m16, V-scale maximum
+        int sig = 0;                                      // O is held times 2^sig
+        const int kb = 32 * wv;                           // this consumer's keys kb .. kb+31 of every chunk
+        for (int c = 0; c < nch; c++) {
+            __syncthreads();  // chunk c is in stage c % WS_NS
+            const int c0 = clo(c), ce = chi(c);
+            if (c0 + kb >= ce) continue;
+            const unsigned char* sb = smem + (c % WS_NS) * WS_STAGE;
+            const float* sks = reinterpret_cast<const float*>(sb + 2 * WS_KB);
+            const float* svs = sks + 128;
+            float ksv[8], vv[8];
+            {
+                const float4 a0 = *reinterpret_cast<const float4*>(sks + kb + 4 * g);
+                const float4 a1 = *reinterpret_cast<const float4*>(sks + kb + 16 + 4 * g);
+                const float4 b0 = *reinterpret_cast<const float4*>(svs + kb + 4 * g);
+                const float4 b1 = *reinterpret_cast<const float4*>(svs + kb + 16 + 4 * g);
+                ksv[0] = a0.x; ksv[1] = a0.y; ksv[2] = a0.z; ksv[3] = a0.w;
+                ksv[4] = a1.x; ksv[5] = a1.y; ksv[6] = a1.z; ksv[7] = a1.w;
+                vv[0] = b0.x; vv[1] = b0.y; vv[2] = b0.z; vv[3] = b0.w;
+                vv[4] = b1.x; vv[5] = b1.y; vv[6] = b1.z; vv[7] = b1.w;
+            }
+            // ---- scores of keys kb + 16 (j / 4) + 4 g + j % 4 for column m16: the 24 MFMAs (6 independent chains)
+            // go out before any score is formed ----
+            int4_t_ acc[2][3];
+#pragma unroll
+            for (int grp = 0; grp < 2; grp++)
+#pragma unroll
+                for (int dig = 0; dig < 3; dig++) acc[grp][dig] = int4_t_{0, 0, 0, 0};
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+                for (int grp = 0; grp < 2; grp++) {
+                    const int4_t_ a = *reinterpret_cast<const int4_t_*>(sb + (kb + 16 * grp + m16) * AHD + 16 * ((4 * ks + g) ^ m16));
+#pragma unroll
+                    for (int dig = 0; dig < 3; dig++)
+                        acc[grp][dig] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qd[dig][ks], acc[grp][dig], 0, 0, 0);
+                }
+            float sc[8];
+#pragma unroll
+            for (int grp = 0; grp < 2; grp++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float raw = ((float)acc[grp][2][i] * 65536.f + (float)acc[grp][1][i] * 256.f) + (float)acc[grp][0][i];
+                    sc[4 * grp + i] = raw * (ksv[4 * grp + i] * qs);
+                }
+            float vm;
+            if (c0 + kb + 32 <= ce) {  // all 32 keys valid (every chunk but the first)
+                vm = fmaxf(fmaxf(fmaxf(vv[0], vv[1]), fmaxf(vv[2], vv[3])), fmaxf(fmaxf(vv[4], vv[5]), fmaxf(vv[6], vv[7])));
+            } else {
+                vm = 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const bool ok = c0 + kb + 16 * (j >> 2) + 4 * g + (j & 3) < ce;
+                    sc[j] = ok ? sc[j] : -INFINITY;
+                    vm = ok ? fmaxf(vm, vv[j]) : vm;
+                }
+            }
+            float M = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+            M = max_x32(max_x16(M));   // over the 4 lane groups: the wave's 32 keys
+            vm = max_x32(max_x16(vm));  // every column of a lane group holds the same keys
+            // ---- lazy rescale: new reference maximum / V-scale exponent ----
+            const float nref = M > mref + WS_SLACK ? M : mref;
+            const float fown = ex2d(mref, nref);
+            vmax = fmaxf(vmax, vm);
+            int ev = 0;
+            if (vmax > 0.f) (void)frexpf(vmax, &ev);  // vmax < 2^ev: p * vs * 2^(7 - ev) < 2^(7 + WS_SLACK)
+            const int nsig = 7 - ev;
+            if (__builtin_amdgcn_ballot_w64(fown != 1.f) != 0 || nsig != sig) {
+                const float sf = ldexpf(1.f, nsig - sig);
+                float fr[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) fr[i] = __shfl(fown, 2 * (2 * g + (i >> 1))) * sf;
+#pragma unroll
+                for (int J = 0; J < 16; J++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) o[J][i] *= fr[i];
+                lacc *= fown;
+                mref = nref;
+                sig = nsig;
+            }
+            // ---- P = 2^(s - mref) * vs * 2^sig as fp16 hi + lo: row 2h + 1 of the P operand is the lo part of row 2h,
+            // written by the lane pair m16 = 2h (hi), 2h + 1 (lo) ----
+            {
+                const float vsc = ldexpf(1.f, sig);
+                half8_t ph;
+                float ls = 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float p = fast_exp2(sc[j] - mref);  // 0 for masked keys (mref is finite once a key is seen)
+                    ls += p;
+                    const float x = p * (vv[j] * vsc);
+                    const _Float16 h = (_Float16)x;
+                    ph[j] = (m16 & 1) ? (_Float16)(x - (float)h) : h;
+                }
+                lacc += ls;
+                Plw[16 * g + m16] = ph;
+            }
+            // ---- O^T += P . V over this consumer's 32 keys, all 256 dims ----
+            const half8_t pa = Plw[lane];
+            const unsigned char* Vs = sb + WS_KB;
+#pragma unroll
+            for (int pc = 0; pc < 4; pc++) {
+                const int rd = 16 * ((4 * pc + (m16 >> 2)) ^ (4 * g)) + 4 * (m16 & 3);
+                uint32_t r[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    r[j] = *reinterpret_cast<const uint32_t*>(Vs + (kb + 16 * (j >> 2) + 4 * g + (j & 3)) * AHD + rd);
+                uint32_t c0v[4], c1v[4];
+                tr4x4_(r[0], r[1], r[2], r[3], c0v);
+                tr4x4_(r[4], r[5], r[6], r[7], c1v);
+#pragma unroll
+                for (int jt = 0; jt < 4; jt++)
+                    o[4 * pc + jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, i8x8_to_h8(c0v[jt], c1v[jt]), o[4 * pc + jt], 0, 0, 0);
+            }
+        }
+        // ---- merge the four consumers: m, l per head, then O rows scaled to the common maximum ----
+        const float l = sum_x32(sum_x16(lacc));
+        __syncthreads();  // every consumer is past its last chunk: stage 0 is free
+        if (lane < 16 && !(lane & 1)) { cm[wv][lane >> 1] = mref; cl[wv][lane >> 1] = l; }
+        __syncthreads();
+        // rows 4g .. 4g+3 of the O tiles are hi, lo of head 2g and hi, lo of head 2g + 1
+        float* Ow = reinterpret_cast<float*>(smem);  // [consumer][head][256]
+        const float un = ldexpf(1.f, -sig);
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const int h = 2 * g + e;
+            float Mh = cm[0][h];
+#pragma unroll
+            for (int w = 1; w < WS_NC; w++) Mh = fmaxf(Mh, cm[w][h]);
+            const float f = ex2d(cm[wv][h], Mh) * un;
+#pragma unroll
+            for (int pc = 0; pc < 4; pc++)
+                *reinterpret_cast<float4*>(Ow + (wv * GQ + h) * AHD + 64 * pc + 4 * m16) =
+                    make_float4((o[4 * pc][2 * e] + o[4 * pc][2 * e + 1]) * f,
+                                (o[4 * pc + 1][2 * e] + o[4 * pc + 1][2 * e + 1]) * f,
+                                (o[4 * pc + 2][2 * e] + o[4 * pc + 2][2 * e + 1]) * f,
+                                (o[4 * pc + 3][2 * e] + o[4 * pc + 3][2 * e + 1]) * f);
+        }
+    }
+    __syncthreads();
+    // ---- partial of the split: item = (head, dims 4 (item % 64) .. +3) ----
+    for (int it = tid; it < GQ * 64; it += 64 * (WS_NC + WS_NP)) {
+        const float* Ow = reinterpret_cast<const float*>(smem);
+        const int h = it >> 6, d4 = 4 * (it & 63);
+        float4 a = *reinterpret_cast<const float4*>(Ow + h * AHD + d4);
+#pragma unroll
+        for (int w = 1; w < WS_NC; w++) {
+            const float4 b = *reinterpret_cast<const float4*>(Ow + (w * GQ + h) * AHD + d4);
+            a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+        }
+        *reinterpret_cast<float4*>(part_acc(part, tok, kvh * GQ + h, s, H, ns) + d4) = a;
+        if ((it & 63) == 0) {
+            float Mh = cm[0][h], lh = 0.f;
+#pragma unroll
+            for (int w = 1; w < WS_NC; w++) Mh = fmaxf(Mh, cm[w][h]);
+#pragma unroll
+            for (int w = 0; w < WS_NC; w++) lh += cl[w][h] * ex2d(cm[w][h], Mh);
+            float* ml = part_ml(part, tok, kvh * GQ + h, s, H, ns, T);
+            ml[0] = Mh;  // -inf when the token has no key in this split
+            ml[1] = lh;
+        }
+    }
+}
+
 template <int TT>
 static void launch_x(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part,
                      int T, int ns, hipStream_t st) {
@@ -704,9 +1013,9 @@ __global__ void __launch_bounds__(256, 2) gqa_xt_kernel(const float* __restrict_
 }
 
 int gqa_splits(int T, int KV, int ns, bool turbo) {
-    // T <= 2 (and turbo) run two workgroups per CU; the four-token kernel runs one, so beyond one workgroup per CU
-    // extra splits only add per-workgroup set-up and partials
-    if (turbo || T <= 2) return ns;
+    // T = 2 (and turbo) run two workgroups per CU; the one-token and four-token kernels run one, so beyond one
+    // workgroup per CU extra splits only add per-workgroup set-up and partials
+    if (turbo || T == 2) return ns;
     static const int cus = [] {
         int dev = 0, v = 0;
         if (hipGetDevice(&dev) == hipSuccess &&
@@ -714,7 +1023,7 @@ int gqa_splits(int T, int KV, int ns, bool turbo) {
             return v;
         return 256;
     }();
-    const int fill = cus / (KV * ((T + 3) / 4));
+    const int fill = cus / (KV * (T == 1 ? 1 : (T + 3) / 4));
     return fill < 1 ? 1 : (fill < ns ? fill : ns);
 }
 
@@ -729,7 +1038,15 @@ void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos
         (void)once;
         hipLaunchKernelGGL(gqa_xt_kernel, dim3(KV * ns * T), dim3(256), XT_LDS, st, qo, kv, H, pos_d, max_t, part, T, ns);
     } else {
-        if (T == 1) launch_x<1>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
+        if (T == 1) {
+            static bool once = [] {
+                MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_ws_kernel),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, WS_LDS));
+                return true;
+            }();
+            (void)once;
+            hipLaunchKernelGGL(gqa_ws_kernel, dim3(KV * ns), dim3(64 * (WS_NC + WS_NP)), WS_LDS, st, qo, kv, H, pos_d, max_t, part, T, ns);
+        }
         else if (T == 2) launch_x<2>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
         else launch_x<4>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
     }

@@ -210,6 +210,8 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
     const float* acc_rows = part_acc(pp, tok, h, 0, H, ns);
     const float2* ml = reinterpret_cast<const float2*>(part_ml(pp, tok, h, 0, H, ns, T));
     const int dl = tid % CDW, gi = tid / CDW, d = blockIdx.z * CDW + dl;
+    // the gate goes out with the partials rather than after the merge
+    const float gt = (q_gate && tid < CDW) ? q_gate[(size_t)tok * ld + h * 2 * AHD + AHD + d] : 0.f;
     float mt = -INFINITY, lt = 0.f, at = 0.f;
     for (int s0 = gi; s0 < ns; s0 += 16 * CNG) {
         float2 q[16];
@@ -250,7 +252,7 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
         acc += sa[g][tid] * f;
     }
     float x = acc / l;
-    if (q_gate) x = x / (1.f + __expf(-q_gate[(size_t)tok * ld + h * 2 * AHD + AHD + d]));
+    if (q_gate) x = x / (1.f + __expf(-gt));
     out[((size_t)tok * H + h) * AHD + d] = x;
 }
 

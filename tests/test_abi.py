@@ -61,10 +61,10 @@ def test_product_never_uses_the_oracle():
 
 
 def test_gqa_splits_policy():
-    """moex_attn_decode keeps ns for one or two query tokens and fills one workgroup per CU (256 on MI355X, the
-    fallback without a device) per four-token group beyond that, never above the caller's ns"""
+    """moex_attn_decode keeps ns for two query tokens (two workgroups per CU) and otherwise fills one workgroup per
+    CU (256 on MI355X, the fallback without a device) per token or four-token group, never above the caller's ns"""
     import moex_amd as M
-    assert M.gqa_splits(1, 2, 256) == 256
+    assert M.gqa_splits(1, 2, 256) == 128
     assert M.gqa_splits(2, 2, 256) == 256
     assert M.gqa_splits(4, 2, 256) == 128
     assert M.gqa_splits(8, 2, 256) == 64

@@ -17,7 +17,8 @@ TOL = 1e-4
 # the MTP-verify windows also cover: a chunk boundary between the tokens' last keys (254, 4, 1), splits where the
 # group's first tokens have no key (3, 4, 16), a partial token group (130, 3, 2) and groups of 4, 4, 1 (777, 9, 7)
 CASES = [(0, 1, 16), (3, 1, 16), (1000, 2, 16), (26000, 1, 64), (5000, 4, 32), (777, 9, 7), (89999, 1, 256),
-         (89996, 4, 256), (254, 4, 1), (3, 4, 16), (130, 3, 2), (2000, 2, 64), (89997, 3, 256)]
+         (89996, 4, 256), (254, 4, 1), (3, 4, 16), (130, 3, 2), (2000, 2, 64), (89997, 3, 256), (255, 1, 2),
+         (127, 1, 1), (40000, 1, 1)]
 
 
 @pytest.fixture(scope="module")
