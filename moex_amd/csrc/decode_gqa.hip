@@ -2,9 +2,9 @@
 //
 // One workgroup = (kv head, key split, group of query tokens); the 8 query heads of the group share every K/V byte.
 // int8 cache: gqa_ws_kernel for a single query token (warp-specialised: producer wavefronts stream K/V into LDS,
-// consumer wavefronts compute), gqa_x_kernel for MTP-verify windows (2 or 4 tokens per workgroup). gqa_xt_kernel serves
-// the TurboQuant cache (gqa_x_kernel's design with the codes unpacked on the way). The partial written per (token,
-// head, split) is {m (log2 units), l, acc[256]}.
+// consumer wavefronts compute), gqa_wsp_kernel for MTP-verify windows (token pairs on the same pipeline). gqa_xt_kernel
+// serves the TurboQuant cache (one token; 4 wavefronts that load and compute, the codes unpacked on the way). The
+// partial written per (token, head, split) is {m (log2 units), l, acc[256]}.
 #include "common.hpp"
 
 namespace moex {
@@ -24,15 +24,15 @@ __device__ __forceinline__ int xcd_work_id(int b, int nb) {
 }  // namespace
 
 // ---------------------------------------------------------------------------------------------------------------
-// int8 KV (gqa_x_kernel below). Q.K runs on v_mfma_i32_16x16x64_i8 with the raw int8 K bytes as operands: the fp32
-// query enters as 24-bit fixed point in three signed base-256 digits (x = d2*2^16 + d1*2^8 + d0, each digit in
-// [-128, 127]), every digit product is accumulated exactly in int32 and the digits are recombined in fp32, so the
-// scores keep fp32-level precision (the reference decode is fp32).
-//   Q.K:  16 keys x 16 columns per MFMA; column m < 8 = digit 2 of head m, m >= 8 = digit 1 of head m-8, a second
-//         MFMA holds digit 0 of the 8 heads. Lane (g = lane/16, m = lane%16) receives keys 4g + i of the group for
-//         column m; the digits of a head are brought together with two row_ror:8 DPP moves.
-// P.V runs on fp16 MFMA (see gqa_x_kernel). Each chunk first computes all its scores and their maximum (pass 1), then
-// forms P (pass 1.5) and accumulates P.V (pass 2).
+// Q.K runs on v_mfma_i32_16x16x64_i8 with the raw int8 K bytes (or the signed turbo K codes) as the A operand: the
+// fp32 query enters as 24-bit fixed point in three signed base-256 digits (x = d2*2^16 + d1*2^8 + d0, each digit in
+// [-128, 127]), every digit product accumulated exactly in int32 and the digits recombined in fp32, so the scores keep
+// fp32-level precision (the reference decode is fp32). The int8 kernels give each digit its own MFMA per 64 dims with
+// column m of the B operand one (token, head) of the query: the lane that receives the score of (key, column m)
+// recombines it from its three accumulators. The turbo kernel packs digits 2 and 1 of the 8 heads into the 16 columns
+// of one MFMA and digit 0 into a second, and brings a head's digits together with two row_ror:8 DPP moves.
+// P.V runs on v_mfma_f32_16x16x32_f16: P = p * vs * 2^sig is split into fp16 hi + lo (~22 bits), V widened exactly to
+// fp16, fp32 accumulation.
 constexpr int ICH = 128;                           // keys per chunk: 32 keys (two 16-key groups) per wavefront
 typedef int int4_t_ __attribute__((ext_vector_type(4)));
 
@@ -57,336 +57,13 @@ __device__ __forceinline__ void tr4x4_(const uint32_t r0, const uint32_t r1, con
 typedef __attribute__((address_space(1))) const void* gptr_t;
 typedef __attribute__((address_space(3))) void* lptr_t;
 
-// One workgroup per (kv head, split, group of TT query tokens), walking the split in chunks of ICH keys with the
-// loads of chunk c+1 in flight while chunk c is computed: the V rows go straight to LDS (global_load_lds_dwordx4,
-// double buffered, 16-byte pieces XOR-swizzled by key/4 so the pass-2 reads of the four lane groups hit disjoint
-// banks), the K rows and the scales to registers (two buffers that swap roles every chunk). Every K/V byte of the
-// chunk serves all TT tokens of the group (MTP verify windows): per token only the MFMAs, the scores and P are
-// repeated. TT = 1 runs two workgroups per CU; TT > 1 holds TT tokens' scores and accumulators (and reads the query
-// digits from LDS) and runs one workgroup per CU.
 constexpr int I8_VBUF = ICH * AHD;                 // 32 KB per V buffer
 constexpr int I8_QL = 2 * 4 * 64 * 16;             // Q digit operands of one token
 static_assert(I8_QL <= I8_VBUF, "query digits of one token stage in V buffer 1");
 // 2^(a - b) with 2^(-inf - -inf) = 1 (a running maximum that has not moved, also while it is still -inf)
 __device__ __forceinline__ float ex2d(float a, float b) { return a == b ? 1.f : fast_exp2(a - b); }
 
-// ---- gqa_x_kernel: Q.K on the int8 MFMA (as gqa_i8_kernel: exact int32 products of the int8 K rows with the
-// query's three base-256 digits), P.V on v_mfma_f32_16x16x32_f16 with fp32 accumulation:
-//   P.V:  A = P, 16 rows (hi parts of the 8 heads, then lo parts: p * vs * 2^sig = hi + lo in fp16, ~22 bits) x 32
-//         keys (a wavefront's keys; lane group g takes keys 4g..4g+3 of both 16-key groups, which is where the Q.K
-//         output layout left them); B = V widened exactly to fp16; output column n of tile j is dim 64*wv + 4n + j,
-//         so each lane reads one dword (4 dims) per key.
-// O stays in the MFMA accumulators across chunks (rescaled by 2^(m_old - m_new) times the change of the per-chunk power
-// of two 2^sig), so a chunk costs no int32 -> fp32 fold and the per-token work is only the MFMAs, the scores and P.
 constexpr int X_PL = 4 * 64 * 16;  // P operands of one token per chunk: [step = wavefront][lane] half8
-// Query-token pairs share the Q.K MFMAs: column m of the B operand is (token 2pp + m/8, head m%8) of pair pp, and
-// the three base-256 digits of the query are three MFMAs, so a lane recombines the score of its own (token, head)
-// from three accumulators without lane exchanges (TT = 1 leaves columns 8..15 as a copy of token 0).
-template <int TT>
-constexpr int x_np() { return (TT + 1) / 2; }
-template <int TT>
-constexpr int x_lds() { return 2 * I8_VBUF + TT * X_PL + (TT > 2 ? x_np<TT>() * 3 * 4 * 64 * 16 : 0); }
-static_assert(3 * 4 * 64 * 16 <= I8_VBUF, "one token pair's query digits stage in V buffer 1");
-
-template <int TT>
-__global__ void __launch_bounds__(256, TT <= 2 ? 2 : 1) gqa_x_kernel(const float* __restrict__ qo, moex_kv_cache kv,
-                                                                     int H, const int* __restrict__ pos_d, int max_t,
-                                                                     float* __restrict__ part, int T, int ns) {
-    constexpr int NP = x_np<TT>(), TE = 2 * NP;  // token pairs, token slots (TT = 1: slot 1 copies token 0)
-    constexpr bool QREG = TT <= 2;               // query digits in registers (else re-read from LDS)
-    extern __shared__ __align__(16) unsigned char smem[];
-    half8_t* Pl = reinterpret_cast<half8_t*>(smem + 2 * I8_VBUF);  // [TT][4][64]
-    int4_t_* Ql = reinterpret_cast<int4_t_*>(QREG ? smem + I8_VBUF : smem + 2 * I8_VBUF + TT * X_PL);  // [NP][3][4][64]
-    __shared__ float mxw[TE][4][GQ], lsum[TE][4][GQ], vmw[4], qsc_s[TE][GQ];
-    const int nb = gridDim.x, w_id = xcd_work_id(blockIdx.x, nb);
-    const int ngr = (T + TT - 1) / TT;
-    const int tg = w_id % ngr, s = (w_id / ngr) % ns, kvh = w_id / (ngr * ns);
-    const int tb = tg * TT, ntok = min(TT, T - tb);
-    const int pos0 = *pos_d, Tmax = pos0 + T;
-    const int L = (Tmax + ns - 1) / ns, lo = s * L;
-    const int hi = min(pos0 + tb + ntok, lo + L);  // keys of the group's last token; token t sees [lo, hit[t])
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 4, m16 = lane & 15, hq = m16 & 7;
-    const int tp = m16 >> 3;                       // this lane's token within each pair
-    int hitl[NP];                                  // key bound of this lane's token of each pair
-#pragma unroll
-    for (int pp = 0; pp < NP; pp++) hitl[pp] = min(pos0 + tb + min(2 * pp + tp, ntok - 1) + 1, lo + L);
-    const size_t rbase = (size_t)kvh * max_t;
-    const int8_t* Kg = kv.k + rbase * AHD;
-    const int8_t* Vg = kv.v + rbase * AHD;
-    const float* ksg = kv.ks + rbase;
-    const float* vsg = kv.vs + rbase;
-    const int nch = hi > lo ? (hi - lo + ICH - 1) / ICH : 0;
-
-    // ---- loaders. V: thread tid moves 16-byte piece (tid%16) ^ (4*wv) of key 16*it + tid/16 into LDS slot tid%16
-    // (the swizzle depends on (key/4)%4 = wv only). K: this wavefront's keys c0 + 32*wv + 16*grp + m16, dims
-    // 64*ks + 16g + 0..15; scales of the keys 16*grp + 4g + i its lane scores. ----
-    const int8_t* vsrc = Vg + 16 * ((tid & 15) ^ (4 * wv));
-    auto issue_v = [&](unsigned char* buf, int c0) {
-        const int nk = min(ICH, hi - c0);
-        if (nk == ICH) {
-            const int8_t* p = vsrc + (size_t)(c0 + (tid >> 4)) * AHD;
-#pragma unroll
-            for (int it = 0; it < ICH / 16; it++)
-                __builtin_amdgcn_global_load_lds((gptr_t)(p + it * 16 * AHD), (lptr_t)(buf + (it * 256 + 64 * wv) * 16), 16, 0, 0);
-        } else {
-            const int nit = (nk + 15) >> 4;
-            for (int it = 0; it < nit; it++) {
-                const int t = min(c0 + 16 * it + (tid >> 4), hi - 1);
-                __builtin_amdgcn_global_load_lds((gptr_t)(vsrc + (size_t)t * AHD), (lptr_t)(buf + (it * 256 + 64 * wv) * 16), 16, 0, 0);
-            }
-        }
-    };
-    auto issue_k = [&](int4_t_ (&kd)[2][4], float (&ksd)[8], float (&vsd)[8], int c0) {
-        const int k0 = c0 + 32 * wv;
-        if (k0 >= hi) return;
-        if (k0 + 32 <= hi) {
-            const int8_t* kp = Kg + (size_t)(k0 + m16) * AHD + 16 * g;
-#pragma unroll
-            for (int grp = 0; grp < 2; grp++)
-#pragma unroll
-                for (int ks = 0; ks < 4; ks++) kd[grp][ks] = *reinterpret_cast<const int4_t_*>(kp + grp * 16 * AHD + 64 * ks);
-#pragma unroll
-            for (int grp = 0; grp < 2; grp++) {
-                const float4 a = *reinterpret_cast<const float4*>(ksg + k0 + 16 * grp + 4 * g);
-                const float4 b = *reinterpret_cast<const float4*>(vsg + k0 + 16 * grp + 4 * g);
-                ksd[4 * grp] = a.x; ksd[4 * grp + 1] = a.y; ksd[4 * grp + 2] = a.z; ksd[4 * grp + 3] = a.w;
-                vsd[4 * grp] = b.x; vsd[4 * grp + 1] = b.y; vsd[4 * grp + 2] = b.z; vsd[4 * grp + 3] = b.w;
-            }
-        } else {
-#pragma unroll
-            for (int grp = 0; grp < 2; grp++) {
-                const int8_t* kp = Kg + (size_t)min(k0 + 16 * grp + m16, hi - 1) * AHD + 16 * g;
-#pragma unroll
-                for (int ks = 0; ks < 4; ks++) kd[grp][ks] = *reinterpret_cast<const int4_t_*>(kp + 64 * ks);
-            }
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int t = min(k0 + 16 * (j >> 2) + 4 * g + (j & 3), hi - 1);
-                ksd[j] = ksg[t]; vsd[j] = vsg[t];
-            }
-        }
-    };
-    int4_t_ kA[2][4], kB[2][4];
-    float ksA[8], vsA[8], ksB[8], vsB[8];
-    if (nch > 0) {
-        issue_k(kA, ksA, vsA, lo);
-        issue_v(smem, lo);
-    }
-
-    // ---- query digits, once per workgroup: thread = (head tid/32, dims 8*(tid%32) .. +7), per token slot; slot t
-    // goes to pair t/2, column 8*(t%2) + head ----
-#pragma unroll
-    for (int t = 0; t < TE; t++) {
-        const int h = tid >> 5, d0 = (tid & 31) * 8;
-        const float* qrow = qo + ((size_t)(tb + min(t, ntok - 1)) * H + kvh * GQ + h) * AHD + d0;
-        const float4 x0 = reinterpret_cast<const float4*>(qrow)[0], x1 = reinterpret_cast<const float4*>(qrow)[1];
-        const float qv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-        float qm = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; j++) qm = fmaxf(qm, fabsf(qv[j]));
-#pragma unroll
-        for (int o = 1; o < 32; o <<= 1) qm = fmaxf(qm, __shfl_xor(qm, o));
-        int e = 0;
-        if (qm > 0.f) (void)frexpf(qm, &e);  // qm < 2^e
-        const float up = ldexpf(1.f, 22 - e);
-        if ((tid & 31) == 0) qsc_s[t][h] = ldexpf(1.f, e - 22) * SL2;
-        int dg[3][8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) digits3((int)__builtin_rintf(qv[j] * up), dg[2][j], dg[1][j], dg[0][j]);
-        // B operand: MFMA (digit, ks), lane 16g + m holds dims 64ks + 16g + 0..15 of column m
-        const int ks = d0 >> 6, gg = (d0 >> 4) & 3, jb = d0 & 15, col = 8 * (t & 1) + h;
-#pragma unroll
-        for (int dig = 0; dig < 3; dig++) {
-            unsigned char* qd = reinterpret_cast<unsigned char*>(Ql + (((t >> 1) * 3 + dig) * 4 + ks) * 64);
-            *reinterpret_cast<uint2*>(qd + (16 * gg + col) * 16 + jb) =
-                make_uint2(pack_bytes(dg[dig][0], dg[dig][1], dg[dig][2], dg[dig][3]),
-                           pack_bytes(dg[dig][4], dg[dig][5], dg[dig][6], dg[dig][7]));
-        }
-    }
-    __syncthreads();
-    int4_t_ qd[QREG ? 3 : 1][4];  // pair 0's digits (TT <= 2)
-    float qs[NP];
-#pragma unroll
-    for (int pp = 0; pp < NP; pp++) qs[pp] = qsc_s[2 * pp + tp][hq];
-    if (QREG) {
-#pragma unroll
-        for (int dig = 0; dig < 3; dig++)
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) qd[dig][ks] = Ql[(dig * 4 + ks) * 64 + lane];
-    }
-
-    float4_t o[TT][4];              // O^T tiles j: lane (g, m16) holds rows 4g + i, column m16
-    float m4[TT][4];                // running max of heads 4(g&1)+i, per token
-    float mo[NP], lacc[NP];         // running max and partial sum of this lane's (token, head) of each pair
-#pragma unroll
-    for (int t = 0; t < TT; t++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) { m4[t][i] = -INFINITY; o[t][i] = float4_t{0.f, 0.f, 0.f, 0.f}; }
-#pragma unroll
-    for (int pp = 0; pp < NP; pp++) { mo[pp] = -INFINITY; lacc[pp] = 0.f; }
-    int sig_ref = 0;  // O is held times 2^sig_ref
-    const int rd = 16 * ((4 * wv + (m16 >> 2)) ^ (4 * g)) + 4 * (m16 & 3);  // swizzled byte offset of my V dims
-
-    auto chunk = [&](int c, const int4_t_ (&kr)[2][4], const float (&ksv)[8], const float (&vv)[8],
-                     int4_t_ (&kn)[2][4], float (&ksn)[8], float (&vn)[8]) __attribute__((always_inline)) {
-        const int c0 = lo + c * ICH, nk = min(ICH, hi - c0), nsteps = (nk + 31) >> 5;
-        const int k0 = c0 + 32 * wv;
-        const bool has = k0 < hi;
-        const unsigned char* Vs = smem + (c & 1) * I8_VBUF;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // chunk c's K, scales and V rows have landed
-        __syncthreads();                                   // ... for every wavefront; chunk c-1 is done with LDS
-        if (c + 1 < nch) {                                 // all loads of chunk c+1 go out now
-            issue_k(kn, ksn, vn, c0 + ICH);
-            issue_v(smem + ((c + 1) & 1) * I8_VBUF, c0 + ICH);
-        }
-        // ---- pass 1: scores of this wavefront's 32 keys, one (token, head) per lane and pair ----
-        float sc[NP][8];
-        float vm = 0.f;
-#pragma unroll
-        for (int pp = 0; pp < NP; pp++)
-#pragma unroll
-            for (int j = 0; j < 8; j++) sc[pp][j] = -INFINITY;
-        if (has) {
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-                if (k0 + 16 * (j >> 2) + 4 * g + (j & 3) < hi) vm = fmaxf(vm, vv[j]);
-#pragma unroll
-            for (int pp = 0; pp < NP; pp++)
-#pragma unroll
-                for (int grp = 0; grp < 2; grp++) {
-                    int4_t_ acc[3] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
-#pragma unroll
-                    for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-                        for (int dig = 0; dig < 3; dig++) {
-                            const int4_t_ b = QREG ? qd[dig][ks] : Ql[((pp * 3 + dig) * 4 + ks) * 64 + lane];
-                            acc[dig] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kr[grp][ks], b, acc[dig], 0, 0, 0);
-                        }
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float raw = ((float)acc[2][i] * 65536.f + (float)acc[1][i] * 256.f) + (float)acc[0][i];
-                        const int j = 4 * grp + i, key = k0 + 16 * grp + 4 * g + i;
-                        sc[pp][j] = key < hitl[pp] ? raw * (ksv[j] * qs[pp]) : -INFINITY;
-                    }
-                }
-        }
-#pragma unroll
-        for (int pp = 0; pp < NP; pp++) {
-            float mx = sc[pp][0];
-#pragma unroll
-            for (int j = 1; j < 8; j++) mx = fmaxf(mx, sc[pp][j]);
-            mx = fmaxf(mx, __shfl_xor(mx, 16)); mx = fmaxf(mx, __shfl_xor(mx, 32));
-            if (g == 0) mxw[2 * pp + tp][wv][hq] = mx;
-        }
-#pragma unroll
-        for (int o2 = 1; o2 < 64; o2 <<= 1) vm = fmaxf(vm, __shfl_xor(vm, o2));
-        if (lane == 0) vmw[wv] = vm;
-        __syncthreads();
-        const float VM = fmaxf(fmaxf(vmw[0], vmw[1]), fmaxf(vmw[2], vmw[3]));
-        int ev = 0;
-        if (VM > 0.f) (void)frexpf(VM, &ev);  // VM < 2^ev: p * vs * 2^(10 - ev) < 2^10
-        const int sig = 10 - ev;
-        const float vsc = ldexpf(1.f, sig);
-        const float sfac = c == 0 ? 1.f : ldexpf(1.f, sig - sig_ref);  // O re-expressed at the new power of two
-        sig_ref = sig;
-        // ---- pass 1.5: P of this lane's (token, head) as hi/lo fp16 rows head / 8 + head of its token's operand ----
-#pragma unroll
-        for (int pp = 0; pp < NP; pp++) {
-            const int tl = 2 * pp + tp;
-            const float M = fmaxf(fmaxf(mxw[tl][0][hq], mxw[tl][1][hq]), fmaxf(mxw[tl][2][hq], mxw[tl][3][hq]));
-            const float mn = fmaxf(mo[pp], M);
-            float ls = 0.f;
-            if (has) {
-                half8_t ph, pl;
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const float p = mn == -INFINITY ? 0.f : fast_exp2(sc[pp][j] - mn);  // 0 for masked keys
-                    ls += p;
-                    const float x = p * (vv[j] * vsc);
-                    const _Float16 h = (_Float16)x;
-                    ph[j] = h;
-                    pl[j] = (_Float16)(x - (float)h);
-                }
-                if (tl < TT) {
-                    Pl[(tl * 4 + wv) * 64 + 16 * g + hq] = ph;
-                    Pl[(tl * 4 + wv) * 64 + 16 * g + 8 + hq] = pl;
-                }
-            }
-            lacc[pp] = lacc[pp] * ex2d(mo[pp], mn) + ls;
-            mo[pp] = mn;
-        }
-#pragma unroll
-        for (int t = 0; t < TT; t++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int h = 4 * (g & 1) + i;
-                const float Mh = fmaxf(fmaxf(mxw[t][0][h], mxw[t][1][h]), fmaxf(mxw[t][2][h], mxw[t][3][h]));
-                const float mnh = fmaxf(m4[t][i], Mh);
-                const float f = ex2d(m4[t][i], mnh) * sfac;
-                m4[t][i] = mnh;
-#pragma unroll
-                for (int jt = 0; jt < 4; jt++) o[t][jt][i] *= f;
-            }
-        __syncthreads();
-        // ---- pass 2: O^T += P . V over the chunk's steps (one per wavefront that had keys), this wavefront's dims ----
-        for (int st = 0; st < nsteps; st++) {
-            uint32_t r[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int key = 32 * st + 16 * (j >> 2) + 4 * g + (j & 3);
-                r[j] = *reinterpret_cast<const uint32_t*>(Vs + key * AHD + rd);
-            }
-            uint32_t c0v[4], c1v[4];
-            tr4x4_(r[0], r[1], r[2], r[3], c0v);
-            tr4x4_(r[4], r[5], r[6], r[7], c1v);
-            half8_t vb[4];
-#pragma unroll
-            for (int jt = 0; jt < 4; jt++) vb[jt] = i8x8_to_h8(c0v[jt], c1v[jt]);
-#pragma unroll
-            for (int t = 0; t < TT; t++) {
-                const half8_t pa = Pl[(t * 4 + st) * 64 + lane];
-#pragma unroll
-                for (int jt = 0; jt < 4; jt++) o[t][jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb[jt], o[t][jt], 0, 0, 0);
-            }
-        }
-    };
-    for (int c = 0; c < nch; c += 2) {  // two chunks per trip: the K/scale register buffers swap roles
-        chunk(c, kA, ksA, vsA, kB, ksB, vsB);
-        if (c + 1 < nch) chunk(c + 1, kB, ksB, vsB, kA, ksA, vsA);
-    }
-    // ---- partials: rows 4g+i of the O^T tiles are the hi parts (g < 2) of head 4(g&1)+i, the lo parts (g >= 2) ----
-    __syncthreads();
-#pragma unroll
-    for (int pp = 0; pp < NP; pp++) {
-        float l = lacc[pp];
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
-        if (g == 0) lsum[2 * pp + tp][wv][hq] = l;
-    }
-    __syncthreads();
-    const float unscale = ldexpf(1.f, -sig_ref);
-#pragma unroll
-    for (int t = 0; t < TT; t++) {
-        float ov[4][4];
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int jt = 0; jt < 4; jt++) ov[i][jt] = (o[t][jt][i] + __shfl_xor(o[t][jt][i], 32)) * unscale;
-        if (g < 2 && t < ntok) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int h = 4 * g + i;
-                float* p = part_acc(part, tb + t, kvh * GQ + h, s, H, ns);
-                *reinterpret_cast<float4*>(p + 64 * wv + 4 * m16) = make_float4(ov[i][0], ov[i][1], ov[i][2], ov[i][3]);
-                if (wv == 0 && m16 == 0) {
-                    float* ml = part_ml(part, tb + t, kvh * GQ + h, s, H, ns, T);
-                    ml[0] = m4[t][i];  // -inf when the token has no key in this split
-                    ml[1] = lsum[t][0][h] + lsum[t][1][h] + lsum[t][2][h] + lsum[t][3][h];
-                }
-            }
-        }
-    }
-}
 
 // x combined with its partner lane l ^ 16 / l ^ 32 (v_permlane16/32_swap: both lanes of a pair receive both values)
 __device__ __forceinline__ float max_x16(float x) {
@@ -415,7 +92,8 @@ __device__ __forceinline__ float sum_x32(float x) {
 // and the other stage back to the producers. The four consumer states merge once at the end.
 //   K stage: row r holds its 16-byte piece p in slot p ^ (r % 16), so the 16 lanes of a ds_read_b128 (16 rows, one
 //            piece) hit 16 different slots.
-//   V stage: as gqa_x_kernel (slot p ^ 4 * ((r / 4) % 4)).
+//   V stage: row r holds its 16-byte piece p in slot p ^ 4 * ((r / 4) % 4), so the four lane groups of a pass-2 read
+//            (keys 4g + i) hit disjoint banks.
 //   O:       16 tiles; column n of tile 4 pc + j is dim 64 pc + 4 n + j, row 2h (2h + 1) is the hi (lo) part of
 //            head h, so lane group g holds heads 2g and 2g + 1 whole. It is rescaled only when the reference maximum of a head moves by more
 //            than WS_SLACK (log2 units; P then stays below 2^WS_SLACK) or the V scale exponent grows.
@@ -435,6 +113,43 @@ template <int n>
 __device__ __forceinline__ void wait_vm() {
     static_assert(n >= 0 && n < 64, "vmcnt");
     __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// The producer side of gqa_ws_kernel / gqa_wsp_kernel: chunk c (keys [clo(c), chi(c)), chunk 0 the short one) ->
+// stage c % WS_NS. Producers 0, 1 move the K rows, 2, 3 the V rows (WS_CH/8 instructions of 4 rows each); producer j
+// also moves 64 scales (ks for j < 2, else vs; 4 bytes a lane). Rows past the chunk repeat its last row: their P is 0.
+// One chunk is in flight at a time, issued the moment a stage frees: chunks issued together are served interleaved,
+// so a deeper queue only delays each of them (and the query the consumers wait for). Takes part in the nch + 2
+// barriers of the chunk loop and the consumer merge.
+__device__ __forceinline__ void ws_producer(unsigned char* smem, const moex_kv_cache& kv, size_t rbase, int pw, int lane,
+                                            int lo, int first, int nch) {
+    const int8_t* src = (pw < 2 ? kv.k : kv.v) + rbase * AHD;
+    const float* ssrc = (pw < 2 ? kv.ks : kv.vs) + rbase;
+    const int r4 = lane >> 4, sl = lane & 15;
+    auto issue = [&](int c) {
+        const int c0 = c == 0 ? lo : lo + first + (c - 1) * WS_CH, ce = c == 0 ? lo + first : lo + first + c * WS_CH;
+        unsigned char* st = smem + (c % WS_NS) * WS_STAGE;
+        unsigned char* sb = st + (pw < 2 ? 0 : WS_KB);
+#pragma unroll
+        for (int u = 0; u < WS_CH / 8; u++) {
+            const int i = (WS_CH / 8) * (pw & 1) + u, r = 4 * i + r4;  // instruction i covers rows 4i .. 4i+3
+            const int piece = pw < 2 ? sl ^ (r & 15) : sl ^ (4 * (i & 3));
+            const int key = min(c0 + r, ce - 1);
+            __builtin_amdgcn_global_load_lds((gptr_t)(src + (size_t)key * AHD + 16 * piece), (lptr_t)(sb + i * 1024), 16,
+                                             0, 0);
+        }
+        const int key = min(c0 + 64 * (pw & 1) + lane, ce - 1);
+        __builtin_amdgcn_global_load_lds((gptr_t)(ssrc + key), (lptr_t)(st + 2 * WS_KB + (pw < 2 ? 0 : 512) + 256 * (pw & 1)),
+                                         4, 0, 0);
+    };
+    if (nch > 0) issue(0);
+    for (int c = 0; c < nch; c++) {
+        wait_vm<0>();     // chunk c has landed
+        __syncthreads();  // ... and the consumers are done with chunk c - 1: its stage takes chunk c + 1
+        if (c + 1 < nch) issue(c + 1);
+    }
+    __syncthreads();
+    __syncthreads();
 }
 
 __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws_kernel(const float* __restrict__ qo, moex_kv_cache kv,
@@ -457,39 +172,7 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws_kernel(const f
     const size_t rbase = (size_t)kvh * max_t;
 
     if (wv >= WS_NC) {
-        // ---- producers: chunk c -> stage c % WS_NS. Producers 0, 1 move the K rows, 2, 3 the V rows (WS_CH/8
-        // instructions of 4 rows each); producer j also moves 64 scales (ks for j < 2, else vs; 4 bytes a lane).
-        // Rows past the chunk repeat its last row: their P is 0. ----
-        const int pw = wv - WS_NC;
-        const int8_t* src = (pw < 2 ? kv.k : kv.v) + rbase * AHD;
-        const float* ssrc = (pw < 2 ? kv.ks : kv.vs) + rbase;
-        const int r4 = lane >> 4, sl = lane & 15;
-        auto issue = [&](int c) {
-            const int c0 = clo(c), ce = chi(c);
-            unsigned char* st = smem + (c % WS_NS) * WS_STAGE;
-            unsigned char* sb = st + (pw < 2 ? 0 : WS_KB);
-#pragma unroll
-            for (int u = 0; u < WS_CH / 8; u++) {
-                const int i = (WS_CH / 8) * (pw & 1) + u, r = 4 * i + r4;  // instruction i covers rows 4i .. 4i+3
-                const int piece = pw < 2 ? sl ^ (r & 15) : sl ^ (4 * (i & 3));
-                const int key = min(c0 + r, ce - 1);
-                __builtin_amdgcn_global_load_lds((gptr_t)(src + (size_t)key * AHD + 16 * piece), (lptr_t)(sb + i * 1024),
-                                                 16, 0, 0);
-            }
-            const int key = min(c0 + 64 * (pw & 1) + lane, ce - 1);
-            __builtin_amdgcn_global_load_lds((gptr_t)(ssrc + key),
-                                             (lptr_t)(st + 2 * WS_KB + (pw < 2 ? 0 : 512) + 256 * (pw & 1)), 4, 0, 0);
-        };
-        // One chunk in flight at a time, issued the moment a stage frees: chunks issued together are served
-        // interleaved, so a deeper queue only delays each of them (and the query the consumers wait for).
-        if (nch > 0) issue(0);
-        for (int c = 0; c < nch; c++) {
-            wait_vm<0>();     // chunk c has landed
-            __syncthreads();  // ... and the consumers are done with chunk c - 1: its stage takes chunk c + 1
-            if (c + 1 < nch) issue(c + 1);
-        }
-        __syncthreads();
-        __syncthreads();
+        ws_producer(smem, kv, rbase, wv - WS_NC, lane, lo, first, nch);
     } else {
         // ---- consumers. Query digits in registers: column m16 of the Q.K MFMA is head m16 / 2 (every head twice);
         // lane (g, m16) holds dims 64 ks + 16 g .. +15 of it, the 4 lanes of a column together hold its 256 dims ----
@@ -695,17 +378,262 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws_kernel(const f
     }
 }
 
-template <int TT>
-static void launch_x(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part,
-                     int T, int ns, hipStream_t st) {
+// ---- gqa_wsp_kernel<NPR>: MTP-verify windows, NPR token pairs (up to 4 tokens) per workgroup, on gqa_ws_kernel's
+// pipeline (same producers, stages and chunk order). Consumer w serves pair w % NPR and owns 32 NPR keys of every
+// chunk (part w / NPR). Column m of the Q.K MFMA is (token m / 8 of the pair, head m % 8), so one set of MFMAs scores
+// both tokens. P enters P.V as two A operands, its hi and lo fp16 parts (row = column), accumulated into the same O
+// tiles against one widened V operand: V is widened once per pair, and O (rows = (token, head)) takes 64 registers.
+constexpr int WSP_LDS = WS_NS * WS_STAGE + WS_NC * 2 * 64 * 16;  // stages + hi and lo P operands per consumer
+static_assert(WS_NC * 16 * AHD * 4 <= WS_STAGE, "the pair merge fits in stage 0");
+static_assert(WSP_LDS <= 160 * 1024, "LDS");
+
+template <int NPR>
+__global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wsp_kernel(const float* __restrict__ qo, moex_kv_cache kv,
+                                                                         int H, const int* __restrict__ pos_d,
+                                                                         int max_t, float* __restrict__ part, int T,
+                                                                         int ns) {
+    constexpr int TT = 2 * NPR, KPC = 32 * NPR;  // tokens per workgroup, keys per consumer per chunk
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ float cm[WS_NC][16], cl[WS_NC][16];
+    const int nb = gridDim.x, w_id = xcd_work_id(blockIdx.x, nb);
+    const int ngr = (T + TT - 1) / TT;
+    const int tg = w_id % ngr, s = (w_id / ngr) % ns, kvh = w_id / (ngr * ns);
+    const int tb = tg * TT, ntok = min(TT, T - tb);
+    const int pos0 = *pos_d, Tmax = pos0 + T;
+    const int L = (Tmax + ns - 1) / ns, lo = s * L;
+    const int hi = min(pos0 + tb + ntok, lo + L);  // keys [lo, hi) of this split that the group's last token sees
+    const int nch = hi > lo ? (hi - lo + WS_CH - 1) / WS_CH : 0;
+    const int first = hi > lo ? hi - lo - (nch - 1) * WS_CH : 0;  // chunk 0 is the short one
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 4, m16 = lane & 15;
+    const size_t rbase = (size_t)kvh * max_t;
+
+    if (wv >= WS_NC) {
+        ws_producer(smem, kv, rbase, wv - WS_NC, lane, lo, first, nch);
+    } else {
+        const int pr = wv % NPR;                                        // token pair
+        const bool live = 2 * pr < ntok;
+        const int tl = 2 * pr + (m16 >> 3);                             // this lane's token (column m16)
+        const int htl = min(pos0 + tb + tl + 1, lo + L);                // ... sees keys below htl
+        const int hlo = min(pos0 + tb + 2 * pr + 1, lo + L);            // keys below hlo: both tokens of the pair
+        const int hhi = min(pos0 + tb + min(2 * pr + 2, ntok), lo + L);  // keys below hhi: some live token of it
+        // ---- query digits: lane (g, m16) holds dims 64 ks + 16 g .. +15 of (token tl, head m16 % 8) ----
+        int4_t_ qd[3][4];
+        float qs;
+        {
+            const float* qrow = qo + ((size_t)(tb + min(tl, ntok - 1)) * H + kvh * GQ + (m16 & 7)) * AHD + 16 * g;
+            float4 qv4[16];
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+                for (int u = 0; u < 4; u++) qv4[4 * ks + u] = *reinterpret_cast<const float4*>(qrow + 64 * ks + 4 * u);
+            float qm = 0.f;
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                qm = fmaxf(fmaxf(qm, fmaxf(fabsf(qv4[u].x), fabsf(qv4[u].y))), fmaxf(fabsf(qv4[u].z), fabsf(qv4[u].w)));
+            qm = max_x32(max_x16(qm));
+            int e = 0;
+            if (qm > 0.f) (void)frexpf(qm, &e);  // qm < 2^e
+            const float up = ldexpf(1.f, 22 - e);
+            qs = ldexpf(1.f, e - 22) * SL2;
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const float4 x = qv4[4 * ks + u];
+                    int d[3][4];
+                    digits3((int)__builtin_rintf(x.x * up), d[2][0], d[1][0], d[0][0]);
+                    digits3((int)__builtin_rintf(x.y * up), d[2][1], d[1][1], d[0][1]);
+                    digits3((int)__builtin_rintf(x.z * up), d[2][2], d[1][2], d[0][2]);
+                    digits3((int)__builtin_rintf(x.w * up), d[2][3], d[1][3], d[0][3]);
+#pragma unroll
+                    for (int dig = 0; dig < 3; dig++)
+                        qd[dig][ks][u] = (int)pack_bytes(d[dig][0], d[dig][1], d[dig][2], d[dig][3]);
+                }
+        }
+        half8_t* Pw = reinterpret_cast<half8_t*>(smem + WS_NS * WS_STAGE) + 128 * wv;  // [hi, lo][lane]
+        float4_t o[16];  // column n of tile 4 pc + j is dim 64 pc + 4 n + j; row r is column r of the Q.K MFMA
+#pragma unroll
+        for (int J = 0; J < 16; J++) o[J] = float4_t{0.f, 0.f, 0.f, 0.f};
+        float mref = -INFINITY, lacc = 0.f, vmax = 0.f;  // reference maximum and sum of column m16, V-scale maximum
+        int sig = 0;                                      // O is held times 2^sig
+        for (int c = 0; c < nch; c++) {
+            __syncthreads();  // chunk c is in stage c % WS_NS
+            if (!live) continue;
+            const int c0 = c == 0 ? lo : lo + first + (c - 1) * WS_CH, ce = c == 0 ? lo + first : lo + first + c * WS_CH;
+            const int cmax = min(ce, hhi), cmin = min(ce, hlo), ctl = min(ce, htl);
+            const unsigned char* sb = smem + (c % WS_NS) * WS_STAGE;
+            const float* sks = reinterpret_cast<const float*>(sb + 2 * WS_KB);
+            const float* svs = sks + 128;
+            const unsigned char* Vs = sb + WS_KB;
+#pragma unroll 1
+            for (int kb = (wv / NPR) * KPC; kb < (wv / NPR + 1) * KPC; kb += 32) {  // keys kb .. kb+31 of the chunk
+                if (c0 + kb >= cmax) break;
+                float ksv[8], vv[8];
+                {
+                    const float4 a0 = *reinterpret_cast<const float4*>(sks + kb + 4 * g);
+                    const float4 a1 = *reinterpret_cast<const float4*>(sks + kb + 16 + 4 * g);
+                    const float4 b0 = *reinterpret_cast<const float4*>(svs + kb + 4 * g);
+                    const float4 b1 = *reinterpret_cast<const float4*>(svs + kb + 16 + 4 * g);
+                    ksv[0] = a0.x; ksv[1] = a0.y; ksv[2] = a0.z; ksv[3] = a0.w;
+                    ksv[4] = a1.x; ksv[5] = a1.y; ksv[6] = a1.z; ksv[7] = a1.w;
+                    vv[0] = b0.x; vv[1] = b0.y; vv[2] = b0.z; vv[3] = b0.w;
+                    vv[4] = b1.x; vv[5] = b1.y; vv[6] = b1.z; vv[7] = b1.w;
+                }
+                int4_t_ acc[2][3];
+#pragma unroll
+                for (int grp = 0; grp < 2; grp++)
+#pragma unroll
+                    for (int dig = 0; dig < 3; dig++) acc[grp][dig] = int4_t_{0, 0, 0, 0};
+#pragma unroll
+                for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+                    for (int grp = 0; grp < 2; grp++) {
+                        const int4_t_ a =
+                            *reinterpret_cast<const int4_t_*>(sb + (kb + 16 * grp + m16) * AHD + 16 * ((4 * ks + g) ^ m16));
+#pragma unroll
+                        for (int dig = 0; dig < 3; dig++)
+                            acc[grp][dig] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qd[dig][ks], acc[grp][dig], 0, 0, 0);
+                    }
+                float sc[8];
+#pragma unroll
+                for (int grp = 0; grp < 2; grp++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float raw =
+                            ((float)acc[grp][2][i] * 65536.f + (float)acc[grp][1][i] * 256.f) + (float)acc[grp][0][i];
+                        sc[4 * grp + i] = raw * (ksv[4 * grp + i] * qs);
+                    }
+                float vm;
+                if (c0 + kb + 32 <= cmin) {  // all 32 keys valid for both tokens
+                    vm = fmaxf(fmaxf(fmaxf(vv[0], vv[1]), fmaxf(vv[2], vv[3])), fmaxf(fmaxf(vv[4], vv[5]), fmaxf(vv[6], vv[7])));
+                } else {
+                    vm = 0.f;
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        const int key = c0 + kb + 16 * (j >> 2) + 4 * g + (j & 3);
+                        sc[j] = key < ctl ? sc[j] : -INFINITY;
+                        vm = key < cmax ? fmaxf(vm, vv[j]) : vm;
+                    }
+                }
+                float M = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+                M = max_x32(max_x16(M));
+                vm = max_x32(max_x16(vm));
+                // ---- lazy rescale: new reference maximum of a column / V-scale exponent ----
+                const float nref = M > mref + WS_SLACK ? M : mref;
+                const float fown = ex2d(mref, nref);
+                vmax = fmaxf(vmax, vm);
+                int ev = 0;
+                if (vmax > 0.f) (void)frexpf(vmax, &ev);  // vmax < 2^ev: p * vs * 2^(7 - ev) < 2^(7 + WS_SLACK)
+                const int nsig = 7 - ev;
+                if (__builtin_amdgcn_ballot_w64(fown != 1.f) != 0 || nsig != sig) {
+                    const float sf = ldexpf(1.f, nsig - sig);
+                    float fr[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) fr[i] = __shfl(fown, 4 * g + i) * sf;  // O row 4g + i = column 4g + i
+#pragma unroll
+                    for (int J = 0; J < 16; J++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++) o[J][i] *= fr[i];
+                    lacc *= fown;
+                    mref = nref;
+                    sig = nsig;
+                }
+                // ---- P = 2^(s - mref) * vs * 2^sig = hi + lo in fp16 (a column with no key yet has P = 0) ----
+                {
+                    const float vsc = ldexpf(1.f, sig), mr = mref == -INFINITY ? 0.f : mref;
+                    half8_t ph, pl;
+                    float ls = 0.f;
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        const float p = fast_exp2(sc[j] - mr);
+                        ls += p;
+                        const float x = p * (vv[j] * vsc);
+                        const _Float16 h = (_Float16)x;
+                        ph[j] = h;
+                        pl[j] = (_Float16)(x - (float)h);
+                    }
+                    lacc += ls;
+                    Pw[16 * g + m16] = ph;
+                    Pw[64 + 16 * g + m16] = pl;
+                }
+                // ---- O^T += (P_hi + P_lo) . V over these 32 keys, all 256 dims ----
+                const half8_t pah = Pw[lane], pal = Pw[64 + lane];
+#pragma unroll
+                for (int pc = 0; pc < 4; pc++) {
+                    const int rd = 16 * ((4 * pc + (m16 >> 2)) ^ (4 * g)) + 4 * (m16 & 3);
+                    uint32_t r[8];
+#pragma unroll
+                    for (int j = 0; j < 8; j++)
+                        r[j] = *reinterpret_cast<const uint32_t*>(Vs + (kb + 16 * (j >> 2) + 4 * g + (j & 3)) * AHD + rd);
+                    uint32_t c0v[4], c1v[4];
+                    tr4x4_(r[0], r[1], r[2], r[3], c0v);
+                    tr4x4_(r[4], r[5], r[6], r[7], c1v);
+#pragma unroll
+                    for (int jt = 0; jt < 4; jt++) {
+                        const half8_t vb = i8x8_to_h8(c0v[jt], c1v[jt]);
+                        o[4 * pc + jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pah, vb, o[4 * pc + jt], 0, 0, 0);
+                        o[4 * pc + jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pal, vb, o[4 * pc + jt], 0, 0, 0);
+                    }
+                }
+            }
+        }
+        // ---- merge the consumers of each pair: m, l per column, then O rows scaled to the common maximum ----
+        const float l = sum_x32(sum_x16(lacc));
+        __syncthreads();  // every consumer is past its last chunk: stage 0 is free
+        if (lane < 16) { cm[wv][lane] = mref; cl[wv][lane] = l; }
+        __syncthreads();
+        float* Ow = reinterpret_cast<float*>(smem);  // [consumer][column][256]
+        const float un = ldexpf(1.f, -sig);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int col = 4 * g + i;
+            float Mc = cm[pr][col];
+#pragma unroll
+            for (int w = pr + NPR; w < WS_NC; w += NPR) Mc = fmaxf(Mc, cm[w][col]);
+            const float f = ex2d(cm[wv][col], Mc) * un;
+#pragma unroll
+            for (int pc = 0; pc < 4; pc++)
+                *reinterpret_cast<float4*>(Ow + (wv * 16 + col) * AHD + 64 * pc + 4 * m16) =
+                    make_float4(o[4 * pc][i] * f, o[4 * pc + 1][i] * f, o[4 * pc + 2][i] * f, o[4 * pc + 3][i] * f);
+        }
+    }
+    __syncthreads();
+    // ---- partials of the split: item = (token, head, dims 4 (item % 64) .. +3) ----
+    for (int it = tid; it < ntok * GQ * 64; it += 64 * (WS_NC + WS_NP)) {
+        const float* Ow = reinterpret_cast<const float*>(smem);
+        const int t = it / (GQ * 64), h = (it >> 6) % GQ, d4 = 4 * (it & 63);
+        const int pr = t >> 1, col = 8 * (t & 1) + h;
+        float4 a = *reinterpret_cast<const float4*>(Ow + (pr * 16 + col) * AHD + d4);
+#pragma unroll
+        for (int w = pr + NPR; w < WS_NC; w += NPR) {
+            const float4 b = *reinterpret_cast<const float4*>(Ow + (w * 16 + col) * AHD + d4);
+            a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+        }
+        *reinterpret_cast<float4*>(part_acc(part, tb + t, kvh * GQ + h, s, H, ns) + d4) = a;
+        if ((it & 63) == 0) {
+            float Mc = cm[pr][col], lc = 0.f;
+#pragma unroll
+            for (int w = pr + NPR; w < WS_NC; w += NPR) Mc = fmaxf(Mc, cm[w][col]);
+#pragma unroll
+            for (int w = pr; w < WS_NC; w += NPR) lc += cl[w][col] * ex2d(cm[w][col], Mc);
+            float* ml = part_ml(part, tb + t, kvh * GQ + h, s, H, ns, T);
+            ml[0] = Mc;  // -inf when the token has no key in this split
+            ml[1] = lc;
+        }
+    }
+}
+
+template <int NPR>
+static void launch_wsp(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part,
+                       int T, int ns, hipStream_t st) {
     static bool once = [] {
-        MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_x_kernel<TT>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, x_lds<TT>()));
+        MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_wsp_kernel<NPR>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, WSP_LDS));
         return true;
     }();
     (void)once;
-    const int nb = KV * ns * ((T + TT - 1) / TT);
-    hipLaunchKernelGGL(gqa_x_kernel<TT>, dim3(nb), dim3(256), x_lds<TT>(), st, qo, kv, H, pos_d, max_t, part, T, ns);
+    hipLaunchKernelGGL(gqa_wsp_kernel<NPR>, dim3(KV * ns * ((T + 2 * NPR - 1) / (2 * NPR))),
+                       dim3(64 * (WS_NC + WS_NP)), WSP_LDS, st, qo, kv, H, pos_d, max_t, part, T, ns);
 }
 
 // ---- gqa_xt_kernel: TurboQuant KV on the same chunked design (one query token per workgroup).
@@ -1013,9 +941,9 @@ __global__ void __launch_bounds__(256, 2) gqa_xt_kernel(const float* __restrict_
 }
 
 int gqa_splits(int T, int KV, int ns, bool turbo) {
-    // T = 2 (and turbo) run two workgroups per CU; the one-token and four-token kernels run one, so beyond one
-    // workgroup per CU extra splits only add per-workgroup set-up and partials
-    if (turbo || T == 2) return ns;
+    // the int8 kernels run one workgroup per CU (one token, or a group of up to 4): beyond one workgroup per CU extra
+    // splits only add per-workgroup set-up and partials. Turbo runs two per CU.
+    if (turbo) return ns;
     static const int cus = [] {
         int dev = 0, v = 0;
         if (hipGetDevice(&dev) == hipSuccess &&
@@ -1023,7 +951,7 @@ int gqa_splits(int T, int KV, int ns, bool turbo) {
             return v;
         return 256;
     }();
-    const int fill = cus / (KV * (T == 1 ? 1 : (T + 3) / 4));
+    const int fill = cus / (KV * (T <= 2 ? 1 : (T + 3) / 4));
     return fill < 1 ? 1 : (fill < ns ? fill : ns);
 }
 
@@ -1047,8 +975,8 @@ void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos
             (void)once;
             hipLaunchKernelGGL(gqa_ws_kernel, dim3(KV * ns), dim3(64 * (WS_NC + WS_NP)), WS_LDS, st, qo, kv, H, pos_d, max_t, part, T, ns);
         }
-        else if (T == 2) launch_x<2>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
-        else launch_x<4>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
+        else if (T == 2) launch_wsp<1>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
+        else launch_wsp<2>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
     }
     MOEX_LAUNCHED();
 }

@@ -65,7 +65,7 @@ def test_gqa_splits_policy():
     CU (256 on MI355X, the fallback without a device) per token or four-token group, never above the caller's ns"""
     import moex_amd as M
     assert M.gqa_splits(1, 2, 256) == 128
-    assert M.gqa_splits(2, 2, 256) == 256
+    assert M.gqa_splits(2, 2, 256) == 128
     assert M.gqa_splits(4, 2, 256) == 128
     assert M.gqa_splits(8, 2, 256) == 64
     assert M.gqa_splits(4, 2, 32) == 32
