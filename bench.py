@@ -185,7 +185,7 @@ def main():
         ct = M.DeviceKVCache(KV, 262144 + 64, 1)
         fill_cache(ct, 262144, seed=12)
         ctx = 262144
-        ns = M.decode_splits(ctx)
+        ns = M.gqa_splits(1, KV, M.decode_splits(ctx), 1)
         part = torch.empty(H * ns * (AHD + 2), device=dev)
         o1 = torch.empty((1, H, AHD), device=dev)
         pd = torch.tensor([ctx - 1], dtype=torch.int32, device=dev)

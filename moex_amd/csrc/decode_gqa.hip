@@ -2,9 +2,9 @@
 //
 // One workgroup = (kv head, key split, group of query tokens); the 8 query heads of the group share every K/V byte.
 // int8 cache: gqa_ws_kernel for a single query token (warp-specialised: producer wavefronts stream K/V into LDS,
-// consumer wavefronts compute), gqa_wsp_kernel for MTP-verify windows (token pairs on the same pipeline). gqa_xt_kernel
-// serves the TurboQuant cache (one token; 4 wavefronts that load and compute, the codes unpacked on the way). The
-// partial written per (token, head, split) is {m (log2 units), l, acc[256]}.
+// consumer wavefronts compute), gqa_wsp_kernel for MTP-verify windows (token pairs on the same pipeline).
+// gqa_wst_kernel serves the TurboQuant cache, one token per workgroup on the same pipeline, the codes unpacked on the
+// way. The partial written per (token, head, split) is {m (log2 units), l, acc[256]}.
 #include "common.hpp"
 
 namespace moex {
@@ -33,7 +33,6 @@ __device__ __forceinline__ int xcd_work_id(int b, int nb) {
 // of one MFMA and digit 0 into a second, and brings a head's digits together with two row_ror:8 DPP moves.
 // P.V runs on v_mfma_f32_16x16x32_f16: P = p * vs * 2^sig is split into fp16 hi + lo (~22 bits), V widened exactly to
 // fp16, fp32 accumulation.
-constexpr int ICH = 128;                           // keys per chunk: 32 keys (two 16-key groups) per wavefront
 typedef int int4_t_ __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int dpp_ror8(int x) { return __builtin_amdgcn_update_dpp(0, x, 0x128, 0xf, 0xf, false); }
@@ -57,13 +56,8 @@ __device__ __forceinline__ void tr4x4_(const uint32_t r0, const uint32_t r1, con
 typedef __attribute__((address_space(1))) const void* gptr_t;
 typedef __attribute__((address_space(3))) void* lptr_t;
 
-constexpr int I8_VBUF = ICH * AHD;                 // 32 KB per V buffer
-constexpr int I8_QL = 2 * 4 * 64 * 16;             // Q digit operands of one token
-static_assert(I8_QL <= I8_VBUF, "query digits of one token stage in V buffer 1");
 // 2^(a - b) with 2^(-inf - -inf) = 1 (a running maximum that has not moved, also while it is still -inf)
 __device__ __forceinline__ float ex2d(float a, float b) { return a == b ? 1.f : fast_exp2(a - b); }
-
-constexpr int X_PL = 4 * 64 * 16;  // P operands of one token per chunk: [step = wavefront][lane] half8
 
 // x combined with its partner lane l ^ 16 / l ^ 32 (v_permlane16/32_swap: both lanes of a pair receive both values)
 __device__ __forceinline__ float max_x16(float x) {
@@ -636,17 +630,11 @@ static void launch_wsp(const float* qo, moex_kv_cache kv, int H, int KV, const i
                        dim3(64 * (WS_NC + WS_NP)), WSP_LDS, st, qo, kv, H, pos_d, max_t, part, T, ns);
 }
 
-// ---- gqa_xt_kernel: TurboQuant KV on the same chunked design (one query token per workgroup).
-//   K: 4-bit codes -> signed centroid codes (two v_perm LUT halves + v_bfi per 4 codes) as the int8 operands of the
-//      Q.K MFMAs, which keep the two 128-dim halves in separate accumulators: s = K4 * (n0 * S0 + n1 * S1). The
-//      operand takes a lane's 16 codes as (even nibbles, odd nibbles) of two dwords; the query digits use the same
-//      dim order.
-//   V: the raw 96-byte rows of a chunk go to LDS by DMA; all threads then rebuild the 3-bit codes from the low-bit
-//      and high-bit planes (two small LDS tables spread the bit fields into bytes) into an int8 code chunk with the
-//      int8 kernel's layout, so P.V is the int8 kernel's. P carries the V half norm: wavefronts 0-1 (dims < 128) and
-//      2-3 read separate P operands.
-constexpr int XT_VRAW = ICH * TQ_VB;                               // 12 KB of raw V rows per chunk
-constexpr int XT_LDS = 2 * XT_VRAW + I8_VBUF + 2 * X_PL + 1024 + 64;  // raw x2, codes, P per half, tables
+// TurboQuant codes -> signed int8 centroid codes (kernels.cuh:1122-1170 tables, scaled by 127 / max centroid):
+//   K: 4-bit codes -> two v_perm LUT halves, a third v_perm picks per byte; the MFMA operand takes a lane's 16 codes
+//      as (even nibbles, odd nibbles) of two dwords, and the query digits use the same dim order.
+//   V: 3-bit codes, the low 2 bits and the high bit in separate planes of the row; two small LDS tables spread the
+//      bit fields into bytes.
 constexpr uint32_t spack(int a, int b, int c, int d) {
     return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) | ((uint32_t)(d & 0xff) << 24);
 }
@@ -657,293 +645,338 @@ constexpr uint32_t SV0 = spack(-127, -79, -45, -14), SV1 = spack(14, 45, 79, 127
 __device__ __forceinline__ int lut16s(uint32_t idx) {
     const uint32_t s3 = idx & 0x07070707u;
     const uint32_t lo = __builtin_amdgcn_perm(SK1, SK0, s3), hi = __builtin_amdgcn_perm(SK3, SK2, s3);
-    const uint32_t mask = ((idx >> 3) & 0x01010101u) * 0xffu;
-    return (int)((hi & mask) | (lo & ~mask));
+    // byte b from hi when bit 3 of index b is set: selector b + 4 picks byte b of the first perm operand
+    return (int)__builtin_amdgcn_perm(hi, lo, 0x03020100u | ((idx >> 1) & 0x04040404u));
 }
 __device__ __forceinline__ int4_t_ k_codes(uint2 x) {  // 16 nibbles -> the MFMA operand (even, odd, even, odd)
     return int4_t_{lut16s(x.x & 0x0f0f0f0fu), lut16s((x.x >> 4) & 0x0f0f0f0fu),
                    lut16s(x.y & 0x0f0f0f0fu), lut16s((x.y >> 4) & 0x0f0f0f0fu)};
 }
 
-__global__ void __launch_bounds__(256, 2) gqa_xt_kernel(const float* __restrict__ qo, moex_kv_cache kv, int H,
-                                                        const int* __restrict__ pos_d, int max_t,
-                                                        float* __restrict__ part, int T, int ns) {
+// ---- gqa_wst_kernel: TurboQuant cache, one query token per workgroup, on gqa_ws_kernel's warp-specialised pipeline.
+// A stage holds a chunk's raw rows: K nibbles (row r keeps 16-byte piece p in slot p ^ ((r / 2) % 8), so the 8-byte
+// fragment reads of 16 rows at a 128-byte stride hit distinct banks), raw V rows (96 bytes, packed), and the K and V
+// half norms. Producers move them by DMA (36 transfers per chunk, 4-byte ones for the norms so every key index is
+// clamped); each consumer unpacks the V codes of its own 32 keys into a private int8 code area (gqa_ws_kernel's V
+// layout), so the chunk loop stays free of exchanges. Q.K packs the query digits 2 and 1 of the 8 heads into one
+// MFMA and digit 0 into a second, per 128-dim half, and recombines a head's digits with two row_ror:8 DPP moves; P
+// carries the V half norm, hi/lo rows interleaved.
+constexpr int WST_KB = 128 * TQ_KB;                      // K nibble rows of a stage
+constexpr int WST_STAGE = WST_KB + 128 * TQ_VB + 2 * 128 * 8;  // + raw V rows + K norms + V norms
+constexpr int WST_VC = 32 * AHD;                         // one consumer's unpacked V codes
+constexpr int WST_LDS = WS_NS * WST_STAGE + WS_NC * WST_VC + WS_NC * 2 * 64 * 16 + 1024 + 64;
+static_assert(WS_NC * GQ * AHD * 4 <= WS_NS * WST_STAGE, "the consumer merge fits in the stages");
+static_assert(WST_LDS <= 160 * 1024, "LDS");
+
+__global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const float* __restrict__ qo, moex_kv_cache kv,
+                                                                         int H, const int* __restrict__ pos_d,
+                                                                         int max_t, float* __restrict__ part, int T,
+                                                                         int ns) {
     extern __shared__ __align__(16) unsigned char smem[];
-    unsigned char* Vd = smem + 2 * XT_VRAW;                                       // int8 code chunk (swizzled)
-    half8_t* Pl = reinterpret_cast<half8_t*>(smem + 2 * XT_VRAW + I8_VBUF);      // [half][4][64]
-    uint32_t* t256 = reinterpret_cast<uint32_t*>(smem + 2 * XT_VRAW + I8_VBUF + 2 * X_PL);
+    __shared__ float cm[WS_NC][GQ], cl[WS_NC][GQ];
+    uint32_t* t256 = reinterpret_cast<uint32_t*>(smem + WS_NS * WST_STAGE + WS_NC * WST_VC + WS_NC * 2 * 64 * 16);
     uint32_t* t16 = t256 + 256;
-    int4_t_* Ql = reinterpret_cast<int4_t_*>(Vd);                                 // set-up only
-    __shared__ float mxw[4][GQ], lsum[4][GQ], vmw[4], qsc_s[GQ];
     const int nb = gridDim.x, w_id = xcd_work_id(blockIdx.x, nb);
     const int tok = w_id % T, s = (w_id / T) % ns, kvh = w_id / (T * ns);
     const int pos0 = *pos_d, Tmax = pos0 + T;
-    const int L = (Tmax + ns - 1) / ns, lo = s * L, hi = min(pos0 + tok + 1, lo + L);
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 4, m16 = lane & 15, hq = m16 & 7;
-    const bool lo8 = m16 < 8;
+    const int L = (Tmax + ns - 1) / ns, lo = s * L;
+    const int hi = min(pos0 + tok + 1, lo + L);  // keys [lo, hi) of this split that the token sees
+    const int nch = hi > lo ? (hi - lo + WS_CH - 1) / WS_CH : 0;
+    const int first = hi > lo ? hi - lo - (nch - 1) * WS_CH : 0;  // chunk 0 is the short one
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 4, m16 = lane & 15;
     const size_t rbase = (size_t)kvh * max_t;
-    const uint8_t* Kg = reinterpret_cast<const uint8_t*>(kv.k) + rbase * TQ_KB;
-    const uint8_t* Vg = reinterpret_cast<const uint8_t*>(kv.v) + rbase * TQ_VB;
-    const float2* kng = reinterpret_cast<const float2*>(kv.ks) + rbase;  // (n0, n1) per key
-    const float2* vng = reinterpret_cast<const float2*>(kv.vs) + rbase;
-    const int nch = hi > lo ? (hi - lo + ICH - 1) / ICH : 0;
-
-    // bit-field spreading tables: t256[b] = the four 2-bit fields of b, one per byte; t16[n] = bit e of n at bit 2 of
-    // byte e
-    {
+    // bit-field spreading tables (read after the first chunk barrier): t256[b] = the four 2-bit fields of b, one per
+    // byte; t16[n] = bit e of n at bit 2 of byte e
+    if (tid < 256) {
         const uint32_t b = tid;
         t256[tid] = (b & 3u) | (((b >> 2) & 3u) << 8) | (((b >> 4) & 3u) << 16) | ((b >> 6) << 24);
         if (tid < 16) t16[tid] = ((b & 1u) << 2) | (((b >> 1) & 1u) << 10) | (((b >> 2) & 1u) << 18) | ((b >> 3) << 26);
     }
 
-    // ---- loaders: raw V rows (DMA, 3 pieces of 16 B per thread), this wavefront's K nibbles and both norm pairs ----
-    auto issue_v = [&](unsigned char* buf, int c0) {
-        const int nk = min(ICH, hi - c0);
+    if (wv >= WS_NC) {
+        // ---- producers: transfer i (0..35) of a chunk goes to producer i % 4: 0-15 K rows (8 rows each), 16-27 raw
+        // V rows (1 KB of the packed rows each), 28-31 K norms, 32-35 V norms (64 floats each) ----
+        const int pw = wv - WS_NC;
+        const uint8_t* Kg = reinterpret_cast<const uint8_t*>(kv.k) + rbase * TQ_KB;
+        const uint8_t* Vg = reinterpret_cast<const uint8_t*>(kv.v) + rbase * TQ_VB;
+        const float* kng = kv.ks + 2 * rbase;
+        const float* vng = kv.vs + 2 * rbase;
+        auto issue = [&](int c) {
+            const int c0 = c == 0 ? lo : lo + first + (c - 1) * WS_CH, ce = c == 0 ? lo + first : lo + first + c * WS_CH;
+            unsigned char* st = smem + (c % WS_NS) * WST_STAGE;
 #pragma unroll
-        for (int it = 0; it < 3; it++) {
-            const int pc = it * 256 + tid, row = pc / 6, col = pc % 6;
-            const int t = min(c0 + row, hi - 1);
-            (void)nk;
-            __builtin_amdgcn_global_load_lds((gptr_t)(Vg + (size_t)t * TQ_VB + 16 * col),
-                                             (lptr_t)(buf + (it * 256 + 64 * wv) * 16), 16, 0, 0);
+            for (int u = 0; u < 9; u++) {
+                const int i = pw + 4 * u;
+                if (i < 16) {
+                    const int r = 8 * i + (lane >> 3), piece = (lane & 7) ^ ((r >> 1) & 7);
+                    __builtin_amdgcn_global_load_lds((gptr_t)(Kg + (size_t)min(c0 + r, ce - 1) * TQ_KB + 16 * piece),
+                                                     (lptr_t)(st + i * 1024), 16, 0, 0);
+                } else if (i < 28) {
+                    const int b = (i - 16) * 1024 + 16 * lane, r = b / TQ_VB;
+                    __builtin_amdgcn_global_load_lds((gptr_t)(Vg + (size_t)min(c0 + r, ce - 1) * TQ_VB + (b - r * TQ_VB)),
+                                                     (lptr_t)(st + WST_KB + (i - 16) * 1024), 16, 0, 0);
+                } else {
+                    const int f = 64 * (i & 3) + lane, key = min(c0 + (f >> 1), ce - 1);
+                    __builtin_amdgcn_global_load_lds((gptr_t)((i < 32 ? kng : vng) + 2 * (size_t)key + (f & 1)),
+                                                     (lptr_t)(st + WST_KB + 128 * TQ_VB + (i < 32 ? 0 : 1024) + 256 * (i & 3)),
+                                                     4, 0, 0);
+                }
+            }
+        };
+        if (nch > 0) issue(0);
+        for (int c = 0; c < nch; c++) {
+            wait_vm<0>();     // chunk c has landed
+            __syncthreads();  // ... and the consumers are done with chunk c - 1: its stage takes chunk c + 1
+            if (c + 1 < nch) issue(c + 1);
         }
-    };
-    auto issue_k = [&](uint2 (&kd)[2][4], float2 (&knd)[8], float2 (&vnd)[8], int c0) {
-        const int k0 = c0 + 32 * wv;
-        if (k0 >= hi) return;
-#pragma unroll
-        for (int grp = 0; grp < 2; grp++) {
-            const uint8_t* kp = Kg + (size_t)min(k0 + 16 * grp + m16, hi - 1) * TQ_KB + 8 * g;
+        __syncthreads();
+        __syncthreads();
+    } else {
+        // ---- consumers. Query digits in registers: MFMA ks, lane (g, m16) holds dims
+        // 64 ks + 16 g + {0,2,4,6, 1,3,5,7, 8,10,12,14, 9,11,13,15} of head m16 % 8; qa = digit 2 (m16 < 8) or 1,
+        // qb = digit 0 (m16 < 8) or 0 ----
+        const int hq = m16 & 7;
+        const bool lo8 = m16 < 8;
+        int4_t_ qa[4], qb[4];
+        float qs;
+        {
+            const float* qrow = qo + ((size_t)tok * H + kvh * GQ + hq) * AHD + 16 * g;
+            float4 qv4[16];
 #pragma unroll
             for (int ks = 0; ks < 4; ks++)
-                kd[grp][ks] = *reinterpret_cast<const uint2*>(kp + 64 * (ks >> 1) + 32 * (ks & 1));
-        }
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int t = min(k0 + 16 * (j >> 2) + 4 * g + (j & 3), hi - 1);
-            knd[j] = kng[t];
-            vnd[j] = vng[t];
-        }
-    };
-    uint2 kA[2][4], kB[2][4];
-    float2 knA[8], vnA[8], knB[8], vnB[8];
-    if (nch > 0) {
-        issue_k(kA, knA, vnA, lo);
-        issue_v(smem, lo);
-    }
-
-    // ---- query digits: thread = (head tid/32, dims 8*(tid%32) .. +7); MFMA ks, lane 16g + m holds dims
-    // 64ks + 16g + {0,2,4,6, 1,3,5,7, 8,10,12,14, 9,11,13,15} of column m ----
-    {
-        const int h = tid >> 5, d0 = (tid & 31) * 8;
-        const float* qrow = qo + ((size_t)tok * H + kvh * GQ + h) * AHD + d0;
-        const float4 x0 = reinterpret_cast<const float4*>(qrow)[0], x1 = reinterpret_cast<const float4*>(qrow)[1];
-        const float qv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-        float qm = 0.f;
+                for (int u = 0; u < 4; u++) qv4[4 * ks + u] = *reinterpret_cast<const float4*>(qrow + 64 * ks + 4 * u);
+            float qm = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; j++) qm = fmaxf(qm, fabsf(qv[j]));
+            for (int u = 0; u < 16; u++)
+                qm = fmaxf(fmaxf(qm, fmaxf(fabsf(qv4[u].x), fabsf(qv4[u].y))), fmaxf(fabsf(qv4[u].z), fabsf(qv4[u].w)));
+            qm = max_x32(max_x16(qm));
+            int e = 0;
+            if (qm > 0.f) (void)frexpf(qm, &e);  // qm < 2^e
+            const float up = ldexpf(1.f, 22 - e);
+            qs = ldexpf(1.f, e - 22) * (SL2 * TK4);
 #pragma unroll
-        for (int o = 1; o < 32; o <<= 1) qm = fmaxf(qm, __shfl_xor(qm, o));
-        int e = 0;
-        if (qm > 0.f) (void)frexpf(qm, &e);  // qm < 2^e
-        const float up = ldexpf(1.f, 22 - e);
-        if ((tid & 31) == 0) qsc_s[h] = ldexpf(1.f, e - 22) * (SL2 * TK4);
-        int d2[8], d1[8], dz[8];
+            for (int ks = 0; ks < 4; ks++) {
+                int da[16], db[16];
 #pragma unroll
-        for (int j = 0; j < 8; j++) digits3((int)__builtin_rintf(qv[j] * up), d2[j], d1[j], dz[j]);
-        const int ks = d0 >> 6, gg = (d0 >> 4) & 3, jb = d0 & 15;
-        unsigned char* qa_b = reinterpret_cast<unsigned char*>(Ql + ks * 64);
-        unsigned char* qb_b = reinterpret_cast<unsigned char*>(Ql + (4 + ks) * 64);
-        *reinterpret_cast<uint2*>(qa_b + (16 * gg + h) * 16 + jb) =
-            make_uint2(pack_bytes(d2[0], d2[2], d2[4], d2[6]), pack_bytes(d2[1], d2[3], d2[5], d2[7]));
-        *reinterpret_cast<uint2*>(qa_b + (16 * gg + h + 8) * 16 + jb) =
-            make_uint2(pack_bytes(d1[0], d1[2], d1[4], d1[6]), pack_bytes(d1[1], d1[3], d1[5], d1[7]));
-        *reinterpret_cast<uint2*>(qb_b + (16 * gg + h) * 16 + jb) =
-            make_uint2(pack_bytes(dz[0], dz[2], dz[4], dz[6]), pack_bytes(dz[1], dz[3], dz[5], dz[7]));
-        *reinterpret_cast<uint2*>(qb_b + (16 * gg + h + 8) * 16 + jb) = make_uint2(0u, 0u);
-    }
-    __syncthreads();
-    int4_t_ qa[4], qb[4];
+                for (int u = 0; u < 4; u++) {
+                    const float4 x = qv4[4 * ks + u];
+                    const float xv[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
-    for (int ks = 0; ks < 4; ks++) { qa[ks] = Ql[ks * 64 + lane]; qb[ks] = Ql[(4 + ks) * 64 + lane]; }
-    const float qs = qsc_s[hq];
-
-    float4_t o[4];
-    float m4[4], mo = -INFINITY, lacc = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) { m4[i] = -INFINITY; o[i] = float4_t{0.f, 0.f, 0.f, 0.f}; }
-    int sig_ref = 0;
-    const int rd = 16 * ((4 * wv + (m16 >> 2)) ^ (4 * g)) + 4 * (m16 & 3);  // swizzled byte offset of my V dims
-    const int vh = wv >> 1;                                                  // the V half of my dims
-
-    auto chunk = [&](int c, const uint2 (&kr)[2][4], const float2 (&kn)[8], const float2 (&vn)[8],
-                     uint2 (&knx)[2][4], float2 (&knn)[8], float2 (&vnn)[8]) __attribute__((always_inline)) {
-        const int c0 = lo + c * ICH, nk = min(ICH, hi - c0), nsteps = (nk + 31) >> 5;
-        const int k0 = c0 + 32 * wv;
-        const bool has = k0 < hi;
-        const unsigned char* Vr = smem + (c & 1) * XT_VRAW;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // chunk c's K, norms and raw V rows have landed
-        __syncthreads();                                   // ... for every wavefront; chunk c-1 is done with LDS
-        if (c + 1 < nch) {
-            issue_k(knx, knn, vnn, c0 + ICH);
-            issue_v(smem + ((c + 1) & 1) * XT_VRAW, c0 + ICH);
-        }
-        // ---- V codes of the chunk: thread = (16-code piece pc = tid%16, keys tid/16 + 16*it): the 16 lanes of a key
-        // write one whole 256-byte code row ----
-        {
-            const int pc = tid & 15, hb = pc >> 3, q = pc & 7;
-#pragma unroll
-            for (int it = 0; it < ICH / 16; it++) {
-                const int kk = (tid >> 4) + 16 * it;
-                const unsigned char* rw = Vr + kk * TQ_VB;
-                const uint32_t L = *reinterpret_cast<const uint32_t*>(rw + 32 * hb + 4 * q);
-                const uint32_t Hh = *reinterpret_cast<const uint16_t*>(rw + 64 + 16 * hb + 2 * q);
-                uint32_t cd[4];
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const uint32_t idx = t256[(L >> (8 * k)) & 0xffu] | t16[(Hh >> (4 * k)) & 15u];
-                    cd[k] = __builtin_amdgcn_perm(SV1, SV0, idx);
+                    for (int k = 0; k < 4; k++) {
+                        int d2, d1, d0;
+                        digits3((int)__builtin_rintf(xv[k] * up), d2, d1, d0);
+                        // dim 4u + k of the lane's 16 goes to operand byte: even dims of each 8 first, then odd
+                        const int dl = 4 * u + k, pos = 8 * (dl >> 3) + ((dl & 1) ? 4 : 0) + ((dl & 7) >> 1);
+                        da[pos] = lo8 ? d2 : d1;
+                        db[pos] = lo8 ? d0 : 0;
+                    }
                 }
-                *reinterpret_cast<uint4*>(Vd + kk * AHD + 16 * (pc ^ (4 * ((kk >> 2) & 3)))) = make_uint4(cd[0], cd[1], cd[2], cd[3]);
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    qa[ks][w] = (int)pack_bytes(da[4 * w], da[4 * w + 1], da[4 * w + 2], da[4 * w + 3]);
+                    qb[ks][w] = (int)pack_bytes(db[4 * w], db[4 * w + 1], db[4 * w + 2], db[4 * w + 3]);
+                }
             }
         }
-        // ---- pass 1: scores of this wavefront's 32 keys ----
-        float sc[8];
-        float vm = 0.f, mx = -INFINITY;
+        unsigned char* Vc = smem + WS_NS * WST_STAGE + wv * WST_VC;  // this consumer's V codes (ws V layout)
+        half8_t* Pw = reinterpret_cast<half8_t*>(smem + WS_NS * WST_STAGE + WS_NC * WST_VC) + 128 * wv;  // [half][lane]
+        float4_t o[16];  // ws layout: row 2h (2h + 1) = hi (lo) part of head h
 #pragma unroll
-        for (int j = 0; j < 8; j++) sc[j] = -INFINITY;
-        if (has) {
+        for (int J = 0; J < 16; J++) o[J] = float4_t{0.f, 0.f, 0.f, 0.f};
+        float mref = -INFINITY, lacc = 0.f, vmax = 0.f;
+        int sig = 0;
+        const int kb = 32 * wv;
+        for (int c = 0; c < nch; c++) {
+            __syncthreads();  // chunk c is in stage c % WS_NS
+            const int c0 = c == 0 ? lo : lo + first + (c - 1) * WS_CH, ce = c == 0 ? lo + first : lo + first + c * WS_CH;
+            if (c0 + kb >= ce) continue;
+            const unsigned char* sb = smem + (c % WS_NS) * WST_STAGE;
+            const float2* skn = reinterpret_cast<const float2*>(sb + WST_KB + 128 * TQ_VB);
+            const float2* svn = skn + 128;
+            float2 kn[8], vn[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                kn[j] = skn[kb + 16 * (j >> 2) + 4 * g + (j & 3)];
+                vn[j] = svn[kb + 16 * (j >> 2) + 4 * g + (j & 3)];
+            }
+            // ---- K codes and the 16 Q.K MFMAs (halves in separate accumulators) ----
+            int4_t_ da0[2], db0[2], da1[2], db1[2];
 #pragma unroll
             for (int grp = 0; grp < 2; grp++) {
-                int4_t_ da0 = {0, 0, 0, 0}, db0 = {0, 0, 0, 0}, da1 = {0, 0, 0, 0}, db1 = {0, 0, 0, 0};
+                da0[grp] = int4_t_{0, 0, 0, 0}; db0[grp] = int4_t_{0, 0, 0, 0};
+                da1[grp] = int4_t_{0, 0, 0, 0}; db1[grp] = int4_t_{0, 0, 0, 0};
+            }
 #pragma unroll
-                for (int ks = 0; ks < 4; ks++) {
-                    const int4_t_ a = k_codes(kr[grp][ks]);
+            for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+                for (int grp = 0; grp < 2; grp++) {
+                    const int byte = 64 * (ks >> 1) + 32 * (ks & 1) + 8 * g;  // row kb + 16 grp + m16
+                    const uint2 nib = *reinterpret_cast<const uint2*>(sb + (kb + 16 * grp + m16) * TQ_KB +
+                                                                      16 * ((byte >> 4) ^ ((m16 >> 1) & 7)) + (byte & 15));
+                    const int4_t_ a = k_codes(nib);
                     if (ks < 2) {
-                        da0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qa[ks], da0, 0, 0, 0);
-                        db0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qb[ks], db0, 0, 0, 0);
+                        da0[grp] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qa[ks], da0[grp], 0, 0, 0);
+                        db0[grp] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qb[ks], db0[grp], 0, 0, 0);
                     } else {
-                        da1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qa[ks], da1, 0, 0, 0);
-                        db1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qb[ks], db1, 0, 0, 0);
+                        da1[grp] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qa[ks], da1[grp], 0, 0, 0);
+                        db1[grp] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qb[ks], db1[grp], 0, 0, 0);
                     }
                 }
+            // ---- V codes of this consumer's 32 keys: lane = (piece pc = lane % 16, keys lane / 16 + 4 it) ----
+            {
+                const int pc = lane & 15, hb = pc >> 3, q = pc & 7;
+                const unsigned char* rw0 = sb + WST_KB + (kb + (lane >> 4)) * TQ_VB;
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int j = 4 * grp + i, key = k0 + 16 * grp + 4 * g + i;
-                    const int x0 = dpp_ror8(da0[i]), y0 = dpp_ror8(db0[i]), x1 = dpp_ror8(da1[i]), y1 = dpp_ror8(db1[i]);
-                    const float r0 = ((float)(lo8 ? da0[i] : x0) * 65536.f + (float)(lo8 ? x0 : da0[i]) * 256.f) + (float)(lo8 ? db0[i] : y0);
-                    const float r1 = ((float)(lo8 ? da1[i] : x1) * 65536.f + (float)(lo8 ? x1 : da1[i]) * 256.f) + (float)(lo8 ? db1[i] : y1);
-                    if (key < hi) {
-                        sc[j] = (r0 * kn[j].x + r1 * kn[j].y) * qs;
-                        vm = fmaxf(vm, fmaxf(vn[j].x, vn[j].y));
+                for (int it = 0; it < 8; it++) {
+                    const int kk = (lane >> 4) + 4 * it;  // 0..31
+                    const unsigned char* rw = rw0 + it * 4 * TQ_VB;
+                    const uint32_t Lw = *reinterpret_cast<const uint32_t*>(rw + 32 * hb + 4 * q);
+                    const uint32_t Hh = *reinterpret_cast<const uint16_t*>(rw + 64 + 16 * hb + 2 * q);
+                    uint32_t cd[4];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const uint32_t idx = t256[(Lw >> (8 * k)) & 0xffu] | t16[(Hh >> (4 * k)) & 15u];
+                        cd[k] = __builtin_amdgcn_perm(SV1, SV0, idx);
                     }
-                    mx = fmaxf(mx, sc[j]);
+                    *reinterpret_cast<uint4*>(Vc + kk * AHD + 16 * (pc ^ (4 * ((kk >> 2) & 3)))) =
+                        make_uint4(cd[0], cd[1], cd[2], cd[3]);
                 }
             }
-        }
-        mx = fmaxf(mx, __shfl_xor(mx, 16)); mx = fmaxf(mx, __shfl_xor(mx, 32));
-        if (g == 0 && lo8) mxw[wv][m16] = mx;
+            // ---- scores: both lanes of a head (m16, m16 ^ 8) recombine its digits ----
+            float sc[8];
 #pragma unroll
-        for (int o2 = 1; o2 < 64; o2 <<= 1) vm = fmaxf(vm, __shfl_xor(vm, o2));
-        if (lane == 0) vmw[wv] = vm;
-        __syncthreads();
-        const float VM = fmaxf(fmaxf(vmw[0], vmw[1]), fmaxf(vmw[2], vmw[3])) * TK3;
-        int ev = 0;
-        if (VM > 0.f) (void)frexpf(VM, &ev);  // VM < 2^ev: p * vn * K3 * 2^(10 - ev) < 2^10
-        const int sig = 10 - ev;
-        const float vsc = ldexpf(1.f, sig) * TK3;
-        const float sfac = c == 0 ? 1.f : ldexpf(1.f, sig - sig_ref);
-        sig_ref = sig;
-        // ---- pass 1.5: P of both V halves (hi/lo fp16) to LDS, running maxima, O rescale ----
-        {
-            const float M = fmaxf(fmaxf(mxw[0][hq], mxw[1][hq]), fmaxf(mxw[2][hq], mxw[3][hq]));
-            const float mn = fmaxf(mo, M);
-            float ls = 0.f;
-            if (has) {
-                half8_t p0v, p1v;
+            for (int grp = 0; grp < 2; grp++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int x0 = dpp_ror8(da0[grp][i]), y0 = dpp_ror8(db0[grp][i]);
+                    const int x1 = dpp_ror8(da1[grp][i]), y1 = dpp_ror8(db1[grp][i]);
+                    const float r0 = ((float)(lo8 ? da0[grp][i] : x0) * 65536.f + (float)(lo8 ? x0 : da0[grp][i]) * 256.f) +
+                                     (float)(lo8 ? db0[grp][i] : y0);
+                    const float r1 = ((float)(lo8 ? da1[grp][i] : x1) * 65536.f + (float)(lo8 ? x1 : da1[grp][i]) * 256.f) +
+                                     (float)(lo8 ? db1[grp][i] : y1);
+                    sc[4 * grp + i] = (r0 * kn[4 * grp + i].x + r1 * kn[4 * grp + i].y) * qs;
+                }
+            float vm;
+            if (c0 + kb + 32 <= ce) {
+                vm = 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; j++) vm = fmaxf(vm, fmaxf(vn[j].x, vn[j].y));
+            } else {
+                vm = 0.f;
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    const float p = mn == -INFINITY ? 0.f : fast_exp2(sc[j] - mn);  // 0 for masked keys
+                    const bool ok = c0 + kb + 16 * (j >> 2) + 4 * g + (j & 3) < ce;
+                    sc[j] = ok ? sc[j] : -INFINITY;
+                    vm = ok ? fmaxf(vm, fmaxf(vn[j].x, vn[j].y)) : vm;
+                }
+            }
+            float M = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+            M = max_x32(max_x16(M));
+            vm = max_x32(max_x16(vm)) * TK3;
+            // ---- lazy rescale ----
+            const float nref = M > mref + WS_SLACK ? M : mref;
+            const float fown = ex2d(mref, nref);
+            vmax = fmaxf(vmax, vm);
+            int ev = 0;
+            if (vmax > 0.f) (void)frexpf(vmax, &ev);  // vmax < 2^ev: p * vn * K3 * 2^(7 - ev) < 2^(7 + WS_SLACK)
+            const int nsig = 7 - ev;
+            if (__builtin_amdgcn_ballot_w64(fown != 1.f) != 0 || nsig != sig) {
+                const float sf = ldexpf(1.f, nsig - sig);
+                float fr[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) fr[i] = __shfl(fown, 2 * g + (i >> 1)) * sf;  // lane h holds head h
+#pragma unroll
+                for (int J = 0; J < 16; J++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) o[J][i] *= fr[i];
+                lacc *= fown;
+                mref = nref;
+                sig = nsig;
+            }
+            // ---- P of both V halves = 2^(s - mref) * vn * K3 * 2^sig as fp16 hi (m16 < 8) / lo (m16 >= 8) at row
+            // 2 * head + (m16 >= 8) ----
+            {
+                const float vsc = ldexpf(1.f, sig) * TK3;
+                half8_t p0v, p1v;
+                float ls = 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float p = fast_exp2(sc[j] - mref);
                     ls += p;
                     const float x0 = p * (vn[j].x * vsc), x1 = p * (vn[j].y * vsc);
                     const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
                     p0v[j] = lo8 ? h0 : (_Float16)(x0 - (float)h0);
                     p1v[j] = lo8 ? h1 : (_Float16)(x1 - (float)h1);
                 }
-                Pl[(0 * 4 + wv) * 64 + lane] = p0v;
-                Pl[(1 * 4 + wv) * 64 + lane] = p1v;
+                lacc += lo8 ? ls : 0.f;
+                const int row = 2 * hq + (lo8 ? 0 : 1);
+                Pw[16 * g + row] = p0v;
+                Pw[64 + 16 * g + row] = p1v;
             }
-            lacc = lacc * ex2d(mo, mn) + ls;
-            mo = mn;
+            // ---- O^T += P . V over these 32 keys: dims < 128 (pc 0, 1) with the half-0 P, the rest with half 1 ----
+            const half8_t pa0 = Pw[lane], pa1 = Pw[64 + lane];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int h = 4 * (g & 1) + i;
-                const float Mh = fmaxf(fmaxf(mxw[0][h], mxw[1][h]), fmaxf(mxw[2][h], mxw[3][h]));
-                const float mnh = fmaxf(m4[i], Mh);
-                const float f = ex2d(m4[i], mnh) * sfac;
-                m4[i] = mnh;
+            for (int pc = 0; pc < 4; pc++) {
+                const int rd = 16 * ((4 * pc + (m16 >> 2)) ^ (4 * g)) + 4 * (m16 & 3);
+                uint32_t r[8];
 #pragma unroll
-                for (int jt = 0; jt < 4; jt++) o[jt][i] *= f;
+                for (int j = 0; j < 8; j++)
+                    r[j] = *reinterpret_cast<const uint32_t*>(Vc + (16 * (j >> 2) + 4 * g + (j & 3)) * AHD + rd);
+                uint32_t c0v[4], c1v[4];
+                tr4x4_(r[0], r[1], r[2], r[3], c0v);
+                tr4x4_(r[4], r[5], r[6], r[7], c1v);
+#pragma unroll
+                for (int jt = 0; jt < 4; jt++)
+                    o[4 * pc + jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pc < 2 ? pa0 : pa1, i8x8_to_h8(c0v[jt], c1v[jt]),
+                                                                         o[4 * pc + jt], 0, 0, 0);
             }
         }
+        // ---- merge the four consumers (as gqa_ws_kernel) ----
+        const float l = sum_x32(sum_x16(lacc));
+        __syncthreads();  // every consumer is past its last chunk: the stages are free
+        if (lane < 8) { cm[wv][lane] = mref; cl[wv][lane] = l; }
         __syncthreads();
-        // ---- pass 2: O^T += P . V over the chunk's steps, this wavefront's dims ----
-        for (int st = 0; st < nsteps; st++) {
-            uint32_t r[8];
+        float* Ow = reinterpret_cast<float*>(smem);  // [consumer][head][256]
+        const float un = ldexpf(1.f, -sig);
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int key = 32 * st + 16 * (j >> 2) + 4 * g + (j & 3);
-                r[j] = *reinterpret_cast<const uint32_t*>(Vd + key * AHD + rd);
-            }
-            uint32_t c0v[4], c1v[4];
-            tr4x4_(r[0], r[1], r[2], r[3], c0v);
-            tr4x4_(r[4], r[5], r[6], r[7], c1v);
-            const half8_t pa = Pl[(vh * 4 + st) * 64 + lane];
+        for (int e = 0; e < 2; e++) {
+            const int h = 2 * g + e;
+            const float Mh = fmaxf(fmaxf(cm[0][h], cm[1][h]), fmaxf(cm[2][h], cm[3][h]));
+            const float f = ex2d(cm[wv][h], Mh) * un;
 #pragma unroll
-            for (int jt = 0; jt < 4; jt++) {
-                const half8_t vb = i8x8_to_h8(c0v[jt], c1v[jt]);
-                o[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[jt], 0, 0, 0);
-            }
+            for (int pc = 0; pc < 4; pc++)
+                *reinterpret_cast<float4*>(Ow + (wv * GQ + h) * AHD + 64 * pc + 4 * m16) =
+                    make_float4((o[4 * pc][2 * e] + o[4 * pc][2 * e + 1]) * f,
+                                (o[4 * pc + 1][2 * e] + o[4 * pc + 1][2 * e + 1]) * f,
+                                (o[4 * pc + 2][2 * e] + o[4 * pc + 2][2 * e + 1]) * f,
+                                (o[4 * pc + 3][2 * e] + o[4 * pc + 3][2 * e + 1]) * f);
         }
-    };
-    for (int c = 0; c < nch; c += 2) {
-        chunk(c, kA, knA, vnA, kB, knB, vnB);
-        if (c + 1 < nch) chunk(c + 1, kB, knB, vnB, kA, knA, vnA);
-    }
-    // ---- partials ----
-    __syncthreads();
-    {
-        float l = lo8 ? lacc : 0.f;
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
-        if (g == 0 && lo8) lsum[wv][m16] = l;
     }
     __syncthreads();
-    const float unscale = ldexpf(1.f, -sig_ref);
-    float ov[4][4];
+    for (int it = tid; it < GQ * 64; it += 64 * (WS_NC + WS_NP)) {
+        const float* Ow = reinterpret_cast<const float*>(smem);
+        const int h = it >> 6, d4 = 4 * (it & 63);
+        float4 a = *reinterpret_cast<const float4*>(Ow + h * AHD + d4);
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int jt = 0; jt < 4; jt++) ov[i][jt] = (o[jt][i] + __shfl_xor(o[jt][i], 32)) * unscale;
-    if (g < 2) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int h = 4 * g + i;
-            float* p = part_acc(part, tok, kvh * GQ + h, s, H, ns);
-            *reinterpret_cast<float4*>(p + 64 * wv + 4 * m16) = make_float4(ov[i][0], ov[i][1], ov[i][2], ov[i][3]);
-            if (wv == 0 && m16 == 0) {
-                float* ml = part_ml(part, tok, kvh * GQ + h, s, H, ns, T);
-                ml[0] = m4[i];
-                ml[1] = lsum[0][h] + lsum[1][h] + lsum[2][h] + lsum[3][h];
-            }
+        for (int w = 1; w < WS_NC; w++) {
+            const float4 b = *reinterpret_cast<const float4*>(Ow + (w * GQ + h) * AHD + d4);
+            a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+        }
+        *reinterpret_cast<float4*>(part_acc(part, tok, kvh * GQ + h, s, H, ns) + d4) = a;
+        if ((it & 63) == 0) {
+            const float Mh = fmaxf(fmaxf(cm[0][h], cm[1][h]), fmaxf(cm[2][h], cm[3][h]));
+            float* ml = part_ml(part, tok, kvh * GQ + h, s, H, ns, T);
+            ml[0] = Mh;  // -inf when the token has no key in this split
+            ml[1] = cl[0][h] * ex2d(cm[0][h], Mh) + cl[1][h] * ex2d(cm[1][h], Mh) + cl[2][h] * ex2d(cm[2][h], Mh) +
+                    cl[3][h] * ex2d(cm[3][h], Mh);
         }
     }
 }
 
 int gqa_splits(int T, int KV, int ns, bool turbo) {
-    // the int8 kernels run one workgroup per CU (one token, or a group of up to 4): beyond one workgroup per CU extra
-    // splits only add per-workgroup set-up and partials. Turbo runs two per CU.
-    if (turbo) return ns;
+    // the decode kernels run one workgroup per CU (int8: one token or a group of up to 4; turbo: one token): beyond one
+    // workgroup per CU extra splits only add per-workgroup set-up and partials
     static const int cus = [] {
         int dev = 0, v = 0;
         if (hipGetDevice(&dev) == hipSuccess &&
@@ -951,7 +984,7 @@ int gqa_splits(int T, int KV, int ns, bool turbo) {
             return v;
         return 256;
     }();
-    const int fill = cus / (KV * (T <= 2 ? 1 : (T + 3) / 4));
+    const int fill = cus / (KV * (turbo ? T : T <= 2 ? 1 : (T + 3) / 4));
     return fill < 1 ? 1 : (fill < ns ? fill : ns);
 }
 
@@ -959,12 +992,13 @@ void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos
                 int ns, hipStream_t st) {
     if (kv.turbo) {
         static bool once = [] {
-            MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_xt_kernel),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, XT_LDS));
+            MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_wst_kernel),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, WST_LDS));
             return true;
         }();
         (void)once;
-        hipLaunchKernelGGL(gqa_xt_kernel, dim3(KV * ns * T), dim3(256), XT_LDS, st, qo, kv, H, pos_d, max_t, part, T, ns);
+        hipLaunchKernelGGL(gqa_wst_kernel, dim3(KV * ns * T), dim3(64 * (WS_NC + WS_NP)), WST_LDS, st, qo, kv, H, pos_d,
+                           max_t, part, T, ns);
     } else {
         if (T == 1) {
             static bool once = [] {

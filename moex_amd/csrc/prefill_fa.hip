@@ -45,8 +45,8 @@ constexpr uint32_t V3T0 = pack4(-127, -79, -45, -14), V3T1 = pack4(14, 45, 79, 1
 __device__ __forceinline__ uint32_t lut16(uint32_t idx) {  // 4 nibble indices (one per byte) -> 4 biased K codes
     const uint32_t s = idx & 0x07070707u;
     const uint32_t lo = __builtin_amdgcn_perm(K4T1, K4T0, s), hi = __builtin_amdgcn_perm(K4T3, K4T2, s);
-    const uint32_t mask = ((idx >> 3) & 0x01010101u) * 0xffu;
-    return (hi & mask) | (lo & ~mask);
+    // byte b from hi when bit 3 of index b is set: selector b + 4 picks byte b of the first perm operand
+    return __builtin_amdgcn_perm(hi, lo, 0x03020100u | ((idx >> 1) & 0x04040404u));
 }
 // 4x4 byte transpose: r[k] = 4 bytes (dims) of key k -> c[d] = 4 bytes (keys) of dim d
 __device__ __forceinline__ void tr4x4(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3, uint32_t c[4]) {

@@ -61,13 +61,14 @@ def test_product_never_uses_the_oracle():
 
 
 def test_gqa_splits_policy():
-    """moex_attn_decode keeps ns for two query tokens (two workgroups per CU) and otherwise fills one workgroup per
-    CU (256 on MI355X, the fallback without a device) per token or four-token group, never above the caller's ns"""
+    """moex_attn_decode fills one workgroup per CU (256 on MI355X, the fallback without a device): per kv head and
+    int8 group of up to 4 tokens (one token or a pair alone), or per kv head and turbo token, never above ns"""
     import moex_amd as M
     assert M.gqa_splits(1, 2, 256) == 128
     assert M.gqa_splits(2, 2, 256) == 128
     assert M.gqa_splits(4, 2, 256) == 128
     assert M.gqa_splits(8, 2, 256) == 64
     assert M.gqa_splits(4, 2, 32) == 32
-    assert M.gqa_splits(4, 2, 256, turbo=1) == 256
+    assert M.gqa_splits(4, 2, 256, turbo=1) == 32
+    assert M.gqa_splits(1, 2, 256, turbo=1) == 128
     assert M.gqa_splits(64, 2, 256) == 8
