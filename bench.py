@@ -180,13 +180,36 @@ def main():
 
             t_k = time_rotating([gqa(c) for c in rot], 200)
             t_f = time_rotating([full(c) for c in rot], 200)
+            # the engine replays its decode step as a graph (moex.cu:1133): 32 steps (split kernel + combine) over the
+            # rotating caches captured once, replayed, timed per step
+            NG = 32
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for i in range(NG):
+                    c = rot[i % NROT]
+                    M.attn_gqa(qo[:Tq], c, H, KV, pd, c.max_t, part, Tq, ns)
+                    M.attn_combine(part, qg[:Tq], o1, H, ns, LD, Tq)
+            for _ in range(3):
+                graph.replay()
+            torch.cuda.synchronize()
+            e0, e1 = ev(), ev()
+            e0.record(torch.cuda.current_stream())
+            for _ in range(10):
+                graph.replay()
+            e1.record(torch.cuda.current_stream())
+            torch.cuda.synchronize()
+            t_g = e0.elapsed_time(e1) / (10 * NG)
+            del graph
             kv_bytes = 2.0 * ctx * 520
             dec[f"T{Tq}"] = {"ns": ns, "split_kernel_us": round(t_k * 1e3, 2), "with_combine_us": round(t_f * 1e3, 2),
+                             "graph_step_us": round(t_g * 1e3, 2),
                              "GBps": round(kv_bytes / (t_f * 1e-3) / 1e9, 1),
+                             "graph_GBps": round(kv_bytes / (t_g * 1e-3) / 1e9, 1),
                              "split_kernel_GBps": round(kv_bytes / (t_k * 1e-3) / 1e9, 1),
                              "hbm_frac": round(kv_bytes / (t_f * 1e-3) / 1e9 / PEAK_HBM, 4)}
             print(f"[bench] config2 decode T={Tq} ctx={ctx} ns={ns}: {t_f * 1e3:.1f} us "
-                  f"({dec[f'T{Tq}']['GBps']} GB/s; split kernel alone {t_k * 1e3:.1f} us)", flush=True)
+                  f"({dec[f'T{Tq}']['GBps']} GB/s; split kernel alone {t_k * 1e3:.1f} us; "
+                  f"graph-replayed step {t_g * 1e3:.1f} us = {dec[f'T{Tq}']['graph_GBps']} GB/s)", flush=True)
         del rot
         extra["config2_decode_int8_90k"] = dec
         # ---------------- config 1 depth comparison / config 4: turbo at 262k ----------------
