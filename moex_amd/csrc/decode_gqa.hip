@@ -654,18 +654,23 @@ __device__ __forceinline__ int4_t_ k_codes(uint2 x) {  // 16 nibbles -> the MFMA
 }
 
 // ---- gqa_wst_kernel: TurboQuant cache, one query token per workgroup, on gqa_ws_kernel's warp-specialised pipeline.
-// A stage holds a chunk's raw rows: K nibbles (row r keeps 16-byte piece p in slot p ^ ((r / 2) % 8), so the 8-byte
-// fragment reads of 16 rows at a 128-byte stride hit distinct banks), raw V rows (96 bytes, packed), and the K and V
-// half norms. Producers move them by DMA (36 transfers per chunk, 4-byte ones for the norms so every key index is
-// clamped); each consumer unpacks the V codes of its own 32 keys into a private int8 code area (gqa_ws_kernel's V
-// layout), so the chunk loop stays free of exchanges. Q.K packs the query digits 2 and 1 of the 8 heads into one
-// MFMA and digit 0 into a second, per 128-dim half, and recombines a head's digits with two row_ror:8 DPP moves; P
-// carries the V half norm, hi/lo rows interleaved.
+// Producers move each 128-key chunk by DMA (36 transfers per chunk, 4-byte ones for the norms so every key index is
+// clamped): the K nibble rows (row r keeps 16-byte piece p in slot p ^ ((r / 2) % 8), so the 8-byte fragment reads of
+// 16 rows at a 128-byte stride hit distinct banks) and the K and V half norms into one of three K stages, the raw V
+// rows (96 bytes, packed) into one of two raw V buffers. Producer j moves the raw V rows of keys 32j .. 32j + 31 and,
+// once they have landed, unpacks their 3-bit codes into consumer j's int8 code area for that chunk (gqa_ws_kernel's
+// V layout, two areas per consumer), so the unpacking runs beside the consumers' work on the previous chunk. Two
+// chunks are in flight: chunk c + 2 is issued at the barrier that starts chunk c. Q.K packs the query digits 2 and
+// 1 of the 8 heads into one MFMA and digit 0 into a second, per 128-dim half, and recombines a head's digits with
+// two row_ror:8 DPP moves; P carries the V half norm, hi/lo rows interleaved.
 constexpr int WST_KB = 128 * TQ_KB;                      // K nibble rows of a stage
-constexpr int WST_STAGE = WST_KB + 128 * TQ_VB + 2 * 128 * 8;  // + raw V rows + K norms + V norms
-constexpr int WST_VC = 32 * AHD;                         // one consumer's unpacked V codes
-constexpr int WST_LDS = WS_NS * WST_STAGE + WS_NC * WST_VC + WS_NC * 2 * 64 * 16 + 1024 + 64;
-static_assert(WS_NC * GQ * AHD * 4 <= WS_NS * WST_STAGE, "the consumer merge fits in the stages");
+constexpr int WST_NS = 3;                                // K stages
+constexpr int WST_STAGE = WST_KB + 2 * 128 * 8;          // K nibble rows + K norms + V norms
+constexpr int WST_RV = 128 * TQ_VB;                      // raw V rows of a chunk (two buffers)
+constexpr int WST_VC = 32 * AHD;                         // one consumer's unpacked V codes (two buffers)
+constexpr int WST_VC0 = WST_NS * WST_STAGE + 2 * WST_RV;  // offset of the V code areas
+constexpr int WST_LDS = WST_VC0 + 2 * WS_NC * WST_VC + WS_NC * 2 * 64 * 16 + WS_NP * 272 * 4;
+static_assert(WS_NC * GQ * AHD * 4 <= WST_NS * WST_STAGE, "the consumer merge fits in the stages");
 static_assert(WST_LDS <= 160 * 1024, "LDS");
 
 __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const float* __restrict__ qo, moex_kv_cache kv,
@@ -674,8 +679,6 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
                                                                          int ns) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float cm[WS_NC][GQ], cl[WS_NC][GQ];
-    uint32_t* t256 = reinterpret_cast<uint32_t*>(smem + WS_NS * WST_STAGE + WS_NC * WST_VC + WS_NC * 2 * 64 * 16);
-    uint32_t* t16 = t256 + 256;
     const int nb = gridDim.x, w_id = xcd_work_id(blockIdx.x, nb);
     const int tok = w_id % T, s = (w_id / T) % ns, kvh = w_id / (T * ns);
     const int pos0 = *pos_d, Tmax = pos0 + T;
@@ -685,25 +688,33 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
     const int first = hi > lo ? hi - lo - (nch - 1) * WS_CH : 0;  // chunk 0 is the short one
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 4, m16 = lane & 15;
     const size_t rbase = (size_t)kvh * max_t;
-    // bit-field spreading tables (read after the first chunk barrier): t256[b] = the four 2-bit fields of b, one per
-    // byte; t16[n] = bit e of n at bit 2 of byte e
-    if (tid < 256) {
-        const uint32_t b = tid;
-        t256[tid] = (b & 3u) | (((b >> 2) & 3u) << 8) | (((b >> 4) & 3u) << 16) | ((b >> 6) << 24);
-        if (tid < 16) t16[tid] = ((b & 1u) << 2) | (((b >> 1) & 1u) << 10) | (((b >> 2) & 1u) << 18) | ((b >> 3) << 26);
-    }
 
     if (wv >= WS_NC) {
         // ---- producers: transfer i (0..35) of a chunk goes to producer i % 4: 0-15 K rows (8 rows each), 16-27 raw
-        // V rows (1 KB of the packed rows each), 28-31 K norms, 32-35 V norms (64 floats each) ----
+        // V rows (1 KB of the packed rows each; producer j takes the 3 KB of keys 32j ..), 28-31 K norms, 32-35 V
+        // norms (64 floats each): 9 per producer ----
         const int pw = wv - WS_NC;
         const uint8_t* Kg = reinterpret_cast<const uint8_t*>(kv.k) + rbase * TQ_KB;
         const uint8_t* Vg = reinterpret_cast<const uint8_t*>(kv.v) + rbase * TQ_VB;
         const float* kng = kv.ks + 2 * rbase;
         const float* vng = kv.vs + 2 * rbase;
+        // this producer's bit-field spreading tables: t256[b] = the four 2-bit fields of b, one per byte; t16[n] = bit e
+        // of n at bit 2 of byte e
+        uint32_t* t256 = reinterpret_cast<uint32_t*>(smem + WST_VC0 + 2 * WS_NC * WST_VC + WS_NC * 2 * 64 * 16) + 272 * pw;
+        uint32_t* t16 = t256 + 256;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint32_t b = 64 * u + lane;
+            t256[b] = (b & 3u) | (((b >> 2) & 3u) << 8) | (((b >> 4) & 3u) << 16) | ((b >> 6) << 24);
+        }
+        if (lane < 16) {
+            const uint32_t b = lane;
+            t16[lane] = ((b & 1u) << 2) | (((b >> 1) & 1u) << 10) | (((b >> 2) & 1u) << 18) | ((b >> 3) << 26);
+        }
         auto issue = [&](int c) {
             const int c0 = c == 0 ? lo : lo + first + (c - 1) * WS_CH, ce = c == 0 ? lo + first : lo + first + c * WS_CH;
-            unsigned char* st = smem + (c % WS_NS) * WST_STAGE;
+            unsigned char* st = smem + (c % WST_NS) * WST_STAGE;
+            unsigned char* rv = smem + WST_NS * WST_STAGE + (c & 1) * WST_RV;
 #pragma unroll
             for (int u = 0; u < 9; u++) {
                 const int i = pw + 4 * u;
@@ -711,23 +722,49 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
                     const int r = 8 * i + (lane >> 3), piece = (lane & 7) ^ ((r >> 1) & 7);
                     __builtin_amdgcn_global_load_lds((gptr_t)(Kg + (size_t)min(c0 + r, ce - 1) * TQ_KB + 16 * piece),
                                                      (lptr_t)(st + i * 1024), 16, 0, 0);
-                } else if (i < 28) {
-                    const int b = (i - 16) * 1024 + 16 * lane, r = b / TQ_VB;
+                } else if (i < 28) {  // the raw V rows of keys 32 pw .. 32 pw + 31 (unpacked by this producer)
+                    const int piece = 3 * pw + (i - 16) / 4, b = piece * 1024 + 16 * lane, r = b / TQ_VB;
                     __builtin_amdgcn_global_load_lds((gptr_t)(Vg + (size_t)min(c0 + r, ce - 1) * TQ_VB + (b - r * TQ_VB)),
-                                                     (lptr_t)(st + WST_KB + (i - 16) * 1024), 16, 0, 0);
+                                                     (lptr_t)(rv + piece * 1024), 16, 0, 0);
                 } else {
                     const int f = 64 * (i & 3) + lane, key = min(c0 + (f >> 1), ce - 1);
                     __builtin_amdgcn_global_load_lds((gptr_t)((i < 32 ? kng : vng) + 2 * (size_t)key + (f & 1)),
-                                                     (lptr_t)(st + WST_KB + 128 * TQ_VB + (i < 32 ? 0 : 1024) + 256 * (i & 3)),
+                                                     (lptr_t)(st + WST_KB + (i < 32 ? 0 : 1024) + 256 * (i & 3)),
                                                      4, 0, 0);
                 }
             }
         };
         if (nch > 0) issue(0);
+        if (nch > 1) issue(1);
         for (int c = 0; c < nch; c++) {
-            wait_vm<0>();     // chunk c has landed
-            __syncthreads();  // ... and the consumers are done with chunk c - 1: its stage takes chunk c + 1
-            if (c + 1 < nch) issue(c + 1);
+            if (c + 1 < nch) wait_vm<9>();  // chunk c has landed (chunk c + 1 may still be in flight)
+            else wait_vm<0>();
+            const int c0 = c == 0 ? lo : lo + first + (c - 1) * WS_CH, ce = c == 0 ? lo + first : lo + first + c * WS_CH;
+            if (c0 + 32 * pw < ce) {
+                // V codes of keys 32 pw + 0..31 into consumer pw's code area of chunk c (its chunk c - 2 user is done):
+                // lane = (piece pc = lane % 16, keys lane / 16 + 4 it)
+                unsigned char* Vc = smem + WST_VC0 + ((c & 1) * WS_NC + pw) * WST_VC;
+                const int pc = lane & 15, hb = pc >> 3, q = pc & 7;
+                const unsigned char* rw0 = smem + WST_NS * WST_STAGE + (c & 1) * WST_RV + (32 * pw + (lane >> 4)) * TQ_VB;
+#pragma unroll
+                for (int it = 0; it < 8; it++) {
+                    const int kk = (lane >> 4) + 4 * it;  // 0..31
+                    const unsigned char* rw = rw0 + it * 4 * TQ_VB;
+                    const uint32_t Lw = *reinterpret_cast<const uint32_t*>(rw + 32 * hb + 4 * q);
+                    const uint32_t Hh = *reinterpret_cast<const uint16_t*>(rw + 64 + 16 * hb + 2 * q);
+                    uint32_t cd[4];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const uint32_t idx = t256[(Lw >> (8 * k)) & 0xffu] | t16[(Hh >> (4 * k)) & 15u];
+                        cd[k] = __builtin_amdgcn_perm(SV1, SV0, idx);
+                    }
+                    *reinterpret_cast<uint4*>(Vc + kk * AHD + 16 * (pc ^ (4 * ((kk >> 2) & 3)))) =
+                        make_uint4(cd[0], cd[1], cd[2], cd[3]);
+                }
+            }
+            __syncthreads();  // chunk c and its V codes are ready, and the consumers are done with chunk c - 1: its
+                              // K stage takes chunk c + 2, as does the raw V buffer of chunk c
+            if (c + 2 < nch) issue(c + 2);
         }
         __syncthreads();
         __syncthreads();
@@ -779,8 +816,7 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
                 }
             }
         }
-        unsigned char* Vc = smem + WS_NS * WST_STAGE + wv * WST_VC;  // this consumer's V codes (ws V layout)
-        half8_t* Pw = reinterpret_cast<half8_t*>(smem + WS_NS * WST_STAGE + WS_NC * WST_VC) + 128 * wv;  // [half][lane]
+        half8_t* Pw = reinterpret_cast<half8_t*>(smem + WST_VC0 + 2 * WS_NC * WST_VC) + 128 * wv;  // [half][lane]
         float4_t o[16];  // ws layout: row 2h (2h + 1) = hi (lo) part of head h
 #pragma unroll
         for (int J = 0; J < 16; J++) o[J] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -788,11 +824,12 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
         int sig = 0;
         const int kb = 32 * wv;
         for (int c = 0; c < nch; c++) {
-            __syncthreads();  // chunk c is in stage c % WS_NS
+            __syncthreads();  // chunk c is in K stage c % WST_NS, its V codes in area c % 2
             const int c0 = c == 0 ? lo : lo + first + (c - 1) * WS_CH, ce = c == 0 ? lo + first : lo + first + c * WS_CH;
             if (c0 + kb >= ce) continue;
-            const unsigned char* sb = smem + (c % WS_NS) * WST_STAGE;
-            const float2* skn = reinterpret_cast<const float2*>(sb + WST_KB + 128 * TQ_VB);
+            const unsigned char* sb = smem + (c % WST_NS) * WST_STAGE;
+            const unsigned char* Vc = smem + WST_VC0 + ((c & 1) * WS_NC + wv) * WST_VC;  // V codes (ws layout)
+            const float2* skn = reinterpret_cast<const float2*>(sb + WST_KB);
             const float2* svn = skn + 128;
             float2 kn[8], vn[8];
 #pragma unroll
@@ -823,26 +860,6 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
                         db1[grp] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qb[ks], db1[grp], 0, 0, 0);
                     }
                 }
-            // ---- V codes of this consumer's 32 keys: lane = (piece pc = lane % 16, keys lane / 16 + 4 it) ----
-            {
-                const int pc = lane & 15, hb = pc >> 3, q = pc & 7;
-                const unsigned char* rw0 = sb + WST_KB + (kb + (lane >> 4)) * TQ_VB;
-#pragma unroll
-                for (int it = 0; it < 8; it++) {
-                    const int kk = (lane >> 4) + 4 * it;  // 0..31
-                    const unsigned char* rw = rw0 + it * 4 * TQ_VB;
-                    const uint32_t Lw = *reinterpret_cast<const uint32_t*>(rw + 32 * hb + 4 * q);
-                    const uint32_t Hh = *reinterpret_cast<const uint16_t*>(rw + 64 + 16 * hb + 2 * q);
-                    uint32_t cd[4];
-#pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        const uint32_t idx = t256[(Lw >> (8 * k)) & 0xffu] | t16[(Hh >> (4 * k)) & 15u];
-                        cd[k] = __builtin_amdgcn_perm(SV1, SV0, idx);
-                    }
-                    *reinterpret_cast<uint4*>(Vc + kk * AHD + 16 * (pc ^ (4 * ((kk >> 2) & 3)))) =
-                        make_uint4(cd[0], cd[1], cd[2], cd[3]);
-                }
-            }
             // ---- scores: both lanes of a head (m16, m16 ^ 8) recombine its digits ----
             float sc[8];
 #pragma unroll
