@@ -53,8 +53,6 @@ __device__ __forceinline__ void tr4x4_(const uint32_t r0, const uint32_t r1, con
     c[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u); c[1] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
     c[2] = __builtin_amdgcn_perm(t3, t1, 0x05040100u); c[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
 }
-typedef __attribute__((address_space(1))) const void* gptr_t;
-typedef __attribute__((address_space(3))) void* lptr_t;
 
 // 2^(a - b) with 2^(-inf - -inf) = 1 (a running maximum that has not moved, also while it is still -inf)
 __device__ __forceinline__ float ex2d(float a, float b) { return a == b ? 1.f : fast_exp2(a - b); }
@@ -102,12 +100,6 @@ constexpr float WS_SLACK = 8.f;
 static_assert(WS_CH % 8 == 0 && WS_CH <= 128, "chunk shape");
 static_assert(WS_NC * GQ * AHD * 4 <= WS_STAGE, "the consumer merge fits in stage 0");
 static_assert(WS_LDS <= 160 * 1024, "LDS");
-// s_waitcnt with only vmcnt = n (expcnt, lgkmcnt left at their no-wait maxima)
-template <int n>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(n >= 0 && n < 64, "vmcnt");
-    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 // The producer side of gqa_ws_kernel / gqa_wsp_kernel: chunk c (keys [clo(c), chi(c)), chunk 0 the short one) ->
 // stage c % WS_NS. Producers 0, 1 move the K rows, 2, 3 the V rows (WS_CH/8 instructions of 4 rows each); producer j

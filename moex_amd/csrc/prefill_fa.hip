@@ -1,21 +1,23 @@
 // FlashAttention-2 chunked causal GQA prefill on gfx950 (replaces attn_fa_k<TB>, kernels.cuh:1443-1728).
 //
 // Workgroup = (kv head, 16 query tokens) = 128 query rows (8 heads x 16 tokens) and 8 wavefronts:
-//   - wavefronts 4-7 stage key tiles of 32: they load int8 (or turbo codes) K and V one tile ahead, widen them to
-//     fp16 and write them to LDS - K as [key][dim] (row stride padded to 528 B: conflict-free reads with immediate
-//     offsets), V transposed as [dim][key] and already multiplied by its row scale (int8: vs; turbo: half norm * K3),
-//     so P enters the P.V product as plain fp16 probabilities. Turbo K is likewise multiplied by its half norm * K4;
-//     int8 K stays exact and its scale is applied to the fp32 score;
+//   - wavefronts 4-7 fill LDS with key tiles of 32, widened to fp16: K as [key][dim] (row stride padded to 528 B:
+//     conflict-free reads with immediate offsets), V transposed as [dim][key] and already multiplied by its row scale
+//     (int8: vs; turbo: half norm * K3), so P enters the P.V product as plain fp16 probabilities. Turbo K is likewise
+//     multiplied by its half norm * K4; int8 K stays exact and its scale is applied to the fp32 score. For a chunk
+//     of at least 8 token tiles per kv head a pre-pass (fa_image_kernel) widens every tile once into a workspace and
+//     the wavefronts copy the images by DMA; for shorter chunks they load and widen each tile themselves;
 //   - wavefronts 0-3 compute, 32 query rows each (wavefront w: tokens 4w .. 4w+3, row r = (token 4w + r/8,
 //     head r%8)): S^T = K . Q^T and O^T += V^T . P^T on v_mfma_f32_32x32x16_f16 with Q fp16 in registers. The 32x32
 //     D layout gives each lane one query row (lane % 32) and 16 keys: row max / row sum are in-lane plus one
 //     cross-half swap. LDS operand reads are issued two MFMAs ahead of their use.
-// A SIMD holds one wavefront of each kind, so the staging VALU work runs beside the other's MFMAs; one barrier per
-// tile (double-buffered LDS).
+// A SIMD holds one wavefront of each kind, so the filling runs beside the other's MFMAs; one barrier per tile.
 // Lazy rescale: O and l are only rescaled when a row's maximum grows by more than 8 (log2 units) over the value the
 // probabilities are referenced to, so p <= 2^8 and the VALU touches O only then.
 // Softmax in base 2 (scale 1/sqrt(256) * log2(e), kernels.cuh:1513). Rounding: Q, P and the scaled V values are
 // fp16 MFMA operands with fp32 accumulation; the reference rounds Q and P * vscale (kernels.cuh:1508,1656).
+#include <map>
+#include <mutex>
 #include <type_traits>
 #include "common.hpp"
 
@@ -29,7 +31,10 @@ constexpr int KST = AHD + 8;                // K row stride in halves (528 B: ro
 constexpr int KT_BYTES = BK * KST * 2;      // 16.5 KB
 constexpr int VT_BYTES = AHD * VST * 2;     // 36 KB
 constexpr int SC_BYTES = BK * 4;            // per-key score scale
-constexpr int LDS_BYTES = 2 * KT_BYTES + 2 * VT_BYTES + 3 * SC_BYTES;  // 2 score-scale slots + a spare
+// One tile buffer in LDS: widened K rows, scaled V^T, the score scales and a spare slot. A tile image in global memory
+// (the pre-pass output) holds the same bytes, so a DMA copies it as is.
+constexpr int TILE_BYTES = KT_BYTES + VT_BYTES + 2 * SC_BYTES;  // 37632 B
+constexpr int FA_IMG_TILES = 8;             // token tiles per kv head from which the tile-image path is used
 constexpr float SL2 = 0.0625f * 1.4426950408889634f;
 constexpr float TK4 = 0.241529f / 127.f, TK3 = 0.190207f / 127.f;
 constexpr int FA_KPF = 2;                   // LDS operand reads in flight ahead of the MFMAs
@@ -221,18 +226,49 @@ int fa_grid(int KV, int T) {
 }
 }  // namespace
 
-// Warp-specialised workgroup of 8 wavefronts. Wavefronts 0-3 compute (32 query rows each); wavefronts 4-7 stage: they
-// load the next tiles' int8/turbo K and V, widen them and write them to the LDS buffers. Each SIMD holds one wavefront of
-// each kind, so the staging VALU work runs beside the other wavefront's MFMAs. One barrier per key tile: during tile j
-// the computing wavefronts read buffers j%2 while the staging wavefronts fill buffers (j+1)%2.
+// Tile images: one workgroup widens one 32-key tile of one kv head (keys past pos0 + T zeroed) into its LDS image,
+// with the staging wavefronts' code. The prefill kernel then copies images into LDS by DMA, so each tile is widened
+// once instead of once per token tile.
 template <bool TB>
+__global__ void __launch_bounds__(256) fa_image_kernel(moex_kv_cache kv, const int* __restrict__ pos_d, int T, int max_t,
+                                                       int ntmax, unsigned char* __restrict__ img) {
+    const int j = blockIdx.x, kvh = blockIdx.y, hi = *pos_d + T, k0 = j * BK, tid = threadIdx.x;
+    if (k0 >= hi) return;
+    const size_t rbase = (size_t)kvh * max_t;
+    unsigned char* t = img + ((size_t)kvh * ntmax + j) * TILE_BYTES;
+    float* sc = reinterpret_cast<float*>(t + KT_BYTES + VT_BYTES);
+    StageK sk;
+    StageV sv;
+    if (k0 + BK <= hi) {
+        load_k<TB, true>(sk, kv, rbase, k0, hi, tid);
+        load_v<TB, true>(sv, kv, rbase, k0, hi, tid);
+        store_k<TB, true>(sk, t, sc, sc + BK, k0, hi, tid);
+        store_v<TB, true>(sv, t + KT_BYTES, k0, hi, tid);
+    } else {
+        load_k<TB>(sk, kv, rbase, k0, hi, tid);
+        load_v<TB>(sv, kv, rbase, k0, hi, tid);
+        store_k<TB>(sk, t, sc, sc + BK, k0, hi, tid);
+        store_v<TB>(sv, t + KT_BYTES, k0, hi, tid);
+    }
+}
+
+// Warp-specialised workgroup of 8 wavefronts. Wavefronts 0-3 compute (32 query rows each); wavefronts 4-7 fill the LDS
+// tile buffers. Each SIMD holds one wavefront of each kind, so the filling runs beside the other wavefront's MFMAs. One
+// barrier per key tile.
+//   IMG = false: the staging wavefronts load the next tiles' int8/turbo K and V and widen them (two buffers: during
+//   tile j the computing wavefronts read buffer j%2 while the staging wavefronts fill buffer (j+1)%2).
+//   IMG = true: the tiles were widened by fa_image_kernel; the staging wavefronts only copy images into a ring of
+//   three buffers by DMA, two tiles ahead, leaving out the padding slots nobody reads.
+template <bool TB, bool IMG>
 __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restrict__ qo, const float* __restrict__ q_gate,
-                                                            moex_kv_cache kv, float* __restrict__ out, int H, int KV,
+                                                            moex_kv_cache kv, const unsigned char* __restrict__ img,
+                                                            int ntmax, float* __restrict__ out, int H, int KV,
                                                             const int* __restrict__ pos_d, int max_t, int ld, int T) {
     extern __shared__ __align__(16) unsigned char smem[];
-#define KBUF(i) (smem + (i) * KT_BYTES)
-#define VBUF(i) (smem + 2 * KT_BYTES + (i) * VT_BYTES)
-#define SBUF(i) (reinterpret_cast<float*>(smem + 2 * KT_BYTES + 2 * VT_BYTES) + (i) * BK)
+    constexpr int NB = IMG ? 3 : 2;
+#define KBUF(i) (smem + (i) * TILE_BYTES)
+#define VBUF(i) (smem + (i) * TILE_BYTES + KT_BYTES)
+#define SBUF(i) (reinterpret_cast<float*>(smem + (i) * TILE_BYTES + KT_BYTES + VT_BYTES))
     const int NT = (T + FT - 1) / FT;
     int kvh, tile;
     if (!map_block(blockIdx.x, KV, NT, kvh, tile)) return;
@@ -240,6 +276,42 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
     const size_t rbase = (size_t)kvh * max_t;
     const int ntiles = (hi + BK - 1) / BK;
 
+    if (threadIdx.x >= 256 && IMG) {
+        // ---------------- DMA wavefronts: image j -> buffer j % 3, 1 KB pieces i = pw, pw + 4, .. ----------------
+        const int pw = (threadIdx.x >> 6) - 4, lane = threadIdx.x & 63;
+        const unsigned char* src = img + (size_t)kvh * ntmax * TILE_BYTES + 16 * lane;
+        constexpr int NP = (TILE_BYTES + 1023) / 1024;  // 37 pieces, the last one partial
+        static_assert(NP == 37 && TILE_BYTES % 16 == 0, "image pieces");
+        auto issue = [&](int j) {
+            const unsigned char* g = src + (size_t)j * TILE_BYTES;
+            unsigned char* l = smem + (j % NB) * TILE_BYTES;
+#pragma unroll
+            for (int u = 0; u < 10; u++) {
+                const int i = pw + 4 * u, sl = 64 * i + lane;  // 16-byte slot of the image
+                // padding: slot 32 of each 33-slot K row, slot 4 of each 5-slot V^T row, the spare scales, the end
+                const bool pad = sl < KT_BYTES / 16 ? sl % 33 == 32
+                                 : sl < (KT_BYTES + VT_BYTES) / 16 ? (sl - KT_BYTES / 16) % 5 == 4
+                                                                   : sl >= (KT_BYTES + VT_BYTES + SC_BYTES) / 16;
+                if (i < NP && !pad)
+                    __builtin_amdgcn_global_load_lds((gptr_t)(g + i * 1024), (lptr_t)(l + i * 1024), 16, 0, 0);
+            }
+        };
+        // piece counts per wavefront: 10 for pw = 0 (pieces 0, 4, .., 36), 9 for the others
+        issue(0);
+        if (ntiles > 1) issue(1);
+        if (ntiles > 1) { if (pw == 0) wait_vm<10>(); else wait_vm<9>(); } else wait_vm<0>();
+        __syncthreads();  // image 0 is in buffer 0
+        for (int j = 0; j < ntiles; j++) {
+            if (j + 2 < ntiles) {
+                issue(j + 2);  // buffer (j + 2) % 3 held tile j - 1, which every computing wavefront is past
+                if (pw == 0) wait_vm<10>(); else wait_vm<9>();  // image j + 1 has landed
+            } else {
+                wait_vm<0>();
+            }
+            __syncthreads();
+        }
+        return;
+    }
     if (threadIdx.x >= 256) {
         // ---------------- staging wavefronts ----------------
         const int tid = threadIdx.x - 256;
@@ -247,7 +319,7 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
         StageV sv;
         load_k<TB>(sk, kv, rbase, 0, hi, tid);
         load_v<TB>(sv, kv, rbase, 0, hi, tid);
-        store_k<TB>(sk, KBUF(0), SBUF(0), SBUF(2), 0, hi, tid);
+        store_k<TB>(sk, KBUF(0), SBUF(0), SBUF(0) + BK, 0, hi, tid);
         store_v<TB>(sv, VBUF(0), 0, hi, tid);
         if (ntiles > 1) {
             load_k<TB>(sk, kv, rbase, BK, hi, tid);
@@ -255,14 +327,14 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
         }
         __syncthreads();
         for (int j = 0; j < ntiles; j++) {
-            const int k1 = (j + 1) * BK;
+            const int k1 = (j + 1) * BK, b = (j + 1) & 1;
             if (j + 1 < ntiles) {
                 if (k1 + BK <= hi) {
-                    store_k<TB, true>(sk, KBUF((j + 1) & 1), SBUF((j + 1) & 1), SBUF(2), k1, hi, tid);
-                    store_v<TB, true>(sv, VBUF((j + 1) & 1), k1, hi, tid);
+                    store_k<TB, true>(sk, KBUF(b), SBUF(b), SBUF(b) + BK, k1, hi, tid);
+                    store_v<TB, true>(sv, VBUF(b), k1, hi, tid);
                 } else {
-                    store_k<TB>(sk, KBUF((j + 1) & 1), SBUF((j + 1) & 1), SBUF(2), k1, hi, tid);
-                    store_v<TB>(sv, VBUF((j + 1) & 1), k1, hi, tid);
+                    store_k<TB>(sk, KBUF(b), SBUF(b), SBUF(b) + BK, k1, hi, tid);
+                    store_v<TB>(sv, VBUF(b), k1, hi, tid);
                 }
             }
             if (j + 2 < ntiles) {
@@ -311,9 +383,9 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
 
     for (int j = 0; j < ntiles; j++) {
         if (j < wtiles) {
-            const _Float16* Kt = reinterpret_cast<const _Float16*>(KBUF(j & 1));
-            const _Float16* Vt = reinterpret_cast<const _Float16*>(VBUF(j & 1));
-            const float* scl = SBUF(j & 1);
+            const _Float16* Kt = reinterpret_cast<const _Float16*>(KBUF(j % NB));
+            const _Float16* Vt = reinterpret_cast<const _Float16*>(VBUF(j % NB));
+            const float* scl = SBUF(j % NB);
             const int k0 = j * BK;
             // ---- S^T = K . Q^T: lane = (row r, key half h32), element i: key 8*(i/4) + 4*h32 + i%4 ----
             float16_t sc;
@@ -418,22 +490,72 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
         }
 }
 
-void launch_fa(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d,
-               int max_t, int ld, int T, hipStream_t st) {
+namespace {
+// Tile-image workspaces, one per (device, stream), grown on demand and kept until the process ends (a call that grows
+// one waits for the stream first). Calls on one stream are ordered, so they can share theirs.
+struct WsKey {
+    int dev;
+    hipStream_t st;
+    bool operator<(const WsKey& o) const { return dev != o.dev ? dev < o.dev : st < o.st; }
+};
+std::mutex g_ws_mu;
+std::map<WsKey, std::pair<unsigned char*, size_t>> g_ws;
+
+unsigned char* fa_workspace(size_t need, hipStream_t st) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    auto& w = g_ws[WsKey{dev, st}];
+    if (w.second >= need) return w.first;
+    if (w.first) {
+        MOEX_CK(hipStreamSynchronize(st));  // earlier calls on this stream may still read the old images
+        MOEX_CK(hipFree(w.first));
+        w = {nullptr, 0};
+    }
+    void* p = nullptr;
+    if (hipMalloc(&p, need) != hipSuccess) {
+        (void)hipGetLastError();  // out of memory: the caller widens in the kernel instead
+        return nullptr;
+    }
+    w = {static_cast<unsigned char*>(p), need};
+    return w.first;
+}
+
+template <bool TB, bool IMG>
+void set_lds() {
     static bool once = [] {
-        MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(fa_prefill_kernel<false>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES));
-        MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(fa_prefill_kernel<true>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES));
+        MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(fa_prefill_kernel<TB, IMG>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (IMG ? 3 : 2) * TILE_BYTES));
         return true;
     }();
     (void)once;
-    const int nb = fa_grid(KV, T);
-    if (kv.turbo)
-        hipLaunchKernelGGL(fa_prefill_kernel<true>, dim3(nb), dim3(512), LDS_BYTES, st, qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T);
-    else
-        hipLaunchKernelGGL(fa_prefill_kernel<false>, dim3(nb), dim3(512), LDS_BYTES, st, qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T);
+}
+
+template <bool TB>
+void launch_fa_t(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d,
+                 int max_t, int ld, int T, hipStream_t st) {
+    const int nb = fa_grid(KV, T), ntmax = (max_t + BK - 1) / BK;
+    unsigned char* img = nullptr;
+    if ((T + FT - 1) / FT >= FA_IMG_TILES) img = fa_workspace((size_t)KV * ntmax * TILE_BYTES, st);
+    if (img) {
+        set_lds<TB, true>();
+        hipLaunchKernelGGL(fa_image_kernel<TB>, dim3(ntmax, KV), dim3(256), 0, st, kv, pos_d, T, max_t, ntmax, img);
+        MOEX_LAUNCHED();
+        hipLaunchKernelGGL((fa_prefill_kernel<TB, true>), dim3(nb), dim3(512), 3 * TILE_BYTES, st, qo, q_gate, kv, img,
+                           ntmax, out, H, KV, pos_d, max_t, ld, T);
+    } else {
+        set_lds<TB, false>();
+        hipLaunchKernelGGL((fa_prefill_kernel<TB, false>), dim3(nb), dim3(512), 2 * TILE_BYTES, st, qo, q_gate, kv,
+                           nullptr, ntmax, out, H, KV, pos_d, max_t, ld, T);
+    }
     MOEX_LAUNCHED();
+}
+}  // namespace
+
+void launch_fa(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d,
+               int max_t, int ld, int T, hipStream_t st) {
+    if (kv.turbo) launch_fa_t<true>(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, st);
+    else launch_fa_t<false>(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, st);
 }
 
 }  // namespace moex
