@@ -9,7 +9,7 @@ Also reported (other configs of BASELINE.json, same JSON line): decode / MTP ver
 HBM GB/s over the 520 B/row KV, rotating over 4 caches that together exceed the MALL), TurboQuant decode at 262144, TurboQuant prefill at
 260096..262143 and the int8 chunk at the same depth, and config 0 (pos0 = 0).
 
-usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--decode-only] [--no-cpu]
 """
 import argparse
 import json
@@ -37,6 +37,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--quick", action="store_true", help="headline only")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the configs[2] and configs[3] decode timings (for counter runs); prints their JSON")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calib", action="store_true",
@@ -136,10 +138,11 @@ def main():
     def prefill():
         M.attn_fa(qo, qg, c8, out, H, KV, pos_d, c8.max_t, LD, T, st)
 
-    ms, wall_ms = time_steps(prefill, a.steps, a.warmup)
-    tflops = flops_prefill(T, pos0) / (ms * 1e-3) / 1e12
-    print(f"[bench] config1 int8 prefill T={T} pos0={pos0}: {ms:.3f} ms/step, {tflops:.1f} TFLOPS "
-          f"({100 * tflops / PEAK_F16:.1f}% of {PEAK_F16:.0f})", flush=True)
+    if not a.decode_only:
+        ms, wall_ms = time_steps(prefill, a.steps, a.warmup)
+        tflops = flops_prefill(T, pos0) / (ms * 1e-3) / 1e12
+        print(f"[bench] config1 int8 prefill T={T} pos0={pos0}: {ms:.3f} ms/step, {tflops:.1f} TFLOPS "
+              f"({100 * tflops / PEAK_F16:.1f}% of {PEAK_F16:.0f})", flush=True)
 
     traffic = None
     tf = os.path.join(ROOT, "profiles", "fa_prefill_int8_c1_traffic.json")
@@ -149,11 +152,13 @@ def main():
     extra = {}
     if not a.quick:
         # ---------------- config 0: pos0 = 0 ----------------
-        pz = torch.tensor([0], dtype=torch.int32, device=dev)
-        ms0, _ = time_steps(lambda: M.attn_fa(qo, qg, c8, out, H, KV, pz, c8.max_t, LD, T, st), 10, 3)
-        extra["config0_prefill_int8"] = {"ms": round(ms0, 4), "tflops": round(flops_prefill(T, 0) / ms0 / 1e9, 1)}
-        print(f"[bench] config0 int8 prefill pos0=0: {ms0:.3f} ms, {extra['config0_prefill_int8']['tflops']} TFLOPS",
-              flush=True)
+        if not a.decode_only:
+            pz = torch.tensor([0], dtype=torch.int32, device=dev)
+            ms0, _ = time_steps(lambda: M.attn_fa(qo, qg, c8, out, H, KV, pz, c8.max_t, LD, T, st), 10, 3)
+            extra["config0_prefill_int8"] = {"ms": round(ms0, 4),
+                                             "tflops": round(flops_prefill(T, 0) / ms0 / 1e9, 1)}
+            print(f"[bench] config0 int8 prefill pos0=0: {ms0:.3f} ms, "
+                  f"{extra['config0_prefill_int8']['tflops']} TFLOPS", flush=True)
         # ---------------- config 2: decode + MTP verify at 90k (int8) ----------------
         dec = {}
         ctx = 90000
@@ -233,6 +238,9 @@ def main():
         extra["config3_decode_turbo_262k"] = {"ns": ns, "us": round(t_td * 1e3, 2),
                                               "GBps": round(tb / (t_td * 1e-3) / 1e9, 1)}
         print(f"[bench] config3 turbo decode ctx={ctx}: {t_td * 1e3:.1f} us ({tb / t_td / 1e6:.0f} GB/s)", flush=True)
+        if a.decode_only:
+            print(json.dumps({"decode_only": True, **extra}), flush=True)
+            return
         p4 = torch.tensor([260096], dtype=torch.int32, device=dev)
         ms_t, _ = time_steps(lambda: M.attn_fa(qo, None, ct, out, H, KV, p4, ct.max_t, LD, T, st), 3, 1)
         ms_i, _ = time_steps(lambda: M.attn_fa(qo, qg, c8, out, H, KV, p4, c8.max_t, LD, T, st), 3, 1)
