@@ -8,7 +8,10 @@
  *   - fp16 weight pointers (qn, kn) are raw binary16 bit patterns (uint16_t);
  *   - raw kernel launches take their grid-defining sizes (T, ns) explicitly instead of a <<<grid>>>.
  * All pointers are device pointers unless stated otherwise. Nothing allocates or synchronizes except
- * moex_kv_alloc / moex_kv_free, so every attention call can be captured into a HIP graph.
+ * moex_kv_alloc / moex_kv_free and moex_attn_fa with T >= 128: that call widens the K/V tiles once into a tile-image
+ * workspace of KV * ceil(max_t / 32) * 37632 bytes, one per (device, stream), allocated on the first such call on a
+ * stream and grown (after waiting for the stream) when a larger max_t comes; it is kept until the process ends.
+ * After one eager call of a given max_t on a stream, every attention call can be captured into a HIP graph.
  *
  * Errors (kernels.cuh:8-11, CK): a failing HIP call prints "HIP <error> at <file>:<line>" and exits(1),
  * unless a soft-error slot is installed (moex_set_soft_error), in which case the first error code is

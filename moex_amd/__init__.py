@@ -63,6 +63,9 @@ def lib():
     L.moex_gqa_splits.argtypes = [i, i, i, i]
     L.moex_gqa_splits.restype = i
     L.moex_version.restype = ctypes.c_char_p
+    L.moex_quantize_rows_i8.argtypes = [vp, vp, vp, i, i, vp]
+    L.moex_gemv_i8.argtypes = [vp, vp, vp, vp, i, i, vp]
+    L.moex_gemm_i8.argtypes = [vp, vp, vp, vp, i, i, i, vp]
     _lib = L
     return L
 
@@ -70,7 +73,8 @@ def lib():
 EXPORTS = ["moex_kv_alloc", "moex_kv_bytes", "moex_kv_free", "moex_attn_decode", "moex_attn_fa", "moex_attn_prefill",
            "moex_qk_norm_rope", "moex_kv_append", "moex_attn_gqa", "moex_attn_combine", "moex_attn_decode_heads",
            "moex_turbo_out", "moex_set_int", "moex_set_soft_error", "moex_set_skip", "moex_fa_on",
-           "moex_fa_supported", "moex_decode_splits", "moex_gqa_splits", "moex_version"]
+           "moex_fa_supported", "moex_decode_splits", "moex_gqa_splits", "moex_version",
+           "moex_quantize_rows_i8", "moex_gemv_i8", "moex_gemm_i8"]
 
 
 def _p(x):
@@ -201,3 +205,19 @@ def fa_on():
 
 def fa_supported():
     return bool(lib().moex_fa_supported())
+
+
+# ---- dense int8 projections (include/moex_dense.h): the qkv projection before attn_decode, o_proj after it ----
+def quantize_rows_i8(W, q, s, O, I, st=None):
+    """quantize_rows_i8_k (kernels.cuh:144-156): fp16 W [O][I] -> int8 q [O][I] + fp32 s [O] (absmax/127)."""
+    lib().moex_quantize_rows_i8(_p(W), _p(q), _p(s), O, I, _s(st))
+
+
+def gemv_i8(q, s, x, y, I, O, st=None):
+    """gemv(Mat{q, s}, x, y, I, O) (kernels.cuh:214-219, gemv_i8 :98-141): y = s * (q . x)."""
+    lib().moex_gemv_i8(_p(q), _p(s), _p(x), _p(y), I, O, _s(st))
+
+
+def gemm_i8(q, s, X, Y, S, I, O, st=None):
+    """gemm(Mat{q, s}, X, Y, S, I, O) (kernels.cuh:339-350): S <= 8 one GEMV pass, else the fp16 MFMA GEMM."""
+    lib().moex_gemm_i8(_p(q), _p(s), _p(X), _p(Y), S, I, O, _s(st))

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include "../../include/moex_attn.h"
+#include "../../include/moex_dense.h"
 
 namespace moex {
 
@@ -89,6 +90,10 @@ void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos
                 int ns, hipStream_t st);
 void launch_fa(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d,
                int max_t, int ld, int T, hipStream_t st);
+// dense int8 projections (dense.hip)
+void launch_quantize_rows_i8(const uint16_t* W, int8_t* q, float* s, int O, int I, hipStream_t st);
+void launch_gemv_i8(const int8_t* q, const float* s, const float* x, float* y, int NT, int I, int O, hipStream_t st);
+void launch_gemm_i8(const int8_t* q, const float* s, const float* X, float* Y, int S, int I, int O, hipStream_t st);
 void launch_prefill_k7p(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
                         const int* pos_d, int max_t, int ld, int T, hipStream_t st);
 }  // namespace moex

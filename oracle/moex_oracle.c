@@ -25,6 +25,12 @@
  *   orc_attn_row_fa_emul   not a parity target: it models the rounding points of attn_fa_k
  *                          (kernels.cuh:1508,1513,1656-1661) to estimate the reference kernel's error.
  *   orc_qk_norm_rope_row   tolerance only (rsqrtf/powf/sinf/cosf bits are parity unpinned).
+ *   orc_quantize_rows_i8   pinned: closed form (max |w| is order-free, IEEE divide, round-half-even), checked
+ *                          against numpy on random and edge rows in tests/test_oracle.py.
+ *   orc_dense_i8_f64       pinned: the exact product of the int8 rows with fp32 inputs in fp64, checked against
+ *                          numpy's float64 matmul in tests/test_oracle.py.
+ *   orc_dense_i8_fp16x     not a parity target: the precision model of the prefill GEMM (activations rounded to
+ *                          fp16, kernels.cuh:250,306-307), used to bound the reference kernel's error.
  */
 #include <math.h>
 #include <stdint.h>
@@ -388,4 +394,42 @@ void orc_qk_norm_rope_row(const float* x, const uint16_t* w, int pos, int rot, f
                 if (!(j & h)) { const double a = v[j], c = v[j + h]; v[j] = a + c; v[j + h] = a - c; }
         for (int j = 0; j < 128; j++) out[b * 128 + j] = (float)(v[j] / sqrt(128.0) * S2[j]);
     }
+}
+
+/* ---- dense int8 projections (the attention's qkv and o projections: kernels.cuh:186-196 Mat, :98-141 gemv_i8,
+ * :143-156 quantize_rows_i8_k, :250-337 gemm) ---- */
+
+/* quantize_rows_i8_k (kernels.cuh:144-156): fp16 rows [O][I] -> int8 [O][I] + a scale per row, absmax / 127
+ * (1 for an all-zero row), q = round-half-even(w / scale) with the IEEE binary32 quotient. */
+void orc_quantize_rows_i8(const uint16_t* W, long O, long I, int8_t* q, float* s) {
+    for (long o = 0; o < O; o++) {
+        const uint16_t* wr = W + o * I;
+        float m = 0.f;
+        for (long i = 0; i < I; i++) { const float a = fabsf(h2f(wr[i])); if (a > m) m = a; }
+        const float sc = m > 0.f ? m / 127.f : 1.f;
+        for (long i = 0; i < I; i++) q[o * I + i] = (int8_t)(int)rintf(h2f(wr[i]) / sc);
+        s[o] = sc;
+    }
+}
+
+/* The exact product y[t][o] = s[o] * sum_i q[o][i] * x[t][i], summed in fp64 and rounded once
+ * (tests/test_kernels.cu:373: the reference's "exact int8 reference" of gemv_i8). */
+void orc_dense_i8_f64(const int8_t* q, const float* s, const float* x, long S, long I, long O, double* y) {
+    for (long t = 0; t < S; t++)
+        for (long o = 0; o < O; o++) {
+            double a = 0;
+            for (long i = 0; i < I; i++) a += (double)q[o * I + i] * x[t * I + i];
+            y[t * O + o] = a * s[o];
+        }
+}
+
+/* The prefill GEMM's rounding points (kernels.cuh:306-307: activations to fp16; the int8 weights are exact in
+ * fp16; fp32 accumulation, here exact in fp64): y = s[o] * sum_i q[o][i] * fp16(x[t][i]). */
+void orc_dense_i8_fp16x(const int8_t* q, const float* s, const float* x, long S, long I, long O, double* y) {
+    for (long t = 0; t < S; t++)
+        for (long o = 0; o < O; o++) {
+            double a = 0;
+            for (long i = 0; i < I; i++) a += (double)q[o * I + i] * orc_round_f16(x[t * I + i]);
+            y[t * O + o] = a * s[o];
+        }
 }

@@ -51,6 +51,9 @@ def lib():
         L.orc_attn_rows_f64.argtypes = rows_args
         L.orc_attn_rows_fa_emul.argtypes = rows_args
         L.orc_qk_norm_rope_row.argtypes = [_f32p, _u16p, c.c_int, c.c_int, c.c_float, c.c_float, c.c_int, _f32p]
+        L.orc_quantize_rows_i8.argtypes = [_u16p, c.c_long, c.c_long, _i8p, _f32p]
+        L.orc_dense_i8_f64.argtypes = [_i8p, _f32p, _f32p, c.c_long, c.c_long, c.c_long, _f64p]
+        L.orc_dense_i8_fp16x.argtypes = [_i8p, _f32p, _f32p, c.c_long, c.c_long, c.c_long, _f64p]
         _lib = L
     return _lib
 
@@ -154,3 +157,33 @@ def qk_norm_rope_row(x, w_f16_bits, pos, rot, theta, eps, wht_fwd=False):
     lib().orc_qk_norm_rope_row(np.ascontiguousarray(x, np.float32), np.ascontiguousarray(w_f16_bits, np.uint16),
                                pos, rot, theta, eps, 1 if wht_fwd else 0, out)
     return out
+
+
+# ---- dense int8 projections ----
+def quantize_rows_i8(w16):
+    """quantize_rows_i8_k (kernels.cuh:144-156): fp16 [O][I] (np.float16) -> (int8 [O][I], float32 [O])."""
+    w16 = np.ascontiguousarray(w16, np.float16)
+    O, I = w16.shape
+    q = np.zeros((O, I), np.int8); s = np.zeros(O, np.float32)
+    lib().orc_quantize_rows_i8(w16.view(np.uint16).reshape(-1), O, I, q.reshape(-1), s)
+    return q, s
+
+
+def dense_i8_f64(q, s, x):
+    """y [S][O] = s * (q . x), exact in fp64 (x: float32 [S][I])."""
+    q = np.ascontiguousarray(q, np.int8); s = np.ascontiguousarray(s, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    O, I = q.shape; S = x.shape[0]
+    y = np.zeros((S, O), np.float64)
+    lib().orc_dense_i8_f64(q.reshape(-1), s, x.reshape(-1), S, I, O, y.reshape(-1))
+    return y
+
+
+def dense_i8_fp16x(q, s, x):
+    """The prefill GEMM's precision model: activations rounded to fp16, products exact, fp64 sums."""
+    q = np.ascontiguousarray(q, np.int8); s = np.ascontiguousarray(s, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    O, I = q.shape; S = x.shape[0]
+    y = np.zeros((S, O), np.float64)
+    lib().orc_dense_i8_fp16x(q.reshape(-1), s, x.reshape(-1), S, I, O, y.reshape(-1))
+    return y

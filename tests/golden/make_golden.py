@@ -50,10 +50,23 @@ def attn_case(turbo, seed):
     return dict(kc=c.k, vc=c.v, ks=c.ks, vs=c.vs, qo=qo, qg=qg, pos0=np.int32(pos0), out=out.astype(np.float64))
 
 
+def dense_case(seed):
+    """A 24 x 512 fp16 weight block (incl. a zero row and a constant row), its int8 rows and scales, and the exact
+    products with 3 input rows."""
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((24, 512)) * np.geomspace(1e-3, 1, 24)[:, None]).astype(np.float16)
+    w[1] = 0
+    w[2] = np.float16(0.125)
+    q, s = orc.quantize_rows_i8(w)
+    x = rng.standard_normal((3, 512)).astype(np.float32)
+    return dict(w=w, q=q, s=s, x=x, y=orc.dense_i8_f64(q, s, x))
+
+
 def main():
     for turbo in (0, 1):
         np.savez_compressed(os.path.join(HERE, f"append_{'turbo' if turbo else 'int8'}.npz"), **append_case(turbo, 100 + turbo))
         np.savez_compressed(os.path.join(HERE, f"attn_{'turbo' if turbo else 'int8'}.npz"), **attn_case(turbo, 200 + turbo))
+    np.savez_compressed(os.path.join(HERE, "dense_i8.npz"), **dense_case(300))
     print("written:", sorted(f for f in os.listdir(HERE) if f.endswith(".npz")))
 
 

@@ -1,5 +1,5 @@
-"""CPU checks of the C ABI: the library loads and exports every entry point include/moex_attn.h declares, the host
-mirror keeps the reference's names, and the product path never touches the oracle."""
+"""CPU checks of the C ABI: the library loads and exports every entry point include/*.h declares, the host mirror
+keeps the reference's names, and the product path never touches the oracle."""
 import os
 import re
 
@@ -9,15 +9,20 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def _declared():
-    txt = open(os.path.join(ROOT, "include", "moex_attn.h")).read()
-    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
-    return sorted(set(re.findall(r"\b(moex_[a-z0-9_]+)\s*\(", txt)))
+    names = set()
+    for h in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if h.endswith(".h"):
+            txt = open(os.path.join(ROOT, "include", h)).read()
+            txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+            names |= set(re.findall(r"\b(moex_[a-z0-9_]+)\s*\(", txt))
+    return sorted(names)
 
 
 def test_header_declares_the_reference_entry_points():
     names = _declared()
     for n in ("moex_attn_decode", "moex_attn_fa", "moex_attn_prefill", "moex_kv_alloc", "moex_kv_bytes",
-              "moex_attn_gqa", "moex_attn_combine", "moex_attn_decode_heads", "moex_turbo_out", "moex_qk_norm_rope"):
+              "moex_attn_gqa", "moex_attn_combine", "moex_attn_decode_heads", "moex_turbo_out", "moex_qk_norm_rope",
+              "moex_quantize_rows_i8", "moex_gemv_i8", "moex_gemm_i8"):
         assert n in names
 
 

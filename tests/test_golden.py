@@ -34,3 +34,11 @@ def test_oracle_attention_matches_golden(orc, fmt, turbo):
     rows = [(t, h) for t in range(T) for h in range(H)]
     out = orc.attn_rows_f64(g["qo"], None if turbo else g["qg"], LD, H, c, int(g["pos0"]), rows).reshape(T, H, AHD)
     assert np.max(np.abs(out - g["out"])) <= 1e-12 * np.max(np.abs(g["out"]))
+
+
+def test_oracle_dense_matches_golden(orc):
+    g = np.load(os.path.join(GOLD, "dense_i8.npz"))
+    q, s = orc.quantize_rows_i8(g["w"])
+    assert np.array_equal(q, g["q"]) and np.array_equal(s.view(np.uint32), g["s"].view(np.uint32))
+    y = orc.dense_i8_f64(q, s, g["x"])
+    assert np.abs(y - g["y"]).max() <= 1e-12 * np.abs(g["y"]).max()

@@ -268,3 +268,45 @@ def test_qk_norm_rope_front(orc):
     # angle of pair j = pos * theta^(-2j/rot): the first pair rotates by exactly pos radians
     a0 = np.arctan2(yn[32], yn[0]); a1 = np.arctan2(y[32], y[0])
     assert abs(((a1 - a0 - 12345) + np.pi) % (2 * np.pi) - np.pi) < 1e-3
+
+
+# ---- dense int8 projections (kernels.cuh:144-156 quantize_rows_i8_k, :98-141 gemv_i8) ----
+def test_quantize_rows_closed_form(orc):
+    """absmax / 127 per row (1 for a zero row), round-half-even of the binary32 quotient: numpy restates it."""
+    rng = np.random.default_rng(31)
+    w = (rng.standard_normal((40, 512)) * np.geomspace(1e-4, 10, 40)[:, None]).astype(np.float16)
+    w[3] = 0
+    w[4] = np.float16(0.25)                       # constant row: every quotient exactly 127
+    w[5, :] = 0; w[5, 10] = np.float16(-2.5)      # one non-zero: +-127 and zeros
+    w[6, :8] = np.float16(65504); w[6, 8:] = np.float16(-6e-8)  # the fp16 extremes
+    q, s = orc.quantize_rows_i8(w)
+    wf = w.astype(np.float32)
+    m = np.abs(wf).max(1)
+    sc = np.where(m > 0, m / np.float32(127), np.float32(1)).astype(np.float32)
+    assert np.array_equal(s.view(np.uint32), sc.view(np.uint32))
+    assert np.array_equal(q, np.rint(wf / sc[:, None]).astype(np.int8))
+    assert np.all(q[4] == 127) and q[5, 10] == -127 and np.all(q[3] == 0) and s[3] == 1.0
+
+
+def test_quantize_rows_ties(orc):
+    """quotients landing exactly on .5 round to even (the scale makes q = w / s exact for these rows)."""
+    w = np.zeros((1, 256), np.float16)
+    w[0, 0] = np.float16(127.0)                    # scale 1
+    w[0, 1:6] = np.array([0.5, 1.5, 2.5, -0.5, -3.5], np.float16)
+    q, s = orc.quantize_rows_i8(w)
+    assert s[0] == 1.0 and list(q[0, :6]) == [127, 0, 2, 2, 0, -4]
+
+
+def test_dense_exact_product(orc):
+    """fp64 sums of int8 x fp32 products are exact for I <= 2^20 terms of 24+8 bits: equal to numpy float64."""
+    rng = np.random.default_rng(32)
+    q = rng.integers(-127, 128, (37, 1024), dtype=np.int8)
+    s = rng.uniform(1e-3, 1e-2, 37).astype(np.float32)
+    x = rng.standard_normal((5, 1024)).astype(np.float32)
+    y = orc.dense_i8_f64(q, s, x)
+    ref = (x.astype(np.float64) @ q.T.astype(np.float64)) * s.astype(np.float64)
+    assert np.abs(y - ref).max() <= 1e-12 * np.abs(ref).max()
+    # the fp16-activation model differs from it exactly by rounding x
+    y16 = orc.dense_i8_fp16x(q, s, x)
+    ref16 = (x.astype(np.float16).astype(np.float64) @ q.T.astype(np.float64)) * s.astype(np.float64)
+    assert np.abs(y16 - ref16).max() <= 1e-12 * np.abs(ref16).max()
