@@ -105,15 +105,15 @@ void moex_quantize_rows_i8(const uint16_t* W, int8_t* q, float* s, int O, int I,
 }
 
 void moex_gemv_i8(const int8_t* q, const float* s, const float* x, float* y, int I, int O, void* stream) {
-    MOEX_REQUIRE(O > 0 && I > 0 && I % 512 == 0 && I <= 40960, "gemv_i8 needs I % 512 == 0 and I <= 40960");
+    MOEX_REQUIRE(O > 0 && I > 0 && I % 512 == 0 && I <= 40448, "gemv_i8 needs I % 512 == 0 and I <= 40448");
     launch_gemv_i8(q, s, x, y, 1, I, O, S(stream));
 }
 
 void moex_gemm_i8(const int8_t* q, const float* s, const float* X, float* Y, int S_, int I, int O, void* stream) {
     MOEX_REQUIRE(O > 0 && I > 0 && S_ > 0, "S, I, O");
     if (S_ <= 8) {  // kernels.cuh:341-349: one GEMV pass for the MTP / draft rows
-        MOEX_REQUIRE(I % 512 == 0 && I <= 40960, "gemm_i8 with S <= 8 needs I % 512 == 0 and I <= 40960");
-        const int per = 40960 / I;  // input rows that fit in LDS (160 KB of fp32) per pass
+        MOEX_REQUIRE(I % 512 == 0 && I <= 40448, "gemm_i8 with S <= 8 needs I % 512 == 0 and I <= 40448");
+        const int per = 40448 / I;  // input rows that fit in LDS (160 KB of fp32 less the partial sums) per pass
         for (int t0 = 0; t0 < S_;) {
             const int nt = S_ - t0 < per ? S_ - t0 : per;
             launch_gemv_i8(q, s, X + (size_t)t0 * I, Y + (size_t)t0 * O, nt, I, O, S(stream));

@@ -4,10 +4,11 @@
 //   quantize_rows_kernel   fp16 [O][I] -> int8 [O][I] + scale absmax/127 per row (bit-exact: IEEE divide, rint).
 //   gemv_kernel<NT>        y[t][o] = s[o] * sum_i q[o][i] x[t][i] for NT <= 8 rows of x, fp32 sums. HBM-bound on the
 //                          weights, which are read once for all NT rows. The NT input rows sit in LDS; a wavefront
-//                          takes 8 weight rows at a time, its lanes walking I in dwords (256 contiguous bytes per row
-//                          and instruction), and reduces each sum across the wavefront. The assignment of rows and of
-//                          the sum order to lanes does not depend on NT, so any row of a multi-row call is
-//                          bit-identical to the same row alone.
+//                          takes 8 weight rows over 1/KS of I, its lanes walking it in 16-byte chunks (1 KB contiguous
+//                          per row and instruction, 16 KB per wavefront issued before any product), reduces each
+//                          sum across the wavefront, and the KS parts of a row are added in LDS. KS and the sum order
+//                          depend on O and I only, so any row of a multi-row call is bit-identical to the same row
+//                          alone.
 //   gemm_kernel            S > 8 rows (prefill): Y = X . W^T * s on v_mfma_f32_32x32x16_f16. Weights are widened to
 //                          fp16 exactly (integers), activations rounded to fp16 as the reference does
 //                          (kernels.cuh:306-307), fp32 accumulation, the row scale applied last. Workgroup tile 128
@@ -45,53 +46,158 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* __re
     if (threadIdx.x == 0) s[row] = sc;
 }
 
-constexpr int GV_R = 8;       // weight rows a wavefront takes at a time
-constexpr int GV_WAVES = 4;   // wavefronts per workgroup
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int GV_R = 8;       // weight rows of a row group
+// 16-byte chunks per lane and row loaded before any is used: 16 KB per wavefront in flight, 8 KB from NT = 5 on
+// (registers)
+template <int NT> constexpr int gv_u() { return NT <= 4 ? 2 : 1; }
+constexpr int GV_WAVES = 8;   // wavefronts per workgroup
 
-// Workgroup b takes row groups b, b + nb, .. (GV_R rows each), its wavefronts one group at a time.
+// A grid of nb workgroups; in round j, wavefront wv of workgroup b takes row group b + nb * (wv / KS + j * 8 / KS)
+// over the KS-th part wv % KS of I, and the KS partial sums of a group are added in LDS in part order. KS (1, 2, 4
+// or 8) depends on O and I only, so the sum order of a row never depends on NT.
 template <int NT>
 __global__ void __launch_bounds__(64 * GV_WAVES) gemv_kernel(const int8_t* __restrict__ q, const float* __restrict__ s,
                                                              const float* __restrict__ x, float* __restrict__ y, int I,
-                                                             int O) {
-    extern __shared__ __align__(16) float xs[];  // [NT][I]
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+                                                             int O, int KS) {
+    constexpr int GV_U = gv_u<NT>();
+    extern __shared__ __align__(16) float xs[];  // [NT][I], then the partial sums [GV_WAVES][NT][GV_R]
+    float* red = xs + NT * I;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nb = gridDim.x;
+    const int ngroups = (O + GV_R - 1) / GV_R, gpr = GV_WAVES / KS;  // groups per workgroup and round
+    const int rounds = (ngroups + nb * gpr - 1) / (nb * gpr);
+    const int part = wv % KS, slice = I / 16 / KS, cb = part * slice, ce = cb + slice;  // 16-byte chunks of a row
+    u32x4 w[GV_U][GV_R];
+#define GV_LOAD(g_, c0_)                                                                                         \
+    do {                                                                                                         \
+        _Pragma("unroll") for (int u = 0; u < GV_U; u++)                                                         \
+        _Pragma("unroll") for (int r = 0; r < GV_R; r++) {                                                       \
+            const u32x4* row_ = reinterpret_cast<const u32x4*>(q + (size_t)min((g_) * GV_R + r, O - 1) * I);     \
+            const int c_ = (c0_) + 64 * u + lane;                                                                \
+            w[u][r] = c_ < ce ? __builtin_nontemporal_load(row_ + c_) : u32x4{0u, 0u, 0u, 0u};                  \
+        }                                                                                                        \
+    } while (0)
     for (int e = tid; e < NT * I / 4; e += 64 * GV_WAVES)
         reinterpret_cast<float4*>(xs)[e] = reinterpret_cast<const float4*>(x)[e];
     __syncthreads();
-    const int ngroups = (O + GV_R - 1) / GV_R;
-    for (int g = blockIdx.x * GV_WAVES + wv; g < ngroups; g += gridDim.x * GV_WAVES) {
-        const int r0 = g * GV_R;
-        float acc[NT][GV_R];
+    for (int j = 0; j < rounds; j++) {
+        const int g = blockIdx.x + nb * (wv / KS + j * gpr);
+        if (g < ngroups) {
+            float acc[NT][GV_R];
 #pragma unroll
-        for (int t = 0; t < NT; t++)
+            for (int t = 0; t < NT; t++)
 #pragma unroll
-            for (int r = 0; r < GV_R; r++) acc[t][r] = 0.f;
-        const uint32_t* qr[GV_R];
+                for (int r = 0; r < GV_R; r++) acc[t][r] = 0.f;
+            for (int c0 = cb; c0 < ce; c0 += 64 * GV_U) {
+                GV_LOAD(g, c0);
 #pragma unroll
-        for (int r = 0; r < GV_R; r++) qr[r] = reinterpret_cast<const uint32_t*>(q + (size_t)min(r0 + r, O - 1) * I);
-        for (int c = lane; c < I / 4; c += 64) {
-            uint32_t w[GV_R];
+                for (int u = 0; u < GV_U; u++) {
+                    const int c = c0 + 64 * u + lane;
+                    if (c >= ce) continue;  // only when a part is shorter than 64 chunks (I % 1024 != 0)
 #pragma unroll
-            for (int r = 0; r < GV_R; r++) w[r] = __builtin_nontemporal_load(qr[r] + c);
+                    for (int t = 0; t < NT; t++) {
 #pragma unroll
-            for (int t = 0; t < NT; t++) {
-                const float4 xv = reinterpret_cast<const float4*>(xs + t * I)[c];
+                        for (int d = 0; d < 4; d++) {
+                            const float4 xv = reinterpret_cast<const float4*>(xs + t * I)[4 * c + d];
+#pragma unroll
+                            for (int r = 0; r < GV_R; r++) {
+                                const uint32_t wd = w[u][r][d];
+                                acc[t][r] += (float)(int8_t)(wd) * xv.x;
+                                acc[t][r] += (float)(int8_t)(wd >> 8) * xv.y;
+                                acc[t][r] += (float)(int8_t)(wd >> 16) * xv.z;
+                                acc[t][r] += (float)(int8_t)(wd >> 24) * xv.w;
+                            }
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < NT; t++)
 #pragma unroll
                 for (int r = 0; r < GV_R; r++) {
-                    acc[t][r] += (float)(int8_t)(w[r]) * xv.x;
-                    acc[t][r] += (float)(int8_t)(w[r] >> 8) * xv.y;
-                    acc[t][r] += (float)(int8_t)(w[r] >> 16) * xv.z;
-                    acc[t][r] += (float)(int8_t)(w[r] >> 24) * xv.w;
+                    const float v = wave_sum(acc[t][r]);
+                    if (lane == 0) red[(wv * NT + t) * GV_R + r] = v;
+                }
+        }
+        __syncthreads();
+        if (g < ngroups && part == 0 && lane < NT * GV_R) {
+            const int t = lane / GV_R, r = lane % GV_R, o = g * GV_R + r;
+            float v = red[(wv * NT + t) * GV_R + r];
+            for (int p = 1; p < KS; p++) v += red[((wv + p) * NT + t) * GV_R + r];
+            if (o < O) y[(size_t)t * O + o] = v * s[o];
+        }
+        __syncthreads();  // the partial sums are read before the next round writes them
+    }
+#undef GV_LOAD
+}
+
+// The same product when every wavefront has at most one row group and one load step (rounds = 1, a part of at most
+// 64 * GV_U chunks: the attention's qkv and o shapes). Without loops the first weights can go out before the input
+// rows are copied into LDS by DMA, so the two memory round trips overlap. Same sum order as gemv_kernel.
+template <int NT>
+__global__ void __launch_bounds__(64 * GV_WAVES) gemv1_kernel(const int8_t* __restrict__ q, const float* __restrict__ s,
+                                                              const float* __restrict__ x, float* __restrict__ y, int I,
+                                                              int O, int KS) {
+    constexpr int GV_U = gv_u<NT>();
+    extern __shared__ __align__(16) float xs[];  // [NT][I], then the partial sums [GV_WAVES][NT][GV_R]
+    float* red = xs + NT * I;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nb = gridDim.x;
+    const int ngroups = (O + GV_R - 1) / GV_R;
+    const int part = wv % KS, slice = I / 16 / KS, cb = part * slice, ce = cb + slice;
+    const int g = blockIdx.x + nb * (wv / KS);
+    const bool on = g < ngroups;
+    u32x4 w[GV_U][GV_R];
+#pragma unroll
+    for (int u = 0; u < GV_U; u++)
+#pragma unroll
+        for (int r = 0; r < GV_R; r++) {
+            const u32x4* row = reinterpret_cast<const u32x4*>(q + (size_t)min(min(g, ngroups - 1) * GV_R + r, O - 1) * I);
+            const int c = cb + 64 * u + lane;
+            w[u][r] = on && c < ce ? __builtin_nontemporal_load(row + c) : u32x4{0u, 0u, 0u, 0u};
+        }
+    for (int i = wv; i < NT * I * 4 / 1024; i += GV_WAVES)  // NT * I * 4 is a multiple of 1 KB (I % 512 == 0)
+        __builtin_amdgcn_global_load_lds((gptr_t)(reinterpret_cast<const char*>(x) + i * 1024 + 16 * lane),
+                                         (lptr_t)(reinterpret_cast<char*>(xs) + i * 1024), 16, 0, 0);
+    wait_vm<0>();
+    __syncthreads();  // the input rows have landed
+    float acc[NT][GV_R];
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < GV_R; r++) acc[t][r] = 0.f;
+#pragma unroll
+    for (int u = 0; u < GV_U; u++) {
+        const int c = cb + 64 * u + lane;
+        if (c >= ce) continue;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                const float4 xv = reinterpret_cast<const float4*>(xs + t * I)[4 * c + d];
+#pragma unroll
+                for (int r = 0; r < GV_R; r++) {
+                    const uint32_t wd = w[u][r][d];
+                    acc[t][r] += (float)(int8_t)(wd) * xv.x;
+                    acc[t][r] += (float)(int8_t)(wd >> 8) * xv.y;
+                    acc[t][r] += (float)(int8_t)(wd >> 16) * xv.z;
+                    acc[t][r] += (float)(int8_t)(wd >> 24) * xv.w;
                 }
             }
         }
+    }
 #pragma unroll
-        for (int t = 0; t < NT; t++)
+    for (int t = 0; t < NT; t++)
 #pragma unroll
-            for (int r = 0; r < GV_R; r++) {
-                const float v = wave_sum(acc[t][r]);
-                if (lane == 0 && r0 + r < O) y[(size_t)t * O + r0 + r] = v * s[r0 + r];
-            }
+        for (int r = 0; r < GV_R; r++) {
+            const float v = wave_sum(acc[t][r]);
+            if (lane == 0) red[(wv * NT + t) * GV_R + r] = v;
+        }
+    __syncthreads();
+    if (on && part == 0 && lane < NT * GV_R) {
+        const int t = lane / GV_R, r = lane % GV_R, o = g * GV_R + r;
+        float v = red[(wv * NT + t) * GV_R + r];
+        for (int p = 1; p < KS; p++) v += red[((wv + p) * NT + t) * GV_R + r];
+        if (o < O) y[(size_t)t * O + o] = v * s[o];
     }
 }
 
@@ -197,6 +303,9 @@ void launch_gemv_t(const int8_t* q, const float* s, const float* x, float* y, in
         return true;
     }();
     (void)once;
+    const int groups = (O + GV_R - 1) / GV_R;
+    int ks = 1;  // split each row over up to 8 wavefronts until ~4 wavefronts per CU have work
+    while (ks < GV_WAVES && groups * ks < 1024 && (I / 16) % (128 * ks) == 0) ks *= 2;
     static const int cus = [] {
         int dev = 0, v = 0;
         if (hipGetDevice(&dev) == hipSuccess &&
@@ -204,9 +313,20 @@ void launch_gemv_t(const int8_t* q, const float* s, const float* x, float* y, in
             return v;
         return 256;
     }();
-    const int groups = (O + GV_R - 1) / GV_R;
-    const int nb = std::min(cus, (groups + GV_WAVES - 1) / GV_WAVES);
-    hipLaunchKernelGGL(gemv_kernel<NT>, dim3(nb), dim3(64 * GV_WAVES), NT * I * 4, st, q, s, x, y, I, O);
+    const int nb = std::min(cus, groups * ks);
+    const size_t lds = (size_t)NT * I * 4 + GV_WAVES * NT * GV_R * 4;
+    const bool one = groups <= nb * (GV_WAVES / ks) && I / 16 / ks <= 64 * gv_u<NT>();
+    if (one) {
+        static bool once1 = [] {
+            MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gemv1_kernel<NT>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+            return true;
+        }();
+        (void)once1;
+        hipLaunchKernelGGL(gemv1_kernel<NT>, dim3(nb), dim3(64 * GV_WAVES), lds, st, q, s, x, y, I, O, ks);
+    } else {
+        hipLaunchKernelGGL(gemv_kernel<NT>, dim3(nb), dim3(64 * GV_WAVES), lds, st, q, s, x, y, I, O, ks);
+    }
     MOEX_LAUNCHED();
 }
 

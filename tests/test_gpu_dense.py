@@ -131,3 +131,23 @@ def test_ragged_rows():
     torch.cuda.synchronize()
     assert _rel(Y.cpu().numpy().astype(np.float64), orc.dense_i8_fp16x(qh, sh, x)) < 1e-5
     assert _rel(y1.cpu().numpy().astype(np.float64), orc.dense_i8_f64(qh, sh, x[:1])[0]) < 1e-5
+
+
+def test_many_row_groups():
+    """O large enough that a wavefront takes several row groups (the looped GEMV: lm_head-like shapes), 1 and 3 rows."""
+    import torch
+    import moex_amd as M
+    O, I = 40000, 1024
+    rng = np.random.default_rng(6)
+    w = (rng.standard_normal((O, I)) * 0.05).astype(np.float16)
+    q, s = _quantize(w)
+    qh, sh = q.cpu().numpy(), s.cpu().numpy()
+    x = rng.standard_normal((3, I)).astype(np.float32)
+    Y = torch.full((3, O), float("nan"), dtype=torch.float32, device="cuda")
+    M.gemm_i8(q, s, dev(x), Y, 3, I, O)
+    y1 = torch.full((O,), float("nan"), dtype=torch.float32, device="cuda")
+    M.gemv_i8(q, s, dev(x[1]), y1, I, O)
+    torch.cuda.synchronize()
+    got = Y.cpu().numpy()
+    assert _rel(got.astype(np.float64), orc.dense_i8_f64(qh, sh, x)) < 1e-5
+    assert np.array_equal(got[1], y1.cpu().numpy())
