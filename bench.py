@@ -250,6 +250,37 @@ def main():
         print(f"[bench] config4 prefill at 260096: turbo {ms_t:.2f} ms ({f4 / ms_t / 1e9:.0f} TFLOPS), "
               f"int8 {ms_i:.2f} ms ({f4 / ms_i / 1e9:.0f} TFLOPS)", flush=True)
         del ct
+        # ---------------- dense int8 projections either side of the attention ----------------
+        dense = {}
+        for nm, O_, I_ in (("qkv", H * 2 * AHD + 2 * KV * AHD, 2048), ("o_proj", 2048, H * AHD)):
+            nrot = int(600e6 // (O_ * I_)) + 1  # > the 256 MB MALL: every call streams its weights from HBM
+            ws = []
+            g = torch.Generator(device=dev).manual_seed(30)
+            for _ in range(nrot):
+                w16 = (torch.randn((O_, I_), generator=g, device=dev) * 0.02).half()
+                qw = torch.empty((O_, I_), dtype=torch.int8, device=dev)
+                sw = torch.empty(O_, device=dev)
+                M.quantize_rows_i8(w16, qw, sw, O_, I_, st)
+                ws.append((qw, sw))
+            del w16
+            ent = {"O": O_, "I": I_}
+            for S_ in (1, 2):
+                Xd = torch.randn((S_, I_), generator=g, device=dev)
+                Yd = torch.empty((S_, O_), device=dev)
+                t_g = time_rotating([lambda qw=qw, sw=sw: M.gemm_i8(qw, sw, Xd, Yd, S_, I_, O_, st) for qw, sw in ws], 200)
+                ent[f"gemv_{S_}row_us"] = round(t_g * 1e3, 2)
+                ent[f"gemv_{S_}row_GBps"] = round(O_ * I_ / (t_g * 1e-3) / 1e9, 1)
+            Xd = torch.randn((T, I_), generator=g, device=dev)
+            Yd = torch.empty((T, O_), device=dev)
+            ms_g, _ = time_steps(lambda: M.gemm_i8(ws[0][0], ws[0][1], Xd, Yd, T, I_, O_, st), 10, 3)
+            ent["gemm_2048_ms"] = round(ms_g, 4)
+            ent["gemm_2048_tflops"] = round(2.0 * T * I_ * O_ / (ms_g * 1e-3) / 1e12, 1)
+            dense[nm] = ent
+            print(f"[bench] dense {nm} int8 [{O_}x{I_}]: GEMV 1 row {ent['gemv_1row_us']} us "
+                  f"({ent['gemv_1row_GBps']} GB/s), 2 rows {ent['gemv_2row_us']} us; prefill GEMM S={T} "
+                  f"{ms_g:.3f} ms ({ent['gemm_2048_tflops']} TFLOPS)", flush=True)
+            del ws
+        extra["dense_int8_projections"] = dense
 
     cpu = None
     if not a.no_cpu:
