@@ -80,3 +80,50 @@ def test_attn_decode_graph_replays(turbo):
     for name in ("k", "v", "ks", "vs"):
         te, tg = getattr(ce, name)[:, :base + 4], getattr(cg, name)[:, :base + 4]
         assert torch.equal(te, tg), name
+
+
+def test_fa_images_and_dense_graph_replays():
+    """attn_fa of a long chunk (tile images: its workspace exists after one eager call on the stream) and the dense
+    projections (GEMV pass, MFMA GEMM) captured on that stream: every replay, with other eager work on the device
+    in between, matches the eager outputs bit for bit."""
+    import torch
+    import moex_amd as M
+    from tests.gpu_util import LD, random_int8_cache, upload
+    rng = np.random.default_rng(17)
+    dc = upload(random_int8_cache(3000, seed=18))
+    T, pos0 = 256, 2500
+    qo = torch.from_numpy(rng.uniform(-2, 2, (T, H, AHD)).astype(np.float32)).cuda()
+    qg = torch.from_numpy(rng.uniform(-2, 2, (T, LD)).astype(np.float32)).cuda()
+    pos = torch.tensor([pos0], dtype=torch.int32, device="cuda")
+    O, I = 1024, 2048
+    w16 = torch.from_numpy((rng.standard_normal((O, I)) * 0.02).astype(np.float16)).cuda()
+    qw = torch.empty((O, I), dtype=torch.int8, device="cuda")
+    sw = torch.empty(O, dtype=torch.float32, device="cuda")
+    M.quantize_rows_i8(w16, qw, sw, O, I)
+    X2 = torch.randn((2, I), device="cuda")
+    X64 = torch.randn((64, I), device="cuda")
+    st = torch.cuda.Stream()
+
+    def run(out, y2, y64):
+        M.attn_fa(qo, qg, dc, out, H, KV, pos, dc.max_t, LD, T, st)
+        M.gemm_i8(qw, sw, X2, y2, 2, I, O, st)
+        M.gemm_i8(qw, sw, X64, y64, 64, I, O, st)
+
+    out_e, y2_e, y64_e = (torch.empty((T, H, AHD), device="cuda"), torch.empty((2, O), device="cuda"),
+                          torch.empty((64, O), device="cuda"))
+    torch.cuda.synchronize()
+    with torch.cuda.stream(st):
+        run(out_e, y2_e, y64_e)  # eager: allocates the stream's workspace, sets the kernels' attributes
+    st.synchronize()
+    out_g, y2_g, y64_g = torch.zeros_like(out_e), torch.zeros_like(y2_e), torch.zeros_like(y64_e)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        run(out_g, y2_g, y64_g)
+    torch.cuda.synchronize()
+    for i in range(3):
+        out_g.zero_(); y2_g.zero_(); y64_g.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, out_e) and torch.equal(y2_g, y2_e) and torch.equal(y64_g, y64_e), i
+        X2.mul_(1.0)  # unrelated eager work between replays
+        torch.cuda.synchronize()
