@@ -95,7 +95,7 @@ constexpr int WS_CH = 32 * WS_NC;                     // keys per chunk: 32 per 
 constexpr int WS_NS = 2;                              // LDS stages: one chunk streams while one is computed
 constexpr int WS_KB = WS_CH * AHD;                    // K rows of a stage; the V rows follow, then ks[128], vs[128]
 constexpr int WS_STAGE = 2 * WS_CH * AHD + 2 * 128 * 4;
-constexpr int WS_LDS = WS_NS * WS_STAGE + WS_NC * 64 * 16;  // stages + one P operand per consumer
+constexpr int WS_LDS = WS_NS * WS_STAGE;  // the two stages
 constexpr float WS_SLACK = 8.f;
 static_assert(WS_CH % 8 == 0 && WS_CH <= 128, "chunk shape");
 static_assert(WS_NC * GQ * AHD * 4 <= WS_STAGE, "the consumer merge fits in stage 0");
@@ -196,7 +196,6 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws_kernel(const f
                         qd[dig][ks][u] = (int)pack_bytes(d[dig][0], d[dig][1], d[dig][2], d[dig][3]);
                 }
         }
-        half8_t* Plw = reinterpret_cast<half8_t*>(smem + WS_NS * WS_STAGE) + 64 * wv;
         float4_t o[16];
 #pragma unroll
         for (int J = 0; J < 16; J++) o[J] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -281,7 +280,8 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws_kernel(const f
                 sig = nsig;
             }
             // ---- P = 2^(s - mref) * vs * 2^sig as fp16 hi + lo: row 2h + 1 of the P operand is the lo part of row 2h,
-            // written by the lane pair m16 = 2h (hi), 2h + 1 (lo) ----
+            // formed by the lane pair m16 = 2h (hi), 2h + 1 (lo), each lane's 8 keys its own A operand ----
+            half8_t pa;
             {
                 const float vsc = ldexpf(1.f, sig);
                 half8_t ph;
@@ -295,10 +295,10 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws_kernel(const f
                     ph[j] = (m16 & 1) ? (_Float16)(x - (float)h) : h;
                 }
                 lacc += ls;
-                Plw[16 * g + m16] = ph;
+                pa = ph;
             }
             // ---- O^T += P . V over this consumer's 32 keys, all 256 dims ----
-            const half8_t pa = Plw[lane];
+
             const unsigned char* Vs = sb + WS_KB;
 #pragma unroll
             for (int pc = 0; pc < 4; pc++) {
@@ -369,7 +369,7 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws_kernel(const f
 // chunk (part w / NPR). Column m of the Q.K MFMA is (token m / 8 of the pair, head m % 8), so one set of MFMAs scores
 // both tokens. P enters P.V as two A operands, its hi and lo fp16 parts (row = column), accumulated into the same O
 // tiles against one widened V operand: V is widened once per pair, and O (rows = (token, head)) takes 64 registers.
-constexpr int WSP_LDS = WS_NS * WS_STAGE + WS_NC * 2 * 64 * 16;  // stages + hi and lo P operands per consumer
+constexpr int WSP_LDS = WS_NS * WS_STAGE;  // the two stages
 static_assert(WS_NC * 16 * AHD * 4 <= WS_STAGE, "the pair merge fits in stage 0");
 static_assert(WSP_LDS <= 160 * 1024, "LDS");
 
@@ -436,7 +436,6 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wsp_kernel(const 
                         qd[dig][ks][u] = (int)pack_bytes(d[dig][0], d[dig][1], d[dig][2], d[dig][3]);
                 }
         }
-        half8_t* Pw = reinterpret_cast<half8_t*>(smem + WS_NS * WS_STAGE) + 128 * wv;  // [hi, lo][lane]
         float4_t o[16];  // column n of tile 4 pc + j is dim 64 pc + 4 n + j; row r is column r of the Q.K MFMA
 #pragma unroll
         for (int J = 0; J < 16; J++) o[J] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -524,7 +523,9 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wsp_kernel(const 
                     mref = nref;
                     sig = nsig;
                 }
-                // ---- P = 2^(s - mref) * vs * 2^sig = hi + lo in fp16 (a column with no key yet has P = 0) ----
+                // ---- P = 2^(s - mref) * vs * 2^sig = hi + lo in fp16 (a column with no key yet has P = 0); each lane's
+                // 8 keys are its own A operand ----
+                half8_t pah, pal;
                 {
                     const float vsc = ldexpf(1.f, sig), mr = mref == -INFINITY ? 0.f : mref;
                     half8_t ph, pl;
@@ -539,11 +540,10 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wsp_kernel(const 
                         pl[j] = (_Float16)(x - (float)h);
                     }
                     lacc += ls;
-                    Pw[16 * g + m16] = ph;
-                    Pw[64 + 16 * g + m16] = pl;
+                    pah = ph;
+                    pal = pl;
                 }
                 // ---- O^T += (P_hi + P_lo) . V over these 32 keys, all 256 dims ----
-                const half8_t pah = Pw[lane], pal = Pw[64 + lane];
 #pragma unroll
                 for (int pc = 0; pc < 4; pc++) {
                     const int rd = 16 * ((4 * pc + (m16 >> 2)) ^ (4 * g)) + 4 * (m16 & 3);
@@ -654,14 +654,16 @@ __device__ __forceinline__ int4_t_ k_codes(uint2 x) {  // 16 nibbles -> the MFMA
 // V layout, two areas per consumer), so the unpacking runs beside the consumers' work on the previous chunk. Two
 // chunks are in flight: chunk c + 2 is issued at the barrier that starts chunk c. Q.K packs the query digits 2 and
 // 1 of the 8 heads into one MFMA and digit 0 into a second, per 128-dim half, and recombines a head's digits with
-// two row_ror:8 DPP moves; P carries the V half norm, hi/lo rows interleaved.
+// two row_ror:8 DPP moves; P carries the V half norm. P rows are (hi / lo part, head), so the P.V key order being the
+// Q.K output order, each lane's probabilities are its own A operand; the hi and lo rows of O are added across lanes at
+// the end.
 constexpr int WST_KB = 128 * TQ_KB;                      // K nibble rows of a stage
 constexpr int WST_NS = 3;                                // K stages
 constexpr int WST_STAGE = WST_KB + 2 * 128 * 8;          // K nibble rows + K norms + V norms
 constexpr int WST_RV = 128 * TQ_VB;                      // raw V rows of a chunk (two buffers)
 constexpr int WST_VC = 32 * AHD;                         // one consumer's unpacked V codes (two buffers)
 constexpr int WST_VC0 = WST_NS * WST_STAGE + 2 * WST_RV;  // offset of the V code areas
-constexpr int WST_LDS = WST_VC0 + 2 * WS_NC * WST_VC + WS_NC * 2 * 64 * 16 + WS_NP * 272 * 4;
+constexpr int WST_LDS = WST_VC0 + 2 * WS_NC * WST_VC + WS_NP * 272 * 4;
 static_assert(WS_NC * GQ * AHD * 4 <= WST_NS * WST_STAGE, "the consumer merge fits in the stages");
 static_assert(WST_LDS <= 160 * 1024, "LDS");
 
@@ -692,7 +694,7 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
         const float* vng = kv.vs + 2 * rbase;
         // this producer's bit-field spreading tables: t256[b] = the four 2-bit fields of b, one per byte; t16[n] = bit e
         // of n at bit 2 of byte e
-        uint32_t* t256 = reinterpret_cast<uint32_t*>(smem + WST_VC0 + 2 * WS_NC * WST_VC + WS_NC * 2 * 64 * 16) + 272 * pw;
+        uint32_t* t256 = reinterpret_cast<uint32_t*>(smem + WST_VC0 + 2 * WS_NC * WST_VC) + 272 * pw;
         uint32_t* t16 = t256 + 256;
 #pragma unroll
         for (int u = 0; u < 4; u++) {
@@ -808,7 +810,6 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
                 }
             }
         }
-        half8_t* Pw = reinterpret_cast<half8_t*>(smem + WST_VC0 + 2 * WS_NC * WST_VC) + 128 * wv;  // [half][lane]
         float4_t o[16];  // ws layout: row 2h (2h + 1) = hi (lo) part of head h
 #pragma unroll
         for (int J = 0; J < 16; J++) o[J] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -894,7 +895,7 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
                 const float sf = ldexpf(1.f, nsig - sig);
                 float fr[4];
 #pragma unroll
-                for (int i = 0; i < 4; i++) fr[i] = __shfl(fown, 2 * g + (i >> 1)) * sf;  // lane h holds head h
+                for (int i = 0; i < 4; i++) fr[i] = __shfl(fown, (4 * g + i) & 7) * sf;  // O row m: head m % 8
 #pragma unroll
                 for (int J = 0; J < 16; J++)
 #pragma unroll
@@ -903,8 +904,10 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
                 mref = nref;
                 sig = nsig;
             }
-            // ---- P of both V halves = 2^(s - mref) * vn * K3 * 2^sig as fp16 hi (m16 < 8) / lo (m16 >= 8) at row
-            // 2 * head + (m16 >= 8) ----
+            // ---- P of both V halves = 2^(s - mref) * vn * K3 * 2^sig as fp16 hi (m16 < 8) / lo (m16 >= 8): row m16 of
+            // the P operand (head m16 % 8), each lane's 8 keys its own A operand (the P.V key order is the Q.K
+            // output order) ----
+            half8_t pa0, pa1;
             {
                 const float vsc = ldexpf(1.f, sig) * TK3;
                 half8_t p0v, p1v;
@@ -919,12 +922,10 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
                     p1v[j] = lo8 ? h1 : (_Float16)(x1 - (float)h1);
                 }
                 lacc += lo8 ? ls : 0.f;
-                const int row = 2 * hq + (lo8 ? 0 : 1);
-                Pw[16 * g + row] = p0v;
-                Pw[64 + 16 * g + row] = p1v;
+                pa0 = p0v;
+                pa1 = p1v;
             }
             // ---- O^T += P . V over these 32 keys: dims < 128 (pc 0, 1) with the half-0 P, the rest with half 1 ----
-            const half8_t pa0 = Pw[lane], pa1 = Pw[64 + lane];
 #pragma unroll
             for (int pc = 0; pc < 4; pc++) {
                 const int rd = 16 * ((4 * pc + (m16 >> 2)) ^ (4 * g)) + 4 * (m16 & 3);
@@ -948,18 +949,22 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
         __syncthreads();
         float* Ow = reinterpret_cast<float*>(smem);  // [consumer][head][256]
         const float un = ldexpf(1.f, -sig);
+        // O rows 4g + i: head (4g + i) % 8, hi for g < 2 and lo for g >= 2: lanes l and l + 32 hold the two parts
 #pragma unroll
-        for (int e = 0; e < 2; e++) {
-            const int h = 2 * g + e;
-            const float Mh = fmaxf(fmaxf(cm[0][h], cm[1][h]), fmaxf(cm[2][h], cm[3][h]));
-            const float f = ex2d(cm[wv][h], Mh) * un;
+        for (int J = 0; J < 16; J++)
 #pragma unroll
-            for (int pc = 0; pc < 4; pc++)
-                *reinterpret_cast<float4*>(Ow + (wv * GQ + h) * AHD + 64 * pc + 4 * m16) =
-                    make_float4((o[4 * pc][2 * e] + o[4 * pc][2 * e + 1]) * f,
-                                (o[4 * pc + 1][2 * e] + o[4 * pc + 1][2 * e + 1]) * f,
-                                (o[4 * pc + 2][2 * e] + o[4 * pc + 2][2 * e + 1]) * f,
-                                (o[4 * pc + 3][2 * e] + o[4 * pc + 3][2 * e + 1]) * f);
+            for (int i = 0; i < 4; i++) o[J][i] += __shfl_xor(o[J][i], 32);
+        if (g < 2) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int h = 4 * g + i;
+                const float Mh = fmaxf(fmaxf(cm[0][h], cm[1][h]), fmaxf(cm[2][h], cm[3][h]));
+                const float f = ex2d(cm[wv][h], Mh) * un;
+#pragma unroll
+                for (int pc = 0; pc < 4; pc++)
+                    *reinterpret_cast<float4*>(Ow + (wv * GQ + h) * AHD + 64 * pc + 4 * m16) =
+                        make_float4(o[4 * pc][i] * f, o[4 * pc + 1][i] * f, o[4 * pc + 2][i] * f, o[4 * pc + 3][i] * f);
+            }
         }
     }
     __syncthreads();
