@@ -12,7 +12,9 @@
 //   gemm_kernel            S > 8 rows (prefill): Y = X . W^T * s on v_mfma_f32_32x32x16_f16. Weights are widened to
 //                          fp16 exactly (integers), activations rounded to fp16 as the reference does
 //                          (kernels.cuh:306-307), fp32 accumulation, the row scale applied last. Workgroup tile 128
-//                          weight rows x 128 tokens, 4 wavefronts of 64 x 64, K steps of 32 double-buffered in LDS.
+//                          weight rows x 128 tokens, 4 wavefronts of 64 x 64, K steps of 32 double-buffered in LDS,
+//                          two workgroups per CU; the blocks of a token tile run on one XCD (its activations are read
+//                          into one L2).
 #include "common.hpp"
 
 namespace moex {
@@ -205,12 +207,24 @@ __global__ void __launch_bounds__(64 * GV_WAVES) gemv1_kernel(const int8_t* __re
 constexpr int GM_BM = 128, GM_BN = 128, GM_BK = 32;
 constexpr int GM_LD = GM_BK + 8;  // halves per LDS row (80 B: conflict-free 16-byte operand reads)
 
-__global__ void __launch_bounds__(256) gemm_kernel(const int8_t* __restrict__ W, const float* __restrict__ s,
+__global__ void __launch_bounds__(256, 2) gemm_kernel(const int8_t* __restrict__ W, const float* __restrict__ s,
                                                    const float* __restrict__ X, float* __restrict__ Y, int S, int I,
                                                    int O) {
     __shared__ __align__(16) _Float16 lds[2][2][GM_BM * GM_LD];  // [buffer][W, X][row][k]
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r = lane & 31, h32 = lane >> 5;
-    const int o0 = blockIdx.x * GM_BM, s0 = blockIdx.y * GM_BN;
+    // XCD-aware order (block b runs on XCD b % 8): with the token tiles a multiple of 8, XCD x takes token tiles
+    // x * spx .. x * spx + spx - 1 against every weight tile, so each token tile is read into one L2 only
+    const int nO = (O + GM_BM - 1) / GM_BM, nS = (S + GM_BN - 1) / GM_BN, bid = blockIdx.x;
+    int ot, stl;
+    if (nS % 8 == 0) {
+        const int spx = nS / 8, i = bid >> 3;
+        ot = i / spx;
+        stl = (bid & 7) * spx + i % spx;
+    } else {
+        ot = bid % nO;
+        stl = bid / nO;
+    }
+    const int o0 = ot * GM_BM, s0 = stl * GM_BN;
     const int wo = (wv >> 1) * 64, ws = (wv & 1) * 64;  // this wavefront's 64 x 64 block of the tile
     // staging: thread tid owns 16 weights (row tid/2, k 16*(tid%2)) and 16 activations (token tid/2, same k)
     const int sr = tid >> 1, sk = (tid & 1) * 16;
@@ -351,8 +365,8 @@ void launch_gemv_i8(const int8_t* q, const float* s, const float* x, float* y, i
 }
 
 void launch_gemm_i8(const int8_t* q, const float* s, const float* X, float* Y, int S, int I, int O, hipStream_t st) {
-    hipLaunchKernelGGL(gemm_kernel, dim3((O + GM_BM - 1) / GM_BM, (S + GM_BN - 1) / GM_BN), dim3(256), 0, st, q, s,
-                       X, Y, S, I, O);
+    hipLaunchKernelGGL(gemm_kernel, dim3(((O + GM_BM - 1) / GM_BM) * ((S + GM_BN - 1) / GM_BN)), dim3(256), 0, st, q,
+                       s, X, Y, S, I, O);
     MOEX_LAUNCHED();
 }
 
