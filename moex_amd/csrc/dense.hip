@@ -15,6 +15,8 @@
 //                          weight rows x 128 tokens, 4 wavefronts of 64 x 64, K steps of 32 double-buffered in LDS,
 //                          two workgroups per CU; the blocks of a token tile run on one XCD (its activations are read
 //                          into one L2).
+//   gemm_ws_kernel         The same product and sum order with split roles: 4 wavefronts widen the next K step into
+//                          LDS while 4 run the MFMAs of this one. Used when the grid fits the chip in one pass.
 #include "common.hpp"
 
 namespace moex {
@@ -309,6 +311,115 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(const int8_t* __restrict__
     }
 }
 
+constexpr int GEMM_WS_MAX_BLOCKS = 512;  // 2 workgroups x 256 CUs
+
+// Warp-specialised variant: wavefronts 4-7 load and widen the next K step into the other LDS buffer while
+// wavefronts 0-3 run the MFMAs of this one (one barrier per K step), so the staging VALU work runs beside the MFMAs.
+__global__ void __launch_bounds__(512, 2) gemm_ws_kernel(const int8_t* __restrict__ W, const float* __restrict__ s,
+                                                         const float* __restrict__ X, float* __restrict__ Y, int S, int I,
+                                                         int O) {
+    __shared__ __align__(16) _Float16 lds[2][2][GM_BM * GM_LD];  // [buffer][W, X][row][k]
+    const int nO = (O + GM_BM - 1) / GM_BM, nS = (S + GM_BN - 1) / GM_BN, bid = blockIdx.x;
+    int ot, stl;
+    if (nS % 8 == 0) {
+        const int spx = nS / 8, i = bid >> 3;
+        ot = i / spx;
+        stl = (bid & 7) * spx + i % spx;
+    } else {
+        ot = bid % nO;
+        stl = bid / nO;
+    }
+    const int o0 = ot * GM_BM, s0 = stl * GM_BN, nk = I / GM_BK;
+    if (threadIdx.x >= 256) {
+        // ---- staging: thread t owns 16 weights (row t/2, k 16*(t%2)) and 16 activations (token t/2, same k) ----
+        const int tid = threadIdx.x - 256, sr = tid >> 1, sk = (tid & 1) * 16;
+        const bool wok = o0 + sr < O, xok = s0 + sr < S;
+        const int8_t* wp = W + (size_t)min(o0 + sr, O - 1) * I + sk;
+        const float* xp = X + (size_t)min(s0 + sr, S - 1) * I + sk;
+        uint4 wreg;
+        float4 xreg[4];
+        auto load = [&](int k0) {
+            wreg = *reinterpret_cast<const uint4*>(wp + k0);
+#pragma unroll
+            for (int j = 0; j < 4; j++) xreg[j] = reinterpret_cast<const float4*>(xp + k0)[j];
+        };
+        auto store = [&](int b) {
+            uint32_t h[8];
+            i8x4_to_h4(wok ? wreg.x : 0u, h[0], h[1]);
+            i8x4_to_h4(wok ? wreg.y : 0u, h[2], h[3]);
+            i8x4_to_h4(wok ? wreg.z : 0u, h[4], h[5]);
+            i8x4_to_h4(wok ? wreg.w : 0u, h[6], h[7]);
+            uint4* wd = reinterpret_cast<uint4*>(&lds[b][0][sr * GM_LD + sk]);
+            wd[0] = make_uint4(h[0], h[1], h[2], h[3]);
+            wd[1] = make_uint4(h[4], h[5], h[6], h[7]);
+            uint32_t xh[8];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float4 v = xok ? xreg[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+                xh[2 * j] = h22u(half2_t{(_Float16)v.x, (_Float16)v.y});
+                xh[2 * j + 1] = h22u(half2_t{(_Float16)v.z, (_Float16)v.w});
+            }
+            uint4* xd = reinterpret_cast<uint4*>(&lds[b][1][sr * GM_LD + sk]);
+            xd[0] = make_uint4(xh[0], xh[1], xh[2], xh[3]);
+            xd[1] = make_uint4(xh[4], xh[5], xh[6], xh[7]);
+        };
+        load(0);
+        store(0);
+        if (nk > 1) load(GM_BK);
+        __syncthreads();
+        for (int kt = 0; kt < nk; kt++) {
+            if (kt + 1 < nk) {
+                store((kt + 1) & 1);  // the buffer the computing wavefronts finished at the last barrier
+                if (kt + 2 < nk) load((kt + 2) * GM_BK);
+            }
+            __syncthreads();
+        }
+        return;
+    }
+    // ---- computing wavefronts ----
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r = lane & 31, h32 = lane >> 5;
+    const int wo = (wv >> 1) * 64, ws = (wv & 1) * 64;  // this wavefront's 64 x 64 block of the tile
+    float16_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+        const int b = kt & 1;
+#pragma unroll
+        for (int kk = 0; kk < GM_BK; kk += 16) {
+            half8_t a[2], bw[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                a[j] = *reinterpret_cast<const half8_t*>(&lds[b][1][(ws + 32 * j + r) * GM_LD + kk + 8 * h32]);
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                bw[i] = *reinterpret_cast<const half8_t*>(&lds[b][0][(wo + 32 * i + r) * GM_LD + kk + 8 * h32]);
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[j], bw[i], acc[i][j], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int o = o0 + wo + 32 * i + r;
+        if (o >= O) continue;
+        const float so = s[o];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int t = s0 + ws + 32 * j + 8 * (e >> 2) + 4 * h32 + (e & 3);
+                if (t < S) Y[(size_t)t * O + o] = acc[i][j][e] * so;
+            }
+    }
+}
+
 template <int NT>
 void launch_gemv_t(const int8_t* q, const float* s, const float* x, float* y, int I, int O, hipStream_t st) {
     static bool once = [] {
@@ -365,8 +476,14 @@ void launch_gemv_i8(const int8_t* q, const float* s, const float* x, float* y, i
 }
 
 void launch_gemm_i8(const int8_t* q, const float* s, const float* X, float* Y, int S, int I, int O, hipStream_t st) {
-    hipLaunchKernelGGL(gemm_kernel, dim3(((O + GM_BM - 1) / GM_BM) * ((S + GM_BN - 1) / GM_BN)), dim3(256), 0, st, q,
-                       s, X, Y, S, I, O);
+    // Both kernels sum in the same order (identical results). A grid that fits the chip in one pass of two
+    // workgroups per CU runs the warp-specialised kernel; a larger one the 4-wavefront kernel, whose extra
+    // workgroups in flight hide the staging better than the split roles do (measured on the qkv/o_proj shapes).
+    const int blocks = ((O + GM_BM - 1) / GM_BM) * ((S + GM_BN - 1) / GM_BN);
+    if (blocks <= GEMM_WS_MAX_BLOCKS)
+        hipLaunchKernelGGL(gemm_ws_kernel, dim3(blocks), dim3(512), 0, st, q, s, X, Y, S, I, O);
+    else
+        hipLaunchKernelGGL(gemm_kernel, dim3(blocks), dim3(256), 0, st, q, s, X, Y, S, I, O);
     MOEX_LAUNCHED();
 }
 

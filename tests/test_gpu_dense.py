@@ -133,6 +133,34 @@ def test_ragged_rows():
     assert _rel(y1.cpu().numpy().astype(np.float64), orc.dense_i8_f64(qh, sh, x[:1])[0]) < 1e-5
 
 
+def test_gemm_both_kernels_ragged():
+    """A grid above one pass of the chip (the 4-wavefront kernel) and one within it (the warp-specialised kernel),
+    both with O and S ragged against the 128 x 128 tile: each against the precision model, and a row shared by the
+    two calls bit-identical (the two kernels sum in the same order)."""
+    import torch
+    import moex_amd as M
+    O, I = 9000, 1024
+    rng = np.random.default_rng(8)
+    w = (rng.standard_normal((O, I)) * 0.05).astype(np.float16)
+    q, s = _quantize(w)
+    qh, sh = q.cpu().numpy(), s.cpu().numpy()
+    x = rng.standard_normal((1000, I)).astype(np.float32)
+    xd = dev(x)
+    outs = {}
+    for S in (1000, 200):  # 71 x 8 = 568 blocks; 71 x 2 = 142 blocks
+        Y = torch.full((S, O), float("nan"), dtype=torch.float32, device="cuda")
+        M.gemm_i8(q, s, xd[:S], Y, S, I, O)
+        torch.cuda.synchronize()
+        got = Y.cpu().numpy()
+        rows = [0, 129, S - 1]
+        cols = np.r_[0:O:97, O - 1]
+        rel = _rel(got[np.ix_(rows, cols)].astype(np.float64), orc.dense_i8_fp16x(qh[cols], sh[cols], x[rows]))
+        report("gemm_i8 ragged", O=O, I=I, S=S, rel_vs_model=rel)
+        assert np.all(np.isfinite(got)) and rel < 1e-5
+        outs[S] = got
+    assert np.array_equal(outs[1000][:200], outs[200])
+
+
 def test_many_row_groups():
     """O large enough that a wavefront takes several row groups (the looped GEMV: lm_head-like shapes), 1 and 3 rows."""
     import torch
