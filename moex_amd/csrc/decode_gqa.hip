@@ -29,8 +29,8 @@ __device__ __forceinline__ int xcd_work_id(int b, int nb) {
 // [-128, 127]), every digit product accumulated exactly in int32 and the digits recombined in fp32, so the scores keep
 // fp32-level precision (the reference decode is fp32). The int8 kernels give each digit its own MFMA per 64 dims with
 // column m of the B operand one (token, head) of the query: the lane that receives the score of (key, column m)
-// recombines it from its three accumulators. The turbo kernel packs digits 2 and 1 of the 8 heads into the 16 columns
-// of one MFMA and digit 0 into a second, and brings a head's digits together with two row_ror:8 DPP moves.
+// recombines it from its three accumulators. The turbo kernel packs digits 2 and 0 of the 8 heads into the 16 columns
+// of one MFMA and digit 1 into a second, and brings a head's digits together with one row_ror:8 DPP move.
 // P.V runs on v_mfma_f32_16x16x32_f16: P = p * vs * 2^sig is split into fp16 hi + lo (~22 bits), V widened exactly to
 // fp16, fp32 accumulation.
 typedef int int4_t_ __attribute__((ext_vector_type(4)));
@@ -625,8 +625,11 @@ static void launch_wsp(const float* qo, moex_kv_cache kv, int H, int KV, const i
 // TurboQuant codes -> signed int8 centroid codes (kernels.cuh:1122-1170 tables, scaled by 127 / max centroid):
 //   K: 4-bit codes -> two v_perm LUT halves, a third v_perm picks per byte; the MFMA operand takes a lane's 16 codes
 //      as (even nibbles, odd nibbles) of two dwords, and the query digits use the same dim order.
-//   V: 3-bit codes, the low 2 bits and the high bit in separate planes of the row; two small LDS tables spread the
-//      bit fields into bytes.
+//   V: 3-bit codes, the low 2 bits and the high bit in separate planes of the row. For 16 codes (one 32-bit word of
+//      low fields, 16 high bits): the four masks (w >> 2f) & 0x03030303 transposed as a 4 x 4 byte matrix put the
+//      low field of code 4k + i in byte i of selector k; the high bits of codes 4k .. 4k + 3 go to bit 2 of those
+//      bytes by one multiply (nibble * 0x810204: bit i lands at 8i + 2, the terms never overlap, so the product is
+//      their OR); a v_perm LUT then maps each selector to 4 codes.
 constexpr uint32_t spack(int a, int b, int c, int d) {
     return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) | ((uint32_t)(d & 0xff) << 24);
 }
@@ -652,9 +655,10 @@ __device__ __forceinline__ int4_t_ k_codes(uint2 x) {  // 16 nibbles -> the MFMA
 // rows (96 bytes, packed) into one of two raw V buffers. Producer j moves the raw V rows of keys 32j .. 32j + 31 and,
 // once they have landed, unpacks their 3-bit codes into consumer j's int8 code area for that chunk (gqa_ws_kernel's
 // V layout, two areas per consumer), so the unpacking runs beside the consumers' work on the previous chunk. Two
-// chunks are in flight: chunk c + 2 is issued at the barrier that starts chunk c. Q.K packs the query digits 2 and
-// 1 of the 8 heads into one MFMA and digit 0 into a second, per 128-dim half, and recombines a head's digits with
-// two row_ror:8 DPP moves; P carries the V half norm. P rows are (hi / lo part, head), so the P.V key order being the
+// chunks are in flight: chunk c + 2 is issued at the barrier that starts chunk c. Q.K puts digit 2 of the 8 heads
+// (columns 0-7) and digit 0 (columns 8-15) into one MFMA and digit 1 (both halves) into a second, per 128-dim half;
+// one row_ror:8 DPP move gives each lane of a head's pair the digit its partner holds, digits 1 and 0 are added
+// exactly in int32 and digit 2 joins in one fma, in the same order in both lanes; P carries the V half norm. P rows are (hi / lo part, head), so the P.V key order being the
 // Q.K output order, each lane's probabilities are its own A operand; the hi and lo rows of O are added across lanes at
 // the end.
 constexpr int WST_KB = 128 * TQ_KB;                      // K nibble rows of a stage
@@ -663,7 +667,7 @@ constexpr int WST_STAGE = WST_KB + 2 * 128 * 8;          // K nibble rows + K no
 constexpr int WST_RV = 128 * TQ_VB;                      // raw V rows of a chunk (two buffers)
 constexpr int WST_VC = 32 * AHD;                         // one consumer's unpacked V codes (two buffers)
 constexpr int WST_VC0 = WST_NS * WST_STAGE + 2 * WST_RV;  // offset of the V code areas
-constexpr int WST_LDS = WST_VC0 + 2 * WS_NC * WST_VC + WS_NP * 272 * 4;
+constexpr int WST_LDS = WST_VC0 + 2 * WS_NC * WST_VC;
 static_assert(WS_NC * GQ * AHD * 4 <= WST_NS * WST_STAGE, "the consumer merge fits in the stages");
 static_assert(WST_LDS <= 160 * 1024, "LDS");
 
@@ -692,19 +696,6 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
         const uint8_t* Vg = reinterpret_cast<const uint8_t*>(kv.v) + rbase * TQ_VB;
         const float* kng = kv.ks + 2 * rbase;
         const float* vng = kv.vs + 2 * rbase;
-        // this producer's bit-field spreading tables: t256[b] = the four 2-bit fields of b, one per byte; t16[n] = bit e
-        // of n at bit 2 of byte e
-        uint32_t* t256 = reinterpret_cast<uint32_t*>(smem + WST_VC0 + 2 * WS_NC * WST_VC) + 272 * pw;
-        uint32_t* t16 = t256 + 256;
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const uint32_t b = 64 * u + lane;
-            t256[b] = (b & 3u) | (((b >> 2) & 3u) << 8) | (((b >> 4) & 3u) << 16) | ((b >> 6) << 24);
-        }
-        if (lane < 16) {
-            const uint32_t b = lane;
-            t16[lane] = ((b & 1u) << 2) | (((b >> 1) & 1u) << 10) | (((b >> 2) & 1u) << 18) | ((b >> 3) << 26);
-        }
         auto issue = [&](int c) {
             const int c0 = c == 0 ? lo : lo + first + (c - 1) * WS_CH, ce = c == 0 ? lo + first : lo + first + c * WS_CH;
             unsigned char* st = smem + (c % WST_NS) * WST_STAGE;
@@ -740,32 +731,42 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
                 unsigned char* Vc = smem + WST_VC0 + ((c & 1) * WS_NC + pw) * WST_VC;
                 const int pc = lane & 15, hb = pc >> 3, q = pc & 7;
                 const unsigned char* rw0 = smem + WST_NS * WST_STAGE + (c & 1) * WST_RV + (32 * pw + (lane >> 4)) * TQ_VB;
+                uint32_t Lw[8], Hh[8];
+#pragma unroll
+                for (int it = 0; it < 8; it++) {
+                    Lw[it] = *reinterpret_cast<const uint32_t*>(rw0 + it * 4 * TQ_VB + 32 * hb + 4 * q);
+                    Hh[it] = *reinterpret_cast<const uint16_t*>(rw0 + it * 4 * TQ_VB + 64 + 16 * hb + 2 * q);
+                }
 #pragma unroll
                 for (int it = 0; it < 8; it++) {
                     const int kk = (lane >> 4) + 4 * it;  // 0..31
-                    const unsigned char* rw = rw0 + it * 4 * TQ_VB;
-                    const uint32_t Lw = *reinterpret_cast<const uint32_t*>(rw + 32 * hb + 4 * q);
-                    const uint32_t Hh = *reinterpret_cast<const uint16_t*>(rw + 64 + 16 * hb + 2 * q);
+                    uint32_t sel[4];
+                    tr4x4_(Lw[it] & 0x03030303u, (Lw[it] >> 2) & 0x03030303u, (Lw[it] >> 4) & 0x03030303u,
+                           (Lw[it] >> 6) & 0x03030303u, sel);
                     uint32_t cd[4];
 #pragma unroll
                     for (int k = 0; k < 4; k++) {
-                        const uint32_t idx = t256[(Lw >> (8 * k)) & 0xffu] | t16[(Hh >> (4 * k)) & 15u];
+                        const uint32_t idx = sel[k] | ((__builtin_amdgcn_ubfe(Hh[it], 4 * k, 4) * 0x810204u) & 0x04040404u);
                         cd[k] = __builtin_amdgcn_perm(SV1, SV0, idx);
                     }
-                    *reinterpret_cast<uint4*>(Vc + kk * AHD + 16 * (pc ^ (4 * ((kk >> 2) & 3)))) =
-                        make_uint4(cd[0], cd[1], cd[2], cd[3]);
+                    // not a C++ store: the compiler would wait for every DMA in flight before it (it cannot tell that the
+                    // code areas are none of their destinations)
+                    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+                    const uint32_t la = (uint32_t)(uintptr_t)(Vc + kk * AHD + 16 * (pc ^ (4 * ((kk >> 2) & 3))));
+                    asm volatile("ds_write_b128 %0, %1" ::"v"(la), "v"(u32x4_t{cd[0], cd[1], cd[2], cd[3]}) : "memory");
                 }
             }
-            __syncthreads();  // chunk c and its V codes are ready, and the consumers are done with chunk c - 1: its
-                              // K stage takes chunk c + 2, as does the raw V buffer of chunk c
+            // chunk c and its V codes are ready, and the consumers are done with chunk c - 1: its K stage takes chunk
+            // c + 2, as does the raw V buffer of chunk c. Not __syncthreads: that waits for chunk c + 1 too.
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
             if (c + 2 < nch) issue(c + 2);
         }
         __syncthreads();
         __syncthreads();
     } else {
         // ---- consumers. Query digits in registers: MFMA ks, lane (g, m16) holds dims
-        // 64 ks + 16 g + {0,2,4,6, 1,3,5,7, 8,10,12,14, 9,11,13,15} of head m16 % 8; qa = digit 2 (m16 < 8) or 1,
-        // qb = digit 0 (m16 < 8) or 0 ----
+        // 64 ks + 16 g + {0,2,4,6, 1,3,5,7, 8,10,12,14, 9,11,13,15} of head m16 % 8; qa = digit 2 (m16 < 8) or 0,
+        // qb = digit 1 ----
         const int hq = m16 & 7;
         const bool lo8 = m16 < 8;
         int4_t_ qa[4], qb[4];
@@ -799,8 +800,8 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
                         digits3((int)__builtin_rintf(xv[k] * up), d2, d1, d0);
                         // dim 4u + k of the lane's 16 goes to operand byte: even dims of each 8 first, then odd
                         const int dl = 4 * u + k, pos = 8 * (dl >> 3) + ((dl & 1) ? 4 : 0) + ((dl & 7) >> 1);
-                        da[pos] = lo8 ? d2 : d1;
-                        db[pos] = lo8 ? d0 : 0;
+                        da[pos] = lo8 ? d2 : d0;
+                        db[pos] = d1;
                     }
                 }
 #pragma unroll
@@ -853,18 +854,16 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
                         db1[grp] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qb[ks], db1[grp], 0, 0, 0);
                     }
                 }
-            // ---- scores: both lanes of a head (m16, m16 ^ 8) recombine its digits ----
+            // ---- scores: both lanes of a head (m16, m16 ^ 8) recombine its digits in the same order (|d1 * 256 + d0|
+            // < 2^30: exact in int32) ----
             float sc[8];
 #pragma unroll
             for (int grp = 0; grp < 2; grp++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int x0 = dpp_ror8(da0[grp][i]), y0 = dpp_ror8(db0[grp][i]);
-                    const int x1 = dpp_ror8(da1[grp][i]), y1 = dpp_ror8(db1[grp][i]);
-                    const float r0 = ((float)(lo8 ? da0[grp][i] : x0) * 65536.f + (float)(lo8 ? x0 : da0[grp][i]) * 256.f) +
-                                     (float)(lo8 ? db0[grp][i] : y0);
-                    const float r1 = ((float)(lo8 ? da1[grp][i] : x1) * 65536.f + (float)(lo8 ? x1 : da1[grp][i]) * 256.f) +
-                                     (float)(lo8 ? db1[grp][i] : y1);
+                    const int a0 = da0[grp][i], x0 = dpp_ror8(a0), a1 = da1[grp][i], x1 = dpp_ror8(a1);
+                    const float r0 = fmaf((float)(lo8 ? a0 : x0), 65536.f, (float)(db0[grp][i] * 256 + (lo8 ? x0 : a0)));
+                    const float r1 = fmaf((float)(lo8 ? a1 : x1), 65536.f, (float)(db1[grp][i] * 256 + (lo8 ? x1 : a1)));
                     sc[4 * grp + i] = (r0 * kn[4 * grp + i].x + r1 * kn[4 * grp + i].y) * qs;
                 }
             float vm;
