@@ -9,11 +9,14 @@
 //     the wavefronts copy the images by DMA; for shorter chunks they load and widen each tile themselves;
 //   - wavefronts 0-3 compute, 32 query rows each (wavefront w: tokens 4w .. 4w+3, row r = (token 4w + r/8,
 //     head r%8)): S^T = K . Q^T and O^T += V^T . P^T on v_mfma_f32_32x32x16_f16 with Q fp16 in registers. The 32x32
-//     D layout gives each lane one query row (lane % 32) and 16 keys: row max / row sum are in-lane plus one
-//     cross-half swap. LDS operand reads are issued two MFMAs ahead of their use.
-// A SIMD holds one wavefront of each kind, so the filling runs beside the other's MFMAs; one barrier per tile.
+//     D layout gives each lane one query row (lane % 32) and 16 keys. LDS operand reads are issued two MFMAs ahead
+//     of their use.
+// A SIMD holds one wavefront of each kind, so the filling runs beside the other's MFMAs; one barrier per tile. The
+// DMA wavefronts' barrier is a bare s_barrier: __syncthreads() would make them wait for the image two tiles ahead.
 // Lazy rescale: O and l are only rescaled when a row's maximum grows by more than 8 (log2 units) over the value the
-// probabilities are referenced to, so p <= 2^8 and the VALU touches O only then.
+// probabilities are referenced to (m_ref, set by tile 0), so p <= 2^8 and the VALU touches O only then. A score
+// enters the softmax as s * scale - m_ref in one fma. Each lane tests its own half of the row against the slack (a
+// wavefront-wide ballot); only a rescale needs the row's full maximum, from the lane ^ 32 exchange.
 // Softmax in base 2 (scale 1/sqrt(256) * log2(e), kernels.cuh:1513). Rounding: Q, P and the scaled V values are
 // fp16 MFMA operands with fp32 accumulation; the reference rounds Q and P * vscale (kernels.cuh:1508,1656).
 #include <map>
@@ -300,7 +303,8 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
         issue(0);
         if (ntiles > 1) issue(1);
         if (ntiles > 1) { if (pw == 0) wait_vm<10>(); else wait_vm<9>(); } else wait_vm<0>();
-        __syncthreads();  // image 0 is in buffer 0
+        // image 0 is in buffer 0. Not __syncthreads, which would also wait for image 1.
+        asm volatile("s_barrier" ::: "memory");
         for (int j = 0; j < ntiles; j++) {
             if (j + 2 < ntiles) {
                 issue(j + 2);  // buffer (j + 2) % 3 held tile j - 1, which every computing wavefront is past
@@ -308,7 +312,7 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
             } else {
                 wait_vm<0>();
             }
-            __syncthreads();
+            asm volatile("s_barrier" ::: "memory");  // image j + 2 stays in flight
         }
         return;
     }
@@ -405,32 +409,40 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
                     sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], sc, 0, 0, 0);
                 }
             }
+            // scores relative to the row's reference maximum: t = s * scale - m_ref in one fma (tile 0 sets m_ref: key 0
+            // is unmasked in every row, so it is finite)
+            const float mneg = j == 0 ? 0.f : -m_ref;
 #pragma unroll
             for (int a4 = 0; a4 < 4; a4++) {
                 const float4 kq = *reinterpret_cast<const float4*>(scl + 8 * a4 + 4 * h32);
-                sc[4 * a4] *= kq.x; sc[4 * a4 + 1] *= kq.y; sc[4 * a4 + 2] *= kq.z; sc[4 * a4 + 3] *= kq.w;
+                sc[4 * a4] = fmaf(sc[4 * a4], kq.x, mneg); sc[4 * a4 + 1] = fmaf(sc[4 * a4 + 1], kq.y, mneg);
+                sc[4 * a4 + 2] = fmaf(sc[4 * a4 + 2], kq.z, mneg); sc[4 * a4 + 3] = fmaf(sc[4 * a4 + 3], kq.w, mneg);
             }
             if (k0 + BK - 1 > wmin) {  // a diagonal tile: causal mask per row
 #pragma unroll
                 for (int i = 0; i < 16; i++)
                     if (k0 + 8 * (i >> 2) + 4 * h32 + (i & 3) > prow) sc[i] = -INFINITY;
             }
-            float mt = sc[0];
+            float mt = sc[0];  // this lane's half of the row; the other half is in lane ^ 32
 #pragma unroll
             for (int i = 1; i < 16; i++) mt = fmaxf(mt, sc[i]);
-            mt = fmaxf(mt, __shfl_xor(mt, 32));
-            // lazy rescale: O and l are referenced to m_ref, moved only when a row's maximum passes it by the slack
-            if (__ballot(mt > m_ref + RESCALE_SLACK)) {
-                const float m_new = fmaxf(m_ref, mt);
-                const float cf = fast_exp2(m_ref - m_new);  // 0 on the first tile
-                if (__ballot(m_ref != -INFINITY)) {
+            if (j == 0) {
+                mt = fmaxf(mt, __shfl_xor(mt, 32));
+                m_ref = mt;
 #pragma unroll
-                    for (int db = 0; db < 8; db++)
+                for (int i = 0; i < 16; i++) sc[i] -= mt;
+            } else if (__ballot(mt > RESCALE_SLACK)) {
+                // lazy rescale: O and l are referenced to m_ref, moved only when a row's maximum passes it by the slack
+                const float d = fmaxf(fmaxf(mt, __shfl_xor(mt, 32)), 0.f);
+                const float cf = fast_exp2(-d);
 #pragma unroll
-                        for (int i = 0; i < 16; i++) o[db][i] *= cf;
-                }
+                for (int db = 0; db < 8; db++)
+#pragma unroll
+                    for (int i = 0; i < 16; i++) o[db][i] *= cf;
                 l_run *= cf;
-                m_ref = m_new;
+                m_ref += d;
+#pragma unroll
+                for (int i = 0; i < 16; i++) sc[i] -= d;
             }
             // ---- P^T (fp16) as B operands: MFMA m (keys 16m ..) takes S elements 8m .. 8m+7 ----
             half8_t pf[2];
@@ -439,7 +451,7 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
             for (int m = 0; m < 2; m++)
 #pragma unroll
                 for (int jj = 0; jj < 8; jj += 2) {
-                    const float p0 = fast_exp2(sc[8 * m + jj] - m_ref), p1 = fast_exp2(sc[8 * m + jj + 1] - m_ref);
+                    const float p0 = fast_exp2(sc[8 * m + jj]), p1 = fast_exp2(sc[8 * m + jj + 1]);
                     const half2_t ph = half2_t{(_Float16)p0, (_Float16)p1};
                     pf[m][jj] = ph[0]; pf[m][jj + 1] = ph[1];
                     ls = __builtin_amdgcn_fdot2(ph, ones, ls, false);
