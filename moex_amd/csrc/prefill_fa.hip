@@ -395,6 +395,7 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
             float16_t sc;
 #pragma unroll
             for (int i = 0; i < 16; i++) sc[i] = 0.f;
+            float4 kq[4];  // the score scales, read during the last Q.K MFMAs
             {   // K operands read FA_KPF MFMAs ahead of their use (LDS latency)
                 const _Float16* krow = Kt + r * KST + 8 * h32;
                 half8_t ka[FA_KPF];
@@ -405,6 +406,10 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
                     const half8_t a = ka[s % FA_KPF];
                     if (s + FA_KPF < 16)
                         ka[s % FA_KPF] = *reinterpret_cast<const half8_t*>(krow + 16 * (s + FA_KPF));
+                    if (s == 16 - 2) {
+#pragma unroll
+                        for (int a4 = 0; a4 < 4; a4++) kq[a4] = *reinterpret_cast<const float4*>(scl + 8 * a4 + 4 * h32);
+                    }
                     __builtin_amdgcn_sched_barrier(0);  // keep each read FA_KPF MFMAs ahead of its use
                     sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], sc, 0, 0, 0);
                 }
@@ -414,9 +419,8 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
             const float mneg = j == 0 ? 0.f : -m_ref;
 #pragma unroll
             for (int a4 = 0; a4 < 4; a4++) {
-                const float4 kq = *reinterpret_cast<const float4*>(scl + 8 * a4 + 4 * h32);
-                sc[4 * a4] = fmaf(sc[4 * a4], kq.x, mneg); sc[4 * a4 + 1] = fmaf(sc[4 * a4 + 1], kq.y, mneg);
-                sc[4 * a4 + 2] = fmaf(sc[4 * a4 + 2], kq.z, mneg); sc[4 * a4 + 3] = fmaf(sc[4 * a4 + 3], kq.w, mneg);
+                sc[4 * a4] = fmaf(sc[4 * a4], kq[a4].x, mneg); sc[4 * a4 + 1] = fmaf(sc[4 * a4 + 1], kq[a4].y, mneg);
+                sc[4 * a4 + 2] = fmaf(sc[4 * a4 + 2], kq[a4].z, mneg); sc[4 * a4 + 3] = fmaf(sc[4 * a4 + 3], kq[a4].w, mneg);
             }
             if (k0 + BK - 1 > wmin) {  // a diagonal tile: causal mask per row
 #pragma unroll
