@@ -11,8 +11,9 @@
 //     head r%8)): S^T = K . Q^T and O^T += V^T . P^T on v_mfma_f32_32x32x16_f16 with Q fp16 in registers. The 32x32
 //     D layout gives each lane one query row (lane % 32) and 16 keys. LDS operand reads are issued two MFMAs ahead
 //     of their use.
-// A SIMD holds one wavefront of each kind, so the filling runs beside the other's MFMAs; one barrier per tile. The
-// DMA wavefronts' barrier is a bare s_barrier: __syncthreads() would make them wait for the image two tiles ahead.
+// A SIMD holds one wavefront of each kind, so the filling runs beside the other's MFMAs; one barrier per tile (per
+// pair of tiles on the image path). The DMA wavefronts' barrier is a bare s_barrier: __syncthreads() would make them
+// wait for the images still in flight.
 // Lazy rescale: O and l are only rescaled when a row's maximum grows by more than 8 (log2 units) over the value the
 // probabilities are referenced to (m_ref, set by tile 0), so p <= 2^8 and the VALU touches O only then. A score
 // enters the softmax as s * scale - m_ref in one fma. Each lane tests its own half of the row against the slack (a
@@ -256,19 +257,20 @@ __global__ void __launch_bounds__(256) fa_image_kernel(moex_kv_cache kv, const i
 }
 
 // Warp-specialised workgroup of 8 wavefronts. Wavefronts 0-3 compute (32 query rows each); wavefronts 4-7 fill the LDS
-// tile buffers. Each SIMD holds one wavefront of each kind, so the filling runs beside the other wavefront's MFMAs. One
-// barrier per key tile.
+// tile buffers. Each SIMD holds one wavefront of each kind, so the filling runs beside the other wavefront's MFMAs.
 //   IMG = false: the staging wavefronts load the next tiles' int8/turbo K and V and widen them (two buffers: during
-//   tile j the computing wavefronts read buffer j%2 while the staging wavefronts fill buffer (j+1)%2).
-//   IMG = true: the tiles were widened by fa_image_kernel; the staging wavefronts only copy images into a ring of
-//   three buffers by DMA, two tiles ahead, leaving out the padding slots nobody reads.
+//   tile j the computing wavefronts read buffer j%2 while the staging wavefronts fill buffer (j+1)%2; one barrier per
+//   tile).
+//   IMG = true: the tiles were widened by fa_image_kernel; the staging wavefronts only copy images by DMA into four
+//   buffers (two pairs of tiles: one computed while the next lands, one barrier per pair), leaving out the padding
+//   slots nobody reads.
 template <bool TB, bool IMG>
 __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restrict__ qo, const float* __restrict__ q_gate,
                                                             moex_kv_cache kv, const unsigned char* __restrict__ img,
                                                             int ntmax, float* __restrict__ out, int H, int KV,
                                                             const int* __restrict__ pos_d, int max_t, int ld, int T) {
     extern __shared__ __align__(16) unsigned char smem[];
-    constexpr int NB = IMG ? 3 : 2;
+    constexpr int NB = IMG ? 4 : 2;
 #define KBUF(i) (smem + (i) * TILE_BYTES)
 #define VBUF(i) (smem + (i) * TILE_BYTES + KT_BYTES)
 #define SBUF(i) (reinterpret_cast<float*>(smem + (i) * TILE_BYTES + KT_BYTES + VT_BYTES))
@@ -280,7 +282,7 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
     const int ntiles = (hi + BK - 1) / BK;
 
     if (threadIdx.x >= 256 && IMG) {
-        // ---------------- DMA wavefronts: image j -> buffer j % 3, 1 KB pieces i = pw, pw + 4, .. ----------------
+        // ---------------- DMA wavefronts: image j -> buffer j % 4, 1 KB pieces i = pw, pw + 4, .. ----------------
         const int pw = (threadIdx.x >> 6) - 4, lane = threadIdx.x & 63;
         const unsigned char* src = img + (size_t)kvh * ntmax * TILE_BYTES + 16 * lane;
         constexpr int NP = (TILE_BYTES + 1023) / 1024;  // 37 pieces, the last one partial
@@ -300,19 +302,18 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
             }
         };
         // piece counts per wavefront: 10 for pw = 0 (pieces 0, 4, .., 36), 9 for the others
-        issue(0);
-        if (ntiles > 1) issue(1);
-        if (ntiles > 1) { if (pw == 0) wait_vm<10>(); else wait_vm<9>(); } else wait_vm<0>();
-        // image 0 is in buffer 0. Not __syncthreads, which would also wait for image 1.
-        asm volatile("s_barrier" ::: "memory");
-        for (int j = 0; j < ntiles; j++) {
-            if (j + 2 < ntiles) {
-                issue(j + 2);  // buffer (j + 2) % 3 held tile j - 1, which every computing wavefront is past
-                if (pw == 0) wait_vm<10>(); else wait_vm<9>();  // image j + 1 has landed
-            } else {
-                wait_vm<0>();
-            }
-            asm volatile("s_barrier" ::: "memory");  // image j + 2 stays in flight
+        // pairs of tiles: pair p = tiles 2p, 2p + 1 in buffers 2 (p % 2), + 1; one barrier per pair
+        for (int j = 0; j < 4 && j < ntiles; j++) issue(j);
+        if (ntiles >= 4) { if (pw == 0) wait_vm<20>(); else wait_vm<18>(); }
+        else if (ntiles == 3) { if (pw == 0) wait_vm<10>(); else wait_vm<9>(); }
+        else wait_vm<0>();
+        asm volatile("s_barrier" ::: "memory");  // pair 0 is in buffers 0, 1
+        const int np = (ntiles + 1) / 2;
+        for (int p = 0; p < np; p++) {
+            wait_vm<0>();                            // pair p + 1 has landed
+            asm volatile("s_barrier" ::: "memory");  // every computing wavefront is past pair p
+            if (2 * p + 4 < ntiles) issue(2 * p + 4);
+            if (2 * p + 5 < ntiles) issue(2 * p + 5);
         }
         return;
     }
@@ -479,7 +480,7 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
                 }
             }
         }
-        __syncthreads();
+        if (!IMG || (j & 1) || j + 1 == ntiles) __syncthreads();
     }
 #undef KBUF
 #undef VBUF
@@ -541,7 +542,7 @@ template <bool TB, bool IMG>
 void set_lds() {
     static bool once = [] {
         MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(fa_prefill_kernel<TB, IMG>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (IMG ? 3 : 2) * TILE_BYTES));
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (IMG ? 4 : 2) * TILE_BYTES));
         return true;
     }();
     (void)once;
@@ -557,7 +558,7 @@ void launch_fa_t(const float* qo, const float* q_gate, moex_kv_cache kv, float* 
         set_lds<TB, true>();
         hipLaunchKernelGGL(fa_image_kernel<TB>, dim3(ntmax, KV), dim3(256), 0, st, kv, pos_d, T, max_t, ntmax, img);
         MOEX_LAUNCHED();
-        hipLaunchKernelGGL((fa_prefill_kernel<TB, true>), dim3(nb), dim3(512), 3 * TILE_BYTES, st, qo, q_gate, kv, img,
+        hipLaunchKernelGGL((fa_prefill_kernel<TB, true>), dim3(nb), dim3(512), 4 * TILE_BYTES, st, qo, q_gate, kv, img,
                            ntmax, out, H, KV, pos_d, max_t, ld, T);
     } else {
         set_lds<TB, false>();
