@@ -257,27 +257,32 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws_kernel(const f
                 }
             }
             float M = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
-            M = max_x32(max_x16(M));   // over the 4 lane groups: the wave's 32 keys
-            vm = max_x32(max_x16(vm));  // every column of a lane group holds the same keys
-            // ---- lazy rescale: new reference maximum / V-scale exponent ----
-            const float nref = M > mref + WS_SLACK ? M : mref;
-            const float fown = ex2d(mref, nref);
-            vmax = fmaxf(vmax, vm);
-            int ev = 0;
-            if (vmax > 0.f) (void)frexpf(vmax, &ev);  // vmax < 2^ev: p * vs * 2^(7 - ev) < 2^(7 + WS_SLACK)
-            const int nsig = 7 - ev;
-            if (__builtin_amdgcn_ballot_w64(fown != 1.f) != 0 || nsig != sig) {
-                const float sf = ldexpf(1.f, nsig - sig);
-                float fr[4];
+            // the reductions over the lane groups only when some lane's own keys pass a bound (rare). A lane's
+            // own maximum passes m_ref + slack exactly when its group's does, and V scales below 2^(7 - sig)
+            // cannot move the exponent: the same decisions as with the reduced values, bit for bit
+            if (__builtin_amdgcn_ballot_w64(M > mref + WS_SLACK || vm >= ldexpf(1.f, 7 - sig)) != 0) {
+                M = max_x32(max_x16(M));
+                vm = max_x32(max_x16(vm));  // every column of a lane group holds the same keys
+                // ---- lazy rescale: new reference maximum / V-scale exponent ----
+                const float nref = M > mref + WS_SLACK ? M : mref;
+                const float fown = ex2d(mref, nref);
+                vmax = fmaxf(vmax, vm);
+                int ev = 0;
+                if (vmax > 0.f) (void)frexpf(vmax, &ev);  // vmax < 2^ev: p * vs * 2^(7 - ev) < 2^(7 + WS_SLACK)
+                const int nsig = 7 - ev;
+                if (__builtin_amdgcn_ballot_w64(fown != 1.f) != 0 || nsig != sig) {
+                    const float sf = ldexpf(1.f, nsig - sig);
+                    float fr[4];
 #pragma unroll
-                for (int i = 0; i < 4; i++) fr[i] = __shfl(fown, 2 * (2 * g + (i >> 1))) * sf;
+                    for (int i = 0; i < 4; i++) fr[i] = __shfl(fown, 2 * (2 * g + (i >> 1))) * sf;
 #pragma unroll
-                for (int J = 0; J < 16; J++)
+                    for (int J = 0; J < 16; J++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++) o[J][i] *= fr[i];
-                lacc *= fown;
-                mref = nref;
-                sig = nsig;
+                        for (int i = 0; i < 4; i++) o[J][i] *= fr[i];
+                    lacc *= fown;
+                    mref = nref;
+                    sig = nsig;
+                }
             }
             // ---- P = 2^(s - mref) * vs * 2^sig as fp16 hi + lo: row 2h + 1 of the P operand is the lo part of row 2h,
             // formed by the lane pair m16 = 2h (hi), 2h + 1 (lo), each lane's 8 keys its own A operand ----
@@ -501,27 +506,32 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wsp_kernel(const 
                     }
                 }
                 float M = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
-                M = max_x32(max_x16(M));
-                vm = max_x32(max_x16(vm));
-                // ---- lazy rescale: new reference maximum of a column / V-scale exponent ----
-                const float nref = M > mref + WS_SLACK ? M : mref;
-                const float fown = ex2d(mref, nref);
-                vmax = fmaxf(vmax, vm);
-                int ev = 0;
-                if (vmax > 0.f) (void)frexpf(vmax, &ev);  // vmax < 2^ev: p * vs * 2^(7 - ev) < 2^(7 + WS_SLACK)
-                const int nsig = 7 - ev;
-                if (__builtin_amdgcn_ballot_w64(fown != 1.f) != 0 || nsig != sig) {
-                    const float sf = ldexpf(1.f, nsig - sig);
-                    float fr[4];
+                // the reductions over the lane groups only when some lane's own keys pass a bound (rare). A lane's
+                // own maximum passes m_ref + slack exactly when its group's does, and V scales below 2^(7 - sig)
+                // cannot move the exponent: the same decisions as with the reduced values, bit for bit
+                if (__builtin_amdgcn_ballot_w64(M > mref + WS_SLACK || vm >= ldexpf(1.f, 7 - sig)) != 0) {
+                    M = max_x32(max_x16(M));
+                    vm = max_x32(max_x16(vm));
+                    // ---- lazy rescale: new reference maximum of a column / V-scale exponent ----
+                    const float nref = M > mref + WS_SLACK ? M : mref;
+                    const float fown = ex2d(mref, nref);
+                    vmax = fmaxf(vmax, vm);
+                    int ev = 0;
+                    if (vmax > 0.f) (void)frexpf(vmax, &ev);  // vmax < 2^ev: p * vs * 2^(7 - ev) < 2^(7 + WS_SLACK)
+                    const int nsig = 7 - ev;
+                    if (__builtin_amdgcn_ballot_w64(fown != 1.f) != 0 || nsig != sig) {
+                        const float sf = ldexpf(1.f, nsig - sig);
+                        float fr[4];
 #pragma unroll
-                    for (int i = 0; i < 4; i++) fr[i] = __shfl(fown, 4 * g + i) * sf;  // O row 4g + i = column 4g + i
+                        for (int i = 0; i < 4; i++) fr[i] = __shfl(fown, 4 * g + i) * sf;  // O row 4g + i = column 4g + i
 #pragma unroll
-                    for (int J = 0; J < 16; J++)
+                        for (int J = 0; J < 16; J++)
 #pragma unroll
-                        for (int i = 0; i < 4; i++) o[J][i] *= fr[i];
-                    lacc *= fown;
-                    mref = nref;
-                    sig = nsig;
+                            for (int i = 0; i < 4; i++) o[J][i] *= fr[i];
+                        lacc *= fown;
+                        mref = nref;
+                        sig = nsig;
+                    }
                 }
                 // ---- P = 2^(s - mref) * vs * 2^sig = hi + lo in fp16 (a column with no key yet has P = 0); each lane's
                 // 8 keys are its own A operand ----
@@ -881,27 +891,32 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
                 }
             }
             float M = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
-            M = max_x32(max_x16(M));
-            vm = max_x32(max_x16(vm)) * TK3;
-            // ---- lazy rescale ----
-            const float nref = M > mref + WS_SLACK ? M : mref;
-            const float fown = ex2d(mref, nref);
-            vmax = fmaxf(vmax, vm);
-            int ev = 0;
-            if (vmax > 0.f) (void)frexpf(vmax, &ev);  // vmax < 2^ev: p * vn * K3 * 2^(7 - ev) < 2^(7 + WS_SLACK)
-            const int nsig = 7 - ev;
-            if (__builtin_amdgcn_ballot_w64(fown != 1.f) != 0 || nsig != sig) {
-                const float sf = ldexpf(1.f, nsig - sig);
-                float fr[4];
+            // the reductions over the lane groups only when some lane's own keys pass a bound (rare). A lane's
+            // own maximum passes m_ref + slack exactly when its group's does, and V scales below 2^(7 - sig)
+            // cannot move the exponent: the same decisions as with the reduced values, bit for bit
+            if (__builtin_amdgcn_ballot_w64(M > mref + WS_SLACK || vm * TK3 >= ldexpf(1.f, 7 - sig)) != 0) {
+                M = max_x32(max_x16(M));
+                vm = max_x32(max_x16(vm)) * TK3;
+                // ---- lazy rescale ----
+                const float nref = M > mref + WS_SLACK ? M : mref;
+                const float fown = ex2d(mref, nref);
+                vmax = fmaxf(vmax, vm);
+                int ev = 0;
+                if (vmax > 0.f) (void)frexpf(vmax, &ev);  // vmax < 2^ev: p * vn * K3 * 2^(7 - ev) < 2^(7 + WS_SLACK)
+                const int nsig = 7 - ev;
+                if (__builtin_amdgcn_ballot_w64(fown != 1.f) != 0 || nsig != sig) {
+                    const float sf = ldexpf(1.f, nsig - sig);
+                    float fr[4];
 #pragma unroll
-                for (int i = 0; i < 4; i++) fr[i] = __shfl(fown, (4 * g + i) & 7) * sf;  // O row m: head m % 8
+                    for (int i = 0; i < 4; i++) fr[i] = __shfl(fown, (4 * g + i) & 7) * sf;  // O row m: head m % 8
 #pragma unroll
-                for (int J = 0; J < 16; J++)
+                    for (int J = 0; J < 16; J++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++) o[J][i] *= fr[i];
-                lacc *= fown;
-                mref = nref;
-                sig = nsig;
+                        for (int i = 0; i < 4; i++) o[J][i] *= fr[i];
+                    lacc *= fown;
+                    mref = nref;
+                    sig = nsig;
+                }
             }
             // ---- P of both V halves = 2^(s - mref) * vn * K3 * 2^sig as fp16 hi (m16 < 8) / lo (m16 >= 8): row m16 of
             // the P operand (head m16 % 8), each lane's 8 keys its own A operand (the P.V key order is the Q.K
