@@ -352,7 +352,8 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
                     load_v<TB>(sv, kv, rbase, k2, hi, tid);
                 }
             }
-            __syncthreads();
+            // tile j + 1 is in LDS; tile j + 2 stays in flight into registers (__syncthreads would wait for it)
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         }
         return;
     }
