@@ -11,7 +11,10 @@
  * moex_kv_alloc / moex_kv_free and moex_attn_fa with T >= 128: that call widens the K/V tiles once into a tile-image
  * workspace of KV * ceil(max_t / 32) * 37632 bytes, one per (device, stream), allocated on the first such call on a
  * stream and grown (after waiting for the stream) when a larger max_t comes; it is kept until the process ends.
- * After one eager call of a given max_t on a stream, every attention call can be captured into a HIP graph.
+ * A chunk whose token tiles leave the chip underfilled (KV * ceil(T / 16) < CUs) may split each token tile's keys
+ * over several workgroups: it uses a second such workspace for their partial results, T * H * pieces * 1040 bytes
+ * (at most 32 pieces; MOEX_FA_SPLIT=n caps them, 1 turns splitting off).
+ * After one eager call of a given max_t and T on a stream, every attention call can be captured into a HIP graph.
  *
  * Errors (kernels.cuh:8-11, CK): a failing HIP call prints "HIP <error> at <file>:<line>" and exits(1),
  * unless a soft-error slot is installed (moex_set_soft_error), in which case the first error code is

@@ -20,6 +20,8 @@
 // wavefront-wide ballot); only a rescale needs the row's full maximum, from the lane ^ 32 exchange.
 // Softmax in base 2 (scale 1/sqrt(256) * log2(e), kernels.cuh:1513). Rounding: Q, P and the scaled V values are
 // fp16 MFMA operands with fp32 accumulation; the reference rounds Q and P * vscale (kernels.cuh:1508,1656).
+#include <algorithm>
+#include <cstdlib>
 #include <map>
 #include <mutex>
 #include <type_traits>
@@ -223,6 +225,25 @@ __device__ __forceinline__ bool map_block(int b, int KV, int NT, int& kvh, int& 
     kvh = b / NT; tile = NT - 1 - b % NT;
     return kvh < KV;
 }
+// Key pieces of token tile t (keys [0, pos0 + min(FT (t + 1), T))), for chunks whose token tiles leave the chip
+// underfilled (KV x tiles < CUs; the host then passes nsf > 1). Computed on the device (pos0 is a device value), the
+// same way by the FA kernel and the merge: a tile of n key tiles takes floor(n / w) pieces (1 to nsf), w = the chip's
+// average share of the work, so the pieces of all tiles fill the chip about once; w is at least
+// max(FA_MINW, 2 x token tiles), as each workgroup first loads its queries (more of them for a longer chunk) and
+// each piece adds merge traffic. Piece s is tiles [s n / ns, (s + 1) n / ns): at least w >= 8 tiles, so its first key
+// is below every row of the token tile (each row sees a key in every piece).
+constexpr int FA_MINW = 8;
+constexpr int FA_NSF_MAX = 32;
+constexpr int FP_ROW = AHD + 4;  // a piece's partial row: O[256], m, l, 2 spare (16-byte aligned rows)
+__host__ __device__ inline int fa_piece_w(int pos0, int T, int KV, int NT, int ncu) {
+    const int total = (NT * ((2 * pos0 + T + FT) / 2) + NT * (BK - 1)) / BK;  // about the sum of n (split chunks: NT <= CUs)
+    const int m = FA_MINW > 2 * NT ? FA_MINW : 2 * NT, v = (KV * total + ncu - 1) / ncu;
+    return m > v ? m : v;
+}
+__host__ __device__ inline int fa_pieces(int t, int pos0, int T, int nsf, int w) {
+    const int n = (pos0 + (FT * (t + 1) < T ? FT * (t + 1) : T) + BK - 1) / BK, k = n / w;
+    return k < 1 ? 1 : k > nsf ? nsf : k;
+}
 int fa_grid(int KV, int T) {
     const int NT = (T + FT - 1) / FT;
     if (8 % KV == 0) { const int xpk = 8 / KV; return 8 * ((NT + xpk - 1) / xpk); }
@@ -264,22 +285,39 @@ __global__ void __launch_bounds__(256) fa_image_kernel(moex_kv_cache kv, const i
 //   IMG = true: the tiles were widened by fa_image_kernel; the staging wavefronts only copy images by DMA into four
 //   buffers (two pairs of tiles: one computed while the next lands, one barrier per pair), leaving out the padding
 //   slots nobody reads.
-template <bool TB, bool IMG>
+template <bool TB, bool IMG, bool SPLIT>
 __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restrict__ qo, const float* __restrict__ q_gate,
                                                             moex_kv_cache kv, const unsigned char* __restrict__ img,
                                                             int ntmax, float* __restrict__ out, int H, int KV,
-                                                            const int* __restrict__ pos_d, int max_t, int ld, int T) {
+                                                            const int* __restrict__ pos_d, int max_t, int ld, int T,
+                                                            float* __restrict__ fpart, int nsf, int ncu) {
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr int NB = IMG ? 4 : 2;
 #define KBUF(i) (smem + (i) * TILE_BYTES)
 #define VBUF(i) (smem + (i) * TILE_BYTES + KT_BYTES)
 #define SBUF(i) (reinterpret_cast<float*>(smem + (i) * TILE_BYTES + KT_BYTES + VT_BYTES))
-    const int NT = (T + FT - 1) / FT;
-    int kvh, tile;
-    if (!map_block(blockIdx.x, KV, NT, kvh, tile)) return;
-    const int t0 = tile * FT, pos0 = *pos_d, nt = min(FT, T - t0), hi = pos0 + t0 + nt;  // keys [0, hi)
+    const int NT = (T + FT - 1) / FT, pos0 = *pos_d;
+    int kvh, tile, piece = 0, nsp = 1;
+    if (SPLIT) {
+        // block b takes the b-th piece, pieces listed heaviest token tile first, so the blocks left without one are
+        // the last ones dispatched (a queued block waits for a whole CU's LDS even when it has nothing to do)
+        const int w = fa_piece_w(pos0, T, KV, NT, ncu);
+        int b = blockIdx.x;
+        for (tile = NT - 1; tile >= 0; tile--) {
+            nsp = fa_pieces(tile, pos0, T, nsf, w);
+            if (b < KV * nsp) break;
+            b -= KV * nsp;
+        }
+        if (tile < 0) return;
+        kvh = b % KV;
+        piece = b / KV;
+    } else if (!map_block(blockIdx.x, KV, NT, kvh, tile)) {
+        return;
+    }
+    const int t0 = tile * FT, nt = min(FT, T - t0), hi = pos0 + t0 + nt;  // keys [0, hi)
     const size_t rbase = (size_t)kvh * max_t;
-    const int ntiles = (hi + BK - 1) / BK;
+    const int nall = (hi + BK - 1) / BK, ja = SPLIT ? piece * nall / nsp : 0;  // this piece: key tiles [ja, ja + ntiles)
+    const int ntiles = SPLIT ? (piece + 1) * nall / nsp - ja : nall;
 
     if (threadIdx.x >= 256 && IMG) {
         // ---------------- DMA wavefronts: image j -> buffer j % 4, 1 KB pieces i = pw, pw + 4, .. ----------------
@@ -288,7 +326,7 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
         constexpr int NP = (TILE_BYTES + 1023) / 1024;  // 37 pieces, the last one partial
         static_assert(NP == 37 && TILE_BYTES % 16 == 0, "image pieces");
         auto issue = [&](int j) {
-            const unsigned char* g = src + (size_t)j * TILE_BYTES;
+            const unsigned char* g = src + (size_t)(ja + j) * TILE_BYTES;
             unsigned char* l = smem + (j % NB) * TILE_BYTES;
 #pragma unroll
             for (int u = 0; u < 10; u++) {
@@ -322,17 +360,18 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
         const int tid = threadIdx.x - 256;
         StageK sk;
         StageV sv;
-        load_k<TB>(sk, kv, rbase, 0, hi, tid);
-        load_v<TB>(sv, kv, rbase, 0, hi, tid);
-        store_k<TB>(sk, KBUF(0), SBUF(0), SBUF(0) + BK, 0, hi, tid);
-        store_v<TB>(sv, VBUF(0), 0, hi, tid);
+        const int ka = ja * BK;
+        load_k<TB>(sk, kv, rbase, ka, hi, tid);
+        load_v<TB>(sv, kv, rbase, ka, hi, tid);
+        store_k<TB>(sk, KBUF(0), SBUF(0), SBUF(0) + BK, ka, hi, tid);
+        store_v<TB>(sv, VBUF(0), ka, hi, tid);
         if (ntiles > 1) {
-            load_k<TB>(sk, kv, rbase, BK, hi, tid);
-            load_v<TB>(sv, kv, rbase, BK, hi, tid);
+            load_k<TB>(sk, kv, rbase, ka + BK, hi, tid);
+            load_v<TB>(sv, kv, rbase, ka + BK, hi, tid);
         }
         __syncthreads();
         for (int j = 0; j < ntiles; j++) {
-            const int k1 = (j + 1) * BK, b = (j + 1) & 1;
+            const int k1 = ka + (j + 1) * BK, b = (j + 1) & 1;
             if (j + 1 < ntiles) {
                 if (k1 + BK <= hi) {
                     store_k<TB, true>(sk, KBUF(b), SBUF(b), SBUF(b) + BK, k1, hi, tid);
@@ -387,12 +426,15 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
     const half2_t ones = half2_t{(_Float16)1.f, (_Float16)1.f};
     __syncthreads();
 
-    for (int j = 0; j < ntiles; j++) {
-        if (j < wtiles) {
+    // split: this wavefront's tiles of the piece, then barriers only while the others finish theirs (one loop with a
+    // per-tile test makes the compiler spill once the trip count is not the tile count)
+    const int wt = max(0, min(ntiles, wtiles - ja));
+    for (int j = 0; j < (SPLIT ? wt : ntiles); j++) {
+        if (SPLIT || j < wtiles) {
             const _Float16* Kt = reinterpret_cast<const _Float16*>(KBUF(j % NB));
             const _Float16* Vt = reinterpret_cast<const _Float16*>(VBUF(j % NB));
             const float* scl = SBUF(j % NB);
-            const int k0 = j * BK;
+            const int k0 = (ja + j) * BK;
             // ---- S^T = K . Q^T: lane = (row r, key half h32), element i: key 8*(i/4) + 4*h32 + i%4 ----
             float16_t sc;
 #pragma unroll
@@ -483,14 +525,28 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
         }
         if (!IMG || (j & 1) || j + 1 == ntiles) __syncthreads();
     }
+    if (SPLIT)
+        for (int j = wt; j < ntiles; j++)
+            if (!IMG || (j & 1) || j + 1 == ntiles) __syncthreads();
 #undef KBUF
 #undef VBUF
 #undef SBUF
-    // ---- epilogue: O / l * sigmoid(gate) ----
+    // ---- epilogue: O / l * sigmoid(gate), or this piece's {O, m, l} for the merge ----
     l_run += __shfl_xor(l_run, 32);
     if (tokw >= nt) return;
-    const float il = 1.f / l_run;
     const size_t t = (size_t)(t0 + tokw);
+    if (SPLIT && nsp > 1) {
+        float* prow = fpart + ((t * H + head) * nsf + piece) * FP_ROW;
+#pragma unroll
+        for (int db = 0; db < 8; db++)
+#pragma unroll
+            for (int a4 = 0; a4 < 4; a4++)
+                *reinterpret_cast<float4*>(prow + 32 * db + 8 * a4 + 4 * h32) =
+                    make_float4(o[db][4 * a4], o[db][4 * a4 + 1], o[db][4 * a4 + 2], o[db][4 * a4 + 3]);
+        if (h32 == 0) *reinterpret_cast<float2*>(prow + AHD) = make_float2(m_ref, l_run);
+        return;
+    }
+    const float il = 1.f / l_run;
     float* orow = out + (t * H + head) * AHD;
     const float* grow = q_gate ? q_gate + t * ld + head * 2 * AHD + AHD : nullptr;
 #pragma unroll
@@ -508,22 +564,62 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
         }
 }
 
+// Merge of the key pieces of the token tiles that fa_prefill_kernel split: out = sum_s O_s 2^(m_s - M) /
+// sum_s l_s 2^(m_s - M), times sigmoid(gate). Grid (ceil(T / 4), H): wavefront w merges token 4 blockIdx.x + w, lane
+// l dims 4l .. 4l + 3 (lane s < pieces also holds piece s's m and l). Tiles with one piece were written by the FA
+// kernel.
+__global__ void __launch_bounds__(256) fa_merge_kernel(const float* __restrict__ fpart, const float* __restrict__ q_gate,
+                                                       float* __restrict__ out, int H, int KV, const int* __restrict__ pos_d,
+                                                       int ld, int T, int nsf, int ncu) {
+    const int tok = 4 * blockIdx.x + (threadIdx.x >> 6), h = blockIdx.y, lane = threadIdx.x & 63, pos0 = *pos_d;
+    if (tok >= T) return;
+    const int nsp = fa_pieces(tok / FT, pos0, T, nsf, fa_piece_w(pos0, T, KV, (T + FT - 1) / FT, ncu));
+    if (nsp <= 1) return;
+    const float* pr = fpart + ((size_t)tok * H + h) * nsf * FP_ROW;
+    const float2 ml = lane < nsp ? *reinterpret_cast<const float2*>(pr + lane * FP_ROW + AHD) : make_float2(-INFINITY, 0.f);
+    float M = ml.x;  // finite: each piece holds keys of every row
+#pragma unroll
+    for (int x = 32; x >= 1; x >>= 1) M = fmaxf(M, __shfl_xor(M, x));
+    const float f = lane < nsp ? fast_exp2(ml.x - M) : 0.f;
+    float l = ml.y * f;
+#pragma unroll
+    for (int x = 32; x >= 1; x >>= 1) l += __shfl_xor(l, x);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+    for (int s = 0; s < nsp; s++) {
+        const float fs = __shfl(f, s);
+        const float4 q = *reinterpret_cast<const float4*>(pr + s * FP_ROW + 4 * lane);
+        acc.x += q.x * fs; acc.y += q.y * fs; acc.z += q.z * fs; acc.w += q.w * fs;
+    }
+    const float il = 1.f / l;
+    float4 res = make_float4(acc.x * il, acc.y * il, acc.z * il, acc.w * il);
+    if (q_gate) {
+        const float4 g = *reinterpret_cast<const float4*>(q_gate + (size_t)tok * ld + h * 2 * AHD + AHD + 4 * lane);
+        res.x /= 1.f + __expf(-g.x); res.y /= 1.f + __expf(-g.y);
+        res.z /= 1.f + __expf(-g.z); res.w /= 1.f + __expf(-g.w);
+    }
+    *reinterpret_cast<float4*>(out + ((size_t)tok * H + h) * AHD + 4 * lane) = res;
+}
+
 namespace {
 // Tile-image workspaces, one per (device, stream), grown on demand and kept until the process ends (a call that grows
 // one waits for the stream first). Calls on one stream are ordered, so they can share theirs.
 struct WsKey {
     int dev;
     hipStream_t st;
-    bool operator<(const WsKey& o) const { return dev != o.dev ? dev < o.dev : st < o.st; }
+    int kind;  // 0: tile images, 1: partials of split token tiles
+    bool operator<(const WsKey& o) const {
+        return dev != o.dev ? dev < o.dev : st != o.st ? st < o.st : kind < o.kind;
+    }
 };
 std::mutex g_ws_mu;
 std::map<WsKey, std::pair<unsigned char*, size_t>> g_ws;
 
-unsigned char* fa_workspace(size_t need, hipStream_t st) {
+unsigned char* fa_workspace(size_t need, hipStream_t st, int kind) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    auto& w = g_ws[WsKey{dev, st}];
+    auto& w = g_ws[WsKey{dev, st, kind}];
     if (w.second >= need) return w.first;
     if (w.first) {
         MOEX_CK(hipStreamSynchronize(st));  // earlier calls on this stream may still read the old images
@@ -532,17 +628,17 @@ unsigned char* fa_workspace(size_t need, hipStream_t st) {
     }
     void* p = nullptr;
     if (hipMalloc(&p, need) != hipSuccess) {
-        (void)hipGetLastError();  // out of memory: the caller widens in the kernel instead
+        (void)hipGetLastError();  // out of memory: the caller widens in the kernel / does not split instead
         return nullptr;
     }
     w = {static_cast<unsigned char*>(p), need};
     return w.first;
 }
 
-template <bool TB, bool IMG>
+template <bool TB, bool IMG, bool SPLIT>
 void set_lds() {
     static bool once = [] {
-        MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(fa_prefill_kernel<TB, IMG>),
+        MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(fa_prefill_kernel<TB, IMG, SPLIT>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (IMG ? 4 : 2) * TILE_BYTES));
         return true;
     }();
@@ -552,21 +648,60 @@ void set_lds() {
 template <bool TB>
 void launch_fa_t(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d,
                  int max_t, int ld, int T, hipStream_t st) {
-    const int nb = fa_grid(KV, T), ntmax = (max_t + BK - 1) / BK;
+    static const int ncu = [] {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            return v;
+        return 256;
+    }();
+    const int NT = (T + FT - 1) / FT, nb = fa_grid(KV, T), ntmax = (max_t + BK - 1) / BK;
+    // key pieces per token tile, at most (the device decides, from pos0): only when the token tiles leave the chip
+    // underfilled. A full grid is not split: blocks queued behind a full chip were measured to start only after many
+    // CUs had freed, so pieces of the heavy tiles gained little and the merge cost more. MOEX_FA_SPLIT=n caps the
+    // pieces (1: no splitting).
+    int nsf = KV * NT >= ncu ? 1 : std::min(FA_NSF_MAX, (2 * ncu + KV * NT - 1) / (KV * NT));
+    if (const char* e = std::getenv("MOEX_FA_SPLIT")) nsf = std::max(1, std::min(nsf, std::atoi(e)));
+    if (nsf > 1) {
+        // pos0 <= max_t - T: if the heaviest token tile would not split at any of these positions, launch unsplit
+        // (the split launch's extra blocks and merge cost a few microseconds even when nothing splits)
+        const int pmax = std::max(0, max_t - T);
+        bool any = false;
+        for (int i = 0; i <= 32 && !any; i++) {
+            const int p0 = (int)((long long)pmax * i / 32);
+            any = fa_pieces(NT - 1, p0, T, nsf, fa_piece_w(p0, T, KV, NT, ncu)) > 1;
+        }
+        if (!any) nsf = 1;
+    }
+    float* fpart = nullptr;
+    if (nsf > 1) {
+        fpart = reinterpret_cast<float*>(fa_workspace((size_t)T * H * nsf * FP_ROW * sizeof(float), st, 1));
+        if (!fpart) nsf = 1;
+    }
     unsigned char* img = nullptr;
-    if ((T + FT - 1) / FT >= FA_IMG_TILES) img = fa_workspace((size_t)KV * ntmax * TILE_BYTES, st);
+    if (NT >= FA_IMG_TILES) img = fa_workspace((size_t)KV * ntmax * TILE_BYTES, st, 0);
     if (img) {
-        set_lds<TB, true>();
         hipLaunchKernelGGL(fa_image_kernel<TB>, dim3(ntmax, KV), dim3(256), 0, st, kv, pos_d, T, max_t, ntmax, img);
         MOEX_LAUNCHED();
-        hipLaunchKernelGGL((fa_prefill_kernel<TB, true>), dim3(nb), dim3(512), 4 * TILE_BYTES, st, qo, q_gate, kv, img,
-                           ntmax, out, H, KV, pos_d, max_t, ld, T);
-    } else {
-        set_lds<TB, false>();
-        hipLaunchKernelGGL((fa_prefill_kernel<TB, false>), dim3(nb), dim3(512), 2 * TILE_BYTES, st, qo, q_gate, kv,
-                           nullptr, ntmax, out, H, KV, pos_d, max_t, ld, T);
     }
+    // a split launch has KV x tiles x nsf blocks: the pieces of every tile, the rest exit at once
+    const dim3 grid(nsf > 1 ? KV * NT * nsf : nb);
+    const size_t lds = (img ? 4 : 2) * TILE_BYTES;
+#define FA_LAUNCH(IMG_, SPLIT_)                                                                                        \
+    do {                                                                                                               \
+        set_lds<TB, IMG_, SPLIT_>();                                                                                   \
+        hipLaunchKernelGGL((fa_prefill_kernel<TB, IMG_, SPLIT_>), grid, dim3(512), lds, st, qo, q_gate, kv, img, ntmax, \
+                           out, H, KV, pos_d, max_t, ld, T, fpart, nsf, ncu);                                          \
+    } while (0)
+    if (img) { if (nsf > 1) FA_LAUNCH(true, true); else FA_LAUNCH(true, false); }
+    else { if (nsf > 1) FA_LAUNCH(false, true); else FA_LAUNCH(false, false); }
+#undef FA_LAUNCH
     MOEX_LAUNCHED();
+    if (nsf > 1) {
+        hipLaunchKernelGGL(fa_merge_kernel, dim3((T + 3) / 4, H), dim3(256), 0, st, fpart, q_gate, out, H, KV, pos_d, ld,
+                           T, nsf, ncu);
+        MOEX_LAUNCHED();
+    }
 }
 }  // namespace
 

@@ -2,8 +2,9 @@
 
 A chunk of 8 or more 16-token tiles per kv head (T >= 128) is widened once by the image pre-pass and copied into LDS
 by DMA; a shorter chunk is widened inside the FA kernel. The two paths feed the same bytes to the same arithmetic, so
-the rows two chunks have in common (same token tiles, same wavefronts) come out bit for bit the same. The workspace
-is per (device, stream) and grows with max_t; growing it, and a second stream, must not change a result.
+the rows two chunks have in common (same token tiles, same wavefronts, key splitting off) come out bit for bit the
+same. The workspace is per (device, stream) and grows with max_t; growing it, and a second stream, must not change a
+result.
 """
 import numpy as np
 import pytest
@@ -32,9 +33,11 @@ def _fa(dc, qo_d, qg_d, pos0, T, stream=None):
 
 @pytest.mark.parametrize("turbo", [0, 1])
 @pytest.mark.parametrize("pos0", [0, 777, 5000])
-def test_image_path_matches_in_kernel_widening(data, turbo, pos0):
+def test_image_path_matches_in_kernel_widening(data, turbo, pos0, monkeypatch):
     import torch
     import moex_amd as M
+    # key splitting off: how a chunk's keys are split depends on T, so the two chunks would split differently
+    monkeypatch.setenv("MOEX_FA_SPLIT", "1")
     qo_d, qg_d = data
     max_t = 5400
     if turbo:

@@ -55,6 +55,29 @@ def test_fa_int8(setup, pos0, T):
     assert np.all(np.isfinite(o)) and np.all(np.abs(o).max(axis=-1) > 0)
 
 
+@pytest.mark.parametrize("pos0,T", [(32000, 64), (0, 1024), (5000, 3), (20000, 200), (34000, 17)])
+def test_fa_key_split(setup, pos0, T, monkeypatch):
+    """Chunks whose token tiles leave the chip underfilled (KV x tiles < CUs) split each token tile's keys over
+    several workgroups, merged by a second kernel: both results meet the gate, and they agree with the unsplit kernel
+    (MOEX_FA_SPLIT=1)."""
+    import torch
+    import moex_amd as M
+    hc, dc, qo, qg, qo_d, qg_d = setup
+    outs = {}
+    for cap in ("32", "1"):
+        monkeypatch.setenv("MOEX_FA_SPLIT", cap)
+        out = torch.full((T, H, AHD), float("nan"), dtype=torch.float32, device="cuda")
+        M.attn_fa(qo_d, qg_d, dc, out, H, KV, pos_tensor(pos0), dc.max_t, LD, T)
+        torch.cuda.synchronize()
+        outs[cap] = out.cpu().numpy()
+        e = _gate(f"fa int8 split cap {cap}", outs[cap], qo, qg, hc, pos0, T)
+        assert np.all(np.isfinite(outs[cap]))
+    mag = float(np.abs(outs["1"]).max())
+    d = float(np.abs(outs["32"] - outs["1"]).max())
+    report("fa split vs unsplit", pos0=pos0, T=T, maxdiff=d, mag=mag)
+    assert d <= 2e-3 * mag
+
+
 @pytest.mark.parametrize("pos0,T", CASES[:5])
 def test_prefill_fallback_int8(setup, pos0, T):
     import torch
