@@ -6,7 +6,9 @@
  * The weights are the reference's default form of these matrices (struct Mat with q and s, kernels.cuh:186-196):
  * int8 [O][I] row-major plus one fp32 scale per row, y = s[o] * (q[o,:] . x). Every entry point replaces one function
  * of src/kernels.cuh, cited on its declaration, with the reference's argument order. All pointers are device pointers;
- * stream is an opaque hipStream_t (NULL = the default stream). Nothing allocates or synchronizes. Errors are reported
+ * stream is an opaque hipStream_t (NULL = the default stream). Nothing allocates or synchronizes, except moex_gemm_i8
+ * with S > 8: it rounds X to fp16 into a per-(device, stream) workspace of S * I * 2 bytes, allocated on first use
+ * and grown (after waiting for the stream) for a larger S * I, kept until the process ends. Errors are reported
  * as in moex_attn.h (print and exit(1), or the soft-error slot).
  */
 #ifndef MOEX_DENSE_H

@@ -93,6 +93,9 @@ void launch_fa(const float* qo, const float* q_gate, moex_kv_cache kv, float* ou
 // dense int8 projections (dense.hip)
 void launch_quantize_rows_i8(const uint16_t* W, int8_t* q, float* s, int O, int I, hipStream_t st);
 void launch_gemv_i8(const int8_t* q, const float* s, const float* x, float* y, int NT, int I, int O, hipStream_t st);
+// Device memory kept per (device, stream, kind) until the process ends, grown on demand (a call that grows it first
+// waits for the stream). nullptr if it cannot be allocated.
+unsigned char* stream_workspace(size_t need, hipStream_t st, int kind);
 void launch_gemm_i8(const int8_t* q, const float* s, const float* X, float* Y, int S, int I, int O, hipStream_t st);
 void launch_prefill_k7p(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
                         const int* pos_d, int max_t, int ld, int T, hipStream_t st);

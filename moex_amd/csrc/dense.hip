@@ -17,6 +17,7 @@
 //                          into one L2).
 //   gemm_ws_kernel         The same product and sum order with split roles: 4 wavefronts widen the next K step into
 //                          LDS while 4 run the MFMAs of this one. Used when the grid fits the chip in one pass.
+#include <algorithm>
 #include "common.hpp"
 
 namespace moex {
@@ -210,7 +211,7 @@ constexpr int GM_BM = 128, GM_BN = 128, GM_BK = 32;
 constexpr int GM_LD = GM_BK + 8;  // halves per LDS row (80 B: conflict-free 16-byte operand reads)
 
 __global__ void __launch_bounds__(256, 2) gemm_kernel(const int8_t* __restrict__ W, const float* __restrict__ s,
-                                                   const float* __restrict__ X, float* __restrict__ Y, int S, int I,
+                                                   const _Float16* __restrict__ X, float* __restrict__ Y, int S, int I,
                                                    int O) {
     __shared__ __align__(16) _Float16 lds[2][2][GM_BM * GM_LD];  // [buffer][W, X][row][k]
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r = lane & 31, h32 = lane >> 5;
@@ -232,13 +233,13 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(const int8_t* __restrict__
     const int sr = tid >> 1, sk = (tid & 1) * 16;
     const bool wok = o0 + sr < O, xok = s0 + sr < S;
     const int8_t* wp = W + (size_t)min(o0 + sr, O - 1) * I + sk;
-    const float* xp = X + (size_t)min(s0 + sr, S - 1) * I + sk;
+    const _Float16* xp = X + (size_t)min(s0 + sr, S - 1) * I + sk;
     uint4 wreg;
-    float4 xreg[4];
+    uint4 xreg[2];
     auto load = [&](int k0) {
         wreg = *reinterpret_cast<const uint4*>(wp + k0);
 #pragma unroll
-        for (int j = 0; j < 4; j++) xreg[j] = reinterpret_cast<const float4*>(xp + k0)[j];
+        for (int j = 0; j < 2; j++) xreg[j] = reinterpret_cast<const uint4*>(xp + k0)[j];
     };
     auto store = [&](int b) {
         uint32_t h[8];
@@ -249,16 +250,9 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(const int8_t* __restrict__
         uint4* wd = reinterpret_cast<uint4*>(&lds[b][0][sr * GM_LD + sk]);
         wd[0] = make_uint4(h[0], h[1], h[2], h[3]);
         wd[1] = make_uint4(h[4], h[5], h[6], h[7]);
-        uint32_t xh[8];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float4 v = xok ? xreg[j] : make_float4(0.f, 0.f, 0.f, 0.f);
-            xh[2 * j] = h22u(half2_t{(_Float16)v.x, (_Float16)v.y});
-            xh[2 * j + 1] = h22u(half2_t{(_Float16)v.z, (_Float16)v.w});
-        }
         uint4* xd = reinterpret_cast<uint4*>(&lds[b][1][sr * GM_LD + sk]);
-        xd[0] = make_uint4(xh[0], xh[1], xh[2], xh[3]);
-        xd[1] = make_uint4(xh[4], xh[5], xh[6], xh[7]);
+        xd[0] = xok ? xreg[0] : make_uint4(0u, 0u, 0u, 0u);
+        xd[1] = xok ? xreg[1] : make_uint4(0u, 0u, 0u, 0u);
     };
     float16_t acc[2][2];
 #pragma unroll
@@ -311,12 +305,21 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(const int8_t* __restrict__
     }
 }
 
+// Activations rounded to fp16 once (round to nearest even, as kernels.cuh:306-307 rounds them inside gemm_i8_k): the
+// GEMM tiles re-read them once per weight tile, so fp16 halves that traffic and takes the rounding off the staging.
+__global__ void __launch_bounds__(256) round_f16_kernel(const float4* __restrict__ X, uint2* __restrict__ Xh, size_t n4) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+        const float4 v = X[i];
+        Xh[i] = make_uint2(h22u(half2_t{(_Float16)v.x, (_Float16)v.y}), h22u(half2_t{(_Float16)v.z, (_Float16)v.w}));
+    }
+}
+
 constexpr int GEMM_WS_MAX_BLOCKS = 512;  // 2 workgroups x 256 CUs
 
 // Warp-specialised variant: wavefronts 4-7 load and widen the next K step into the other LDS buffer while
 // wavefronts 0-3 run the MFMAs of this one (one barrier per K step), so the staging VALU work runs beside the MFMAs.
 __global__ void __launch_bounds__(512, 2) gemm_ws_kernel(const int8_t* __restrict__ W, const float* __restrict__ s,
-                                                         const float* __restrict__ X, float* __restrict__ Y, int S, int I,
+                                                         const _Float16* __restrict__ X, float* __restrict__ Y, int S, int I,
                                                          int O) {
     __shared__ __align__(16) _Float16 lds[2][2][GM_BM * GM_LD];  // [buffer][W, X][row][k]
     const int nO = (O + GM_BM - 1) / GM_BM, nS = (S + GM_BN - 1) / GM_BN, bid = blockIdx.x;
@@ -335,13 +338,13 @@ __global__ void __launch_bounds__(512, 2) gemm_ws_kernel(const int8_t* __restric
         const int tid = threadIdx.x - 256, sr = tid >> 1, sk = (tid & 1) * 16;
         const bool wok = o0 + sr < O, xok = s0 + sr < S;
         const int8_t* wp = W + (size_t)min(o0 + sr, O - 1) * I + sk;
-        const float* xp = X + (size_t)min(s0 + sr, S - 1) * I + sk;
+        const _Float16* xp = X + (size_t)min(s0 + sr, S - 1) * I + sk;
         uint4 wreg;
-        float4 xreg[4];
+        uint4 xreg[2];
         auto load = [&](int k0) {
             wreg = *reinterpret_cast<const uint4*>(wp + k0);
 #pragma unroll
-            for (int j = 0; j < 4; j++) xreg[j] = reinterpret_cast<const float4*>(xp + k0)[j];
+            for (int j = 0; j < 2; j++) xreg[j] = reinterpret_cast<const uint4*>(xp + k0)[j];
         };
         auto store = [&](int b) {
             uint32_t h[8];
@@ -352,16 +355,9 @@ __global__ void __launch_bounds__(512, 2) gemm_ws_kernel(const int8_t* __restric
             uint4* wd = reinterpret_cast<uint4*>(&lds[b][0][sr * GM_LD + sk]);
             wd[0] = make_uint4(h[0], h[1], h[2], h[3]);
             wd[1] = make_uint4(h[4], h[5], h[6], h[7]);
-            uint32_t xh[8];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float4 v = xok ? xreg[j] : make_float4(0.f, 0.f, 0.f, 0.f);
-                xh[2 * j] = h22u(half2_t{(_Float16)v.x, (_Float16)v.y});
-                xh[2 * j + 1] = h22u(half2_t{(_Float16)v.z, (_Float16)v.w});
-            }
             uint4* xd = reinterpret_cast<uint4*>(&lds[b][1][sr * GM_LD + sk]);
-            xd[0] = make_uint4(xh[0], xh[1], xh[2], xh[3]);
-            xd[1] = make_uint4(xh[4], xh[5], xh[6], xh[7]);
+            xd[0] = xok ? xreg[0] : make_uint4(0u, 0u, 0u, 0u);
+            xd[1] = xok ? xreg[1] : make_uint4(0u, 0u, 0u, 0u);
         };
         load(0);
         store(0);
@@ -479,11 +475,20 @@ void launch_gemm_i8(const int8_t* q, const float* s, const float* X, float* Y, i
     // Both kernels sum in the same order (identical results). A grid that fits the chip in one pass of two
     // workgroups per CU runs the warp-specialised kernel; a larger one the 4-wavefront kernel, whose extra
     // workgroups in flight hide the staging better than the split roles do (measured on the qkv/o_proj shapes).
+    const size_t n4 = (size_t)S * I / 4;  // I % 32 == 0
+    _Float16* Xh = reinterpret_cast<_Float16*>(stream_workspace(n4 * 8, st, 2));
+    if (!Xh) {
+        report(hipErrorOutOfMemory, __FILE__, __LINE__);
+        return;
+    }
+    hipLaunchKernelGGL(round_f16_kernel, dim3((unsigned)std::min<size_t>((n4 + 255) / 256, 4096)), dim3(256), 0, st,
+                       reinterpret_cast<const float4*>(X), reinterpret_cast<uint2*>(Xh), n4);
+    MOEX_LAUNCHED();
     const int blocks = ((O + GM_BM - 1) / GM_BM) * ((S + GM_BN - 1) / GM_BN);
     if (blocks <= GEMM_WS_MAX_BLOCKS)
-        hipLaunchKernelGGL(gemm_ws_kernel, dim3(blocks), dim3(512), 0, st, q, s, X, Y, S, I, O);
+        hipLaunchKernelGGL(gemm_ws_kernel, dim3(blocks), dim3(512), 0, st, q, s, Xh, Y, S, I, O);
     else
-        hipLaunchKernelGGL(gemm_kernel, dim3(blocks), dim3(256), 0, st, q, s, X, Y, S, I, O);
+        hipLaunchKernelGGL(gemm_kernel, dim3(blocks), dim3(256), 0, st, q, s, Xh, Y, S, I, O);
     MOEX_LAUNCHED();
 }
 

@@ -601,13 +601,13 @@ __global__ void __launch_bounds__(256) fa_merge_kernel(const float* __restrict__
     *reinterpret_cast<float4*>(out + ((size_t)tok * H + h) * AHD + 4 * lane) = res;
 }
 
+// Workspaces, one per (device, stream, kind), grown on demand and kept until the process ends (a call that grows one
+// waits for the stream first). Calls on one stream are ordered, so they can share theirs.
 namespace {
-// Tile-image workspaces, one per (device, stream), grown on demand and kept until the process ends (a call that grows
-// one waits for the stream first). Calls on one stream are ordered, so they can share theirs.
 struct WsKey {
     int dev;
     hipStream_t st;
-    int kind;  // 0: tile images, 1: partials of split token tiles
+    int kind;  // 0: FA tile images, 1: FA partials of split token tiles, 2: fp16 GEMM activations
     bool operator<(const WsKey& o) const {
         return dev != o.dev ? dev < o.dev : st != o.st ? st < o.st : kind < o.kind;
     }
@@ -615,7 +615,9 @@ struct WsKey {
 std::mutex g_ws_mu;
 std::map<WsKey, std::pair<unsigned char*, size_t>> g_ws;
 
-unsigned char* fa_workspace(size_t need, hipStream_t st, int kind) {
+}  // namespace
+
+unsigned char* stream_workspace(size_t need, hipStream_t st, int kind) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
     std::lock_guard<std::mutex> lk(g_ws_mu);
@@ -628,13 +630,14 @@ unsigned char* fa_workspace(size_t need, hipStream_t st, int kind) {
     }
     void* p = nullptr;
     if (hipMalloc(&p, need) != hipSuccess) {
-        (void)hipGetLastError();  // out of memory: the caller widens in the kernel / does not split instead
+        (void)hipGetLastError();  // out of memory: the caller takes a path without it, or reports the error
         return nullptr;
     }
     w = {static_cast<unsigned char*>(p), need};
     return w.first;
 }
 
+namespace {
 template <bool TB, bool IMG, bool SPLIT>
 void set_lds() {
     static bool once = [] {
@@ -675,11 +678,11 @@ void launch_fa_t(const float* qo, const float* q_gate, moex_kv_cache kv, float* 
     }
     float* fpart = nullptr;
     if (nsf > 1) {
-        fpart = reinterpret_cast<float*>(fa_workspace((size_t)T * H * nsf * FP_ROW * sizeof(float), st, 1));
+        fpart = reinterpret_cast<float*>(stream_workspace((size_t)T * H * nsf * FP_ROW * sizeof(float), st, 1));
         if (!fpart) nsf = 1;
     }
     unsigned char* img = nullptr;
-    if (NT >= FA_IMG_TILES) img = fa_workspace((size_t)KV * ntmax * TILE_BYTES, st, 0);
+    if (NT >= FA_IMG_TILES) img = stream_workspace((size_t)KV * ntmax * TILE_BYTES, st, 0);
     if (img) {
         hipLaunchKernelGGL(fa_image_kernel<TB>, dim3(ntmax, KV), dim3(256), 0, st, kv, pos_d, T, max_t, ntmax, img);
         MOEX_LAUNCHED();
