@@ -315,14 +315,28 @@ __global__ void __launch_bounds__(256) round_f16_kernel(const float4* __restrict
 }
 
 constexpr int GEMM_WS_MAX_BLOCKS = 512;  // 2 workgroups x 256 CUs
+constexpr int GEMM_MIN_KSTEPS = 16;        // K steps of a split, at least
+
+// Sum of the K splits of gemm_ws_kernel, in split order (deterministic), times the row scale.
+__global__ void __launch_bounds__(256) gemm_reduce_kernel(const float* __restrict__ part, const float* __restrict__ s,
+                                                          float* __restrict__ Y, int S, int O, int nks) {
+    const size_t n = (size_t)S * O;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        float a = 0.f;
+        for (int k = 0; k < nks; k++) a += part[k * n + i];
+        Y[i] = a * s[i % O];
+    }
+}
 
 // Warp-specialised variant: wavefronts 4-7 load and widen the next K step into the other LDS buffer while
 // wavefronts 0-3 run the MFMAs of this one (one barrier per K step), so the staging VALU work runs beside the MFMAs.
 __global__ void __launch_bounds__(512, 2) gemm_ws_kernel(const int8_t* __restrict__ W, const float* __restrict__ s,
                                                          const _Float16* __restrict__ X, float* __restrict__ Y, int S, int I,
-                                                         int O) {
+                                                         int O, int nks, float* __restrict__ part) {
     __shared__ __align__(16) _Float16 lds[2][2][GM_BM * GM_LD];  // [buffer][W, X][row][k]
-    const int nO = (O + GM_BM - 1) / GM_BM, nS = (S + GM_BN - 1) / GM_BN, bid = blockIdx.x;
+    const int nO = (O + GM_BM - 1) / GM_BM, nS = (S + GM_BN - 1) / GM_BN, tiles = nO * nS;
+    const int ks = blockIdx.x / tiles, bid = blockIdx.x % tiles;  // K split ks of tile bid (nks = 1: no split)
+    const int kb = ks * (I / GM_BK) / nks, nk = (ks + 1) * (I / GM_BK) / nks - kb;
     int ot, stl;
     if (nS % 8 == 0) {
         const int spx = nS / 8, i = bid >> 3;
@@ -332,13 +346,13 @@ __global__ void __launch_bounds__(512, 2) gemm_ws_kernel(const int8_t* __restric
         ot = bid % nO;
         stl = bid / nO;
     }
-    const int o0 = ot * GM_BM, s0 = stl * GM_BN, nk = I / GM_BK;
+    const int o0 = ot * GM_BM, s0 = stl * GM_BN;
     if (threadIdx.x >= 256) {
         // ---- staging: thread t owns 16 weights (row t/2, k 16*(t%2)) and 16 activations (token t/2, same k) ----
         const int tid = threadIdx.x - 256, sr = tid >> 1, sk = (tid & 1) * 16;
         const bool wok = o0 + sr < O, xok = s0 + sr < S;
-        const int8_t* wp = W + (size_t)min(o0 + sr, O - 1) * I + sk;
-        const _Float16* xp = X + (size_t)min(s0 + sr, S - 1) * I + sk;
+        const int8_t* wp = W + (size_t)min(o0 + sr, O - 1) * I + kb * GM_BK + sk;
+        const _Float16* xp = X + (size_t)min(s0 + sr, S - 1) * I + kb * GM_BK + sk;
         uint4 wreg;
         uint4 xreg[2];
         auto load = [&](int k0) {
@@ -405,13 +419,14 @@ __global__ void __launch_bounds__(512, 2) gemm_ws_kernel(const int8_t* __restric
     for (int i = 0; i < 2; i++) {
         const int o = o0 + wo + 32 * i + r;
         if (o >= O) continue;
-        const float so = s[o];
+        const float so = nks > 1 ? 1.f : s[o];  // a K split leaves the scale to the reduction
+        float* Yo = nks > 1 ? part + (size_t)ks * S * O : Y;
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const int t = s0 + ws + 32 * j + 8 * (e >> 2) + 4 * h32 + (e & 3);
-                if (t < S) Y[(size_t)t * O + o] = acc[i][j][e] * so;
+                if (t < S) Yo[(size_t)t * O + o] = acc[i][j][e] * so;
             }
     }
 }
@@ -485,9 +500,21 @@ void launch_gemm_i8(const int8_t* q, const float* s, const float* X, float* Y, i
                        reinterpret_cast<const float4*>(X), reinterpret_cast<uint2*>(Xh), n4);
     MOEX_LAUNCHED();
     const int blocks = ((O + GM_BM - 1) / GM_BM) * ((S + GM_BN - 1) / GM_BN);
-    if (blocks <= GEMM_WS_MAX_BLOCKS)
-        hipLaunchKernelGGL(gemm_ws_kernel, dim3(blocks), dim3(512), 0, st, q, s, Xh, Y, S, I, O);
-    else
+    if (blocks <= GEMM_WS_MAX_BLOCKS) {
+        // a grid short of one workgroup per CU splits K (each split at least GEMM_MIN_KSTEPS steps), summed by a
+        // second kernel; at one per CU and above, the partials' traffic cost more than the extra workgroups gained
+        int nks = 2 * blocks > GEMM_WS_MAX_BLOCKS ? 1 : std::max(1, std::min(GEMM_WS_MAX_BLOCKS / blocks, I / GM_BK / GEMM_MIN_KSTEPS));
+        float* part = nullptr;
+        if (nks > 1) {
+            part = reinterpret_cast<float*>(stream_workspace((size_t)nks * S * O * sizeof(float), st, 3));
+            if (!part) nks = 1;
+        }
+        hipLaunchKernelGGL(gemm_ws_kernel, dim3(blocks * nks), dim3(512), 0, st, q, s, Xh, Y, S, I, O, nks, part);
+        if (nks > 1) {
+            MOEX_LAUNCHED();
+            hipLaunchKernelGGL(gemm_reduce_kernel, dim3(1024), dim3(256), 0, st, part, s, Y, S, O, nks);
+        }
+    } else
         hipLaunchKernelGGL(gemm_kernel, dim3(blocks), dim3(256), 0, st, q, s, Xh, Y, S, I, O);
     MOEX_LAUNCHED();
 }

@@ -607,7 +607,8 @@ namespace {
 struct WsKey {
     int dev;
     hipStream_t st;
-    int kind;  // 0: FA tile images, 1: FA partials of split token tiles, 2: fp16 GEMM activations
+    int kind;  // 0: FA tile images, 1: FA partials of split token tiles, 2: fp16 GEMM activations,
+               // 3: GEMM K-split partials
     bool operator<(const WsKey& o) const {
         return dev != o.dev ? dev < o.dev : st != o.st ? st < o.st : kind < o.kind;
     }

@@ -3,8 +3,9 @@
   - quantize_rows_i8: codes and scales bit-exact (the golden fixture and random rows with edge cases);
   - gemv_i8 vs the exact int8 product: rel < 1e-5 (K10), at the qkv (2048 -> 9216) and o_proj (4096 -> 2048) shapes;
   - gemm_i8 with S <= 8 rows: every row bit-identical to gemv_i8 of that row (K10 asks 1e-7);
-  - gemm_i8 with S > 8 (the fp16 MFMA GEMM) vs the per-token GEMV: rel < 5e-3 (K12), and vs the precision model of
-    its own rounding (fp16 activations, exact products) at rel < 1e-5; ragged S and O included.
+  - gemm_i8 with S > 8 (the fp16 MFMA GEMM, K split over workgroups when the tile grid is short of one pass) vs the
+    per-token GEMV: rel < 5e-3 (K12), and vs the precision model of its own rounding (fp16 activations, exact
+    products) at rel < 1e-5; ragged S and O included.
 """
 import os
 
@@ -134,9 +135,9 @@ def test_ragged_rows():
 
 
 def test_gemm_both_kernels_ragged():
-    """A grid above one pass of the chip (the 4-wavefront kernel) and one within it (the warp-specialised kernel),
-    both with O and S ragged against the 128 x 128 tile: each against the precision model, and a row shared by the
-    two calls bit-identical (the two kernels sum in the same order)."""
+    """A grid above one pass of the chip (the 4-wavefront kernel) and one within it (the warp-specialised kernel, here
+    with K split in two and summed by a second kernel), both with O and S ragged against the 128 x 128 tile: each
+    against the precision model, and a row shared by the two calls equal up to the fp32 order of the K sums."""
     import torch
     import moex_amd as M
     O, I = 9000, 1024
@@ -158,7 +159,7 @@ def test_gemm_both_kernels_ragged():
         report("gemm_i8 ragged", O=O, I=I, S=S, rel_vs_model=rel)
         assert np.all(np.isfinite(got)) and rel < 1e-5
         outs[S] = got
-    assert np.array_equal(outs[1000][:200], outs[200])
+    assert _rel(outs[200].astype(np.float64), outs[1000][:200].astype(np.float64)) < 1e-6
 
 
 def test_many_row_groups():
