@@ -503,7 +503,7 @@ void launch_gemm_i8(const int8_t* q, const float* s, const float* X, float* Y, i
     if (blocks <= GEMM_WS_MAX_BLOCKS) {
         // a grid short of one workgroup per CU splits K (each split at least GEMM_MIN_KSTEPS steps), summed by a
         // second kernel; at one per CU and above, the partials' traffic cost more than the extra workgroups gained
-        int nks = 2 * blocks > GEMM_WS_MAX_BLOCKS ? 1 : std::max(1, std::min(GEMM_WS_MAX_BLOCKS / blocks, I / GM_BK / GEMM_MIN_KSTEPS));
+        int nks = 2 * blocks >= GEMM_WS_MAX_BLOCKS ? 1 : std::max(1, std::min(GEMM_WS_MAX_BLOCKS / blocks, I / GM_BK / GEMM_MIN_KSTEPS));
         float* part = nullptr;
         if (nks > 1) {
             part = reinterpret_cast<float*>(stream_workspace((size_t)nks * S * O * sizeof(float), st, 3));
