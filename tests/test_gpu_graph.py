@@ -127,3 +127,38 @@ def test_fa_images_and_dense_graph_replays():
         assert torch.equal(out_g, out_e) and torch.equal(y2_g, y2_e) and torch.equal(y64_g, y64_e), i
         X2.mul_(1.0)  # unrelated eager work between replays
         torch.cuda.synchronize()
+
+
+def test_fa_key_pieces_graph_new_position():
+    """A short chunk splits its token tiles' keys into pieces chosen on the device from pos_d: one captured attn_fa
+    (FA kernel + merge), replayed after the position changes, matches an eager call at each position bit for bit."""
+    import torch
+    import moex_amd as M
+    from tests.gpu_util import LD, random_int8_cache, upload
+    rng = np.random.default_rng(23)
+    dc = upload(random_int8_cache(12000, seed=24))
+    T = 64
+    qo = torch.from_numpy(rng.uniform(-2, 2, (T, H, AHD)).astype(np.float32)).cuda()
+    qg = torch.from_numpy(rng.uniform(-2, 2, (T, LD)).astype(np.float32)).cuda()
+    pos = torch.zeros(1, dtype=torch.int32, device="cuda")
+    st = torch.cuda.Stream()
+    eager = {}
+    for p0 in (11000, 3000, 500):
+        out = torch.empty((T, H, AHD), device="cuda")
+        with torch.cuda.stream(st):
+            M.set_int(pos, p0, st)
+            M.attn_fa(qo, qg, dc, out, H, KV, pos, dc.max_t, LD, T, st)
+        st.synchronize()
+        eager[p0] = out
+    out_g = torch.zeros((T, H, AHD), device="cuda")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        M.attn_fa(qo, qg, dc, out_g, H, KV, pos, dc.max_t, LD, T, st)
+    torch.cuda.synchronize()
+    for p0 in (3000, 11000, 500):
+        M.set_int(pos, p0)
+        torch.cuda.synchronize()
+        out_g.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, eager[p0]), p0
