@@ -13,7 +13,7 @@
 //                          fp16 exactly (integers), activations rounded to fp16 as the reference does
 //                          (kernels.cuh:306-307), fp32 accumulation, the row scale applied last. Workgroup tile 128
 //                          weight rows x 128 tokens, 4 wavefronts of 64 x 64, K steps of 32 double-buffered in LDS,
-//                          two workgroups per CU; the blocks of a token tile run on one XCD (its activations are read
+//                          up to three workgroups per CU; the blocks of a token tile run on one XCD (its activations are read
 //                          into one L2).
 //   gemm_ws_kernel         The same product and sum order with split roles: 4 wavefronts widen the next K step into
 //                          LDS while 4 run the MFMAs of this one. Used when the grid fits the chip in one pass.
@@ -210,7 +210,7 @@ __global__ void __launch_bounds__(64 * GV_WAVES) gemv1_kernel(const int8_t* __re
 constexpr int GM_BM = 128, GM_BN = 128, GM_BK = 32;
 constexpr int GM_LD = GM_BK + 8;  // halves per LDS row (80 B: conflict-free 16-byte operand reads)
 
-__global__ void __launch_bounds__(256, 2) gemm_kernel(const int8_t* __restrict__ W, const float* __restrict__ s,
+__global__ void __launch_bounds__(256, 3) gemm_kernel(const int8_t* __restrict__ W, const float* __restrict__ s,
                                                    const _Float16* __restrict__ X, float* __restrict__ Y, int S, int I,
                                                    int O) {
     __shared__ __align__(16) _Float16 lds[2][2][GM_BM * GM_LD];  // [buffer][W, X][row][k]
