@@ -13,8 +13,8 @@
 //                          fp16 exactly (integers), activations rounded to fp16 as the reference does
 //                          (kernels.cuh:306-307), fp32 accumulation, the row scale applied last. Workgroup tile 128
 //                          weight rows x 128 tokens, 4 wavefronts of 64 x 64, K steps of 32 double-buffered in LDS,
-//                          up to three workgroups per CU; the blocks of a token tile run on one XCD (its activations are read
-//                          into one L2).
+//                          up to three workgroups per CU; the blocks of a token tile run on one XCD (its activations
+//                          are read into one L2).
 //   gemm_ws_kernel         The same product and sum order with split roles: 4 wavefronts widen the next K step into
 //                          LDS while 4 run the MFMAs of this one. Used when the grid fits the chip in one pass.
 #include <algorithm>
