@@ -8,13 +8,19 @@
  *   - fp16 weight pointers (qn, kn) are raw binary16 bit patterns (uint16_t);
  *   - raw kernel launches take their grid-defining sizes (T, ns) explicitly instead of a <<<grid>>>.
  * All pointers are device pointers unless stated otherwise. Nothing allocates or synchronizes except
- * moex_kv_alloc / moex_kv_free and moex_attn_fa with T >= 128: that call widens the K/V tiles once into a tile-image
- * workspace of KV * ceil(max_t / 32) * 37632 bytes, one per (device, stream), allocated on the first such call on a
- * stream and grown (after waiting for the stream) when a larger max_t comes; it is kept until the process ends.
- * A chunk whose token tiles leave the chip underfilled (KV * ceil(T / 16) < CUs) may split each token tile's keys
- * over several workgroups: it uses a second such workspace for their partial results, T * H * pieces * 1040 bytes
- * (at most 32 pieces; MOEX_FA_SPLIT=n caps them, 1 turns splitting off).
- * After one eager call of a given max_t and T on a stream, every attention call can be captured into a HIP graph.
+ * moex_kv_alloc / moex_kv_free and the per-stream workspaces below.
+ *
+ * Workspaces. moex_attn_fa with T >= 128 widens the K/V tiles once into a tile-image workspace of
+ * KV * ceil(max_t / 32) * 37632 bytes. A chunk whose token tiles leave the chip underfilled (KV * ceil(T / 16) < CUs)
+ * may split each token tile's keys over several workgroups, with a second workspace for their partial results,
+ * T * H * pieces * 1040 bytes (at most 32 pieces; MOEX_FA_SPLIT=n caps them, 1 turns splitting off). The dense GEMM
+ * (moex_dense.h) keeps two more. Each is one per (device, stream), allocated on first use with hipMalloc and grown
+ * when a larger call comes. An outgrown buffer is not freed before the process ends, because a HIP graph captured
+ * earlier may still replay into it. No workspace is allocated while the stream is being captured: a call that would
+ * need to grow one reports hipErrorStreamCaptureUnsupported. So after one eager call of a given max_t and T on a
+ * stream, the same call can be captured into a HIP graph. A graph's replays use the capturing stream's workspaces:
+ * replays and eager calls that overlap in time on different streams race on them. moex_attn_workspace_bytes gives
+ * the bytes one call needs, moex_workspace_held the bytes held now (for a VRAM audit next to moex_kv_bytes).
  *
  * Errors (kernels.cuh:8-11, CK): a failing HIP call prints "HIP <error> at <file>:<line>" and exits(1),
  * unless a soft-error slot is installed (moex_set_soft_error), in which case the first error code is
@@ -121,6 +127,13 @@ int moex_decode_splits(int n_ctx);
  * cache with KV heads (turbo != 0 for a turbo cache): at most ns. A caller that launches moex_attn_gqa and
  * moex_attn_combine itself passes this value to both. No counterpart in the reference. */
 int moex_gqa_splits(int T, int KV, int ns, int turbo);
+/* Workspace bytes one moex_attn_fa (or moex_attn_decode prefill) call with these sizes takes on its stream: tile
+ * images plus the partials of split token tiles. No counterpart in the reference (its attn_fa_k needs none); for the
+ * engine's VRAM audit (moex.cu:960) beside moex_kv_bytes. */
+size_t moex_attn_workspace_bytes(int H, int KV, int max_t, int T);
+/* Bytes the library's per-stream workspaces hold now, on every device and stream, outgrown buffers included. No
+ * counterpart in the reference. */
+size_t moex_workspace_held(void);
 /* Library build identifier. */
 const char* moex_version(void);
 

@@ -63,6 +63,9 @@ def lib():
     L.moex_gqa_splits.argtypes = [i, i, i, i]
     L.moex_gqa_splits.restype = i
     L.moex_version.restype = ctypes.c_char_p
+    L.moex_attn_workspace_bytes.argtypes = [i, i, i, i]
+    L.moex_attn_workspace_bytes.restype = ctypes.c_size_t
+    L.moex_workspace_held.restype = ctypes.c_size_t
     L.moex_quantize_rows_i8.argtypes = [vp, vp, vp, i, i, vp]
     L.moex_gemv_i8.argtypes = [vp, vp, vp, vp, i, i, vp]
     L.moex_gemm_i8.argtypes = [vp, vp, vp, vp, i, i, i, vp]
@@ -74,6 +77,7 @@ EXPORTS = ["moex_kv_alloc", "moex_kv_bytes", "moex_kv_free", "moex_attn_decode",
            "moex_qk_norm_rope", "moex_kv_append", "moex_attn_gqa", "moex_attn_combine", "moex_attn_decode_heads",
            "moex_turbo_out", "moex_set_int", "moex_set_soft_error", "moex_set_skip", "moex_fa_on",
            "moex_fa_supported", "moex_decode_splits", "moex_gqa_splits", "moex_version",
+           "moex_attn_workspace_bytes", "moex_workspace_held",
            "moex_quantize_rows_i8", "moex_gemv_i8", "moex_gemm_i8"]
 
 
@@ -205,6 +209,16 @@ def fa_on():
 
 def fa_supported():
     return bool(lib().moex_fa_supported())
+
+
+def attn_workspace_bytes(H, KV, max_t, T):
+    """Workspace bytes one attn_fa call of these sizes takes on its stream (for a VRAM audit beside kv_bytes)."""
+    return int(lib().moex_attn_workspace_bytes(H, KV, max_t, T))
+
+
+def workspace_held():
+    """Bytes the library's per-stream workspaces hold now."""
+    return int(lib().moex_workspace_held())
 
 
 # ---- dense int8 projections (include/moex_dense.h): the qkv projection before attn_decode, o_proj after it ----

@@ -125,6 +125,13 @@ void moex_gemm_i8(const int8_t* q, const float* s, const float* X, float* Y, int
     launch_gemm_i8(q, s, X, Y, S_, I, O, S(stream));
 }
 
+size_t moex_attn_workspace_bytes(int H, int KV, int max_t, int T) {
+    if (!(KV > 0 && H == KV * GQ && T > 0 && max_t > 0)) return 0;
+    return fa_workspace_bytes(H, KV, max_t, T);
+}
+
+size_t moex_workspace_held(void) { return stream_workspace_bytes(); }
+
 const char* moex_version(void) { return "moex_attn gfx950 0.1"; }
 
 void moex_set_soft_error(int* slot) { g_soft = slot; }

@@ -96,6 +96,10 @@ void launch_gemv_i8(const int8_t* q, const float* s, const float* x, float* y, i
 // Device memory kept per (device, stream, kind) until the process ends, grown on demand (a call that grows it first
 // waits for the stream). nullptr if it cannot be allocated.
 unsigned char* stream_workspace(size_t need, hipStream_t st, int kind);
+// bytes the workspaces hold on every device and stream, outgrown buffers included
+size_t stream_workspace_bytes();
+// the most workspace bytes one attn_fa call with these sizes takes on its stream
+size_t fa_workspace_bytes(int H, int KV, int max_t, int T);
 void launch_gemm_i8(const int8_t* q, const float* s, const float* X, float* Y, int S, int I, int O, hipStream_t st);
 void launch_prefill_k7p(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
                         const int* pos_d, int max_t, int ld, int T, hipStream_t st);

@@ -601,8 +601,12 @@ __global__ void __launch_bounds__(256) fa_merge_kernel(const float* __restrict__
     *reinterpret_cast<float4*>(out + ((size_t)tok * H + h) * AHD + 4 * lane) = res;
 }
 
-// Workspaces, one per (device, stream, kind), grown on demand and kept until the process ends (a call that grows one
-// waits for the stream first). Calls on one stream are ordered, so they can share theirs.
+// Workspaces, one per (device, stream, kind), grown on demand. Calls on one stream are ordered, so they can share
+// theirs. A buffer that is outgrown is never freed: a HIP graph captured earlier may still hold its address and
+// replay into it, so it stays allocated until the process ends (growth goes to at least 1.5x, which bounds the
+// retired bytes by twice the live ones). While the stream is being captured nothing is allocated: a workspace that
+// would have to grow is reported as hipErrorStreamCaptureUnsupported and nullptr is returned (one eager call of the
+// same shape on the stream before the capture avoids that).
 namespace {
 struct WsKey {
     int dev;
@@ -615,6 +619,7 @@ struct WsKey {
 };
 std::mutex g_ws_mu;
 std::map<WsKey, std::pair<unsigned char*, size_t>> g_ws;
+size_t g_ws_retired = 0;  // bytes of outgrown buffers kept alive for captured graphs
 
 }  // namespace
 
@@ -624,18 +629,27 @@ unsigned char* stream_workspace(size_t need, hipStream_t st, int kind) {
     std::lock_guard<std::mutex> lk(g_ws_mu);
     auto& w = g_ws[WsKey{dev, st, kind}];
     if (w.second >= need) return w.first;
-    if (w.first) {
-        MOEX_CK(hipStreamSynchronize(st));  // earlier calls on this stream may still read the old images
-        MOEX_CK(hipFree(w.first));
-        w = {nullptr, 0};
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+        report(hipErrorStreamCaptureUnsupported, __FILE__, __LINE__);
+        return nullptr;
     }
+    const size_t want = std::max(need, w.second + w.second / 2);
     void* p = nullptr;
-    if (hipMalloc(&p, need) != hipSuccess) {
+    if (hipMalloc(&p, want) != hipSuccess) {
         (void)hipGetLastError();  // out of memory: the caller takes a path without it, or reports the error
         return nullptr;
     }
-    w = {static_cast<unsigned char*>(p), need};
+    if (w.first) g_ws_retired += w.second;  // kept, not freed (see above)
+    w = {static_cast<unsigned char*>(p), want};
     return w.first;
+}
+
+size_t stream_workspace_bytes() {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    size_t b = g_ws_retired;
+    for (auto& kv : g_ws) b += kv.second.second;
+    return b;
 }
 
 namespace {
@@ -649,9 +663,7 @@ void set_lds() {
     (void)once;
 }
 
-template <bool TB>
-void launch_fa_t(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d,
-                 int max_t, int ld, int T, hipStream_t st) {
+int fa_ncu() {
     static const int ncu = [] {
         int dev = 0, v = 0;
         if (hipGetDevice(&dev) == hipSuccess &&
@@ -659,7 +671,22 @@ void launch_fa_t(const float* qo, const float* q_gate, moex_kv_cache kv, float* 
             return v;
         return 256;
     }();
-    const int NT = (T + FT - 1) / FT, nb = fa_grid(KV, T), ntmax = (max_t + BK - 1) / BK;
+    return ncu;
+}
+
+// What one attn_fa call of T tokens over a cache of max_t positions needs: the most key pieces per token tile
+// (the device picks the actual count from pos0), the bytes of their partial rows, and the bytes of the tile images.
+struct FaPlan {
+    int NT, ntmax, nsf;
+    size_t part_bytes, img_bytes;
+};
+
+FaPlan fa_plan(int H, int KV, int max_t, int T) {
+    const int ncu = fa_ncu();
+    FaPlan p;
+    p.NT = (T + FT - 1) / FT;
+    p.ntmax = (max_t + BK - 1) / BK;
+    const int NT = p.NT;
     // key pieces per token tile, at most (the device decides, from pos0): only when the token tiles leave the chip
     // underfilled. A full grid is not split: blocks queued behind a full chip were measured to start only after many
     // CUs had freed, so pieces of the heavy tiles gained little and the merge cost more. MOEX_FA_SPLIT=n caps the
@@ -677,13 +704,20 @@ void launch_fa_t(const float* qo, const float* q_gate, moex_kv_cache kv, float* 
         }
         if (!any) nsf = 1;
     }
-    float* fpart = nullptr;
-    if (nsf > 1) {
-        fpart = reinterpret_cast<float*>(stream_workspace((size_t)T * H * nsf * FP_ROW * sizeof(float), st, 1));
-        if (!fpart) nsf = 1;
-    }
-    unsigned char* img = nullptr;
-    if (NT >= FA_IMG_TILES) img = stream_workspace((size_t)KV * ntmax * TILE_BYTES, st, 0);
+    p.nsf = nsf;
+    p.part_bytes = nsf > 1 ? (size_t)T * H * nsf * FP_ROW * sizeof(float) : 0;
+    p.img_bytes = NT >= FA_IMG_TILES ? (size_t)KV * p.ntmax * TILE_BYTES : 0;
+    return p;
+}
+
+// One attn_fa call on given buffers: img (tile images, or nullptr to widen in the kernel) and fpart (room for nsf
+// pieces' partial rows when nsf > 1).
+template <bool TB>
+void launch_fa_bufs(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
+                    const int* pos_d, int max_t, int ld, int T, hipStream_t st, const FaPlan& p, unsigned char* img,
+                    float* fpart, int nsf) {
+    const int ncu = fa_ncu(), NT = p.NT, ntmax = p.ntmax, nb = fa_grid(KV, T);
+    if (nsf > 1 && !fpart) nsf = 1;
     if (img) {
         hipLaunchKernelGGL(fa_image_kernel<TB>, dim3(ntmax, KV), dim3(256), 0, st, kv, pos_d, T, max_t, ntmax, img);
         MOEX_LAUNCHED();
@@ -707,12 +741,26 @@ void launch_fa_t(const float* qo, const float* q_gate, moex_kv_cache kv, float* 
         MOEX_LAUNCHED();
     }
 }
+
+template <bool TB>
+void launch_fa_t(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d,
+                 int max_t, int ld, int T, hipStream_t st) {
+    const FaPlan p = fa_plan(H, KV, max_t, T);
+    float* fpart = p.part_bytes ? reinterpret_cast<float*>(stream_workspace(p.part_bytes, st, 1)) : nullptr;
+    unsigned char* img = p.img_bytes ? stream_workspace(p.img_bytes, st, 0) : nullptr;
+    launch_fa_bufs<TB>(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, st, p, img, fpart, fpart ? p.nsf : 1);
+}
 }  // namespace
 
 void launch_fa(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d,
                int max_t, int ld, int T, hipStream_t st) {
     if (kv.turbo) launch_fa_t<true>(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, st);
     else launch_fa_t<false>(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, st);
+}
+
+size_t fa_workspace_bytes(int H, int KV, int max_t, int T) {
+    const FaPlan p = fa_plan(H, KV, max_t, T);
+    return p.part_bytes + p.img_bytes;
 }
 
 }  // namespace moex

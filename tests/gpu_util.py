@@ -67,3 +67,31 @@ def max_err(got, ref):
 
 def report(name, **kw):
     print(name, " ".join(f"{k}={v:.3e}" if isinstance(v, float) else f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+def _threads():
+    import os
+    return max(1, min(16, os.cpu_count() or 1))  # the GPU box grants 16 host cores to a job
+
+
+def rows_threaded(fn, qo, gate, ld, Hq, cache, pos0, rows):
+    """fn (orc.attn_rows_f64 / orc.attn_rows_fa_emul) over the rows, spread over host threads (the C oracle releases
+    the GIL): the long-context configs take ~0.5 s of fp64 work per row."""
+    from concurrent.futures import ThreadPoolExecutor
+    rows = list(rows)
+    n = _threads()
+    parts = [rows[i::n] for i in range(n) if rows[i::n]]
+    with ThreadPoolExecutor(len(parts)) as ex:
+        res = list(ex.map(lambda r: fn(qo, gate, ld, Hq, cache, pos0, r), parts))
+    out = np.zeros((len(rows), AHD), np.float64)
+    for i, r in enumerate(res):
+        out[i::n][:len(r)] = r
+    return out
+
+
+def append_threaded(cache, k, v, ld, T, pos0, chunk=8192):
+    """orc.kv_append in chunks of tokens over host threads (rows are independent)."""
+    from concurrent.futures import ThreadPoolExecutor
+    jobs = [(t, min(chunk, T - t)) for t in range(0, T, chunk)]
+    with ThreadPoolExecutor(_threads()) as ex:
+        list(ex.map(lambda j: orc.kv_append(cache, k[j[0]:j[0] + j[1]], v[j[0]:j[0] + j[1]], ld, j[1], pos0 + j[0]), jobs))
