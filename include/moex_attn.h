@@ -72,6 +72,19 @@ void moex_attn_decode(const float* q, const float* k, const float* v, const uint
                       float* qo, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d, int max_t,
                       int rot, float theta, float eps, int T, int ld, void* stream, float* part, int ns);
 
+/* No counterpart in the reference: moex_attn_decode for callers that cannot allocate (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc). Same arguments and result, without part: the split-K partials
+ * (T*H*ns*(256+2) floats) live in a device array of the library, MOEX_NOALLOC_SCRATCH_BYTES per GPU, held from the
+ * library's load until the process ends; a larger T*H*ns is rejected (argument error). The prefill branch (T > 2,
+ * ns == 1) runs FA without tile images (the same bits) and puts its key pieces' partials in that array, with fewer
+ * pieces when they would not fit (results then within the FA tolerance of moex_attn_decode, not bit-identical).
+ * Calls nothing that allocates. Every call on a GPU shares that GPU's array: calls that overlap in time on one GPU
+ * (different streams, or a replayed graph beside an eager call) race on it. */
+#define MOEX_NOALLOC_SCRATCH_BYTES (32u << 20)
+void moex_attn_decode_noalloc(const float* q, const float* k, const float* v, const uint16_t* qn, const uint16_t* kn,
+                              float* qo, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d, int max_t,
+                              int rot, float theta, float eps, int T, int ld, void* stream, int ns);
+
 /* attn_fa (kernels.cuh:1713): FlashAttention-2 causal GQA prefill of T query tokens at *pos_d..*pos_d+T-1.
  * qo [T][H][256] f32 (rotated for turbo); q_gate: the q rows (gate at [t*ld + h*512 + 256]); NULL = no gate
  * (turbo, followed by moex_turbo_out). Needs H / KV == 8. */

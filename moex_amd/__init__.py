@@ -45,6 +45,7 @@ def lib():
     L.moex_kv_bytes.restype = ctypes.c_size_t
     L.moex_kv_free.argtypes = [KVCache]
     L.moex_attn_decode.argtypes = [vp, vp, vp, vp, vp, vp, KVCache, vp, i, i, vp, i, i, f, f, i, i, vp, vp, i]
+    L.moex_attn_decode_noalloc.argtypes = [vp, vp, vp, vp, vp, vp, KVCache, vp, i, i, vp, i, i, f, f, i, i, vp, i]
     L.moex_attn_fa.argtypes = [vp, vp, KVCache, vp, i, i, vp, i, i, i, vp]
     L.moex_attn_prefill.argtypes = [vp, vp, KVCache, vp, i, i, vp, i, i, i, vp]
     L.moex_qk_norm_rope.argtypes = [vp, vp, vp, vp, vp, vp, KVCache, i, i, vp, i, i, f, f, i, i, vp]
@@ -73,7 +74,7 @@ def lib():
     return L
 
 
-EXPORTS = ["moex_kv_alloc", "moex_kv_bytes", "moex_kv_free", "moex_attn_decode", "moex_attn_fa", "moex_attn_prefill",
+EXPORTS = ["moex_kv_alloc", "moex_kv_bytes", "moex_kv_free", "moex_attn_decode", "moex_attn_decode_noalloc", "moex_attn_fa", "moex_attn_prefill",
            "moex_qk_norm_rope", "moex_kv_append", "moex_attn_gqa", "moex_attn_combine", "moex_attn_decode_heads",
            "moex_turbo_out", "moex_set_int", "moex_set_soft_error", "moex_set_skip", "moex_fa_on",
            "moex_fa_supported", "moex_decode_splits", "moex_gqa_splits", "moex_version",
@@ -141,6 +142,12 @@ def attn_decode(q, k, v, qn, kn, qo, kv, out, H, KV, pos_d, max_t, rot, theta, e
     """attn_decode (kernels.cuh:1850): norm + RoPE + KV append + attention + gate."""
     lib().moex_attn_decode(_p(q), _p(k), _p(v), _p(qn), _p(kn), _p(qo), _kv(kv), _p(out), H, KV, _p(pos_d), max_t,
                            rot, theta, eps, T, ld, _s(st), _p(part), ns)
+
+
+def attn_decode_noalloc(q, k, v, qn, kn, qo, kv, out, H, KV, pos_d, max_t, rot, theta, eps, T, ld, st=None, ns=1):
+    """attn_decode without part: the split partials in the library's own device array (no allocation)."""
+    lib().moex_attn_decode_noalloc(_p(q), _p(k), _p(v), _p(qn), _p(kn), _p(qo), _kv(kv), _p(out), H, KV, _p(pos_d),
+                                   max_t, rot, theta, eps, T, ld, _s(st), ns)
 
 
 def attn_fa(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, st=None):

@@ -199,19 +199,20 @@ void moex_attn_prefill(const float* qo, const float* q_gate, moex_kv_cache kv, f
     launch_prefill_k7p(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, S(stream));
 }
 
-void moex_attn_decode(const float* q, const float* k, const float* v, const uint16_t* qn, const uint16_t* kn, float* qo,
-                      moex_kv_cache kv, float* out, int H, int KV, const int* pos_d, int max_t, int rot, float theta,
-                      float eps, int T, int ld, void* stream, float* part, int ns) {
-    MOEX_REQUIRE(H > 0 && KV > 0 && H % KV == 0 && T > 0 && ns > 0, "H, KV, T, ns");
-    MOEX_REQUIRE(ns == 1 || part, "part is needed when ns > 1");
-    MOEX_REQUIRE(((uintptr_t)part & 15) == 0, "part must be 16-byte aligned");
-    MOEX_REQUIRE(rot >= 0 && rot <= AHD && rot % 2 == 0, "rot");
-    hipStream_t st = S(stream);
+}  // extern "C"
+
+namespace {
+// The step of moex_attn_decode after its argument checks. fa_scr: nullptr, or a scratch of fa_bytes for the prefill
+// branch's key-piece partials (the no-allocation entry point).
+void decode_step(const float* q, const float* k, const float* v, const uint16_t* qn, const uint16_t* kn, float* qo,
+                 moex_kv_cache kv, float* out, int H, int KV, const int* pos_d, int max_t, int rot, float theta,
+                 float eps, int T, int ld, hipStream_t st, float* part, int ns, float* fa_scr, size_t fa_bytes) {
     launch_qk_norm_rope(q, k, v, qn, kn, qo, kv, H, KV, pos_d, max_t, rot, theta, eps, ld, T, st);
     const int G = H / KV;
     const float* gate = kv.turbo ? nullptr : q;  // turbo: gated after the inverse rotation
     if (T > 2 && ns == 1 && G == GQ && (moex_fa_on() || kv.turbo) && moex_fa_supported()) {
-        launch_fa(qo, gate, kv, out, H, KV, pos_d, max_t, ld, T, st);
+        if (fa_scr) launch_fa_scratch(qo, gate, kv, out, H, KV, pos_d, max_t, ld, T, st, fa_scr, fa_bytes);
+        else launch_fa(qo, gate, kv, out, H, KV, pos_d, max_t, ld, T, st);
     } else if (T > 2 && ns == 1 && G == GQ && !kv.turbo) {
         launch_prefill_k7p(qo, q, kv, out, H, KV, pos_d, max_t, ld, T, st);
     } else if (ns > 1 && G == GQ) {
@@ -223,6 +224,33 @@ void moex_attn_decode(const float* q, const float* k, const float* v, const uint
         if (ns > 1) launch_combine(part, gate, out, H, ns, ld, T, st);
     }
     if (kv.turbo) launch_turbo_out(out, q, H, ld, T, st);
+}
+}  // namespace
+
+extern "C" {
+
+void moex_attn_decode(const float* q, const float* k, const float* v, const uint16_t* qn, const uint16_t* kn, float* qo,
+                      moex_kv_cache kv, float* out, int H, int KV, const int* pos_d, int max_t, int rot, float theta,
+                      float eps, int T, int ld, void* stream, float* part, int ns) {
+    MOEX_REQUIRE(H > 0 && KV > 0 && H % KV == 0 && T > 0 && ns > 0, "H, KV, T, ns");
+    MOEX_REQUIRE(ns == 1 || part, "part is needed when ns > 1");
+    MOEX_REQUIRE(((uintptr_t)part & 15) == 0, "part must be 16-byte aligned");
+    MOEX_REQUIRE(rot >= 0 && rot <= AHD && rot % 2 == 0, "rot");
+    decode_step(q, k, v, qn, kn, qo, kv, out, H, KV, pos_d, max_t, rot, theta, eps, T, ld, S(stream), part, ns, nullptr,
+                0);
+}
+
+void moex_attn_decode_noalloc(const float* q, const float* k, const float* v, const uint16_t* qn, const uint16_t* kn,
+                              float* qo, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d, int max_t,
+                              int rot, float theta, float eps, int T, int ld, void* stream, int ns) {
+    MOEX_REQUIRE(H > 0 && KV > 0 && H % KV == 0 && T > 0 && ns > 0, "H, KV, T, ns");
+    MOEX_REQUIRE(rot >= 0 && rot <= AHD && rot % 2 == 0, "rot");
+    MOEX_REQUIRE(ns == 1 || (size_t)T * H * ns * (AHD + 2) * sizeof(float) <= MOEX_NOALLOC_SCRATCH_BYTES,
+                 "attn_decode_noalloc: the split partials T*H*ns*1032 bytes exceed MOEX_NOALLOC_SCRATCH_BYTES");
+    float* scr = noalloc_scratch();
+    if (!scr) return;  // reported
+    decode_step(q, k, v, qn, kn, qo, kv, out, H, KV, pos_d, max_t, rot, theta, eps, T, ld, S(stream),
+                ns > 1 ? scr : nullptr, ns, scr, MOEX_NOALLOC_SCRATCH_BYTES);
 }
 
 }  // extern "C"

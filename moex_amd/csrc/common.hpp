@@ -98,6 +98,13 @@ void launch_gemv_i8(const int8_t* q, const float* s, const float* x, float* y, i
 unsigned char* stream_workspace(size_t need, hipStream_t st, int kind);
 // bytes the workspaces hold on every device and stream, outgrown buffers included
 size_t stream_workspace_bytes();
+// attn_fa that allocates nothing: no tile images, the key pieces' partials in the given scratch (fewer pieces if they
+// would not fit it)
+void launch_fa_scratch(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
+                       const int* pos_d, int max_t, int ld, int T, hipStream_t st, float* scratch, size_t bytes);
+// this device's copy of the no-allocation scratch (MOEX_NOALLOC_SCRATCH_BYTES), nullptr (error reported) if its
+// address cannot be had
+float* noalloc_scratch();
 // the most workspace bytes one attn_fa call with these sizes takes on its stream
 size_t fa_workspace_bytes(int H, int KV, int max_t, int T);
 void launch_gemm_i8(const int8_t* q, const float* s, const float* X, float* Y, int S, int I, int O, hipStream_t st);

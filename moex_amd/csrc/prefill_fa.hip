@@ -758,6 +758,20 @@ void launch_fa(const float* qo, const float* q_gate, moex_kv_cache kv, float* ou
     else launch_fa_t<false>(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, st);
 }
 
+void launch_fa_scratch(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
+                       const int* pos_d, int max_t, int ld, int T, hipStream_t st, float* scratch, size_t bytes) {
+    const FaPlan p = fa_plan(H, KV, max_t, T);
+    // the pieces' partial rows must fit the scratch: fewer pieces when they do not (no tile images: the staging
+    // wavefronts widen every tile, which gives the same bits)
+    const size_t per = (size_t)T * H * FP_ROW * sizeof(float);
+    int nsf = p.nsf;
+    if (nsf > 1 && per * nsf > bytes) nsf = (int)std::min<size_t>(nsf, bytes / per);
+    if (nsf < 2) nsf = 1;
+    float* fpart = nsf > 1 ? scratch : nullptr;
+    if (kv.turbo) launch_fa_bufs<true>(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, st, p, nullptr, fpart, nsf);
+    else launch_fa_bufs<false>(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, st, p, nullptr, fpart, nsf);
+}
+
 size_t fa_workspace_bytes(int H, int KV, int max_t, int T) {
     const FaPlan p = fa_plan(H, KV, max_t, T);
     return p.part_bytes + p.img_bytes;

@@ -1,0 +1,105 @@
+"""moex_attn_decode_noalloc (no counterpart in the reference: attn_decode for callers that cannot allocate) against
+moex_attn_decode on the same inputs, through the C ABI: the same bits wherever both run the same kernels with the
+same split / piece counts (decode, per-head, short prefill chunks), two calls in a row with the second one smaller;
+the FA tolerance where the scratch caps the key pieces; a clear argument error beyond the scratch's size."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from tests.gpu_util import AHD, H, KV, random_int8_cache, report, upload
+
+pytestmark = pytest.mark.gpu
+LQ = H * 2 * AHD + 2 * KV * AHD
+
+
+def _args(M, torch, T, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    qkv = torch.randn((T, LQ), generator=g, device="cuda")
+    return qkv
+
+
+def _both(M, torch, caches, qkv, pos, T, ns, max_t):
+    """One step through each entry point, each on its own copy of the cache (the step appends the T rows)."""
+    qn = torch.zeros(AHD, dtype=torch.int16, device="cuda")
+    pos_d = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    L = M.lib()
+    res = []
+    for which, c in zip(("alloc", "noalloc"), caches):
+        qo = torch.full((T, H, AHD), float("nan"), device="cuda")
+        out = torch.full((T, H, AHD), float("nan"), device="cuda")
+        q, k, v = qkv, qkv[:, H * 2 * AHD:], qkv[:, H * 2 * AHD + KV * AHD:]
+        st = torch.cuda.current_stream().cuda_stream
+        if which == "alloc":
+            part = torch.empty(max(1, T * H * ns * (AHD + 2)), device="cuda")
+            L.moex_attn_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), qn.data_ptr(), qn.data_ptr(), qo.data_ptr(),
+                               c.c, out.data_ptr(), H, KV, pos_d.data_ptr(), max_t, 64, 1e7, 1e-6, T, LQ, st,
+                               part.data_ptr(), ns)
+        else:
+            L.moex_attn_decode_noalloc(q.data_ptr(), k.data_ptr(), v.data_ptr(), qn.data_ptr(), qn.data_ptr(),
+                                       qo.data_ptr(), c.c, out.data_ptr(), H, KV, pos_d.data_ptr(), max_t, 64, 1e7,
+                                       1e-6, T, LQ, st, ns)
+        torch.cuda.synchronize()
+        res.append((qo.cpu().numpy(), out.cpu().numpy()))
+    return res
+
+
+@pytest.mark.parametrize("turbo", [0, 1])
+def test_noalloc_matches_attn_decode(turbo):
+    import torch
+    import moex_amd as M
+    max_t = 40064
+    hc = random_int8_cache(max_t, seed=21) if not turbo else None
+    if turbo:
+        caches = [M.DeviceKVCache(KV, max_t, 1) for _ in range(2)]
+        g = torch.Generator(device="cuda").manual_seed(22)
+        kv = torch.randn((max_t, 2 * KV * AHD), generator=g, device="cuda")
+        for c in caches:
+            M.kv_append(kv[:, :KV * AHD], kv[:, KV * AHD:], c, KV, torch.zeros(1, dtype=torch.int32, device="cuda"),
+                        max_t, 2 * KV * AHD, max_t)
+    else:
+        caches = [upload(hc), upload(hc)]
+    torch.cuda.synchronize()
+    # (pos, T, ns): split-K decode, then a smaller one; MTP window; per-head path (ns == 1, T <= 2); short prefill
+    # chunks whose key pieces fit the scratch
+    for i, (pos, T, ns) in enumerate([(39999, 1, 256), (5000, 1, 16), (30000, 4, 64), (1000, 2, 1),
+                                      (34000, 17, 1), (5000, 3, 1)]):
+        qkv = _args(M, torch, T, 100 + i)
+        (qa, oa), (qb, ob) = _both(M, torch, caches, qkv, pos, T, ns, max_t)
+        same = np.array_equal(oa.view(np.uint32), ob.view(np.uint32)) and np.array_equal(qa.view(np.uint32),
+                                                                                      qb.view(np.uint32))
+        report("noalloc vs attn_decode", turbo=turbo, pos=pos, T=T, ns=ns, identical=same)
+        assert np.all(np.isfinite(ob)) and same
+
+
+def test_noalloc_capped_pieces_and_rejection():
+    """T = 64 at 32000 would take 32 key pieces (34 MB of partials): the scratch (32 MiB) holds 31, so the result
+    is within the FA split tolerance (2e-3 of max |out|, as split vs unsplit). T*H*ns*1032 beyond the scratch is an
+    argument error that leaves out untouched."""
+    import torch
+    import moex_amd as M
+    max_t = 32064
+    hc = random_int8_cache(max_t, seed=23)
+    caches = [upload(hc), upload(hc)]
+    T, pos = 64, 32000
+    qkv = _args(M, torch, T, 7)
+    (_, oa), (_, ob) = _both(M, torch, caches, qkv, pos, T, 1, max_t)
+    d, mag = float(np.abs(oa - ob).max()), float(np.abs(oa).max())
+    report("noalloc capped pieces", maxdiff=d, mag=mag)
+    assert np.all(np.isfinite(ob)) and d <= 2e-3 * mag
+    slot = ctypes.c_int(0)
+    L = M.lib()
+    L.moex_set_soft_error(ctypes.byref(slot))
+    try:
+        out = torch.zeros((4, H, AHD), device="cuda")
+        qkv = _args(M, torch, 4, 8)
+        qn = torch.zeros(AHD, dtype=torch.int16, device="cuda")
+        pos_d = torch.tensor([100], dtype=torch.int32, device="cuda")
+        L.moex_attn_decode_noalloc(qkv.data_ptr(), qkv[:, H * 2 * AHD:].data_ptr(),
+                                   qkv[:, H * 2 * AHD + KV * AHD:].data_ptr(), qn.data_ptr(), qn.data_ptr(),
+                                   out.data_ptr(), caches[1].c, out.data_ptr(), H, KV, pos_d.data_ptr(), max_t, 64,
+                                   1e7, 1e-6, 4, LQ, torch.cuda.current_stream().cuda_stream, 1024)
+        torch.cuda.synchronize()
+    finally:
+        L.moex_set_soft_error(None)
+    assert slot.value == 1 and float(out.abs().max()) == 0.0
