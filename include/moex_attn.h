@@ -91,7 +91,9 @@ void moex_attn_decode_noalloc(const float* q, const float* k, const float* v, co
 void moex_attn_fa(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
                   const int* pos_d, int max_t, int ld, int T, void* stream);
 
-/* attn_prefill (kernels.cuh:1435): the int8-only prefill fallback (K7P), same arguments and result. */
+/* attn_prefill (kernels.cuh:1435): the int8-only prefill fallback (K7P), same arguments and result. Any GQA group
+ * G = H / KV that divides 32 (kernels.cuh:1856); moex_attn_decode routes T > 2, ns == 1 int8 steps of such G here
+ * when FA does not apply (MOEX_FA=0, or G != 8). */
 void moex_attn_prefill(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
                        const int* pos_d, int max_t, int ld, int T, void* stream);
 

@@ -193,7 +193,7 @@ void moex_attn_fa(const float* qo, const float* q_gate, moex_kv_cache kv, float*
 
 void moex_attn_prefill(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
                        const int* pos_d, int max_t, int ld, int T, void* stream) {
-    MOEX_REQUIRE(KV > 0 && H == KV * GQ, "attn_prefill needs H / KV == 8");
+    MOEX_REQUIRE(KV > 0 && H % KV == 0 && 32 % (H / KV) == 0, "attn_prefill needs H / KV to divide 32");
     MOEX_REQUIRE(!kv.turbo, "attn_prefill reads int8 KV only");
     MOEX_REQUIRE(T > 0, "T");
     launch_prefill_k7p(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, S(stream));
@@ -213,7 +213,7 @@ void decode_step(const float* q, const float* k, const float* v, const uint16_t*
     if (T > 2 && ns == 1 && G == GQ && (moex_fa_on() || kv.turbo) && moex_fa_supported()) {
         if (fa_scr) launch_fa_scratch(qo, gate, kv, out, H, KV, pos_d, max_t, ld, T, st, fa_scr, fa_bytes);
         else launch_fa(qo, gate, kv, out, H, KV, pos_d, max_t, ld, T, st);
-    } else if (T > 2 && ns == 1 && G == GQ && !kv.turbo) {
+    } else if (T > 2 && ns == 1 && 32 % G == 0 && !kv.turbo) {  // kernels.cuh:1856: any G dividing 32
         launch_prefill_k7p(qo, q, kv, out, H, KV, pos_d, max_t, ld, T, st);
     } else if (ns > 1 && G == GQ) {
         ns = gqa_splits(T, KV, ns, kv.turbo != 0);

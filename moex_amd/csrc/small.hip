@@ -256,93 +256,144 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
     out[((size_t)tok * H + h) * AHD + d] = x;
 }
 
-// attn_decode_k (kernels.cuh:1238-1315): one block per (query head, token, split), 256 threads, any H / KV.
-// Keys in tiles of 1024 scores; one wavefront scores 4 keys at a time (16 lanes per key, 16 dims per lane);
-// base-2 online softmax; thread d accumulates dim d. ns == 1: gated output; else partials.
-constexpr int DT = 1024;
+// Per-query-head decode (the contract of attn_decode_k, kernels.cuh:1238-1315): any H / KV, int8 or turbo.
+// Workgroup = (query head, token, split), 4 wavefronts. Wavefront w walks the split's keys in chunks of 64 taken
+// round-robin (chunk c goes to wavefront c % 4) and keeps its own online softmax state:
+//   - lane i scores key i of the chunk alone, over the whole row (the query sits in LDS and every lane reads the
+//     same word, a broadcast);
+//   - the chunk's maximum and sum are wavefront reductions, the probabilities (times the key's V scale) stay in the
+//     lane of their key;
+//   - lane i then accumulates dims 4i .. 4i+3 over the chunk's keys, reading each V row with one coalesced 256-byte
+//     wavefront load and taking the key's probability by a wavefront broadcast.
+// The four states {m, l, acc} merge through LDS at the end. Base-2 softmax with the scale log2(e) / 16.
+// ns == 1: the gated output (no gate if q_gate is NULL); else partials for combine_kernel.
+constexpr int DH_CH = 64;  // keys per wavefront chunk
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
 __global__ void __launch_bounds__(256) decode_heads_kernel(const float* __restrict__ qo, const float* __restrict__ q_gate,
                                                            moex_kv_cache kv, float* __restrict__ out, int H, int KV,
                                                            const int* __restrict__ pos_d, int max_t, int ld,
                                                            float* __restrict__ part) {
-    __shared__ float sc[DT];
-    __shared__ __align__(16) float qs[AHD];
-    __shared__ float c4[16], c3[8], sh8[16];
-    const int tok = blockIdx.y, Tk = *pos_d + tok + 1;
-    const int ns = gridDim.z, L = (Tk + ns - 1) / ns, lo = blockIdx.z * L, hi = min(Tk, lo + L);
-    const int h = blockIdx.x, kvh = h / (H / KV), tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    qo += (size_t)tok * H * AHD;
-    if (q_gate) q_gate += (size_t)tok * ld;
-    out += (size_t)tok * H * AHD;
-    qs[tid] = qo[h * AHD + tid];
-    if (tid < 16) c4[tid] = (float)c_I4[tid] * K4;
-    if (tid < 8) c3[tid] = (float)c_I3[tid] * K3;
-    __syncthreads();
+    __shared__ __align__(16) float qv[AHD];
+    __shared__ float klut[16], vlut[8];
+    __shared__ float wm[4], wl[4];
+    __shared__ __align__(16) float wacc[4][AHD];
+    const int h = blockIdx.x, tok = blockIdx.y, sp = blockIdx.z, ns = gridDim.z;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int nk = *pos_d + tok + 1, per = (nk + ns - 1) / ns, lo = sp * per, hi = min(nk, lo + per);
+    const int kvh = h / (H / KV);
     const bool tb = kv.turbo;
-    const float sl2 = 0.0625f * 1.4426950408889634f;  // 1/sqrt(256) * log2(e)
+    qv[tid] = qo[((size_t)tok * H + h) * AHD + tid];
+    if (tid < 16) klut[tid] = (float)c_I4[tid] * K4;
+    if (tid < 8) vlut[tid] = (float)c_I3[tid] * K3;
+    __syncthreads();
+    const float sl2 = 0.0625f * 1.4426950408889634f;
     const size_t rbase = (size_t)kvh * max_t;
-    // turbo V of dim tid: low 2 bits at byte vq (shift vsh), high bit at byte vg (bit vgb)
-    const int vq = (tid >> 7) * 32 + ((tid & 127) >> 2), vsh = 2 * (tid & 3), vg = 64 + (tid >> 7) * 16 + ((tid & 127) >> 3), vgb = tid & 7;
-    const int sub = lane >> 4, l16 = lane & 15;  // key slot within the wavefront, lane within the key
-    float m = -INFINITY, l = 0.f, acc = 0.f;
-    for (int t0 = lo; t0 < hi; t0 += DT) {
-        const int n = min(DT, hi - t0);
-        for (int i = wv * 4 + sub; i < n; i += 16) {  // 16 lanes per key, dims l16*16 .. +15
-            const size_t row = rbase + t0 + i;
-            float s = 0.f;
-            if (tb) {  // 8 bytes of nibbles = 16 dims of half l16 / 8
-                const uint2 u = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(kv.k) + row * TQ_KB + (l16 >> 3) * 64 + (l16 & 7) * 8);
-                const uint32_t w2[2] = {u.x, u.y};
+    // turbo V fields of this lane's dims 4 lane .. +3 (half hb, in-half dims j0 .. j0 + 3): the low 2-bit codes are
+    // one byte, the high bits a nibble of another
+    const int hb = lane >> 5, j0 = 4 * (lane & 31);
+    const int vlo = hb * 32 + (j0 >> 2), vhi = 64 + hb * 16 + (j0 >> 3), vsh = j0 & 7;
+    float m = -INFINITY, l = 0.f;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    for (int c0 = lo + DH_CH * w; c0 < hi; c0 += 4 * DH_CH) {
+        const int n = min(DH_CH, hi - c0), key = c0 + min(lane, n - 1);
+        const size_t row = rbase + key;
+        float sc;
+        if (tb) {  // two half sums over 4-bit codes, each times its half norm
+            const uint4* kp = reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(kv.k) + row * TQ_KB);
+            float d[2] = {0.f, 0.f};
 #pragma unroll
-                for (int a = 0; a < 2; a++)
+            for (int u = 0; u < 8; u++) {
+                const uint4 x = kp[u];
+                const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
-                    for (int b = 0; b < 8; b++) s += c4[(w2[a] >> (4 * b)) & 15] * qs[l16 * 16 + a * 8 + b];
-                s *= kv.ks[row * 2 + (l16 >> 3)];
-            } else {
-                const uint4 u = *reinterpret_cast<const uint4*>(kv.k + row * AHD + l16 * 16);
-                const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+                for (int b = 0; b < 4; b++)
 #pragma unroll
-                for (int a = 0; a < 4; a++)
-#pragma unroll
-                    for (int b = 0; b < 4; b++) s += (float)(int8_t)(w4[a] >> (8 * b)) * qs[l16 * 16 + a * 4 + b];
+                    for (int e = 0; e < 8; e++)
+                        d[u >> 2] += klut[(xw[b] >> (4 * e)) & 15] * qv[32 * u + 8 * b + e];
             }
+            sc = (d[0] * kv.ks[row * 2] + d[1] * kv.ks[row * 2 + 1]) * sl2;
+        } else {
+            const uint4* kp = reinterpret_cast<const uint4*>(kv.k + row * AHD);
+            float d = 0.f;
+#pragma unroll 4
+            for (int u = 0; u < 16; u++) {
+                const uint4 x = kp[u];
+                const float4* q4 = reinterpret_cast<const float4*>(qv + 16 * u);
+                const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
-            for (int o = 8; o; o >>= 1) s += __shfl_xor(s, o);
-            if (l16 == 0) sc[i] = s * (tb ? 1.f : kv.ks[row]) * sl2;
+                for (int b = 0; b < 4; b++) {
+                    const float4 qq = q4[b];
+                    d += (float)(int8_t)(xw[b]) * qq.x + (float)(int8_t)(xw[b] >> 8) * qq.y +
+                         (float)(int8_t)(xw[b] >> 16) * qq.z + (float)(int8_t)(xw[b] >> 24) * qq.w;
+                }
+            }
+            sc = d * kv.ks[row] * sl2;
         }
-        __syncthreads();
-        float mt = -INFINITY;
-        for (int i = tid; i < n; i += 256) mt = fmaxf(mt, sc[i]);
-        const float mn = fmaxf(m, block_max(mt, sh8)), c = fast_exp2(m - mn);  // m = -inf on the first tile: c = 0
-        float s = 0.f;
-        for (int i = tid; i < n; i += 256) {
-            const float e = fast_exp2(sc[i] - mn);
-            s += e;
-            sc[i] = tb ? e : e * kv.vs[rbase + t0 + i];  // V's scale folded in
-        }
-        l = l * c + block_sum(s, sh8 + 8);  // syncs: sc[] complete after it
-        acc *= c;
+        if (lane >= n) sc = -INFINITY;
+        const float mn = fmaxf(m, wave_max(sc));  // finite: every chunk has a key
+        const float cr = fast_exp2(m - mn);       // 0 while m = -inf
+        const float p = lane < n ? fast_exp2(sc - mn) : 0.f;
+        l = l * cr + wave_sum(p);
+        m = mn;
+        a0 *= cr; a1 *= cr; a2 *= cr; a3 *= cr;
+        float pv0, pv1 = 0.f;  // p times the V scale (turbo: of each half)
+        if (tb) { pv0 = p * kv.vs[row * 2]; pv1 = p * kv.vs[row * 2 + 1]; }
+        else pv0 = p * kv.vs[row];
         if (tb) {
-            const uint8_t* Vt = reinterpret_cast<const uint8_t*>(kv.v) + (rbase + t0) * TQ_VB;
-            const float* vn = kv.vs + (rbase + t0) * 2 + (tid >> 7);
+            const uint8_t* vr = reinterpret_cast<const uint8_t*>(kv.v) + (rbase + c0) * TQ_VB;
             for (int i = 0; i < n; i++) {
-                const uint8_t* r = Vt + (size_t)i * TQ_VB;
-                acc += sc[i] * (c3[((r[vq] >> vsh) & 3) | (((r[vg] >> vgb) & 1) << 2)] * vn[(size_t)i * 2]);
+                const float p0 = __shfl(pv0, i), p1 = __shfl(pv1, i), pk = hb ? p1 : p0;
+                const uint32_t lo2 = vr[(size_t)i * TQ_VB + vlo], hi1 = vr[(size_t)i * TQ_VB + vhi] >> vsh;
+                a0 += pk * vlut[(lo2 & 3) | ((hi1 & 1) << 2)];
+                a1 += pk * vlut[((lo2 >> 2) & 3) | ((hi1 & 2) << 1)];
+                a2 += pk * vlut[((lo2 >> 4) & 3) | (hi1 & 4)];
+                a3 += pk * vlut[((lo2 >> 6) & 3) | ((hi1 & 8) >> 1)];
             }
         } else {
-            const int8_t* V = kv.v + (rbase + t0) * AHD + tid;
-            for (int i = 0; i < n; i++) acc += sc[i] * (float)V[(size_t)i * AHD];
+            const int8_t* vr = kv.v + (rbase + c0) * AHD + 4 * lane;
+            for (int i = 0; i < n; i++) {
+                const float pk = __shfl(pv0, i);
+                const uint32_t x = *reinterpret_cast<const uint32_t*>(vr + (size_t)i * AHD);
+                a0 += pk * (float)(int8_t)x; a1 += pk * (float)(int8_t)(x >> 8);
+                a2 += pk * (float)(int8_t)(x >> 16); a3 += pk * (float)(int8_t)(x >> 24);
+            }
         }
-        m = mn;
-        __syncthreads();  // sc[] is overwritten by the next tile
+    }
+    if (lane == 0) { wm[w] = m; wl[w] = l; }
+    *reinterpret_cast<float4*>(&wacc[w][4 * lane]) = make_float4(a0, a1, a2, a3);
+    __syncthreads();
+    // thread d: dim d of the merged state (a wavefront without keys has m = -inf and weighs nothing)
+    float M = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 4; v++) M = fmaxf(M, wm[v]);
+    float L = 0.f, A = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const float f = fast_exp2(wm[v] - M);
+            L += wl[v] * f;
+            A += wacc[v][tid] * f;
+        }
     }
     if (ns == 1) {
-        out[h * AHD + tid] = q_gate ? acc / l / (1.f + __expf(-q_gate[h * 2 * AHD + AHD + tid])) : acc / l;
+        const float x = A / L;
+        out[((size_t)tok * H + h) * AHD + tid] =
+            q_gate ? x / (1.f + __expf(-q_gate[(size_t)tok * ld + h * 2 * AHD + AHD + tid])) : x;
         return;
     }
-    part_acc(part, tok, h, blockIdx.z, H, ns)[tid] = acc;
-    if (tid == 0) {  // an empty split leaves m = -inf, l = 0, acc = 0
-        float* ml = part_ml(part, tok, h, blockIdx.z, H, ns, gridDim.y);
-        ml[0] = m; ml[1] = l;
+    part_acc(part, tok, h, sp, H, ns)[tid] = A;  // an empty split: m = -inf, l = 0, acc = 0
+    if (tid == 0) {
+        float* ml = part_ml(part, tok, h, sp, H, ns, gridDim.y);
+        ml[0] = M; ml[1] = L;
     }
 }
 

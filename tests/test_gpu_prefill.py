@@ -128,3 +128,31 @@ def test_fa_turbo(turbo_setup, pos0, T):
     M.turbo_out(out, qg_d, H, LD, T)
     torch.cuda.synchronize()
     _gate("fa turbo + turbo_out", out.cpu().numpy(), qo, qg, hc, pos0, T)
+
+
+@pytest.mark.parametrize("Hq,KVq,pos0,T", [(16, 4, 1000, 100), (16, 1, 300, 37), (32, 1, 0, 64), (2, 2, 500, 9),
+                                           (16, 4, 0, 3)])
+def test_prefill_fallback_other_groups(Hq, KVq, pos0, T):
+    """attn_prefill takes any GQA group G = H / KV that divides 32 (kernels.cuh:1856; its kernel puts 32 / G tokens
+    of G heads in a workgroup): G = 4, 16, 32 and 1 against the fp64 oracle with the test_fa.cu:114 rule."""
+    import torch
+    import moex_amd as M
+    max_t = pos0 + T + 40
+    hc = random_int8_cache(max_t, seed=31 + Hq + KVq, kv=KVq)
+    dc = upload(hc)
+    rng = np.random.default_rng(32)
+    ld = Hq * 2 * AHD
+    qo = rng.uniform(-2, 2, (T, Hq, AHD)).astype(np.float32)
+    qg = rng.uniform(-2, 2, (T, ld)).astype(np.float32)
+    out = torch.full((T, Hq, AHD), float("nan"), dtype=torch.float32, device="cuda")
+    M.attn_prefill(dev(qo), dev(qg), dc, out, Hq, KVq, pos_tensor(pos0), max_t, ld, T)
+    torch.cuda.synchronize()
+    o = out.cpu().numpy()
+    rows = sample_rows(T, range(Hq))
+    ref = orc.attn_rows_f64(qo, qg, ld, Hq, hc, pos0, rows)
+    emu = orc.attn_rows_fa_emul(qo, qg, ld, Hq, hc, pos0, rows)
+    got = np.stack([o[t, h] for t, h in rows])
+    mag = float(np.abs(ref).max())
+    e_new, e_ref = float(np.abs(got - ref).max()), float(np.abs(emu - ref).max())
+    report("prefill(K7P) G", G=Hq // KVq, pos0=pos0, T=T, e_new=e_new, e_ref=e_ref, mag=mag)
+    assert np.all(np.isfinite(o)) and e_new <= 2.0 * e_ref + 1e-3 * mag
