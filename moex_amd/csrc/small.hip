@@ -60,10 +60,8 @@ __device__ __forceinline__ float block_sum(float v, float* sh8) {
     __syncthreads();
     if ((threadIdx.x & 31) == 0) sh8[g] = v;
     __syncthreads();
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; i++) s += sh8[i];
-    return s;
+    // the reference's second xor tree over the 8 partials (kernels.cuh:19-28): xor 4, then 2, then 1
+    return ((sh8[0] + sh8[4]) + (sh8[2] + sh8[6])) + ((sh8[1] + sh8[5]) + (sh8[3] + sh8[7]));
 }
 __device__ __forceinline__ float block_max(float v, float* sh8) {
     v = max32(v);

@@ -95,3 +95,33 @@ def test_checkpoint_restore_reprefill(turbo):
     report("checkpoint restore", turbo=turbo, maxdiff=float(np.abs(oa - ob).max()))
     assert all(np.array_equal(x, y) for x, y in zip(ra, rb))
     assert np.all(np.isfinite(oa)) and np.array_equal(oa, ob)
+
+
+@pytest.mark.parametrize("turbo", [0, 1])
+def test_kv_alloc_cache_serves_attention(turbo):
+    """kv_alloc (kernels.cuh:1867) arrays hold the appended rows exactly as caller-owned ones do: the same rows
+    appended into a kv_alloc cache and into torch-backed arrays give bit-identical attention, then kv_free."""
+    import torch
+    import moex_amd as M
+    max_t, n = 2048, 1500
+    assert M.kv_bytes(KV, max_t, turbo) == KV * max_t * (240 if turbo else 520)
+    a = M.kv_alloc(KV, max_t, turbo)
+    assert a.k and a.v and a.ks and a.vs and a.turbo == turbo
+    b = M.DeviceKVCache(KV, max_t, turbo)
+    g = torch.Generator(device="cuda").manual_seed(60 + turbo)
+    k = torch.randn((n, KV * AHD), generator=g, device="cuda")
+    v = torch.randn((n, KV * AHD), generator=g, device="cuda")
+    qo = torch.randn((3, H, AHD), generator=g, device="cuda")
+    pos = torch.tensor([0], dtype=torch.int32, device="cuda")
+    outs = []
+    for c in (a, b):
+        M.kv_append(k, v, c, KV, pos, max_t, KV * AHD, n)
+        o = torch.full((3, H, AHD), float("nan"), device="cuda")
+        M.attn_decode_heads(qo, None, c, o, H, KV, torch.tensor([n - 3], dtype=torch.int32, device="cuda"), max_t,
+                            H * 2 * AHD, None, 3, 1)
+        torch.cuda.synchronize()
+        outs.append(o.cpu().numpy())
+    M.kv_free(a)
+    torch.cuda.synchronize()
+    report("kv_alloc cache", turbo=turbo, identical=bool(np.array_equal(outs[0], outs[1])))
+    assert np.all(np.isfinite(outs[0])) and np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
