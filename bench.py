@@ -40,7 +40,6 @@ def main():
     ap.add_argument("--decode-only", action="store_true",
                     help="only the configs[2] and configs[3] decode timings (for counter runs); prints their JSON")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     a = ap.parse_args()
@@ -138,6 +137,10 @@ def main():
     def prefill():
         M.attn_fa(qo, qg, c8, out, H, KV, pos_d, c8.max_t, LD, T, st)
 
+    threads = cpu_threads()
+    want_cpu = not a.no_cpu and not a.decode_only
+    hc8 = host_cache(c8, n) if want_cpu else None
+    qh, gh = (qo.cpu().numpy(), qg.cpu().numpy()) if want_cpu else (None, None)
     if not a.decode_only:
         ms, wall_ms = time_steps(prefill, a.steps, a.warmup)
         tflops = flops_prefill(T, pos0) / (ms * 1e-3) / 1e12
@@ -157,6 +160,8 @@ def main():
             ms0, _ = time_steps(lambda: M.attn_fa(qo, qg, c8, out, H, KV, pz, c8.max_t, LD, T, st), 10, 3)
             extra["config0_prefill_int8"] = {"ms": round(ms0, 4),
                                              "tflops": round(flops_prefill(T, 0) / ms0 / 1e9, 1)}
+            if want_cpu:
+                extra["config0_prefill_int8"]["cpu"] = cpu_prefill(hc8, qh, gh, 0, T, threads, full=True)
             print(f"[bench] config0 int8 prefill pos0=0: {ms0:.3f} ms, "
                   f"{extra['config0_prefill_int8']['tflops']} TFLOPS", flush=True)
         # ---------------- config 2: decode + MTP verify at 90k (int8) ----------------
@@ -212,6 +217,10 @@ def main():
                              "graph_GBps": round(kv_bytes / (t_g * 1e-3) / 1e9, 1),
                              "split_kernel_GBps": round(kv_bytes / (t_k * 1e-3) / 1e9, 1),
                              "hbm_frac": round(kv_bytes / (t_f * 1e-3) / 1e9 / PEAK_HBM, 4)}
+            if want_cpu:
+                if Tq == 1:
+                    hrot = host_cache(rot[0], ctx)
+                dec[f"T{Tq}"]["cpu"] = cpu_decode(hrot, qh[:Tq], gh[:Tq], ctx - Tq, Tq, kv_bytes, threads)
             print(f"[bench] config2 decode T={Tq} ctx={ctx} ns={ns}: {t_f * 1e3:.1f} us "
                   f"({dec[f'T{Tq}']['GBps']} GB/s; split kernel alone {t_k * 1e3:.1f} us; "
                   f"graph-replayed step {t_g * 1e3:.1f} us = {dec[f'T{Tq}']['graph_GBps']} GB/s)", flush=True)
@@ -237,6 +246,10 @@ def main():
         tb = 2.0 * ctx * 240
         extra["config3_decode_turbo_262k"] = {"ns": ns, "us": round(t_td * 1e3, 2),
                                               "GBps": round(tb / (t_td * 1e-3) / 1e9, 1)}
+        hct = None
+        if want_cpu:
+            hct = host_cache(ct, ctx)
+            extra["config3_decode_turbo_262k"]["cpu"] = cpu_decode(hct, qh[:1], gh[:1], ctx - 1, 1, tb, threads)
         print(f"[bench] config3 turbo decode ctx={ctx}: {t_td * 1e3:.1f} us ({tb / t_td / 1e6:.0f} GB/s)", flush=True)
         if a.decode_only:
             print(json.dumps({"decode_only": True, **extra}), flush=True)
@@ -247,6 +260,9 @@ def main():
         f4 = flops_prefill(T, 260096)
         extra["config4_prefill_260k"] = {"turbo_ms": round(ms_t, 3), "turbo_tflops": round(f4 / ms_t / 1e9, 1),
                                          "int8_ms": round(ms_i, 3), "int8_tflops": round(f4 / ms_i / 1e9, 1)}
+        if want_cpu:
+            extra["config4_prefill_260k"]["cpu_turbo"] = cpu_prefill(hct, qh, gh, 260096, T,
+                                                                     threads, full=False)
         print(f"[bench] config4 prefill at 260096: turbo {ms_t:.2f} ms ({f4 / ms_t / 1e9:.0f} TFLOPS), "
               f"int8 {ms_i:.2f} ms ({f4 / ms_i / 1e9:.0f} TFLOPS)", flush=True)
         del ct
@@ -283,8 +299,9 @@ def main():
         extra["dense_int8_projections"] = dense
 
     cpu = None
-    if not a.no_cpu:
-        cpu = cpu_baseline(c8, qo, qg, pos0, T, a.cpu_seconds)
+    if want_cpu:
+        cpu = cpu_prefill(hc8, qh, gh, pos0, T, threads, full=False)
+        cpu["sample"] += f"; nproc={os.cpu_count()}"
         print(f"[bench] cpu fp64 baseline: {cpu['value']:.4f} {cpu['unit']} on {cpu['cores']} threads "
               f"({cpu['sample']})", flush=True)
 
@@ -305,46 +322,70 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def cpu_baseline(c8, qo, qg, pos0, T, seconds):
-    """The fp64 reference attention (tests/test_fa.cu:59-80 semantics, oracle/moex_oracle.c) on the host cores,
-    threaded over (token, head) rows, on a time-bounded sample of the headline chunk's rows; reported as TFLOPS with
-    the same per-row flop count (4 * D * keys)."""
-    import concurrent.futures as cf
-    import numpy as np
+def cpu_threads():
+    """Host threads for the CPU baseline: every core this process may run on, but no more than the job's CPU share
+    when the environment states one (OMP_NUM_THREADS; 16 on a one-GPU box)."""
+    n = len(os.sched_getaffinity(0))
+    share = os.environ.get("OMP_NUM_THREADS")
+    if share and share.isdigit() and int(share) > 0:
+        n = min(n, int(share))
+    return max(1, n)
+
+
+def host_cache(dc, n):
+    """Host copy of the first n positions of a device cache, for the oracle."""
     from oracle import oracle as orc
-    n = pos0 + T
-    hc = orc.HostCache(KV, n, 0)
-    hc.k[:] = c8.k[:, :n].cpu().numpy()
-    hc.v[:] = c8.v[:, :n].cpu().numpy()
-    hc.ks[:] = c8.ks[:, :n].cpu().numpy()
-    hc.vs[:] = c8.vs[:, :n].cpu().numpy()
-    q = qo.cpu().numpy()
-    g = qg.cpu().numpy()
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
-    # rows in an order that spreads over the chunk: tokens by bit-reversed stride, all heads
-    toks = [t for s0 in range(37) for t in range((s0 * 19) % 37, T, 37)]
-    rows = [(t, h) for t in toks for h in range(H)]
-    deadline = time.perf_counter() + seconds
-    done, flops = 0, 0.0
+    hc = orc.HostCache(KV, n, dc.turbo)
+    hc.k[:] = dc.k[:, :n].cpu().numpy().view(hc.k.dtype)
+    hc.v[:] = dc.v[:, :n].cpu().numpy().view(hc.v.dtype)
+    hc.ks[:] = dc.ks[:, :n].cpu().numpy()
+    hc.vs[:] = dc.vs[:, :n].cpu().numpy()
+    return hc
 
-    def work(chunk):
-        orc.attn_rows_f64(q, g, LD, H, hc, pos0, chunk)
-        return sum(4.0 * AHD * (pos0 + t + 1) for t, _ in chunk)
 
+def cpu_rows(hc, q, g, pos0, rows, threads, min_s=1.5):
+    """The fp64 reference attention (tests/test_fa.cu:59-80 semantics, oracle/moex_oracle.c; turbo: dequantized codes
+    and the inverse rotation) over (token, head) rows, threaded; returns (seconds, flops by the reference's per-row
+    count 4 * D * keys); seconds is per pass over the rows."""
+    import concurrent.futures as cf
+    from oracle import oracle as orc
+    rows = list(rows)
+    nch = min(len(rows), 4 * threads)
+    chunks = [rows[i::nch] for i in range(nch)]
+    reps = 0
     t0 = time.perf_counter()
     with cf.ThreadPoolExecutor(threads) as ex:
-        i = 0
-        while time.perf_counter() < deadline and i < len(rows):
-            batch = [rows[i + j * 4: i + j * 4 + 4] for j in range(threads)]
-            batch = [b for b in batch if b]
-            i += 4 * threads
-            for f in ex.map(work, batch):
-                flops += f
-            done += sum(len(b) for b in batch)
-    el = time.perf_counter() - t0
-    return {"value": round(flops / el / 1e12, 6), "unit": "TFLOPS", "cores": threads, "kind": "port",
-            "sample": f"{done} of the {T * H} (token, head) rows of the configs[1] chunk (each over its "
-                      f"{pos0 + 1}..{n} causal keys), fp64, {el:.1f} s; nproc={os.cpu_count()}"}
+        while reps == 0 or time.perf_counter() - t0 < min_s:  # short samples repeat: ~min_s of wall time at least
+            list(ex.map(lambda c: orc.attn_rows_f64(q, g, LD, H, hc, pos0, c), chunks))
+            reps += 1
+    el = (time.perf_counter() - t0) / reps
+    return el, sum(4.0 * AHD * (pos0 + t + 1) for t, _ in rows)
+
+
+def sample_rows(T):
+    """tests/test_fa.cu:95: tokens {0, T/3, T/2, T-2, T-1} x all heads."""
+    return [(t, h) for t in sorted({0, T // 3, T // 2, T - 2, T - 1}) for h in range(H)]
+
+
+def cpu_prefill(hc, q, g, pos0, T, threads, full):
+    rows = [(t, h) for t in range(T) for h in range(H)] if full else sample_rows(T)
+    el, fl = cpu_rows(hc, q, g, pos0, rows, threads)
+    rate = fl / el
+    d = {"value": round(rate / 1e12, 6), "unit": "TFLOPS", "cores": threads, "kind": "port",
+         "seconds": round(el, 3)}
+    if full:
+        d["sample"] = f"all {T * H} (token, head) rows, fp64"
+    else:
+        d["sample"] = (f"the test_fa.cu:95 row sample ({len(rows)} rows of {T * H}), fp64, {el:.2f} s; "
+                       f"full chunk extrapolated linearly in flops: {flops_prefill(T, pos0) / rate:.1f} s")
+        d["extrapolated_full_s"] = round(flops_prefill(T, pos0) / rate, 2)
+    return d
+
+
+def cpu_decode(hc, q, g, pos, Tq, kv_bytes, threads):
+    el, _ = cpu_rows(hc, q, g, pos, [(t, h) for t in range(Tq) for h in range(H)], threads)
+    return {"value": round(kv_bytes / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "seconds": round(el, 3), "sample": f"all {Tq * H} (token, head) rows over {pos + Tq} keys, fp64"}
 
 
 if __name__ == "__main__":
