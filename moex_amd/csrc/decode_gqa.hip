@@ -645,7 +645,19 @@ constexpr uint32_t spack(int a, int b, int c, int d) {
 }
 constexpr uint32_t SK0 = spack(-127, -96, -75, -58), SK1 = spack(-44, -31, -18, -6);
 constexpr uint32_t SK2 = spack(6, 18, 31, 44), SK3 = spack(58, 75, 96, 127);
-constexpr uint32_t SV0 = spack(-127, -79, -45, -14), SV1 = spack(14, 45, 79, 127);
+// V codes biased by 128 (1 .. 255): the consumers read a biased byte b as the fp16 subnormal b * 2^-24, one v_perm
+// per two codes, and remove the bias 128 * sum(P) once at the end
+constexpr uint32_t SV0 = spack(1, 49, 83, 114), SV1 = spack(142, 173, 207, 255);
+constexpr int VBIAS = 128;
+// fp16 operand of 8 keys of one dim from 8 key rows of biased codes: half k = byte j of r[k] as a subnormal
+// (b * 2^-24; MFMA takes fp16 subnormals exactly)
+__device__ __forceinline__ half8_t bsub8(const uint32_t r[8], int j) {
+    const uint32_t sel = (uint32_t)j | 0x0c00u | ((uint32_t)(4 + j) << 16) | 0x0c000000u;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 u = {__builtin_amdgcn_perm(r[1], r[0], sel), __builtin_amdgcn_perm(r[3], r[2], sel),
+               __builtin_amdgcn_perm(r[5], r[4], sel), __builtin_amdgcn_perm(r[7], r[6], sel)};
+    return __builtin_bit_cast(half8_t, u);
+}
 // 4 nibble indices (one per byte) -> 4 signed K codes
 __device__ __forceinline__ int lut16s(uint32_t idx) {
     const uint32_t s3 = idx & 0x07070707u;
@@ -825,6 +837,7 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
 #pragma unroll
         for (int J = 0; J < 16; J++) o[J] = float4_t{0.f, 0.f, 0.f, 0.f};
         float mref = -INFINITY, lacc = 0.f, vmax = 0.f;
+        float xsum0 = 0.f, xsum1 = 0.f;  // sum of P * vn * K3 * 2^sig of this lane's keys (V halves 0, 1): the bias
         int sig = 0;
         const int kb = 32 * wv;
         for (int c = 0; c < nch; c++) {
@@ -914,6 +927,7 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
 #pragma unroll
                         for (int i = 0; i < 4; i++) o[J][i] *= fr[i];
                     lacc *= fown;
+                    xsum0 *= fown * sf; xsum1 *= fown * sf;
                     mref = nref;
                     sig = nsig;
                 }
@@ -925,17 +939,19 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
             {
                 const float vsc = ldexpf(1.f, sig) * TK3;
                 half8_t p0v, p1v;
-                float ls = 0.f;
+                float ls = 0.f, xs0 = 0.f, xs1 = 0.f;
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
                     const float p = fast_exp2(sc[j] - mref);
                     ls += p;
                     const float x0 = p * (vn[j].x * vsc), x1 = p * (vn[j].y * vsc);
+                    xs0 += x0; xs1 += x1;
                     const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
                     p0v[j] = lo8 ? h0 : (_Float16)(x0 - (float)h0);
                     p1v[j] = lo8 ? h1 : (_Float16)(x1 - (float)h1);
                 }
                 lacc += lo8 ? ls : 0.f;
+                xsum0 += xs0; xsum1 += xs1;
                 pa0 = p0v;
                 pa1 = p1v;
             }
@@ -947,12 +963,9 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
 #pragma unroll
                 for (int j = 0; j < 8; j++)
                     r[j] = *reinterpret_cast<const uint32_t*>(Vc + (16 * (j >> 2) + 4 * g + (j & 3)) * AHD + rd);
-                uint32_t c0v[4], c1v[4];
-                tr4x4_(r[0], r[1], r[2], r[3], c0v);
-                tr4x4_(r[4], r[5], r[6], r[7], c1v);
 #pragma unroll
                 for (int jt = 0; jt < 4; jt++)
-                    o[4 * pc + jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pc < 2 ? pa0 : pa1, i8x8_to_h8(c0v[jt], c1v[jt]),
+                    o[4 * pc + jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pc < 2 ? pa0 : pa1, bsub8(r, jt),
                                                                          o[4 * pc + jt], 0, 0, 0);
             }
         }
@@ -968,16 +981,22 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
         for (int J = 0; J < 16; J++)
 #pragma unroll
             for (int i = 0; i < 4; i++) o[J][i] += __shfl_xor(o[J][i], 32);
+        // the V operands were (code + 128) * 2^-24: O = 2^24 o - 128 * sum(P * vn * K3 * 2^sig), per head and V half
+        const float xb0 = sum_x32(sum_x16(xsum0)) * VBIAS, xb1 = sum_x32(sum_x16(xsum1)) * VBIAS;
         if (g < 2) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int h = 4 * g + i;
                 const float Mh = fmaxf(fmaxf(cm[0][h], cm[1][h]), fmaxf(cm[2][h], cm[3][h]));
                 const float f = ex2d(cm[wv][h], Mh) * un;
+                const float b0 = __shfl(xb0, h), b1 = __shfl(xb1, h);  // lane h: head h's sums (its hi lanes)
 #pragma unroll
-                for (int pc = 0; pc < 4; pc++)
+                for (int pc = 0; pc < 4; pc++) {
+                    const float b = pc < 2 ? b0 : b1;
                     *reinterpret_cast<float4*>(Ow + (wv * GQ + h) * AHD + 64 * pc + 4 * m16) =
-                        make_float4(o[4 * pc][i] * f, o[4 * pc + 1][i] * f, o[4 * pc + 2][i] * f, o[4 * pc + 3][i] * f);
+                        make_float4(fmaf(o[4 * pc][i], 16777216.f, -b) * f, fmaf(o[4 * pc + 1][i], 16777216.f, -b) * f,
+                                    fmaf(o[4 * pc + 2][i], 16777216.f, -b) * f, fmaf(o[4 * pc + 3][i], 16777216.f, -b) * f);
+                }
             }
         }
     }
