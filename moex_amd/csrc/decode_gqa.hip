@@ -54,6 +54,19 @@ __device__ __forceinline__ void tr4x4_(const uint32_t r0, const uint32_t r1, con
     c[2] = __builtin_amdgcn_perm(t3, t1, 0x05040100u); c[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
 }
 
+// P.V takes V as biased bytes b = v + 128 (1 .. 255) read as the fp16 subnormal b * 2^-24: one v_perm per two codes
+// builds the operand (MFMA takes fp16 subnormals exactly), and O = 2^24 o - 128 * sum(P) is restored once at the end.
+constexpr int VBIAS = 128;
+// fp16 operand of 8 keys of one dim from 8 key rows of biased codes: half k = byte j of r[k] as a subnormal
+// (b * 2^-24; MFMA takes fp16 subnormals exactly)
+__device__ __forceinline__ half8_t bsub8(const uint32_t r[8], int j) {
+    const uint32_t sel = (uint32_t)j | 0x0c00u | ((uint32_t)(4 + j) << 16) | 0x0c000000u;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 u = {__builtin_amdgcn_perm(r[1], r[0], sel), __builtin_amdgcn_perm(r[3], r[2], sel),
+               __builtin_amdgcn_perm(r[5], r[4], sel), __builtin_amdgcn_perm(r[7], r[6], sel)};
+    return __builtin_bit_cast(half8_t, u);
+}
+
 // 2^(a - b) with 2^(-inf - -inf) = 1 (a running maximum that has not moved, also while it is still -inf)
 __device__ __forceinline__ float ex2d(float a, float b) { return a == b ? 1.f : fast_exp2(a - b); }
 
@@ -200,6 +213,7 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws_kernel(const f
 #pragma unroll
         for (int J = 0; J < 16; J++) o[J] = float4_t{0.f, 0.f, 0.f, 0.f};
         float mref = -INFINITY, lacc = 0.f, vmax = 0.f;  // reference maximum and sum of column m16, V-scale maximum
+        float xsum = 0.f;                                 // sum of P * vs * 2^sig of this lane's keys: the V bias
         int sig = 0;                                      // O is held times 2^sig
         const int kb = 32 * wv;                           // this consumer's keys kb .. kb+31 of every chunk
         for (int c = 0; c < nch; c++) {
@@ -280,6 +294,7 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws_kernel(const f
 #pragma unroll
                         for (int i = 0; i < 4; i++) o[J][i] *= fr[i];
                     lacc *= fown;
+                    xsum *= fown * sf;
                     mref = nref;
                     sig = nsig;
                 }
@@ -290,16 +305,18 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws_kernel(const f
             {
                 const float vsc = ldexpf(1.f, sig);
                 half8_t ph;
-                float ls = 0.f;
+                float ls = 0.f, xs = 0.f;
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
                     const float p = fast_exp2(sc[j] - mref);  // 0 for masked keys (mref is finite once a key is seen)
                     ls += p;
                     const float x = p * (vv[j] * vsc);
+                    xs += x;
                     const _Float16 h = (_Float16)x;
                     ph[j] = (m16 & 1) ? (_Float16)(x - (float)h) : h;
                 }
                 lacc += ls;
+                xsum += xs;
                 pa = ph;
             }
             // ---- O^T += P . V over this consumer's 32 keys, all 256 dims ----
@@ -312,12 +329,11 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws_kernel(const f
 #pragma unroll
                 for (int j = 0; j < 8; j++)
                     r[j] = *reinterpret_cast<const uint32_t*>(Vs + (kb + 16 * (j >> 2) + 4 * g + (j & 3)) * AHD + rd);
-                uint32_t c0v[4], c1v[4];
-                tr4x4_(r[0], r[1], r[2], r[3], c0v);
-                tr4x4_(r[4], r[5], r[6], r[7], c1v);
+#pragma unroll
+                for (int j = 0; j < 8; j++) r[j] ^= 0x80808080u;  // biased codes
 #pragma unroll
                 for (int jt = 0; jt < 4; jt++)
-                    o[4 * pc + jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, i8x8_to_h8(c0v[jt], c1v[jt]), o[4 * pc + jt], 0, 0, 0);
+                    o[4 * pc + jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, bsub8(r, jt), o[4 * pc + jt], 0, 0, 0);
             }
         }
         // ---- merge the four consumers: m, l per head, then O rows scaled to the common maximum ----
@@ -328,20 +344,27 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws_kernel(const f
         // rows 4g .. 4g+3 of the O tiles are hi, lo of head 2g and hi, lo of head 2g + 1
         float* Ow = reinterpret_cast<float*>(smem);  // [consumer][head][256]
         const float un = ldexpf(1.f, -sig);
+        // the V operands were (v + 128) * 2^-24: O = 2^24 o - 128 * sum(P * vs * 2^sig) per head
+        const float xb = sum_x32(sum_x16(xsum)) * VBIAS;
 #pragma unroll
         for (int e = 0; e < 2; e++) {
             const int h = 2 * g + e;
             float Mh = cm[0][h];
 #pragma unroll
             for (int w = 1; w < WS_NC; w++) Mh = fmaxf(Mh, cm[w][h]);
-            const float f = ex2d(cm[wv][h], Mh) * un;
+            const float f = ex2d(cm[wv][h], Mh) * un, b = __shfl(xb, 2 * h);
+            float4 y[4];
+#pragma unroll
+            for (int pc = 0; pc < 4; pc++) {
+                float t[4];
+#pragma unroll
+                for (int jt = 0; jt < 4; jt++)
+                    t[jt] = fmaf(o[4 * pc + jt][2 * e] + o[4 * pc + jt][2 * e + 1], 16777216.f, -b) * f;
+                y[pc] = make_float4(t[0], t[1], t[2], t[3]);
+            }
 #pragma unroll
             for (int pc = 0; pc < 4; pc++)
-                *reinterpret_cast<float4*>(Ow + (wv * GQ + h) * AHD + 64 * pc + 4 * m16) =
-                    make_float4((o[4 * pc][2 * e] + o[4 * pc][2 * e + 1]) * f,
-                                (o[4 * pc + 1][2 * e] + o[4 * pc + 1][2 * e + 1]) * f,
-                                (o[4 * pc + 2][2 * e] + o[4 * pc + 2][2 * e + 1]) * f,
-                                (o[4 * pc + 3][2 * e] + o[4 * pc + 3][2 * e + 1]) * f);
+                *reinterpret_cast<float4*>(Ow + (wv * GQ + h) * AHD + 64 * pc + 4 * m16) = y[pc];
         }
     }
     __syncthreads();
@@ -445,6 +468,7 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wsp_kernel(const 
 #pragma unroll
         for (int J = 0; J < 16; J++) o[J] = float4_t{0.f, 0.f, 0.f, 0.f};
         float mref = -INFINITY, lacc = 0.f, vmax = 0.f;  // reference maximum and sum of column m16, V-scale maximum
+        float xsum = 0.f;                                 // sum of P * vs * 2^sig of this lane's keys: the V bias
         int sig = 0;                                      // O is held times 2^sig
         for (int c = 0; c < nch; c++) {
             __syncthreads();  // chunk c is in stage c % WS_NS
@@ -529,6 +553,7 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wsp_kernel(const 
 #pragma unroll
                             for (int i = 0; i < 4; i++) o[J][i] *= fr[i];
                         lacc *= fown;
+                        xsum *= fown * sf;
                         mref = nref;
                         sig = nsig;
                     }
@@ -539,17 +564,19 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wsp_kernel(const 
                 {
                     const float vsc = ldexpf(1.f, sig), mr = mref == -INFINITY ? 0.f : mref;
                     half8_t ph, pl;
-                    float ls = 0.f;
+                    float ls = 0.f, xs = 0.f;
 #pragma unroll
                     for (int j = 0; j < 8; j++) {
                         const float p = fast_exp2(sc[j] - mr);
                         ls += p;
                         const float x = p * (vv[j] * vsc);
+                        xs += x;
                         const _Float16 h = (_Float16)x;
                         ph[j] = h;
                         pl[j] = (_Float16)(x - (float)h);
                     }
                     lacc += ls;
+                    xsum += xs;
                     pah = ph;
                     pal = pl;
                 }
@@ -561,12 +588,11 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wsp_kernel(const 
 #pragma unroll
                     for (int j = 0; j < 8; j++)
                         r[j] = *reinterpret_cast<const uint32_t*>(Vs + (kb + 16 * (j >> 2) + 4 * g + (j & 3)) * AHD + rd);
-                    uint32_t c0v[4], c1v[4];
-                    tr4x4_(r[0], r[1], r[2], r[3], c0v);
-                    tr4x4_(r[4], r[5], r[6], r[7], c1v);
+#pragma unroll
+                    for (int j = 0; j < 8; j++) r[j] ^= 0x80808080u;  // biased codes
 #pragma unroll
                     for (int jt = 0; jt < 4; jt++) {
-                        const half8_t vb = i8x8_to_h8(c0v[jt], c1v[jt]);
+                        const half8_t vb = bsub8(r, jt);
                         o[4 * pc + jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pah, vb, o[4 * pc + jt], 0, 0, 0);
                         o[4 * pc + jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pal, vb, o[4 * pc + jt], 0, 0, 0);
                     }
@@ -580,17 +606,20 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wsp_kernel(const 
         __syncthreads();
         float* Ow = reinterpret_cast<float*>(smem);  // [consumer][column][256]
         const float un = ldexpf(1.f, -sig);
+        // the V operands were (v + 128) * 2^-24: O = 2^24 o - 128 * sum(P * vs * 2^sig) per column
+        const float xb = sum_x32(sum_x16(xsum)) * VBIAS;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int col = 4 * g + i;
             float Mc = cm[pr][col];
 #pragma unroll
             for (int w = pr + NPR; w < WS_NC; w += NPR) Mc = fmaxf(Mc, cm[w][col]);
-            const float f = ex2d(cm[wv][col], Mc) * un;
+            const float f = ex2d(cm[wv][col], Mc) * un, b = __shfl(xb, col);
 #pragma unroll
             for (int pc = 0; pc < 4; pc++)
                 *reinterpret_cast<float4*>(Ow + (wv * 16 + col) * AHD + 64 * pc + 4 * m16) =
-                    make_float4(o[4 * pc][i] * f, o[4 * pc + 1][i] * f, o[4 * pc + 2][i] * f, o[4 * pc + 3][i] * f);
+                    make_float4(fmaf(o[4 * pc][i], 16777216.f, -b) * f, fmaf(o[4 * pc + 1][i], 16777216.f, -b) * f,
+                                fmaf(o[4 * pc + 2][i], 16777216.f, -b) * f, fmaf(o[4 * pc + 3][i], 16777216.f, -b) * f);
         }
     }
     __syncthreads();
@@ -645,19 +674,8 @@ constexpr uint32_t spack(int a, int b, int c, int d) {
 }
 constexpr uint32_t SK0 = spack(-127, -96, -75, -58), SK1 = spack(-44, -31, -18, -6);
 constexpr uint32_t SK2 = spack(6, 18, 31, 44), SK3 = spack(58, 75, 96, 127);
-// V codes biased by 128 (1 .. 255): the consumers read a biased byte b as the fp16 subnormal b * 2^-24, one v_perm
-// per two codes, and remove the bias 128 * sum(P) once at the end
+// V codes biased by 128 (1 .. 255), read by the consumers as fp16 subnormals (bsub8)
 constexpr uint32_t SV0 = spack(1, 49, 83, 114), SV1 = spack(142, 173, 207, 255);
-constexpr int VBIAS = 128;
-// fp16 operand of 8 keys of one dim from 8 key rows of biased codes: half k = byte j of r[k] as a subnormal
-// (b * 2^-24; MFMA takes fp16 subnormals exactly)
-__device__ __forceinline__ half8_t bsub8(const uint32_t r[8], int j) {
-    const uint32_t sel = (uint32_t)j | 0x0c00u | ((uint32_t)(4 + j) << 16) | 0x0c000000u;
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    u32x4 u = {__builtin_amdgcn_perm(r[1], r[0], sel), __builtin_amdgcn_perm(r[3], r[2], sel),
-               __builtin_amdgcn_perm(r[5], r[4], sel), __builtin_amdgcn_perm(r[7], r[6], sel)};
-    return __builtin_bit_cast(half8_t, u);
-}
 // 4 nibble indices (one per byte) -> 4 signed K codes
 __device__ __forceinline__ int lut16s(uint32_t idx) {
     const uint32_t s3 = idx & 0x07070707u;
