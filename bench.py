@@ -237,10 +237,9 @@ def main():
         o1 = torch.empty((1, H, AHD), device=dev)
         pd = torch.tensor([ctx - 1], dtype=torch.int32, device=dev)
 
-        def tdec():
-            M.attn_gqa(qo[:1], ct, H, KV, pd, ct.max_t, part, 1, ns, st)
-            M.attn_combine(part, None, o1, H, ns, LD, 1, st)
-            M.turbo_out(o1, qg[:1], H, LD, 1, st)
+        def tdec():  # what attn_decode runs: partials rotated back in the split kernel, gated combine
+            M.attn_gqa_out(qo[:1], ct, H, KV, pd, ct.max_t, part, 1, ns, st)
+            M.attn_combine(part, qg[:1], o1, H, ns, LD, 1, st)
 
         t_td = time_rotating([tdec, lambda: flush_read.sum()], 20) * 2 - t_flush
         tb = 2.0 * ctx * 240

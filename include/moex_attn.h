@@ -112,6 +112,12 @@ void moex_kv_append(const float* k, const float* v, moex_kv_cache kv, int KV, co
  * part must be 16-byte aligned (any hipMalloc / cudaMalloc pointer is). */
 void moex_attn_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part,
                    int T, int ns, void* stream);
+/* No counterpart in the reference: moex_attn_gqa whose turbo partials come out rotated back to the output domain (the
+ * inverse WHT of turbo_out_k applied per split, which the combine's weighted sum commutes with), so that
+ * moex_attn_combine with the gate gives the final output and no moex_turbo_out follows. moex_attn_decode's split-K
+ * branch runs this. For an int8 cache it is moex_attn_gqa. */
+void moex_attn_gqa_out(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part,
+                       int T, int ns, void* stream);
 /* attn_combine_k (kernels.cuh:1317), grid (H, T): merges ns partials, out = acc/l * sigmoid(gate) (no gate if
  * q_gate is NULL). */
 void moex_attn_combine(const float* part, const float* q_gate, float* out, int H, int ns, int ld, int T,

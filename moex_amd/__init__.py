@@ -51,6 +51,7 @@ def lib():
     L.moex_qk_norm_rope.argtypes = [vp, vp, vp, vp, vp, vp, KVCache, i, i, vp, i, i, f, f, i, i, vp]
     L.moex_kv_append.argtypes = [vp, vp, KVCache, i, vp, i, i, i, vp]
     L.moex_attn_gqa.argtypes = [vp, KVCache, i, i, vp, i, vp, i, i, vp]
+    L.moex_attn_gqa_out.argtypes = [vp, KVCache, i, i, vp, i, vp, i, i, vp]
     L.moex_attn_combine.argtypes = [vp, vp, vp, i, i, i, i, vp]
     L.moex_attn_decode_heads.argtypes = [vp, vp, KVCache, vp, i, i, vp, i, i, vp, i, i, vp]
     L.moex_turbo_out.argtypes = [vp, vp, i, i, i, vp]
@@ -75,7 +76,7 @@ def lib():
 
 
 EXPORTS = ["moex_kv_alloc", "moex_kv_bytes", "moex_kv_free", "moex_attn_decode", "moex_attn_decode_noalloc", "moex_attn_fa", "moex_attn_prefill",
-           "moex_qk_norm_rope", "moex_kv_append", "moex_attn_gqa", "moex_attn_combine", "moex_attn_decode_heads",
+           "moex_qk_norm_rope", "moex_kv_append", "moex_attn_gqa", "moex_attn_gqa_out", "moex_attn_combine", "moex_attn_decode_heads",
            "moex_turbo_out", "moex_set_int", "moex_set_soft_error", "moex_set_skip", "moex_fa_on",
            "moex_fa_supported", "moex_decode_splits", "moex_gqa_splits", "moex_version",
            "moex_attn_workspace_bytes", "moex_workspace_held",
@@ -174,6 +175,11 @@ def kv_append(k, v, kv, KV, pos_d, max_t, ld, T, st=None):
 def attn_gqa(qo, kv, H, KV, pos_d, max_t, part, T, ns, st=None):
     """attn_gqa_k (kernels.cuh:1745), grid (KV, T, ns)."""
     lib().moex_attn_gqa(_p(qo), _kv(kv), H, KV, _p(pos_d), max_t, _p(part), T, ns, _s(st))
+
+
+def attn_gqa_out(qo, kv, H, KV, pos_d, max_t, part, T, ns, st=None):
+    """attn_gqa whose turbo partials are rotated back (combine with the gate then gives the output; no turbo_out)."""
+    lib().moex_attn_gqa_out(_p(qo), _kv(kv), H, KV, _p(pos_d), max_t, _p(part), T, ns, _s(st))
 
 
 def attn_combine(part, q_gate, out, H, ns, ld, T, st=None):

@@ -162,6 +162,14 @@ void moex_attn_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* 
     launch_gqa(qo, kv, H, KV, pos_d, max_t, part, T, ns, S(stream));
 }
 
+void moex_attn_gqa_out(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part,
+                       int T, int ns, void* stream) {
+    MOEX_REQUIRE(KV > 0 && H == KV * GQ, "the GQA kernel needs H / KV == 8");
+    MOEX_REQUIRE(T > 0 && ns > 0 && part, "T, ns, part");
+    MOEX_REQUIRE(((uintptr_t)part & 15) == 0, "part must be 16-byte aligned");
+    launch_gqa(qo, kv, H, KV, pos_d, max_t, part, T, ns, S(stream), kv.turbo != 0);
+}
+
 void moex_attn_combine(const float* part, const float* q_gate, float* out, int H, int ns, int ld, int T, void* stream) {
     MOEX_REQUIRE(H > 0 && T > 0 && ns > 0, "H, T, ns");
     launch_combine(part, q_gate, out, H, ns, ld, T, S(stream));
@@ -217,8 +225,10 @@ void decode_step(const float* q, const float* k, const float* v, const uint16_t*
         launch_prefill_k7p(qo, q, kv, out, H, KV, pos_d, max_t, ld, T, st);
     } else if (ns > 1 && G == GQ) {
         ns = gqa_splits(T, KV, ns, kv.turbo != 0);
-        launch_gqa(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
-        launch_combine(part, gate, out, H, ns, ld, T, st);
+        // turbo: the split kernel rotates its partials back, so the combine gates them and turbo_out is not needed
+        launch_gqa(qo, kv, H, KV, pos_d, max_t, part, T, ns, st, kv.turbo != 0);
+        launch_combine(part, q, out, H, ns, ld, T, st);
+        return;
     } else {
         launch_decode_heads(qo, gate, kv, out, H, KV, pos_d, max_t, ld, part, T, ns, st);
         if (ns > 1) launch_combine(part, gate, out, H, ns, ld, T, st);

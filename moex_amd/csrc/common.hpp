@@ -86,8 +86,10 @@ void launch_set_int(int* p, int v, hipStream_t st);
 void launch_set_skip(int v, hipStream_t st);
 // split count moex_attn_decode uses for the GQA kernel when the caller allows ns splits (never more than ns)
 int gqa_splits(int T, int KV, int ns, bool turbo);
+// rot_out (turbo caches): the partials come out rotated back to the output domain, for a gated combine with no
+// turbo_out after it
 void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part, int T,
-                int ns, hipStream_t st);
+                int ns, hipStream_t st, bool rot_out = false);
 void launch_fa(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d,
                int max_t, int ld, int T, hipStream_t st);
 // dense int8 projections (dense.hip)

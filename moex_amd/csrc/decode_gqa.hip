@@ -708,13 +708,22 @@ constexpr int WST_RV = 128 * TQ_VB;                      // raw V rows of a chun
 constexpr int WST_VC = 32 * AHD;                         // one consumer's unpacked V codes (two buffers)
 constexpr int WST_VC0 = WST_NS * WST_STAGE + 2 * WST_RV;  // offset of the V code areas
 constexpr int WST_LDS = WST_VC0 + 2 * WS_NC * WST_VC;
-static_assert(WS_NC * GQ * AHD * 4 <= WST_NS * WST_STAGE, "the consumer merge fits in the stages");
+static_assert((WS_NC + 1) * GQ * AHD * 4 <= WST_NS * WST_STAGE, "the consumer merge and the merged rows fit in the stages");
 static_assert(WST_LDS <= 160 * 1024, "LDS");
 
+// Sign tables of the inverse rotation (kernels.cuh:1123-1132, TQ_S1 / TQ_S2) as bit masks: bit j set = -1.
+constexpr uint32_t WS1[4] = {0xe46a0359u, 0x42f85949u, 0xa4c63bbbu, 0x49f250a9u};
+constexpr uint32_t WS2[4] = {0x16acee90u, 0x3f628fdcu, 0xb7a5357au, 0xbea56562u};
+__device__ __forceinline__ float sgn(const uint32_t* m, int j, float x) {
+    return (m[j >> 5] >> (j & 31)) & 1 ? -x : x;
+}
+
+// rot != 0: the partial's acc is rotated back (the inverse WHT of turbo_out_k, kernels.cuh:1730-1738, is linear, so
+// it commutes with the combine's weighted sum): the combine then gates it directly and no turbo_out launch follows.
 __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const float* __restrict__ qo, moex_kv_cache kv,
                                                                          int H, const int* __restrict__ pos_d,
                                                                          int max_t, float* __restrict__ part, int T,
-                                                                         int ns) {
+                                                                         int ns, int rot) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float cm[WS_NC][GQ], cl[WS_NC][GQ];
     const int nb = gridDim.x, w_id = xcd_work_id(blockIdx.x, nb);
@@ -1019,6 +1028,7 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
         }
     }
     __syncthreads();
+    float* Om = reinterpret_cast<float*>(smem) + WS_NC * GQ * AHD;  // [head][256]: the merged acc, when rotating back
     for (int it = tid; it < GQ * 64; it += 64 * (WS_NC + WS_NP)) {
         const float* Ow = reinterpret_cast<const float*>(smem);
         const int h = it >> 6, d4 = 4 * (it & 63);
@@ -1028,13 +1038,35 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
             const float4 b = *reinterpret_cast<const float4*>(Ow + (w * GQ + h) * AHD + d4);
             a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
         }
-        *reinterpret_cast<float4*>(part_acc(part, tok, kvh * GQ + h, s, H, ns) + d4) = a;
+        if (rot) *reinterpret_cast<float4*>(Om + h * AHD + d4) = a;
+        else *reinterpret_cast<float4*>(part_acc(part, tok, kvh * GQ + h, s, H, ns) + d4) = a;
         if ((it & 63) == 0) {
             const float Mh = fmaxf(fmaxf(cm[0][h], cm[1][h]), fmaxf(cm[2][h], cm[3][h]));
             float* ml = part_ml(part, tok, kvh * GQ + h, s, H, ns, T);
             ml[0] = Mh;  // -inf when the token has no key in this split
             ml[1] = cl[0][h] * ex2d(cm[0][h], Mh) + cl[1][h] * ex2d(cm[1][h], Mh) + cl[2][h] * ex2d(cm[2][h], Mh) +
                     cl[3][h] * ex2d(cm[3][h], Mh);
+        }
+    }
+    if (rot) {
+        // wavefront w: head w, both halves; lane L holds in-half dims L and L + 64 (stages 1..32 by xor shuffles,
+        // stage 64 in the lane), in the order of the reference's inverse: x S2, butterflies, / sqrt(128), x S1
+        __syncthreads();
+        const int h = wv;
+        float* dst = part_acc(part, tok, kvh * GQ + h, s, H, ns);
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            float v0 = sgn(WS2, lane, Om[h * AHD + 128 * b + lane]);
+            float v1 = sgn(WS2, lane + 64, Om[h * AHD + 128 * b + 64 + lane]);
+#pragma unroll
+            for (int st = 1; st < 64; st <<= 1) {
+                const float o0 = __shfl_xor(v0, st), o1 = __shfl_xor(v1, st);
+                v0 = (lane & st) ? o0 - v0 : v0 + o0;
+                v1 = (lane & st) ? o1 - v1 : v1 + o1;
+            }
+            const float a0 = v0 + v1, a1 = v0 - v1;
+            dst[128 * b + lane] = sgn(WS1, lane, a0 * 0.08838834764831845f);
+            dst[128 * b + 64 + lane] = sgn(WS1, lane + 64, a1 * 0.08838834764831845f);
         }
     }
 }
@@ -1054,7 +1086,7 @@ int gqa_splits(int T, int KV, int ns, bool turbo) {
 }
 
 void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part, int T,
-                int ns, hipStream_t st) {
+                int ns, hipStream_t st, bool rot_out) {
     if (kv.turbo) {
         static bool once = [] {
             MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_wst_kernel),
@@ -1063,7 +1095,7 @@ void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos
         }();
         (void)once;
         hipLaunchKernelGGL(gqa_wst_kernel, dim3(KV * ns * T), dim3(64 * (WS_NC + WS_NP)), WST_LDS, st, qo, kv, H, pos_d,
-                           max_t, part, T, ns);
+                           max_t, part, T, ns, rot_out ? 1 : 0);
     } else {
         if (T == 1) {
             static bool once = [] {

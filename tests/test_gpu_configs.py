@@ -113,6 +113,15 @@ def test_config3_turbo_decode(turbo_long):
     err, mag = float(np.abs(got - ref).max()), float(np.abs(ref).max())
     report("configs[3] gqa+combine+turbo_out", splits=nsg, err=err, mag=mag, rel=err / mag)
     assert np.all(np.isfinite(got)) and err <= 1e-4 * mag
+    # what attn_decode runs: the split kernel rotates its partials back, the combine gates them
+    out.fill_(float("nan"))
+    M.attn_gqa_out(dev(qo), dc, H, KV, pos_tensor(pos), N_LONG, part, 1, nsg)
+    M.attn_combine(part, dev(qg), out, H, nsg, LD, 1)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()[0]
+    err = float(np.abs(got - ref).max())
+    report("configs[3] gqa_out+combine", splits=nsg, err=err, mag=mag, rel=err / mag)
+    assert np.all(np.isfinite(got)) and err <= 1e-4 * mag
 
 
 def test_config3_turbo_attn_decode(turbo_long):

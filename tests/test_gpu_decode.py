@@ -108,6 +108,21 @@ def test_gqa_turbo(turbo_setup, pos0, T, ns):
     _check(f"gqa turbo + turbo_out ns={ns}", out.cpu().numpy(), qo, qg, hc, pos0, T)
 
 
+@pytest.mark.parametrize("pos0,T,ns", [(0, 1, 16), (1000, 2, 16), (39999, 1, 128), (39990, 4, 32)])
+def test_gqa_out_turbo(turbo_setup, pos0, T, ns):
+    """attn_gqa_out: the split kernel rotates its partials back, the gated combine then gives the full turbo output
+    (what attn_decode runs); against the fp64 reference with the inverse WHT and the gate."""
+    import torch
+    import moex_amd as M
+    hc, dc, qo, qg = turbo_setup
+    part = torch.empty(T * H * ns * (AHD + 2), dtype=torch.float32, device="cuda")
+    out = torch.zeros((T, H, AHD), dtype=torch.float32, device="cuda")
+    M.attn_gqa_out(dev(qo[:T]), dc, H, KV, pos_tensor(pos0), dc.max_t, part, T, ns)
+    M.attn_combine(part, dev(qg[:T]), out, H, ns, LD, T)
+    torch.cuda.synchronize()
+    _check(f"gqa_out turbo ns={ns}", out.cpu().numpy(), qo, qg, hc, pos0, T)
+
+
 @pytest.mark.parametrize("pos0,T,ns", [(0, 1, 1), (1000, 2, 8)])
 def test_decode_heads_turbo(turbo_setup, pos0, T, ns):
     import torch
