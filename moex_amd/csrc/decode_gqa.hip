@@ -745,10 +745,44 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
         const uint8_t* Vg = reinterpret_cast<const uint8_t*>(kv.v) + rbase * TQ_VB;
         const float* kng = kv.ks + 2 * rbase;
         const float* vng = kv.vs + 2 * rbase;
+        // a full chunk's sources sit at lane-constant byte offsets from its first row: computed once
+        int offs[9];
+#pragma unroll
+        for (int u = 0; u < 9; u++) {
+            const int i = pw + 4 * u;
+            if (i < 16) {
+                const int r = 8 * i + (lane >> 3);
+                offs[u] = r * TQ_KB + 16 * ((lane & 7) ^ ((r >> 1) & 7));
+            } else if (i < 28) {
+                offs[u] = (3 * pw + (i - 16) / 4) * 1024 + 16 * lane;  // the chunk's raw V rows are contiguous
+            } else {
+                offs[u] = 4 * (64 * (i & 3) + lane);                   // two norms per key, contiguous
+            }
+        }
         auto issue = [&](int c) {
             const int c0 = c == 0 ? lo : lo + first + (c - 1) * WS_CH, ce = c == 0 ? lo + first : lo + first + c * WS_CH;
             unsigned char* st = smem + (c % WST_NS) * WST_STAGE;
             unsigned char* rv = smem + WST_NS * WST_STAGE + (c & 1) * WST_RV;
+            if (ce - c0 == WS_CH) {
+                const uint8_t* kb0 = Kg + (size_t)c0 * TQ_KB;
+                const uint8_t* vb0 = Vg + (size_t)c0 * TQ_VB;
+                const uint8_t* nk0 = reinterpret_cast<const uint8_t*>(kng + 2 * (size_t)c0);
+                const uint8_t* nv0 = reinterpret_cast<const uint8_t*>(vng + 2 * (size_t)c0);
+#pragma unroll
+                for (int u = 0; u < 9; u++) {
+                    const int i = pw + 4 * u;
+                    if (i < 16)
+                        __builtin_amdgcn_global_load_lds((gptr_t)(kb0 + offs[u]), (lptr_t)(st + i * 1024), 16, 0, 0);
+                    else if (i < 28)
+                        __builtin_amdgcn_global_load_lds((gptr_t)(vb0 + offs[u]),
+                                                         (lptr_t)(rv + (3 * pw + (i - 16) / 4) * 1024), 16, 0, 0);
+                    else
+                        __builtin_amdgcn_global_load_lds((gptr_t)((i < 32 ? nk0 : nv0) + offs[u]),
+                                                         (lptr_t)(st + WST_KB + (i < 32 ? 0 : 1024) + 256 * (i & 3)),
+                                                         4, 0, 0);
+                }
+                return;
+            }
 #pragma unroll
             for (int u = 0; u < 9; u++) {
                 const int i = pw + 4 * u;
