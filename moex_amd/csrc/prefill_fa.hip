@@ -44,7 +44,7 @@ constexpr int FA_IMG_TILES = 8;             // token tiles per kv head from whic
 constexpr float SL2 = 0.0625f * 1.4426950408889634f;
 constexpr float TK4 = 0.241529f / 127.f, TK3 = 0.190207f / 127.f;
 constexpr int FA_KPF = 2;                   // LDS operand reads in flight ahead of the MFMAs
-constexpr float RESCALE_SLACK = 8.f;        // p <= 2^8 between rescales
+constexpr float RESCALE_LSUM = 256.f;       // p <= 2^8 between rescales: a lane's sum of p beyond it asks for the row max
 
 constexpr uint32_t pack4(int a, int b, int c, int d) {
     return (uint32_t)(a + 128) | ((uint32_t)(b + 128) << 8) | ((uint32_t)(c + 128) << 16) | ((uint32_t)(d + 128) << 24);
@@ -471,39 +471,54 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
                 for (int i = 0; i < 16; i++)
                     if (k0 + 8 * (i >> 2) + 4 * h32 + (i & 3) > prow) sc[i] = -INFINITY;
             }
-            float mt = sc[0];  // this lane's half of the row; the other half is in lane ^ 32
+            // ---- P^T (fp16) as B operands: MFMA m (keys 16m ..) takes S elements 8m .. 8m+7 ----
+            half8_t pf[2];
+            float ls = 0.f;
+            auto make_p = [&]() {
+                ls = 0.f;
 #pragma unroll
-            for (int i = 1; i < 16; i++) mt = fmaxf(mt, sc[i]);
+                for (int m = 0; m < 2; m++)
+#pragma unroll
+                    for (int jj = 0; jj < 8; jj += 2) {
+                        const float p0 = fast_exp2(sc[8 * m + jj]), p1 = fast_exp2(sc[8 * m + jj + 1]);
+                        const half2_t ph = half2_t{(_Float16)p0, (_Float16)p1};
+                        pf[m][jj] = ph[0]; pf[m][jj + 1] = ph[1];
+                        ls = __builtin_amdgcn_fdot2(ph, ones, ls, false);
+                    }
+            };
+            auto row_max = [&]() {  // this lane's half of the row; the other half is in lane ^ 32
+                float mt = sc[0];
+#pragma unroll
+                for (int i = 1; i < 16; i++) mt = fmaxf(mt, sc[i]);
+                return mt;
+            };
             if (j == 0) {
+                float mt = row_max();
                 mt = fmaxf(mt, __shfl_xor(mt, 32));
                 m_ref = mt;
 #pragma unroll
                 for (int i = 0; i < 16; i++) sc[i] -= mt;
-            } else if (__ballot(mt > RESCALE_SLACK)) {
-                // lazy rescale: O and l are referenced to m_ref, moved only when a row's maximum passes it by the slack
-                const float d = fmaxf(fmaxf(mt, __shfl_xor(mt, 32)), 0.f);
-                const float cf = fast_exp2(-d);
+                make_p();
+            } else {
+                // lazy rescale: O and l are referenced to m_ref and move only when a row's maximum passes it by the
+                // slack. No score of a lane's half passes m_ref + slack while its probabilities sum to at most 2^slack,
+                // so the row maximum is needed only when some lane's sum exceeds that (or overflowed)
+                make_p();
+                if (__ballot(!(ls <= RESCALE_LSUM))) {
+                    const float mt = row_max();
+                    const float d = fmaxf(fmaxf(mt, __shfl_xor(mt, 32)), 0.f);
+                    const float cf = fast_exp2(-d);
 #pragma unroll
-                for (int db = 0; db < 8; db++)
+                    for (int db = 0; db < 8; db++)
 #pragma unroll
-                    for (int i = 0; i < 16; i++) o[db][i] *= cf;
-                l_run *= cf;
-                m_ref += d;
+                        for (int i = 0; i < 16; i++) o[db][i] *= cf;
+                    l_run *= cf;
+                    m_ref += d;
 #pragma unroll
-                for (int i = 0; i < 16; i++) sc[i] -= d;
-            }
-            // ---- P^T (fp16) as B operands: MFMA m (keys 16m ..) takes S elements 8m .. 8m+7 ----
-            half8_t pf[2];
-            float ls = 0.f;
-#pragma unroll
-            for (int m = 0; m < 2; m++)
-#pragma unroll
-                for (int jj = 0; jj < 8; jj += 2) {
-                    const float p0 = fast_exp2(sc[8 * m + jj]), p1 = fast_exp2(sc[8 * m + jj + 1]);
-                    const half2_t ph = half2_t{(_Float16)p0, (_Float16)p1};
-                    pf[m][jj] = ph[0]; pf[m][jj + 1] = ph[1];
-                    ls = __builtin_amdgcn_fdot2(ph, ones, ls, false);
+                    for (int i = 0; i < 16; i++) sc[i] -= d;
+                    make_p();
                 }
+            }
             l_run += ls;
             // ---- O^T += V^T . P^T ----
             {   // V^T operands read FA_KPF MFMAs ahead (MFMA q: dims 32*(q/2) + r, keys 16*(q%2) ..)
