@@ -570,10 +570,10 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
         for (int a4 = 0; a4 < 4; a4++) {
             const int d = 32 * db + 8 * a4 + 4 * h32;
             float4 res = make_float4(o[db][4 * a4] * il, o[db][4 * a4 + 1] * il, o[db][4 * a4 + 2] * il, o[db][4 * a4 + 3] * il);
-            if (grow) {
+            if (grow) {  // sigmoid(g) by the hardware reciprocal (1 ulp; the output's tolerance is fp16-level)
                 const float4 g = *reinterpret_cast<const float4*>(grow + d);
-                res.x /= 1.f + __expf(-g.x); res.y /= 1.f + __expf(-g.y);
-                res.z /= 1.f + __expf(-g.z); res.w /= 1.f + __expf(-g.w);
+                res.x *= __builtin_amdgcn_rcpf(1.f + __expf(-g.x)); res.y *= __builtin_amdgcn_rcpf(1.f + __expf(-g.y));
+                res.z *= __builtin_amdgcn_rcpf(1.f + __expf(-g.z)); res.w *= __builtin_amdgcn_rcpf(1.f + __expf(-g.w));
             }
             *reinterpret_cast<float4*>(orow + d) = res;
         }
