@@ -683,9 +683,25 @@ __device__ __forceinline__ int lut16s(uint32_t idx) {
     // byte b from hi when bit 3 of index b is set: selector b + 4 picks byte b of the first perm operand
     return (int)__builtin_amdgcn_perm(hi, lo, 0x03020100u | ((idx >> 1) & 0x04040404u));
 }
+// 8 nibbles of x -> the 4 signed K codes of its even nibbles (ev) and of its odd nibbles (od). The low 3 bits of a
+// nibble index a half-table (bytes 0-7 of the two v_perm sources); bit 3 moves the final pick to the upper half,
+// selector byte b + 4. 13 VALU per 8 codes.
+__device__ __forceinline__ void k_codes8(uint32_t x, int& ev, int& od) {
+    const uint32_t t = x >> 4;
+    const uint32_t se = x & 0x07070707u, so = t & 0x07070707u;
+    uint32_t pe, po;  // (y & 0x04040404) | 0x03020100 in one v_and_or_b32 (the constants held in registers)
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(pe) : "v"(x >> 1), "v"(0x04040404u), "v"(0x03020100u));
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(po) : "v"(t >> 1), "v"(0x04040404u), "v"(0x03020100u));
+    const uint32_t le = __builtin_amdgcn_perm(SK1, SK0, se), he = __builtin_amdgcn_perm(SK3, SK2, se);
+    const uint32_t lo = __builtin_amdgcn_perm(SK1, SK0, so), ho = __builtin_amdgcn_perm(SK3, SK2, so);
+    ev = (int)__builtin_amdgcn_perm(he, le, pe);
+    od = (int)__builtin_amdgcn_perm(ho, lo, po);
+}
 __device__ __forceinline__ int4_t_ k_codes(uint2 x) {  // 16 nibbles -> the MFMA operand (even, odd, even, odd)
-    return int4_t_{lut16s(x.x & 0x0f0f0f0fu), lut16s((x.x >> 4) & 0x0f0f0f0fu),
-                   lut16s(x.y & 0x0f0f0f0fu), lut16s((x.y >> 4) & 0x0f0f0f0fu)};
+    int a, b, c, d;
+    k_codes8(x.x, a, b);
+    k_codes8(x.y, c, d);
+    return int4_t_{a, b, c, d};
 }
 
 // ---- gqa_wst_kernel: TurboQuant cache, one query token per workgroup, on gqa_ws_kernel's warp-specialised pipeline.
