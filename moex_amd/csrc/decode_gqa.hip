@@ -1,7 +1,7 @@
 // Split-K GQA decode / MTP-verify attention on gfx950 (replaces attn_gqa_k, kernels.cuh:1740-1844).
 //
 // One workgroup = (kv head, key split, group of query tokens); the 8 query heads of the group share every K/V byte.
-// int8 cache: gqa_ws_kernel for a single query token (warp-specialised: producer wavefronts stream K/V into LDS,
+// int8 cache: gqa_ws1_kernel for a single query token (warp-specialised: producer wavefronts stream K/V into LDS,
 // consumer wavefronts compute), gqa_wsp_kernel for MTP-verify windows (token pairs on the same pipeline).
 // gqa_wst_kernel serves the TurboQuant cache, one token per workgroup on the same pipeline, the codes unpacked on the
 // way. The partial written per (token, head, split) is {m (log2 units), l, acc[256]}.
@@ -88,13 +88,14 @@ __device__ __forceinline__ float sum_x32(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// ---- gqa_ws_kernel: one query token (plain decode), warp-specialised. A vector-memory instruction waits at issue
-// while the CU's request queue is full, which under the chip-wide K/V stream is most of the time; a wavefront that
-// both loads and computes therefore cannot compute while its next chunk goes out. Here waves 4..7 only move rows
-// (global_load_lds: K, V and the scales of a chunk into one of two LDS stages) and waves 0..3 only compute, one per
-// SIMD. Each consumer owns 32 keys of every chunk and keeps its own running maximum, sum and O over all 256 dims, so
-// the chunk loop needs no exchange between consumers: one barrier per chunk hands a landed stage to the consumers
-// and the other stage back to the producers. The four consumer states merge once at the end.
+// ---- The warp-specialised decode pipeline (gqa_ws1_kernel, gqa_wsp_kernel, gqa_wst_kernel). A vector-memory
+// instruction waits at issue while the CU's request queue is full, which under the chip-wide K/V stream is most of
+// the time; a wavefront that both loads and computes therefore cannot compute while its next chunk goes out. Here
+// waves 4..7 only move rows (global_load_lds: K, V and the scales of a chunk into a ring of LDS stages) and waves
+// 0..3 only compute, one per SIMD. Each consumer owns a fixed slice of the keys of every chunk and keeps its own
+// running maximum, sum and O over all 256 dims, so the chunk loop needs no exchange between consumers: one barrier
+// per chunk hands a landed stage to the consumers and a consumed one back to the producers. The four consumer states
+// merge once at the end.
 //   K stage: row r holds its 16-byte piece p in slot p ^ (r % 16), so the 16 lanes of a ds_read_b128 (16 rows, one
 //            piece) hit 16 different slots.
 //   V stage: row r holds its 16-byte piece p in slot p ^ 4 * ((r / 4) % 4), so the four lane groups of a pass-2 read
@@ -114,7 +115,7 @@ static_assert(WS_CH % 8 == 0 && WS_CH <= 128, "chunk shape");
 static_assert(WS_NC * GQ * AHD * 4 <= WS_STAGE, "the consumer merge fits in stage 0");
 static_assert(WS_LDS <= 160 * 1024, "LDS");
 
-// The producer side of gqa_ws_kernel / gqa_wsp_kernel: chunk c (keys [clo(c), chi(c)), chunk 0 the short one) ->
+// The producer side of gqa_wsp_kernel (128-key chunks, two stages): chunk c (keys [clo(c), chi(c)), chunk 0 the short one) ->
 // stage c % WS_NS. Producers 0, 1 move the K rows, 2, 3 the V rows (WS_CH/8 instructions of 4 rows each); producer j
 // also moves 64 scales (ks for j < 2, else vs; 4 bytes a lane). Rows past the chunk repeat its last row: their P is 0.
 // One chunk is in flight at a time, issued the moment a stage frees: chunks issued together are served interleaved,
@@ -151,34 +152,79 @@ __device__ __forceinline__ void ws_producer(unsigned char* smem, const moex_kv_c
     __syncthreads();
 }
 
-__global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws_kernel(const float* __restrict__ qo, moex_kv_cache kv,
-                                                                        int H, const int* __restrict__ pos_d,
-                                                                        int max_t, float* __restrict__ part, int T,
-                                                                        int ns) {
+// ---- gqa_ws1_kernel: one query token, chunks of 64 keys with three in flight. A pure DMA stream of the decode's size
+// measured 5.35-5.46 TB/s with one 64 KB chunk in flight per CU and 5.7-5.8 TB/s with 96-128 KB in flight, and a
+// smaller last chunk shortens the tail; so the chunk is 64 keys (33 KB) in a ring of four LDS stages, and consumer w
+// owns keys 16w .. 16w + 15 of every chunk. The stage layouts, the Q.K fixed-point digits, the P hi / lo rows and the
+// lazy rescale are those of the pipeline above; P.V runs on v_mfma_f32_16x16x16_f16, whose A operand is exactly the lane's
+// 4 probabilities (keys 4g .. 4g + 3) and whose B operand is 4 keys of one dim (two v_perm of biased V bytes).
+constexpr int W1_CH = 16 * WS_NC;                     // keys per chunk: 16 per consumer
+constexpr int W1_NS = 4;                              // stages: three chunks in flight, one being computed
+constexpr int W1_KB = W1_CH * AHD;                    // K rows of a stage; the V rows follow, then ks[64], vs[64]
+constexpr int W1_STAGE = 2 * W1_CH * AHD + 2 * W1_CH * 4;
+constexpr int W1_LDS = W1_NS * W1_STAGE;
+static_assert(WS_NC * GQ * AHD * 4 <= W1_LDS, "the consumer merge fits in the stages");
+static_assert(W1_LDS <= 160 * 1024, "LDS");
+
+__global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws1_kernel(const float* __restrict__ qo, moex_kv_cache kv,
+                                                                         int H, const int* __restrict__ pos_d,
+                                                                         int max_t, float* __restrict__ part, int ns) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float cm[WS_NC][GQ], cl[WS_NC][GQ];
     const int nb = gridDim.x, w_id = xcd_work_id(blockIdx.x, nb);
-    const int tok = w_id % T, s = (w_id / T) % ns, kvh = w_id / (T * ns);
-    const int pos0 = *pos_d, Tmax = pos0 + T;
+    const int s = w_id % ns, kvh = w_id / ns;
+    const int pos0 = *pos_d, Tmax = pos0 + 1;
     const int L = (Tmax + ns - 1) / ns, lo = s * L;
-    const int hi = min(pos0 + tok + 1, lo + L);  // keys [lo, hi) of this split that the token sees
-    const int nch = hi > lo ? (hi - lo + WS_CH - 1) / WS_CH : 0;
-    // chunk 0 is the short one (the remainder of the split over WS_CH), so the first chunk lands soonest
-    const int first = hi > lo ? hi - lo - (nch - 1) * WS_CH : 0;
-    auto clo = [&](int c) { return c == 0 ? lo : lo + first + (c - 1) * WS_CH; };  // chunk c is keys [clo, chi)
-    auto chi = [&](int c) { return c == 0 ? lo + first : lo + first + c * WS_CH; };
+    const int hi = min(Tmax, lo + L);  // keys [lo, hi) of this split
+    const int nch = hi > lo ? (hi - lo + W1_CH - 1) / W1_CH : 0;
+    const int first = hi > lo ? hi - lo - (nch - 1) * W1_CH : 0;  // chunk 0 is the short one
+    auto clo = [&](int c) { return c == 0 ? lo : lo + first + (c - 1) * W1_CH; };
+    auto chi = [&](int c) { return c == 0 ? lo + first : lo + first + c * W1_CH; };
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 4, m16 = lane & 15;
     const size_t rbase = (size_t)kvh * max_t;
 
     if (wv >= WS_NC) {
-        ws_producer(smem, kv, rbase, wv - WS_NC, lane, lo, first, nch);
+        // ---- producers: 0, 1 move the K rows (8 instructions of 4 rows each), 2, 3 the V rows; 0 also the 64 K
+        // scales, 2 the V scales (4 bytes a lane). Rows past the chunk repeat its last row (their P is 0). ----
+        const int pw = wv - WS_NC;
+        const int8_t* src = (pw < 2 ? kv.k : kv.v) + rbase * AHD;
+        const float* ssrc = (pw < 2 ? kv.ks : kv.vs) + rbase;
+        const int r4 = lane >> 4, sl = lane & 15;
+        auto issue = [&](int c) {
+            const int c0 = clo(c), ce = chi(c);
+            unsigned char* st = smem + (c % W1_NS) * W1_STAGE;
+            unsigned char* sb = st + (pw < 2 ? 0 : W1_KB);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = 8 * (pw & 1) + u, r = 4 * i + r4;  // instruction i covers rows 4i .. 4i+3
+                const int piece = pw < 2 ? sl ^ (r & 15) : sl ^ (4 * (i & 3));
+                __builtin_amdgcn_global_load_lds((gptr_t)(src + (size_t)min(c0 + r, ce - 1) * AHD + 16 * piece),
+                                                 (lptr_t)(sb + i * 1024), 16, 0, 0);
+            }
+            if (!(pw & 1))
+                __builtin_amdgcn_global_load_lds((gptr_t)(ssrc + min(c0 + lane, ce - 1)),
+                                                 (lptr_t)(st + 2 * W1_KB + (pw < 2 ? 0 : 4 * W1_CH)), 4, 0, 0);
+        };
+        for (int c = 0; c < W1_NS - 1 && c < nch; c++) issue(c);
+        for (int c = 0; c < nch; c++) {
+            // chunk c has landed when at most the chunks issued after it are in flight (9 or 8 instructions each)
+            const int after = min(nch - 1 - c, W1_NS - 2);
+            if (pw & 1) { if (after >= 2) wait_vm<16>(); else if (after == 1) wait_vm<8>(); else wait_vm<0>(); }
+            else { if (after >= 2) wait_vm<18>(); else if (after == 1) wait_vm<9>(); else wait_vm<0>(); }
+            // chunk c is in stage c % 4 and the consumers are done with chunk c - 1: its stage takes chunk c + 3.
+            // Not __syncthreads: that would also wait for the chunks still in flight.
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (c + W1_NS - 1 < nch) issue(c + W1_NS - 1);
+        }
+        __syncthreads();
+        __syncthreads();
     } else {
         // ---- consumers. Query digits in registers: column m16 of the Q.K MFMA is head m16 / 2 (every head twice);
         // lane (g, m16) holds dims 64 ks + 16 g .. +15 of it, the 4 lanes of a column together hold its 256 dims ----
         int4_t_ qd[3][4];
         float qs;
         {
-            const float* qrow = qo + ((size_t)tok * H + kvh * GQ + (m16 >> 1)) * AHD + 16 * g;
+            const float* qrow = qo + ((size_t)kvh * GQ + (m16 >> 1)) * AHD + 16 * g;
             float4 qv4[16];
 #pragma unroll
             for (int ks = 0; ks < 4; ks++)
@@ -212,77 +258,63 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws_kernel(const f
         float4_t o[16];
 #pragma unroll
         for (int J = 0; J < 16; J++) o[J] = float4_t{0.f, 0.f, 0.f, 0.f};
-        float mref = -INFINITY, lacc = 0.f, vmax = 0.f;  // reference maximum and sum of column m16, V-scale maximum
-        float xsum = 0.f;                                 // sum of P * vs * 2^sig of this lane's keys: the V bias
-        int sig = 0;                                      // O is held times 2^sig
-        const int kb = 32 * wv;                           // this consumer's keys kb .. kb+31 of every chunk
+        float mref = -INFINITY, lacc = 0.f, vmax = 0.f, xsum = 0.f;
+        int sig = 0;
+        const int kb = 16 * wv;  // this consumer's keys kb .. kb + 15 of every chunk
         for (int c = 0; c < nch; c++) {
-            __syncthreads();  // chunk c is in stage c % WS_NS
+            __syncthreads();  // chunk c is in stage c % 4
             const int c0 = clo(c), ce = chi(c);
             if (c0 + kb >= ce) continue;
-            const unsigned char* sb = smem + (c % WS_NS) * WS_STAGE;
-            const float* sks = reinterpret_cast<const float*>(sb + 2 * WS_KB);
-            const float* svs = sks + 128;
-            float ksv[8], vv[8];
-            {
-                const float4 a0 = *reinterpret_cast<const float4*>(sks + kb + 4 * g);
-                const float4 a1 = *reinterpret_cast<const float4*>(sks + kb + 16 + 4 * g);
-                const float4 b0 = *reinterpret_cast<const float4*>(svs + kb + 4 * g);
-                const float4 b1 = *reinterpret_cast<const float4*>(svs + kb + 16 + 4 * g);
-                ksv[0] = a0.x; ksv[1] = a0.y; ksv[2] = a0.z; ksv[3] = a0.w;
-                ksv[4] = a1.x; ksv[5] = a1.y; ksv[6] = a1.z; ksv[7] = a1.w;
-                vv[0] = b0.x; vv[1] = b0.y; vv[2] = b0.z; vv[3] = b0.w;
-                vv[4] = b1.x; vv[5] = b1.y; vv[6] = b1.z; vv[7] = b1.w;
+            const unsigned char* sb = smem + (c % W1_NS) * W1_STAGE;
+            const float* sks = reinterpret_cast<const float*>(sb + 2 * W1_KB);
+            const float* svs = sks + W1_CH;
+            const float4 ksv = *reinterpret_cast<const float4*>(sks + kb + 4 * g);
+            const float4 vv4 = *reinterpret_cast<const float4*>(svs + kb + 4 * g);
+            float vv[4] = {vv4.x, vv4.y, vv4.z, vv4.w};
+            // ---- scores of keys kb + 4 g + i for column m16: 12 MFMAs in 3 chains ----
+            int4_t_ acc[3];
+#pragma unroll
+            for (int dig = 0; dig < 3; dig++) acc[dig] = int4_t_{0, 0, 0, 0};
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                const int4_t_ a = *reinterpret_cast<const int4_t_*>(sb + (kb + m16) * AHD + 16 * ((4 * ks + g) ^ m16));
+#pragma unroll
+                for (int dig = 0; dig < 3; dig++)
+                    acc[dig] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qd[dig][ks], acc[dig], 0, 0, 0);
             }
-            // ---- scores of keys kb + 16 (j / 4) + 4 g + j % 4 for column m16: the 24 MFMAs (6 independent chains)
-            // go out before any score is formed ----
-            int4_t_ acc[2][3];
-#pragma unroll
-            for (int grp = 0; grp < 2; grp++)
-#pragma unroll
-                for (int dig = 0; dig < 3; dig++) acc[grp][dig] = int4_t_{0, 0, 0, 0};
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-                for (int grp = 0; grp < 2; grp++) {
-                    const int4_t_ a = *reinterpret_cast<const int4_t_*>(sb + (kb + 16 * grp + m16) * AHD + 16 * ((4 * ks + g) ^ m16));
-#pragma unroll
-                    for (int dig = 0; dig < 3; dig++)
-                        acc[grp][dig] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qd[dig][ks], acc[grp][dig], 0, 0, 0);
-                }
-            float sc[8];
-#pragma unroll
-            for (int grp = 0; grp < 2; grp++)
+            float sc[4];
+            {
+                const float kq[4] = {ksv.x, ksv.y, ksv.z, ksv.w};
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const float raw = ((float)acc[grp][2][i] * 65536.f + (float)acc[grp][1][i] * 256.f) + (float)acc[grp][0][i];
-                    sc[4 * grp + i] = raw * (ksv[4 * grp + i] * qs);
+                    const float raw = ((float)acc[2][i] * 65536.f + (float)acc[1][i] * 256.f) + (float)acc[0][i];
+                    sc[i] = raw * (kq[i] * qs);
                 }
+            }
             float vm;
-            if (c0 + kb + 32 <= ce) {  // all 32 keys valid (every chunk but the first)
-                vm = fmaxf(fmaxf(fmaxf(vv[0], vv[1]), fmaxf(vv[2], vv[3])), fmaxf(fmaxf(vv[4], vv[5]), fmaxf(vv[6], vv[7])));
+            if (c0 + kb + 16 <= ce) {
+                vm = fmaxf(fmaxf(vv[0], vv[1]), fmaxf(vv[2], vv[3]));
             } else {
                 vm = 0.f;
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const bool ok = c0 + kb + 16 * (j >> 2) + 4 * g + (j & 3) < ce;
-                    sc[j] = ok ? sc[j] : -INFINITY;
-                    vm = ok ? fmaxf(vm, vv[j]) : vm;
+                for (int i = 0; i < 4; i++) {
+                    const bool ok = c0 + kb + 4 * g + i < ce;
+                    sc[i] = ok ? sc[i] : -INFINITY;
+                    vm = ok ? fmaxf(vm, vv[i]) : vm;
                 }
             }
-            float M = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
-            // the reductions over the lane groups only when some lane's own keys pass a bound (rare). A lane's
-            // own maximum passes m_ref + slack exactly when its group's does, and V scales below 2^(7 - sig)
-            // cannot move the exponent: the same decisions as with the reduced values, bit for bit
+            float M = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+            // the reductions over the lane groups only when some lane's own keys pass a bound (rare). A lane's own
+            // maximum passes m_ref + slack exactly when its group's does, and V scales below 2^(7 - sig) cannot move
+            // the exponent: the same decisions as with the reduced values, bit for bit
             if (__builtin_amdgcn_ballot_w64(M > mref + WS_SLACK || vm >= ldexpf(1.f, 7 - sig)) != 0) {
                 M = max_x32(max_x16(M));
-                vm = max_x32(max_x16(vm));  // every column of a lane group holds the same keys
-                // ---- lazy rescale: new reference maximum / V-scale exponent ----
+                vm = max_x32(max_x16(vm));
                 const float nref = M > mref + WS_SLACK ? M : mref;
                 const float fown = ex2d(mref, nref);
                 vmax = fmaxf(vmax, vm);
                 int ev = 0;
-                if (vmax > 0.f) (void)frexpf(vmax, &ev);  // vmax < 2^ev: p * vs * 2^(7 - ev) < 2^(7 + WS_SLACK)
+                if (vmax > 0.f) (void)frexpf(vmax, &ev);
                 const int nsig = 7 - ev;
                 if (__builtin_amdgcn_ballot_w64(fown != 1.f) != 0 || nsig != sig) {
                     const float sf = ldexpf(1.f, nsig - sig);
@@ -299,52 +331,49 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws_kernel(const f
                     sig = nsig;
                 }
             }
-            // ---- P = 2^(s - mref) * vs * 2^sig as fp16 hi + lo: row 2h + 1 of the P operand is the lo part of row 2h,
-            // formed by the lane pair m16 = 2h (hi), 2h + 1 (lo), each lane's 8 keys its own A operand ----
-            half8_t pa;
+            // ---- P = 2^(s - mref) * vs * 2^sig: row m16 of the A operand (hi for even m16, lo for odd), keys 4g .. ----
+            half4_t pa;
             {
                 const float vsc = ldexpf(1.f, sig);
-                half8_t ph;
                 float ls = 0.f, xs = 0.f;
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const float p = fast_exp2(sc[j] - mref);  // 0 for masked keys (mref is finite once a key is seen)
+                for (int i = 0; i < 4; i++) {
+                    const float p = fast_exp2(sc[i] - mref);
                     ls += p;
-                    const float x = p * (vv[j] * vsc);
+                    const float x = p * (vv[i] * vsc);
                     xs += x;
                     const _Float16 h = (_Float16)x;
-                    ph[j] = (m16 & 1) ? (_Float16)(x - (float)h) : h;
+                    pa[i] = (m16 & 1) ? (_Float16)(x - (float)h) : h;
                 }
                 lacc += ls;
                 xsum += xs;
-                pa = ph;
             }
-            // ---- O^T += P . V over this consumer's 32 keys, all 256 dims ----
-
-            const unsigned char* Vs = sb + WS_KB;
+            // ---- O^T += P . V: B operand = 4 keys of one dim, biased bytes as fp16 subnormals ----
+            const unsigned char* Vs = sb + W1_KB;
 #pragma unroll
             for (int pc = 0; pc < 4; pc++) {
                 const int rd = 16 * ((4 * pc + (m16 >> 2)) ^ (4 * g)) + 4 * (m16 & 3);
-                uint32_t r[8];
+                uint32_t r[4];
 #pragma unroll
-                for (int j = 0; j < 8; j++)
-                    r[j] = *reinterpret_cast<const uint32_t*>(Vs + (kb + 16 * (j >> 2) + 4 * g + (j & 3)) * AHD + rd);
+                for (int j = 0; j < 4; j++)
+                    r[j] = *reinterpret_cast<const uint32_t*>(Vs + (kb + 4 * g + j) * AHD + rd) ^ 0x80808080u;
 #pragma unroll
-                for (int j = 0; j < 8; j++) r[j] ^= 0x80808080u;  // biased codes
-#pragma unroll
-                for (int jt = 0; jt < 4; jt++)
-                    o[4 * pc + jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, bsub8(r, jt), o[4 * pc + jt], 0, 0, 0);
+                for (int jt = 0; jt < 4; jt++) {
+                    const uint32_t sel = (uint32_t)jt | 0x0c00u | ((uint32_t)(4 + jt) << 16) | 0x0c000000u;
+                    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                    const u32x2 u = {__builtin_amdgcn_perm(r[1], r[0], sel), __builtin_amdgcn_perm(r[3], r[2], sel)};
+                    o[4 * pc + jt] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(half4_t, u),
+                                                                            o[4 * pc + jt], 0, 0, 0);
+                }
             }
         }
-        // ---- merge the four consumers: m, l per head, then O rows scaled to the common maximum ----
+        // ---- merge the four consumers: m, l per head, then O rows (hi + lo) scaled to the common maximum ----
         const float l = sum_x32(sum_x16(lacc));
-        __syncthreads();  // every consumer is past its last chunk: stage 0 is free
+        __syncthreads();  // every consumer is past its last chunk: the stages are free
         if (lane < 16 && !(lane & 1)) { cm[wv][lane >> 1] = mref; cl[wv][lane >> 1] = l; }
         __syncthreads();
-        // rows 4g .. 4g+3 of the O tiles are hi, lo of head 2g and hi, lo of head 2g + 1
         float* Ow = reinterpret_cast<float*>(smem);  // [consumer][head][256]
         const float un = ldexpf(1.f, -sig);
-        // the V operands were (v + 128) * 2^-24: O = 2^24 o - 128 * sum(P * vs * 2^sig) per head
         const float xb = sum_x32(sum_x16(xsum)) * VBIAS;
 #pragma unroll
         for (int e = 0; e < 2; e++) {
@@ -353,22 +382,18 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws_kernel(const f
 #pragma unroll
             for (int w = 1; w < WS_NC; w++) Mh = fmaxf(Mh, cm[w][h]);
             const float f = ex2d(cm[wv][h], Mh) * un, b = __shfl(xb, 2 * h);
-            float4 y[4];
 #pragma unroll
             for (int pc = 0; pc < 4; pc++) {
                 float t[4];
 #pragma unroll
                 for (int jt = 0; jt < 4; jt++)
                     t[jt] = fmaf(o[4 * pc + jt][2 * e] + o[4 * pc + jt][2 * e + 1], 16777216.f, -b) * f;
-                y[pc] = make_float4(t[0], t[1], t[2], t[3]);
+                *reinterpret_cast<float4*>(Ow + (wv * GQ + h) * AHD + 64 * pc + 4 * m16) =
+                    make_float4(t[0], t[1], t[2], t[3]);
             }
-#pragma unroll
-            for (int pc = 0; pc < 4; pc++)
-                *reinterpret_cast<float4*>(Ow + (wv * GQ + h) * AHD + 64 * pc + 4 * m16) = y[pc];
         }
     }
     __syncthreads();
-    // ---- partial of the split: item = (head, dims 4 (item % 64) .. +3) ----
     for (int it = tid; it < GQ * 64; it += 64 * (WS_NC + WS_NP)) {
         const float* Ow = reinterpret_cast<const float*>(smem);
         const int h = it >> 6, d4 = 4 * (it & 63);
@@ -378,21 +403,21 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws_kernel(const f
             const float4 b = *reinterpret_cast<const float4*>(Ow + (w * GQ + h) * AHD + d4);
             a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
         }
-        *reinterpret_cast<float4*>(part_acc(part, tok, kvh * GQ + h, s, H, ns) + d4) = a;
+        *reinterpret_cast<float4*>(part_acc(part, 0, kvh * GQ + h, s, H, ns) + d4) = a;
         if ((it & 63) == 0) {
             float Mh = cm[0][h], lh = 0.f;
 #pragma unroll
             for (int w = 1; w < WS_NC; w++) Mh = fmaxf(Mh, cm[w][h]);
 #pragma unroll
             for (int w = 0; w < WS_NC; w++) lh += cl[w][h] * ex2d(cm[w][h], Mh);
-            float* ml = part_ml(part, tok, kvh * GQ + h, s, H, ns, T);
-            ml[0] = Mh;  // -inf when the token has no key in this split
+            float* ml = part_ml(part, 0, kvh * GQ + h, s, H, ns, 1);
+            ml[0] = Mh;  // -inf when the split has no key
             ml[1] = lh;
         }
     }
 }
 
-// ---- gqa_wsp_kernel<NPR>: MTP-verify windows, NPR token pairs (up to 4 tokens) per workgroup, on gqa_ws_kernel's
+// ---- gqa_wsp_kernel<NPR>: MTP-verify windows, NPR token pairs (up to 4 tokens) per workgroup, on the
 // pipeline (same producers, stages and chunk order). Consumer w serves pair w % NPR and owns 32 NPR keys of every
 // chunk (part w / NPR). Column m of the Q.K MFMA is (token m / 8 of the pair, head m % 8), so one set of MFMAs scores
 // both tokens. P enters P.V as two A operands, its hi and lo fp16 parts (row = column), accumulated into the same O
@@ -704,13 +729,13 @@ __device__ __forceinline__ int4_t_ k_codes(uint2 x) {  // 16 nibbles -> the MFMA
     return int4_t_{a, b, c, d};
 }
 
-// ---- gqa_wst_kernel: TurboQuant cache, one query token per workgroup, on gqa_ws_kernel's warp-specialised pipeline.
+// ---- gqa_wst_kernel: TurboQuant cache, one query token per workgroup, on the warp-specialised pipeline.
 // Producers move each 128-key chunk by DMA (36 transfers per chunk, 4-byte ones for the norms so every key index is
 // clamped): the K nibble rows (row r keeps 16-byte piece p in slot p ^ ((r / 2) % 8), so the 8-byte fragment reads of
 // 16 rows at a 128-byte stride hit distinct banks) and the K and V half norms into one of three K stages, the raw V
 // rows (96 bytes, packed) into one of two raw V buffers. Producer j moves the raw V rows of keys 32j .. 32j + 31 and,
-// once they have landed, unpacks their 3-bit codes into consumer j's int8 code area for that chunk (gqa_ws_kernel's
-// V layout, two areas per consumer), so the unpacking runs beside the consumers' work on the previous chunk. Two
+// once they have landed, unpacks their 3-bit codes into consumer j's int8 code area for that chunk (the int8
+// kernels' V layout, two areas per consumer), so the unpacking runs beside the consumers' work on the previous chunk. Two
 // chunks are in flight: chunk c + 2 is issued at the barrier that starts chunk c. Q.K puts digit 2 of the 8 heads
 // (columns 0-7) and digit 0 (columns 8-15) into one MFMA and digit 1 (both halves) into a second, per 128-dim half;
 // one row_ror:8 DPP move gives each lane of a head's pair the digit its partner holds, digits 1 and 0 are added
@@ -1046,7 +1071,7 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
                                                                          o[4 * pc + jt], 0, 0, 0);
             }
         }
-        // ---- merge the four consumers (as gqa_ws_kernel) ----
+        // ---- merge the four consumers: m, l per head, then O rows (hi + lo) scaled to the common maximum ----
         const float l = sum_x32(sum_x16(lacc));
         __syncthreads();  // every consumer is past its last chunk: the stages are free
         if (lane < 8) { cm[wv][lane] = mref; cl[wv][lane] = l; }
@@ -1149,12 +1174,13 @@ void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos
     } else {
         if (T == 1) {
             static bool once = [] {
-                MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_ws_kernel),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, WS_LDS));
+                MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_ws1_kernel),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, W1_LDS));
                 return true;
             }();
             (void)once;
-            hipLaunchKernelGGL(gqa_ws_kernel, dim3(KV * ns), dim3(64 * (WS_NC + WS_NP)), WS_LDS, st, qo, kv, H, pos_d, max_t, part, T, ns);
+            hipLaunchKernelGGL(gqa_ws1_kernel, dim3(KV * ns), dim3(64 * (WS_NC + WS_NP)), W1_LDS, st, qo, kv, H, pos_d,
+                               max_t, part, ns);
         }
         else if (T == 2) launch_wsp<1>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
         else launch_wsp<2>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
