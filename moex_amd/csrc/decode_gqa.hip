@@ -105,48 +105,56 @@ __device__ __forceinline__ float sum_x32(float x) {
 //            than WS_SLACK (log2 units; P then stays below 2^WS_SLACK) or the V scale exponent grows.
 constexpr int WS_NC = 4;                              // consumer wavefronts (waves 0 .. WS_NC-1)
 constexpr int WS_NP = 4;                              // producer wavefronts (the next WS_NP waves)
-constexpr int WS_CH = 32 * WS_NC;                     // keys per chunk: 32 per consumer
-constexpr int WS_NS = 2;                              // LDS stages: one chunk streams while one is computed
-constexpr int WS_KB = WS_CH * AHD;                    // K rows of a stage; the V rows follow, then ks[128], vs[128]
-constexpr int WS_STAGE = 2 * WS_CH * AHD + 2 * 128 * 4;
-constexpr int WS_LDS = WS_NS * WS_STAGE;  // the two stages
+constexpr int WS_CH = 32 * WS_NC;                     // keys per chunk of the turbo kernel: 32 per consumer
 constexpr float WS_SLACK = 8.f;
-static_assert(WS_CH % 8 == 0 && WS_CH <= 128, "chunk shape");
-static_assert(WS_NC * GQ * AHD * 4 <= WS_STAGE, "the consumer merge fits in stage 0");
-static_assert(WS_LDS <= 160 * 1024, "LDS");
 
-// The producer side of gqa_wsp_kernel (128-key chunks, two stages): chunk c (keys [clo(c), chi(c)), chunk 0 the short one) ->
-// stage c % WS_NS. Producers 0, 1 move the K rows, 2, 3 the V rows (WS_CH/8 instructions of 4 rows each); producer j
-// also moves 64 scales (ks for j < 2, else vs; 4 bytes a lane). Rows past the chunk repeat its last row: their P is 0.
-// One chunk is in flight at a time, issued the moment a stage frees: chunks issued together are served interleaved,
-// so a deeper queue only delays each of them (and the query the consumers wait for). Takes part in the nch + 2
+// The producer side of gqa_ws1_kernel / gqa_wsp_kernel: chunks of CH keys (keys [clo(c), chi(c)), chunk 0 the short
+// one) in a ring of NS LDS stages, NS - 1 chunks in flight. A stage holds the K rows, the V rows, then ks[CH] and
+// vs[CH]. Producers 0, 1 move the K rows, 2, 3 the V rows (CH / 8 instructions of 4 rows each); with 128-key chunks
+// each producer also moves 64 scales (ks for 0, 1, vs for 2, 3), with 64-key chunks producers 0 and 2 move all 64
+// (4 bytes a lane). Rows past the chunk repeat its last row: their P is 0. Chunk c + NS - 1 is issued at the barrier
+// that hands chunk c to the consumers (its stage held chunk c - 1, now consumed); the producers end each chunk with a
+// bare s_barrier, as __syncthreads would also wait for the chunks still in flight. Takes part in the nch + 2
 // barriers of the chunk loop and the consumer merge.
-__device__ __forceinline__ void ws_producer(unsigned char* smem, const moex_kv_cache& kv, size_t rbase, int pw, int lane,
-                                            int lo, int first, int nch) {
+template <int CH>
+constexpr int ring_stage() { return 2 * CH * AHD + 2 * CH * 4; }
+
+template <int CH, int NS>
+__device__ __forceinline__ void ring_producer(unsigned char* smem, const moex_kv_cache& kv, size_t rbase, int pw,
+                                              int lane, int lo, int first, int nch) {
+    static_assert((CH == 64 || CH == 128) && NS >= 2 && NS <= 4, "ring shape");
+    constexpr int KB = CH * AHD, STAGE = ring_stage<CH>(), NI = CH / 8;
+    constexpr bool SC_ALL = CH == 128;
+    const bool sc = SC_ALL || !(pw & 1);
     const int8_t* src = (pw < 2 ? kv.k : kv.v) + rbase * AHD;
     const float* ssrc = (pw < 2 ? kv.ks : kv.vs) + rbase;
     const int r4 = lane >> 4, sl = lane & 15;
     auto issue = [&](int c) {
-        const int c0 = c == 0 ? lo : lo + first + (c - 1) * WS_CH, ce = c == 0 ? lo + first : lo + first + c * WS_CH;
-        unsigned char* st = smem + (c % WS_NS) * WS_STAGE;
-        unsigned char* sb = st + (pw < 2 ? 0 : WS_KB);
+        const int c0 = c == 0 ? lo : lo + first + (c - 1) * CH, ce = c == 0 ? lo + first : lo + first + c * CH;
+        unsigned char* st = smem + (c % NS) * STAGE;
+        unsigned char* sb = st + (pw < 2 ? 0 : KB);
 #pragma unroll
-        for (int u = 0; u < WS_CH / 8; u++) {
-            const int i = (WS_CH / 8) * (pw & 1) + u, r = 4 * i + r4;  // instruction i covers rows 4i .. 4i+3
+        for (int u = 0; u < NI; u++) {
+            const int i = NI * (pw & 1) + u, r = 4 * i + r4;  // instruction i covers rows 4i .. 4i+3
             const int piece = pw < 2 ? sl ^ (r & 15) : sl ^ (4 * (i & 3));
-            const int key = min(c0 + r, ce - 1);
-            __builtin_amdgcn_global_load_lds((gptr_t)(src + (size_t)key * AHD + 16 * piece), (lptr_t)(sb + i * 1024), 16,
-                                             0, 0);
+            __builtin_amdgcn_global_load_lds((gptr_t)(src + (size_t)min(c0 + r, ce - 1) * AHD + 16 * piece),
+                                             (lptr_t)(sb + i * 1024), 16, 0, 0);
         }
-        const int key = min(c0 + 64 * (pw & 1) + lane, ce - 1);
-        __builtin_amdgcn_global_load_lds((gptr_t)(ssrc + key), (lptr_t)(st + 2 * WS_KB + (pw < 2 ? 0 : 512) + 256 * (pw & 1)),
-                                         4, 0, 0);
+        if (sc) {
+            const int k0 = SC_ALL ? 64 * (pw & 1) : 0;
+            __builtin_amdgcn_global_load_lds((gptr_t)(ssrc + min(c0 + k0 + lane, ce - 1)),
+                                             (lptr_t)(st + 2 * KB + (pw < 2 ? 0 : 4 * CH) + 4 * k0), 4, 0, 0);
+        }
     };
-    if (nch > 0) issue(0);
+    for (int c = 0; c < NS - 1 && c < nch; c++) issue(c);
     for (int c = 0; c < nch; c++) {
-        wait_vm<0>();     // chunk c has landed
-        __syncthreads();  // ... and the consumers are done with chunk c - 1: its stage takes chunk c + 1
-        if (c + 1 < nch) issue(c + 1);
+        // chunk c has landed when at most the chunks issued after it are in flight (NI or NI + 1 instructions each)
+        const int after = min(nch - 1 - c, NS - 2);
+        if (after == 0) wait_vm<0>();
+        else if (sc) { if (after == 1) wait_vm<NI + 1>(); else wait_vm<2 * (NI + 1)>(); }
+        else { if (after == 1) wait_vm<NI>(); else wait_vm<2 * NI>(); }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (c + NS - 1 < nch) issue(c + NS - 1);
     }
     __syncthreads();
     __syncthreads();
@@ -161,7 +169,7 @@ __device__ __forceinline__ void ws_producer(unsigned char* smem, const moex_kv_c
 constexpr int W1_CH = 16 * WS_NC;                     // keys per chunk: 16 per consumer
 constexpr int W1_NS = 4;                              // stages: three chunks in flight, one being computed
 constexpr int W1_KB = W1_CH * AHD;                    // K rows of a stage; the V rows follow, then ks[64], vs[64]
-constexpr int W1_STAGE = 2 * W1_CH * AHD + 2 * W1_CH * 4;
+constexpr int W1_STAGE = ring_stage<W1_CH>();
 constexpr int W1_LDS = W1_NS * W1_STAGE;
 static_assert(WS_NC * GQ * AHD * 4 <= W1_LDS, "the consumer merge fits in the stages");
 static_assert(W1_LDS <= 160 * 1024, "LDS");
@@ -184,40 +192,7 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws1_kernel(const 
     const size_t rbase = (size_t)kvh * max_t;
 
     if (wv >= WS_NC) {
-        // ---- producers: 0, 1 move the K rows (8 instructions of 4 rows each), 2, 3 the V rows; 0 also the 64 K
-        // scales, 2 the V scales (4 bytes a lane). Rows past the chunk repeat its last row (their P is 0). ----
-        const int pw = wv - WS_NC;
-        const int8_t* src = (pw < 2 ? kv.k : kv.v) + rbase * AHD;
-        const float* ssrc = (pw < 2 ? kv.ks : kv.vs) + rbase;
-        const int r4 = lane >> 4, sl = lane & 15;
-        auto issue = [&](int c) {
-            const int c0 = clo(c), ce = chi(c);
-            unsigned char* st = smem + (c % W1_NS) * W1_STAGE;
-            unsigned char* sb = st + (pw < 2 ? 0 : W1_KB);
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int i = 8 * (pw & 1) + u, r = 4 * i + r4;  // instruction i covers rows 4i .. 4i+3
-                const int piece = pw < 2 ? sl ^ (r & 15) : sl ^ (4 * (i & 3));
-                __builtin_amdgcn_global_load_lds((gptr_t)(src + (size_t)min(c0 + r, ce - 1) * AHD + 16 * piece),
-                                                 (lptr_t)(sb + i * 1024), 16, 0, 0);
-            }
-            if (!(pw & 1))
-                __builtin_amdgcn_global_load_lds((gptr_t)(ssrc + min(c0 + lane, ce - 1)),
-                                                 (lptr_t)(st + 2 * W1_KB + (pw < 2 ? 0 : 4 * W1_CH)), 4, 0, 0);
-        };
-        for (int c = 0; c < W1_NS - 1 && c < nch; c++) issue(c);
-        for (int c = 0; c < nch; c++) {
-            // chunk c has landed when at most the chunks issued after it are in flight (9 or 8 instructions each)
-            const int after = min(nch - 1 - c, W1_NS - 2);
-            if (pw & 1) { if (after >= 2) wait_vm<16>(); else if (after == 1) wait_vm<8>(); else wait_vm<0>(); }
-            else { if (after >= 2) wait_vm<18>(); else if (after == 1) wait_vm<9>(); else wait_vm<0>(); }
-            // chunk c is in stage c % 4 and the consumers are done with chunk c - 1: its stage takes chunk c + 3.
-            // Not __syncthreads: that would also wait for the chunks still in flight.
-            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            if (c + W1_NS - 1 < nch) issue(c + W1_NS - 1);
-        }
-        __syncthreads();
-        __syncthreads();
+        ring_producer<W1_CH, W1_NS>(smem, kv, rbase, wv - WS_NC, lane, lo, first, nch);
     } else {
         // ---- consumers. Query digits in registers: column m16 of the Q.K MFMA is head m16 / 2 (every head twice);
         // lane (g, m16) holds dims 64 ks + 16 g .. +15 of it, the 4 lanes of a column together hold its 256 dims ----
@@ -422,16 +397,22 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws1_kernel(const 
 // chunk (part w / NPR). Column m of the Q.K MFMA is (token m / 8 of the pair, head m % 8), so one set of MFMAs scores
 // both tokens. P enters P.V as two A operands, its hi and lo fp16 parts (row = column), accumulated into the same O
 // tiles against one widened V operand: V is widened once per pair, and O (rows = (token, head)) takes 64 registers.
-constexpr int WSP_LDS = WS_NS * WS_STAGE;  // the two stages
-static_assert(WS_NC * 16 * AHD * 4 <= WS_STAGE, "the pair merge fits in stage 0");
-static_assert(WSP_LDS <= 160 * 1024, "LDS");
+// Chunks of 64 keys, three in flight, for two token pairs (each consumer then owns 32 keys of a chunk); chunks of 128
+// keys, one in flight, for one pair (four consumers x 32 keys).
+template <int NPR> constexpr int wsp_ch() { return NPR == 2 ? 64 : 128; }
+template <int NPR> constexpr int wsp_ns() { return NPR == 2 ? 4 : 2; }
+template <int NPR> constexpr int wsp_lds() { return wsp_ns<NPR>() * ring_stage<wsp_ch<NPR>()>(); }
+static_assert(WS_NC * 16 * AHD * 4 <= wsp_lds<1>() && WS_NC * 16 * AHD * 4 <= wsp_lds<2>(), "the pair merge fits");
+static_assert(wsp_lds<1>() <= 160 * 1024 && wsp_lds<2>() <= 160 * 1024, "LDS");
 
 template <int NPR>
 __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wsp_kernel(const float* __restrict__ qo, moex_kv_cache kv,
                                                                          int H, const int* __restrict__ pos_d,
                                                                          int max_t, float* __restrict__ part, int T,
                                                                          int ns) {
-    constexpr int TT = 2 * NPR, KPC = 32 * NPR;  // tokens per workgroup, keys per consumer per chunk
+    constexpr int CH = wsp_ch<NPR>(), NS = wsp_ns<NPR>(), KB = CH * AHD, STAGE = ring_stage<CH>();
+    constexpr int TT = 2 * NPR, KPC = CH * NPR / WS_NC;  // tokens per workgroup, keys per consumer per chunk
+    static_assert(KPC == 32, "one 32-key block per consumer and chunk");
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float cm[WS_NC][16], cl[WS_NC][16];
     const int nb = gridDim.x, w_id = xcd_work_id(blockIdx.x, nb);
@@ -441,13 +422,13 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wsp_kernel(const 
     const int pos0 = *pos_d, Tmax = pos0 + T;
     const int L = (Tmax + ns - 1) / ns, lo = s * L;
     const int hi = min(pos0 + tb + ntok, lo + L);  // keys [lo, hi) of this split that the group's last token sees
-    const int nch = hi > lo ? (hi - lo + WS_CH - 1) / WS_CH : 0;
-    const int first = hi > lo ? hi - lo - (nch - 1) * WS_CH : 0;  // chunk 0 is the short one
+    const int nch = hi > lo ? (hi - lo + CH - 1) / CH : 0;
+    const int first = hi > lo ? hi - lo - (nch - 1) * CH : 0;  // chunk 0 is the short one
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 4, m16 = lane & 15;
     const size_t rbase = (size_t)kvh * max_t;
 
     if (wv >= WS_NC) {
-        ws_producer(smem, kv, rbase, wv - WS_NC, lane, lo, first, nch);
+        ring_producer<CH, NS>(smem, kv, rbase, wv - WS_NC, lane, lo, first, nch);
     } else {
         const int pr = wv % NPR;                                        // token pair
         const bool live = 2 * pr < ntok;
@@ -496,14 +477,14 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wsp_kernel(const 
         float xsum = 0.f;                                 // sum of P * vs * 2^sig of this lane's keys: the V bias
         int sig = 0;                                      // O is held times 2^sig
         for (int c = 0; c < nch; c++) {
-            __syncthreads();  // chunk c is in stage c % WS_NS
+            __syncthreads();  // chunk c is in stage c % NS
             if (!live) continue;
-            const int c0 = c == 0 ? lo : lo + first + (c - 1) * WS_CH, ce = c == 0 ? lo + first : lo + first + c * WS_CH;
+            const int c0 = c == 0 ? lo : lo + first + (c - 1) * CH, ce = c == 0 ? lo + first : lo + first + c * CH;
             const int cmax = min(ce, hhi), cmin = min(ce, hlo), ctl = min(ce, htl);
-            const unsigned char* sb = smem + (c % WS_NS) * WS_STAGE;
-            const float* sks = reinterpret_cast<const float*>(sb + 2 * WS_KB);
-            const float* svs = sks + 128;
-            const unsigned char* Vs = sb + WS_KB;
+            const unsigned char* sb = smem + (c % NS) * STAGE;
+            const float* sks = reinterpret_cast<const float*>(sb + 2 * KB);
+            const float* svs = sks + CH;
+            const unsigned char* Vs = sb + KB;
 #pragma unroll 1
             for (int kb = (wv / NPR) * KPC; kb < (wv / NPR + 1) * KPC; kb += 32) {  // keys kb .. kb+31 of the chunk
                 if (c0 + kb >= cmax) break;
@@ -678,12 +659,12 @@ static void launch_wsp(const float* qo, moex_kv_cache kv, int H, int KV, const i
                        int T, int ns, hipStream_t st) {
     static bool once = [] {
         MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_wsp_kernel<NPR>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, WSP_LDS));
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, wsp_lds<NPR>()));
         return true;
     }();
     (void)once;
     hipLaunchKernelGGL(gqa_wsp_kernel<NPR>, dim3(KV * ns * ((T + 2 * NPR - 1) / (2 * NPR))),
-                       dim3(64 * (WS_NC + WS_NP)), WSP_LDS, st, qo, kv, H, pos_d, max_t, part, T, ns);
+                       dim3(64 * (WS_NC + WS_NP)), wsp_lds<NPR>(), st, qo, kv, H, pos_d, max_t, part, T, ns);
 }
 
 // TurboQuant codes -> signed int8 centroid codes (kernels.cuh:1122-1170 tables, scaled by 127 / max centroid):
