@@ -398,6 +398,7 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
     }
 
     // ---------------- computing wavefronts ----------------
+    __builtin_amdgcn_s_setprio(2);  // ahead of the staging wavefronts at the SIMD's issue arbiter
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h32 = lane >> 5, r = lane & 31;
     const int tokw = 4 * w + (r >> 3), head = kvh * GQ + (r & 7);                     // this lane's row
     const int prow = min(pos0 + t0 + tokw, hi - 1);                                     // its last visible key
