@@ -869,6 +869,8 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const 
         __syncthreads();
         __syncthreads();
     } else {
+        __builtin_amdgcn_s_setprio(2);  // consumers ahead of the unpacking producers at the SIMD's issue arbiter
+        // (the other way round measured 3 us slower)
         // ---- consumers. Query digits in registers: MFMA ks, lane (g, m16) holds dims
         // 64 ks + 16 g + {0,2,4,6, 1,3,5,7, 8,10,12,14, 9,11,13,15} of head m16 % 8; qa = digit 2 (m16 < 8) or 0,
         // qb = digit 1 ----
