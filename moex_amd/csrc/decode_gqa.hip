@@ -3,8 +3,8 @@
 // One workgroup = (kv head, key split, group of query tokens); the 8 query heads of the group share every K/V byte.
 // int8 cache: gqa_ws1_kernel for a single query token (warp-specialised: producer wavefronts stream K/V into LDS,
 // consumer wavefronts compute), gqa_wsp_kernel for MTP-verify windows (token pairs on the same pipeline).
-// gqa_wst_kernel serves the TurboQuant cache, one token per workgroup on the same pipeline, the codes unpacked on the
-// way. The partial written per (token, head, split) is {m (log2 units), l, acc[256]}.
+// gqa_wst_kernel serves the TurboQuant cache, one token per workgroup, on eight symmetric wavefronts that each stream
+// and decode their own keys. The partial written per (token, head, split) is {m (log2 units), l, acc[256]}.
 #include "common.hpp"
 
 namespace moex {
@@ -88,6 +88,23 @@ __device__ __forceinline__ float sum_x32(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// x reduced over the 16 lanes of its DPP row (lanes 16r .. 16r + 15); every lane of the row receives the result
+template <int CTRL> __device__ __forceinline__ float dppf(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float max_row16(float x) {
+    x = fmaxf(x, dppf<0x128>(x));  // row_ror:8
+    x = fmaxf(x, dppf<0x124>(x));  // row_ror:4
+    x = fmaxf(x, dppf<0x4e>(x));   // quad_perm [2, 3, 0, 1]
+    return fmaxf(x, dppf<0xb1>(x));  // quad_perm [1, 0, 3, 2]
+}
+__device__ __forceinline__ float sum_row16(float x) {
+    x += dppf<0x128>(x);
+    x += dppf<0x124>(x);
+    x += dppf<0x4e>(x);
+    return x + dppf<0xb1>(x);
+}
+
 // ---- The warp-specialised decode pipeline (gqa_ws1_kernel, gqa_wsp_kernel, gqa_wst_kernel). A vector-memory
 // instruction waits at issue while the CU's request queue is full, which under the chip-wide K/V stream is most of
 // the time; a wavefront that both loads and computes therefore cannot compute while its next chunk goes out. Here
@@ -105,7 +122,6 @@ __device__ __forceinline__ float sum_x32(float x) {
 //            than WS_SLACK (log2 units; P then stays below 2^WS_SLACK) or the V scale exponent grows.
 constexpr int WS_NC = 4;                              // consumer wavefronts (waves 0 .. WS_NC-1)
 constexpr int WS_NP = 4;                              // producer wavefronts (the next WS_NP waves)
-constexpr int WS_CH = 32 * WS_NC;                     // keys per chunk of the turbo kernel: 32 per consumer
 constexpr float WS_SLACK = 8.f;
 
 // The producer side of gqa_ws1_kernel / gqa_wsp_kernel: chunks of CH keys (keys [clo(c), chi(c)), chunk 0 the short
@@ -682,13 +698,6 @@ constexpr uint32_t SK0 = spack(-127, -96, -75, -58), SK1 = spack(-44, -31, -18, 
 constexpr uint32_t SK2 = spack(6, 18, 31, 44), SK3 = spack(58, 75, 96, 127);
 // V codes biased by 128 (1 .. 255), read by the consumers as fp16 subnormals (bsub8)
 constexpr uint32_t SV0 = spack(1, 49, 83, 114), SV1 = spack(142, 173, 207, 255);
-// 4 nibble indices (one per byte) -> 4 signed K codes
-__device__ __forceinline__ int lut16s(uint32_t idx) {
-    const uint32_t s3 = idx & 0x07070707u;
-    const uint32_t lo = __builtin_amdgcn_perm(SK1, SK0, s3), hi = __builtin_amdgcn_perm(SK3, SK2, s3);
-    // byte b from hi when bit 3 of index b is set: selector b + 4 picks byte b of the first perm operand
-    return (int)__builtin_amdgcn_perm(hi, lo, 0x03020100u | ((idx >> 1) & 0x04040404u));
-}
 // 8 nibbles of x -> the 4 signed K codes of its even nibbles (ev) and of its odd nibbles (od). The low 3 bits of a
 // nibble index a half-table (bytes 0-7 of the two v_perm sources); bit 3 moves the final pick to the upper half,
 // selector byte b + 4. 13 VALU per 8 codes.
@@ -710,28 +719,38 @@ __device__ __forceinline__ int4_t_ k_codes(uint2 x) {  // 16 nibbles -> the MFMA
     return int4_t_{a, b, c, d};
 }
 
-// ---- gqa_wst_kernel: TurboQuant cache, one query token per workgroup, on the warp-specialised pipeline.
-// Producers move each 128-key chunk by DMA (36 transfers per chunk, 4-byte ones for the norms so every key index is
-// clamped): the K nibble rows (row r keeps 16-byte piece p in slot p ^ ((r / 2) % 8), so the 8-byte fragment reads of
-// 16 rows at a 128-byte stride hit distinct banks) and the K and V half norms into one of three K stages, the raw V
-// rows (96 bytes, packed) into one of two raw V buffers. Producer j moves the raw V rows of keys 32j .. 32j + 31 and,
-// once they have landed, unpacks their 3-bit codes into consumer j's int8 code area for that chunk (the int8
-// kernels' V layout, two areas per consumer), so the unpacking runs beside the consumers' work on the previous chunk. Two
-// chunks are in flight: chunk c + 2 is issued at the barrier that starts chunk c. Q.K puts digit 2 of the 8 heads
-// (columns 0-7) and digit 0 (columns 8-15) into one MFMA and digit 1 (both halves) into a second, per 128-dim half;
-// one row_ror:8 DPP move gives each lane of a head's pair the digit its partner holds, digits 1 and 0 are added
-// exactly in int32 and digit 2 joins in one fma, in the same order in both lanes; P carries the V half norm. P rows are (hi / lo part, head), so the P.V key order being the
-// Q.K output order, each lane's probabilities are its own A operand; the hi and lo rows of O are added across lanes at
-// the end.
-constexpr int WST_KB = 128 * TQ_KB;                      // K nibble rows of a stage
-constexpr int WST_NS = 3;                                // K stages
-constexpr int WST_STAGE = WST_KB + 2 * 128 * 8;          // K nibble rows + K norms + V norms
-constexpr int WST_RV = 128 * TQ_VB;                      // raw V rows of a chunk (two buffers)
-constexpr int WST_VC = 32 * AHD;                         // one consumer's unpacked V codes (two buffers)
-constexpr int WST_VC0 = WST_NS * WST_STAGE + 2 * WST_RV;  // offset of the V code areas
-constexpr int WST_LDS = WST_VC0 + 2 * WS_NC * WST_VC;
-static_assert((WS_NC + 1) * GQ * AHD * 4 <= WST_NS * WST_STAGE, "the consumer merge and the merged rows fit in the stages");
-static_assert(WST_LDS <= 160 * 1024, "LDS");
+// ---- gqa_wst_kernel: TurboQuant cache, one query token per workgroup. Eight symmetric wavefronts with no roles:
+// chunk c of the split (128 keys, chunk 0 the short one) gives keys 16w .. 16w + 15 to wavefront w, which streams
+// them through a private ring of four LDS stages by its own DMA (K nibble rows, both half-norm pairs, raw V rows),
+// decodes its own codes and keeps its own online softmax state; the eight states merge once, at the end. No barrier
+// runs inside the key loop, the transfers are spread over all wavefronts, and the two wavefronts of a SIMD cover each
+// other's stalls.
+//   Q.K as S^T = Qd . K^T on v_mfma_i32_16x16x64_i8: the A operand holds query digits, row r = digit r % 4 (2, 1, 0,
+//     then a zero row) of head r / 4 in the first MFMA and of head r / 4 + 4 in the second; the B operand holds the K
+//     codes, column = key. Lane (g, m) then receives all three digits of heads g and g + 4 against key m and forms
+//     both scores itself: every score is formed once.
+//   P = 2^(s - m_ref) * vn * K3 * 2^sig per V half (the V half norm rides in P), split into fp16 hi + lo parts, goes
+//     through a 1 KB LDS tile per wavefront into the P.V operand layout: row m = hi part of head m (m < 8) or lo part
+//     of head m - 8, keys 4g .. 4g + 3 in lane (g, m).
+//   V: P.V on v_mfma_f32_16x16x16_f16, one MFMA per V half h and slot b (0..7); column n is dim 128 h + 8 n + b, so
+//     lane (g, n) decodes dims 8n .. 8n + 7 of both halves of keys 4g .. 4g + 3 straight from the raw rows (per key two
+//     16-bit words of low fields and two bytes of high bits): one v_perm LUT per 4 codes gives the codes biased by
+//     128, one v_perm per 2 codes the fp16-subnormal operand (as in the int8 kernels; the bias comes out at the end).
+constexpr int WT_NW = 8;                         // wavefronts
+constexpr int WT_K = 16;                         // keys per wavefront and chunk
+constexpr int WT_CH = WT_K * WT_NW;              // keys per chunk
+constexpr int WT_NS = 4;                         // stages per wavefront
+constexpr int WT_NRM = WT_K * TQ_KB;             // stage: K nibble rows at 0, then the norms (K pairs, V pairs)
+constexpr int WT_RV = WT_NRM + 2 * WT_K * 8;     // then the raw V rows
+constexpr int WT_STAGE = WT_RV + WT_K * TQ_VB;   // 3840 B
+constexpr int WT_PT = 2 * 16 * WT_K * 2;         // P tiles of a wavefront: two V halves of [16 rows][16 keys] fp16
+constexpr int WT_P0 = WT_NW * WT_NS * WT_STAGE;
+constexpr int WT_QT = WT_P0 + WT_NW * WT_PT;     // query digit table: [digit 2, 1, 0, zero][head][256] int8
+constexpr int WT_QS = WT_QT + 4 * GQ * AHD;      // the heads' score scales
+constexpr int WT_LDS = WT_QS + GQ * 4;
+static_assert((WT_NW + 1) * GQ * AHD * 4 <= WT_P0, "the merge and the merged rows fit in the stages");
+static_assert(WT_LDS <= 160 * 1024, "LDS");
+static_assert(WT_NW == GQ, "one wavefront per head in the inverse rotation");
 
 // Sign tables of the inverse rotation (kernels.cuh:1123-1132, TQ_S1 / TQ_S2) as bit masks: bit j set = -1.
 constexpr uint32_t WS1[4] = {0xe46a0359u, 0x42f85949u, 0xa4c63bbbu, 0x49f250a9u};
@@ -740,370 +759,362 @@ __device__ __forceinline__ float sgn(const uint32_t* m, int j, float x) {
     return (m[j >> 5] >> (j & 31)) & 1 ? -x : x;
 }
 
+// LDS transfers of 16 (4) bytes per active lane, lane l to lds + 16 l (4 l), written in inline asm: the compiler cannot
+// tell which LDS bytes a transfer writes and would make the wavefront's next LDS read wait for every transfer in
+// flight; the kernel waits for its own transfers with vm_wait. dma16s: wave-uniform base + per-lane 32-bit offset.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved: every other use of it in this kernel sets it first
+__device__ __forceinline__ void dma16(const void* g, const unsigned char* lds) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m) : "memory", "m0");
+}
+__device__ __forceinline__ void dma16s(const void* base, uint32_t off, const unsigned char* lds) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* g, const unsigned char* lds) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+template <int N> __device__ __forceinline__ void vm_wait() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+// 16 V codes -> biased code bytes. w = 2-bit low fields (code c at bits 2c); x = high bits, codes 0-7 in bits 0-7 and
+// codes 8-15 in bits 16-23. Word f of the result holds codes f, 4 + f, 8 + f, 12 + f in bytes 0..3: byte i of
+// (w >> 2f) & 0x03030303 is the low field of code 4i + f; with the high-bit nibbles moved one per byte (nibble i's bits
+// in the low half of byte i; the upper halves keep bits that the masks below drop), bit f of byte i is its high bit,
+// brought to bit 2 by one shift; one v_perm LUT maps the 3-bit selectors to codes.
+__device__ __forceinline__ void v_codes16(uint32_t w, uint32_t x, uint32_t cd[4]) {
+    const uint32_t hs = (x & ~0x0f000f00u) | ((x << 4) & 0x0f000f00u);
+    cd[0] = __builtin_amdgcn_perm(SV1, SV0, (w & 0x03030303u) | ((hs << 2) & 0x04040404u));
+    cd[1] = __builtin_amdgcn_perm(SV1, SV0, ((w >> 2) & 0x03030303u) | ((hs << 1) & 0x04040404u));
+    cd[2] = __builtin_amdgcn_perm(SV1, SV0, ((w >> 4) & 0x03030303u) | (hs & 0x04040404u));
+    cd[3] = __builtin_amdgcn_perm(SV1, SV0, ((w >> 6) & 0x03030303u) | ((hs >> 1) & 0x04040404u));
+}
+
 // rot != 0: the partial's acc is rotated back (the inverse WHT of turbo_out_k, kernels.cuh:1730-1738, is linear, so
 // it commutes with the combine's weighted sum): the combine then gates it directly and no turbo_out launch follows.
-__global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wst_kernel(const float* __restrict__ qo, moex_kv_cache kv,
-                                                                         int H, const int* __restrict__ pos_d,
-                                                                         int max_t, float* __restrict__ part, int T,
-                                                                         int ns, int rot) {
+__global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __restrict__ qo, moex_kv_cache kv, int H,
+                                                                const int* __restrict__ pos_d, int max_t,
+                                                                float* __restrict__ part, int T, int ns, int rot) {
     extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ float cm[WS_NC][GQ], cl[WS_NC][GQ];
+    __shared__ float cm[WT_NW][GQ], cl[WT_NW][GQ];
     const int nb = gridDim.x, w_id = xcd_work_id(blockIdx.x, nb);
     const int tok = w_id % T, s = (w_id / T) % ns, kvh = w_id / (T * ns);
     const int pos0 = *pos_d, Tmax = pos0 + T;
     const int L = (Tmax + ns - 1) / ns, lo = s * L;
     const int hi = min(pos0 + tok + 1, lo + L);  // keys [lo, hi) of this split that the token sees
-    const int nch = hi > lo ? (hi - lo + WS_CH - 1) / WS_CH : 0;
-    const int first = hi > lo ? hi - lo - (nch - 1) * WS_CH : 0;  // chunk 0 is the short one
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 4, m16 = lane & 15;
+    const int nch = hi > lo ? (hi - lo + WT_CH - 1) / WT_CH : 0;
+    const int first = hi > lo ? hi - lo - (nch - 1) * WT_CH : 0;  // chunk 0 is the short one
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, m16 = lane & 15;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: the step addresses stay scalar
     const size_t rbase = (size_t)kvh * max_t;
+    const uint8_t* Kg = reinterpret_cast<const uint8_t*>(kv.k) + rbase * TQ_KB;
+    const uint8_t* Vg = reinterpret_cast<const uint8_t*>(kv.v) + rbase * TQ_VB;
+    const float* kng = kv.ks + 2 * rbase;
+    const float* vng = kv.vs + 2 * rbase;
+    // this wavefront's steps: chunks cs .. nch - 1 (chunk 0 may hold none of its keys); step j uses stage j % WT_NS
+    const int cs = (nch > 0 && WT_K * wv >= first) ? 1 : 0, nst = nch - cs;
+    unsigned char* ring = smem + wv * WT_NS * WT_STAGE;
+    auto keys = [&](int j, int& k0, int& ke) {  // the step's first key and the end of its chunk
+        const int c = cs + j;
+        k0 = (c == 0 ? lo : lo + first + (c - 1) * WT_CH) + WT_K * wv;
+        ke = c == 0 ? lo + first : lo + first + c * WT_CH;
+    };
+    // five transfers per step: the 16 K rows (two of 8 rows; row r keeps 16-byte piece p in slot p ^ ((r / 2) % 8), so
+    // the 8-byte reads of 16 rows at a 128-byte stride hit distinct banks), the norms (lanes 0-31 the K pairs, 32-63
+    // the V pairs) and the 1536 raw V bytes (1 KB, then 512 B from lanes 0-31); past the chunk's end keys are clamped
+    const int kr0 = lane >> 3, kr1 = 8 + (lane >> 3);
+    const uint32_t ko0 = kr0 * TQ_KB + 16 * ((lane & 7) ^ ((kr0 >> 1) & 7));
+    const uint32_t ko1 = kr1 * TQ_KB + 16 * ((lane & 7) ^ ((kr1 >> 1) & 7));
+    auto issue = [&](int j) {
+        int k0, ke;
+        keys(j, k0, ke);
+        unsigned char* st = ring + (j % WT_NS) * WT_STAGE;
+        const float* nsrc = lane < 32 ? kng : vng;
+        if (k0 + WT_K <= ke) {
+            const uint8_t* kb = Kg + (size_t)k0 * TQ_KB;
+            const uint8_t* vb = Vg + (size_t)k0 * TQ_VB;
+            dma16s(kb, ko0, st);
+            dma16s(kb, ko1, st + 1024);
+            dma4(nsrc + 2 * (size_t)k0 + (lane & 31), st + WT_NRM);
+            dma16s(vb, 16 * lane, st + WT_RV);
+            if (lane < 32) dma16s(vb, 1024 + 16 * lane, st + WT_RV + 1024);
+        } else {
+            dma16(Kg + (size_t)min(k0 + kr0, ke - 1) * TQ_KB + (ko0 - kr0 * TQ_KB), st);
+            dma16(Kg + (size_t)min(k0 + kr1, ke - 1) * TQ_KB + (ko1 - kr1 * TQ_KB), st + 1024);
+            dma4(nsrc + 2 * (size_t)min(k0 + ((lane & 31) >> 1), ke - 1) + (lane & 1), st + WT_NRM);
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int b = 1024 * i + 16 * lane, r = b / TQ_VB;
+                if (i == 0 || lane < 32)
+                    dma16(Vg + (size_t)min(k0 + r, ke - 1) * TQ_VB + (b - r * TQ_VB), st + WT_RV + 1024 * i);
+            }
+        }
+    };
+    // step j's operands from its stage into registers: the K nibbles of key m16 (per MFMA ks), its norm pairs, and
+    // the raw V words of keys 4g .. 4g + 3 (dims 8 m16 .. 8 m16 + 7 of both halves)
+    struct StepRegs {
+        uint2 nib[4];
+        float2 kn, vn;
+        uint32_t vw[4], vx[4];
+    };
+    auto load_regs = [&](int j, StepRegs& r) {
+        const unsigned char* st = ring + (j % WT_NS) * WT_STAGE;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const int byte = 32 * ks + 8 * g;  // row m16
+            r.nib[ks] = *reinterpret_cast<const uint2*>(st + m16 * TQ_KB + 16 * ((byte >> 4) ^ ((m16 >> 1) & 7)) +
+                                                         (byte & 15));
+        }
+        r.kn = *reinterpret_cast<const float2*>(st + WT_NRM + 8 * m16);
+        r.vn = *reinterpret_cast<const float2*>(st + WT_NRM + 8 * WT_K + 8 * m16);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            typedef unsigned short us2_t __attribute__((ext_vector_type(2)));
+            const unsigned char* row = st + WT_RV + (4 * g + i) * TQ_VB;
+            r.vw[i] = __builtin_bit_cast(uint32_t, us2_t{*reinterpret_cast<const unsigned short*>(row + 2 * m16),
+                                                         *reinterpret_cast<const unsigned short*>(row + 32 + 2 * m16)});
+            r.vx[i] = __builtin_bit_cast(uint32_t, us2_t{row[64 + m16], row[80 + m16]});
+        }
+    };
+    // step j has landed once at most 5 * min(a, nst - 1 - j) transfers are in flight (a = steps issued past it)
+    auto wait_step = [&](int j, int a) {
+        const int ahead = min(a, nst - 1 - j);
+        if (ahead >= 3) vm_wait<15>();
+        else if (ahead == 2) vm_wait<10>();
+        else if (ahead == 1) vm_wait<5>();
+        else vm_wait<0>();
+    };
 
-    if (wv >= WS_NC) {
-        // ---- producers: transfer i (0..35) of a chunk goes to producer i % 4: 0-15 K rows (8 rows each), 16-27 raw
-        // V rows (1 KB of the packed rows each; producer j takes the 3 KB of keys 32j ..), 28-31 K norms, 32-35 V
-        // norms (64 floats each): 9 per producer ----
-        const int pw = wv - WS_NC;
-        const uint8_t* Kg = reinterpret_cast<const uint8_t*>(kv.k) + rbase * TQ_KB;
-        const uint8_t* Vg = reinterpret_cast<const uint8_t*>(kv.v) + rbase * TQ_VB;
-        const float* kng = kv.ks + 2 * rbase;
-        const float* vng = kv.vs + 2 * rbase;
-        // a full chunk's sources sit at lane-constant byte offsets from its first row: computed once
-        int offs[9];
+    // ---- query digits, once per workgroup: wavefront w turns head w (lane l: dims 4l .. 4l + 3) into three signed
+    // base-256 digits of a 2^(22 - e) fixed point (|q| < 2^e over the head) and writes them to the digit table in
+    // the operand order: dim d at byte 16 (d / 16) + pos(d % 16), pos = the K codes' order {0,2,4,6, 1,3,5,7, 8,..} ----
+    {
+        const float4 q4 = *reinterpret_cast<const float4*>(qo + ((size_t)tok * H + kvh * GQ + wv) * AHD + 4 * lane);
+        float qm = fmaxf(fmaxf(fabsf(q4.x), fabsf(q4.y)), fmaxf(fabsf(q4.z), fabsf(q4.w)));
+        qm = max_x32(max_x16(max_row16(qm)));
+        // the first steps' transfers go out while the digits are formed (the query rows have arrived)
 #pragma unroll
-        for (int u = 0; u < 9; u++) {
-            const int i = pw + 4 * u;
-            if (i < 16) {
-                const int r = 8 * i + (lane >> 3);
-                offs[u] = r * TQ_KB + 16 * ((lane & 7) ^ ((r >> 1) & 7));
-            } else if (i < 28) {
-                offs[u] = (3 * pw + (i - 16) / 4) * 1024 + 16 * lane;  // the chunk's raw V rows are contiguous
-            } else {
-                offs[u] = 4 * (64 * (i & 3) + lane);                   // two norms per key, contiguous
-            }
+        for (int j = 0; j < WT_NS - 1; j++)
+            if (j < nst) issue(j);
+        int e = 0;
+        if (qm > 0.f) (void)frexpf(qm, &e);  // qm < 2^e
+        const float up = ldexpf(1.f, 22 - e);
+        int8_t* qt = reinterpret_cast<int8_t*>(smem + WT_QT) + wv * AHD;
+        const float xv[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            int d2, d1, d0;
+            digits3((int)__builtin_rintf(xv[k] * up), d2, d1, d0);
+            const int d = 4 * lane + k, dl = d & 15;
+            const int at = 16 * (d >> 4) + 8 * (dl >> 3) + ((dl & 1) ? 4 : 0) + ((dl & 7) >> 1);
+            qt[at] = (int8_t)d2;
+            qt[GQ * AHD + at] = (int8_t)d1;
+            qt[2 * GQ * AHD + at] = (int8_t)d0;
         }
-        auto issue = [&](int c) {
-            const int c0 = c == 0 ? lo : lo + first + (c - 1) * WS_CH, ce = c == 0 ? lo + first : lo + first + c * WS_CH;
-            unsigned char* st = smem + (c % WST_NS) * WST_STAGE;
-            unsigned char* rv = smem + WST_NS * WST_STAGE + (c & 1) * WST_RV;
-            if (ce - c0 == WS_CH) {
-                const uint8_t* kb0 = Kg + (size_t)c0 * TQ_KB;
-                const uint8_t* vb0 = Vg + (size_t)c0 * TQ_VB;
-                const uint8_t* nk0 = reinterpret_cast<const uint8_t*>(kng + 2 * (size_t)c0);
-                const uint8_t* nv0 = reinterpret_cast<const uint8_t*>(vng + 2 * (size_t)c0);
+        reinterpret_cast<uint32_t*>(qt + 3 * GQ * AHD)[lane] = 0u;  // the zero rows
+        if (lane == 0) reinterpret_cast<float*>(smem + WT_QS)[wv] = ldexpf(1.f, e - 22) * (SL2 * TK4);
+    }
+    __syncthreads();
+    // the A operand of MFMA ks: lane (g, m16) holds the 16 bytes of dims 64 ks + 16 g .. + 15 of its row, digit m16 % 4
+    // of head m16 / 4 (qx) and of head m16 / 4 + 4 (qy)
+    const int dg = m16 & 3, hr = m16 >> 2;
+    int4_t_ qx[4], qy[4];
+    {
+        const unsigned char* qt = smem + WT_QT + dg * GQ * AHD;
 #pragma unroll
-                for (int u = 0; u < 9; u++) {
-                    const int i = pw + 4 * u;
-                    if (i < 16)
-                        __builtin_amdgcn_global_load_lds((gptr_t)(kb0 + offs[u]), (lptr_t)(st + i * 1024), 16, 0, 0);
-                    else if (i < 28)
-                        __builtin_amdgcn_global_load_lds((gptr_t)(vb0 + offs[u]),
-                                                         (lptr_t)(rv + (3 * pw + (i - 16) / 4) * 1024), 16, 0, 0);
-                    else
-                        __builtin_amdgcn_global_load_lds((gptr_t)((i < 32 ? nk0 : nv0) + offs[u]),
-                                                         (lptr_t)(st + WST_KB + (i < 32 ? 0 : 1024) + 256 * (i & 3)),
-                                                         4, 0, 0);
-                }
-                return;
-            }
-#pragma unroll
-            for (int u = 0; u < 9; u++) {
-                const int i = pw + 4 * u;
-                if (i < 16) {
-                    const int r = 8 * i + (lane >> 3), piece = (lane & 7) ^ ((r >> 1) & 7);
-                    __builtin_amdgcn_global_load_lds((gptr_t)(Kg + (size_t)min(c0 + r, ce - 1) * TQ_KB + 16 * piece),
-                                                     (lptr_t)(st + i * 1024), 16, 0, 0);
-                } else if (i < 28) {  // the raw V rows of keys 32 pw .. 32 pw + 31 (unpacked by this producer)
-                    const int piece = 3 * pw + (i - 16) / 4, b = piece * 1024 + 16 * lane, r = b / TQ_VB;
-                    __builtin_amdgcn_global_load_lds((gptr_t)(Vg + (size_t)min(c0 + r, ce - 1) * TQ_VB + (b - r * TQ_VB)),
-                                                     (lptr_t)(rv + piece * 1024), 16, 0, 0);
-                } else {
-                    const int f = 64 * (i & 3) + lane, key = min(c0 + (f >> 1), ce - 1);
-                    __builtin_amdgcn_global_load_lds((gptr_t)((i < 32 ? kng : vng) + 2 * (size_t)key + (f & 1)),
-                                                     (lptr_t)(st + WST_KB + (i < 32 ? 0 : 1024) + 256 * (i & 3)),
-                                                     4, 0, 0);
-                }
-            }
-        };
-        if (nch > 0) issue(0);
-        if (nch > 1) issue(1);
-        for (int c = 0; c < nch; c++) {
-            if (c + 1 < nch) wait_vm<9>();  // chunk c has landed (chunk c + 1 may still be in flight)
-            else wait_vm<0>();
-            const int c0 = c == 0 ? lo : lo + first + (c - 1) * WS_CH, ce = c == 0 ? lo + first : lo + first + c * WS_CH;
-            if (c0 + 32 * pw < ce) {
-                // V codes of keys 32 pw + 0..31 into consumer pw's code area of chunk c (its chunk c - 2 user is done):
-                // lane = (piece pc = lane % 16, keys lane / 16 + 4 it)
-                unsigned char* Vc = smem + WST_VC0 + ((c & 1) * WS_NC + pw) * WST_VC;
-                const int pc = lane & 15, hb = pc >> 3, q = pc & 7;
-                const unsigned char* rw0 = smem + WST_NS * WST_STAGE + (c & 1) * WST_RV + (32 * pw + (lane >> 4)) * TQ_VB;
-                uint32_t Lw[8], Hh[8];
-#pragma unroll
-                for (int it = 0; it < 8; it++) {
-                    Lw[it] = *reinterpret_cast<const uint32_t*>(rw0 + it * 4 * TQ_VB + 32 * hb + 4 * q);
-                    Hh[it] = *reinterpret_cast<const uint16_t*>(rw0 + it * 4 * TQ_VB + 64 + 16 * hb + 2 * q);
-                }
-#pragma unroll
-                for (int it = 0; it < 8; it++) {
-                    const int kk = (lane >> 4) + 4 * it;  // 0..31
-                    uint32_t sel[4];
-                    tr4x4_(Lw[it] & 0x03030303u, (Lw[it] >> 2) & 0x03030303u, (Lw[it] >> 4) & 0x03030303u,
-                           (Lw[it] >> 6) & 0x03030303u, sel);
-                    uint32_t cd[4];
-#pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        const uint32_t idx = sel[k] | ((__builtin_amdgcn_ubfe(Hh[it], 4 * k, 4) * 0x810204u) & 0x04040404u);
-                        cd[k] = __builtin_amdgcn_perm(SV1, SV0, idx);
-                    }
-                    // not a C++ store: the compiler would wait for every DMA in flight before it (it cannot tell that the
-                    // code areas are none of their destinations)
-                    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-                    const uint32_t la = (uint32_t)(uintptr_t)(Vc + kk * AHD + 16 * (pc ^ (4 * ((kk >> 2) & 3))));
-                    asm volatile("ds_write_b128 %0, %1" ::"v"(la), "v"(u32x4_t{cd[0], cd[1], cd[2], cd[3]}) : "memory");
-                }
-            }
-            // chunk c and its V codes are ready, and the consumers are done with chunk c - 1: its K stage takes chunk
-            // c + 2, as does the raw V buffer of chunk c. Not __syncthreads: that waits for chunk c + 1 too.
-            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            if (c + 2 < nch) issue(c + 2);
+        for (int ks = 0; ks < 4; ks++) {
+            qx[ks] = *reinterpret_cast<const int4_t_*>(qt + hr * AHD + 64 * ks + 16 * g);
+            qy[ks] = *reinterpret_cast<const int4_t_*>(qt + (hr + 4) * AHD + 64 * ks + 16 * g);
         }
-        __syncthreads();
-        __syncthreads();
-    } else {
-        __builtin_amdgcn_s_setprio(2);  // consumers ahead of the unpacking producers at the SIMD's issue arbiter
-        // (the other way round measured 3 us slower)
-        // ---- consumers. Query digits in registers: MFMA ks, lane (g, m16) holds dims
-        // 64 ks + 16 g + {0,2,4,6, 1,3,5,7, 8,10,12,14, 9,11,13,15} of head m16 % 8; qa = digit 2 (m16 < 8) or 0,
-        // qb = digit 1 ----
-        const int hq = m16 & 7;
-        const bool lo8 = m16 < 8;
-        int4_t_ qa[4], qb[4];
-        float qs;
+    }
+    const float qsA = reinterpret_cast<const float*>(smem + WT_QS)[g];
+    const float qsB = reinterpret_cast<const float*>(smem + WT_QS)[g + 4];  // the lane's score heads g and g + 4
+    float4_t o[16];  // o[8 h + b]: rows 4g .. 4g + 3 (hi rows for g < 2, lo rows for g >= 2), column m16: dim 128h + 8 m16 + b
+#pragma unroll
+    for (int J = 0; J < 16; J++) o[J] = float4_t{0.f, 0.f, 0.f, 0.f};
+    float mA = -INFINITY, mB = -INFINITY, lA = 0.f, lB = 0.f, vmax = 0.f;
+    // sums of P * vn * K3 * 2^sig over the lane's keys per score head and V half: the bias taken out at the end
+    float xA0 = 0.f, xA1 = 0.f, xB0 = 0.f, xB1 = 0.f;
+    int sig = 0;
+    unsigned char* Pt = smem + WT_P0 + wv * WT_PT;  // [V half][row 8 hl + h][16 keys] fp16
+    StepRegs cur;
+    if (nst > 0) {
+        wait_step(0, WT_NS - 2);
+        load_regs(0, cur);
+    }
+    for (int j = 0; j < nst; j++) {
+        // step j + 3 goes to the stage of step j - 1, whose operands are in registers already
+        if (j + WT_NS - 1 < nst) issue(j + WT_NS - 1);
+        int k0, ke;
+        keys(j, k0, ke);
+        // ---- K codes and Q.K: [128-dim half], heads g (sx) and g + 4 (sy) against key m16 ----
+        int4_t_ sx[2], sy[2];
+        sx[0] = sx[1] = sy[0] = sy[1] = int4_t_{0, 0, 0, 0};
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const int4_t_ b = k_codes(cur.nib[ks]);
+            sx[ks >> 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qx[ks], b, sx[ks >> 1], 0, 0, 0);
+            sy[ks >> 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qy[ks], b, sy[ks >> 1], 0, 0, 0);
+        }
+        // the next step's operands start on their way while this step computes
+        StepRegs nxt;
+        if (j + 1 < nst) {
+            wait_step(j + 1, WT_NS - 2);
+            load_regs(j + 1, nxt);
+        }
+        const float2 kn = cur.kn, vn = cur.vn;
+        // ---- scores: per half d2 * 65536 + (d1 * 256 + d0), the latter exact in int32 (|d1 * 256 + d0| < 2^30) ----
+        float scA, scB;
         {
-            const float* qrow = qo + ((size_t)tok * H + kvh * GQ + hq) * AHD + 16 * g;
-            float4 qv4[16];
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-                for (int u = 0; u < 4; u++) qv4[4 * ks + u] = *reinterpret_cast<const float4*>(qrow + 64 * ks + 4 * u);
-            float qm = 0.f;
-#pragma unroll
-            for (int u = 0; u < 16; u++)
-                qm = fmaxf(fmaxf(qm, fmaxf(fabsf(qv4[u].x), fabsf(qv4[u].y))), fmaxf(fabsf(qv4[u].z), fabsf(qv4[u].w)));
-            qm = max_x32(max_x16(qm));
-            int e = 0;
-            if (qm > 0.f) (void)frexpf(qm, &e);  // qm < 2^e
-            const float up = ldexpf(1.f, 22 - e);
-            qs = ldexpf(1.f, e - 22) * (SL2 * TK4);
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                int da[16], db[16];
-#pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    const float4 x = qv4[4 * ks + u];
-                    const float xv[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        int d2, d1, d0;
-                        digits3((int)__builtin_rintf(xv[k] * up), d2, d1, d0);
-                        // dim 4u + k of the lane's 16 goes to operand byte: even dims of each 8 first, then odd
-                        const int dl = 4 * u + k, pos = 8 * (dl >> 3) + ((dl & 1) ? 4 : 0) + ((dl & 7) >> 1);
-                        da[pos] = lo8 ? d2 : d0;
-                        db[pos] = d1;
-                    }
-                }
-#pragma unroll
-                for (int w = 0; w < 4; w++) {
-                    qa[ks][w] = (int)pack_bytes(da[4 * w], da[4 * w + 1], da[4 * w + 2], da[4 * w + 3]);
-                    qb[ks][w] = (int)pack_bytes(db[4 * w], db[4 * w + 1], db[4 * w + 2], db[4 * w + 3]);
-                }
-            }
+            const float a0 = fmaf((float)sx[0][0], 65536.f, (float)(sx[0][1] * 256 + sx[0][2]));
+            const float a1 = fmaf((float)sx[1][0], 65536.f, (float)(sx[1][1] * 256 + sx[1][2]));
+            const float b0 = fmaf((float)sy[0][0], 65536.f, (float)(sy[0][1] * 256 + sy[0][2]));
+            const float b1 = fmaf((float)sy[1][0], 65536.f, (float)(sy[1][1] * 256 + sy[1][2]));
+            scA = (a0 * kn.x + a1 * kn.y) * qsA;
+            scB = (b0 * kn.x + b1 * kn.y) * qsB;
         }
-        float4_t o[16];  // ws layout: row 2h (2h + 1) = hi (lo) part of head h
-#pragma unroll
-        for (int J = 0; J < 16; J++) o[J] = float4_t{0.f, 0.f, 0.f, 0.f};
-        float mref = -INFINITY, lacc = 0.f, vmax = 0.f;
-        float xsum0 = 0.f, xsum1 = 0.f;  // sum of P * vn * K3 * 2^sig of this lane's keys (V halves 0, 1): the bias
-        int sig = 0;
-        const int kb = 32 * wv;
-        for (int c = 0; c < nch; c++) {
-            __syncthreads();  // chunk c is in K stage c % WST_NS, its V codes in area c % 2
-            const int c0 = c == 0 ? lo : lo + first + (c - 1) * WS_CH, ce = c == 0 ? lo + first : lo + first + c * WS_CH;
-            if (c0 + kb >= ce) continue;
-            const unsigned char* sb = smem + (c % WST_NS) * WST_STAGE;
-            const unsigned char* Vc = smem + WST_VC0 + ((c & 1) * WS_NC + wv) * WST_VC;  // V codes (ws layout)
-            const float2* skn = reinterpret_cast<const float2*>(sb + WST_KB);
-            const float2* svn = skn + 128;
-            float2 kn[8], vn[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                kn[j] = skn[kb + 16 * (j >> 2) + 4 * g + (j & 3)];
-                vn[j] = svn[kb + 16 * (j >> 2) + 4 * g + (j & 3)];
-            }
-            // ---- K codes and the 16 Q.K MFMAs (halves in separate accumulators) ----
-            int4_t_ da0[2], db0[2], da1[2], db1[2];
-#pragma unroll
-            for (int grp = 0; grp < 2; grp++) {
-                da0[grp] = int4_t_{0, 0, 0, 0}; db0[grp] = int4_t_{0, 0, 0, 0};
-                da1[grp] = int4_t_{0, 0, 0, 0}; db1[grp] = int4_t_{0, 0, 0, 0};
-            }
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-                for (int grp = 0; grp < 2; grp++) {
-                    const int byte = 64 * (ks >> 1) + 32 * (ks & 1) + 8 * g;  // row kb + 16 grp + m16
-                    const uint2 nib = *reinterpret_cast<const uint2*>(sb + (kb + 16 * grp + m16) * TQ_KB +
-                                                                      16 * ((byte >> 4) ^ ((m16 >> 1) & 7)) + (byte & 15));
-                    const int4_t_ a = k_codes(nib);
-                    if (ks < 2) {
-                        da0[grp] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qa[ks], da0[grp], 0, 0, 0);
-                        db0[grp] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qb[ks], db0[grp], 0, 0, 0);
-                    } else {
-                        da1[grp] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qa[ks], da1[grp], 0, 0, 0);
-                        db1[grp] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qb[ks], db1[grp], 0, 0, 0);
-                    }
-                }
-            // ---- scores: both lanes of a head (m16, m16 ^ 8) recombine its digits in the same order (|d1 * 256 + d0|
-            // < 2^30: exact in int32) ----
-            float sc[8];
-#pragma unroll
-            for (int grp = 0; grp < 2; grp++)
+        float vm = fmaxf(vn.x, vn.y);
+        if (k0 + WT_K > ke && k0 + m16 >= ke) {
+            scA = scB = -INFINITY;
+            vm = 0.f;
+        }
+        // the reductions over a head's 16 lanes only when some lane's own key passes a bound (rare). A lane's own
+        // score passes m_ref + slack exactly when its head's maximum does, and V scales below 2^(7 - sig) cannot move
+        // the exponent: the same decisions as with the reduced values
+        if (__builtin_amdgcn_ballot_w64(scA > mA + WS_SLACK || scB > mB + WS_SLACK || vm * TK3 >= ldexpf(1.f, 7 - sig)) !=
+            0) {
+            const float MA = max_row16(scA), MB = max_row16(scB);
+            vm = max_row16(vm) * TK3;  // every lane group g holds the step's 16 keys: uniform over the wavefront
+            // ---- lazy rescale ----
+            const float nA = MA > mA + WS_SLACK ? MA : mA, nB = MB > mB + WS_SLACK ? MB : mB;
+            const float fA = ex2d(mA, nA), fB = ex2d(mB, nB);
+            vmax = fmaxf(vmax, vm);
+            int ev = 0;
+            if (vmax > 0.f) (void)frexpf(vmax, &ev);  // vmax < 2^ev: p * vn * K3 * 2^(7 - ev) < 2^(7 + WS_SLACK)
+            const int nsig = 7 - ev;
+            if (__builtin_amdgcn_ballot_w64(fA != 1.f || fB != 1.f) != 0 || nsig != sig) {
+                const float sf = ldexpf(1.f, nsig - sig);
+                float fr[4];  // O row 4g + i is head 4 (g & 1) + i: its factor from lane 16 i
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int a0 = da0[grp][i], x0 = dpp_ror8(a0), a1 = da1[grp][i], x1 = dpp_ror8(a1);
-                    const float r0 = fmaf((float)(lo8 ? a0 : x0), 65536.f, (float)(db0[grp][i] * 256 + (lo8 ? x0 : a0)));
-                    const float r1 = fmaf((float)(lo8 ? a1 : x1), 65536.f, (float)(db1[grp][i] * 256 + (lo8 ? x1 : a1)));
-                    sc[4 * grp + i] = (r0 * kn[4 * grp + i].x + r1 * kn[4 * grp + i].y) * qs;
+                    const float a = __shfl(fA, 16 * i), b = __shfl(fB, 16 * i);
+                    fr[i] = ((g & 1) ? b : a) * sf;
                 }
-            float vm;
-            if (c0 + kb + 32 <= ce) {
-                vm = 0.f;
 #pragma unroll
-                for (int j = 0; j < 8; j++) vm = fmaxf(vm, fmaxf(vn[j].x, vn[j].y));
-            } else {
-                vm = 0.f;
+                for (int J = 0; J < 16; J++)
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const bool ok = c0 + kb + 16 * (j >> 2) + 4 * g + (j & 3) < ce;
-                    sc[j] = ok ? sc[j] : -INFINITY;
-                    vm = ok ? fmaxf(vm, fmaxf(vn[j].x, vn[j].y)) : vm;
-                }
-            }
-            float M = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
-            // the reductions over the lane groups only when some lane's own keys pass a bound (rare). A lane's
-            // own maximum passes m_ref + slack exactly when its group's does, and V scales below 2^(7 - sig)
-            // cannot move the exponent: the same decisions as with the reduced values, bit for bit
-            if (__builtin_amdgcn_ballot_w64(M > mref + WS_SLACK || vm * TK3 >= ldexpf(1.f, 7 - sig)) != 0) {
-                M = max_x32(max_x16(M));
-                vm = max_x32(max_x16(vm)) * TK3;
-                // ---- lazy rescale ----
-                const float nref = M > mref + WS_SLACK ? M : mref;
-                const float fown = ex2d(mref, nref);
-                vmax = fmaxf(vmax, vm);
-                int ev = 0;
-                if (vmax > 0.f) (void)frexpf(vmax, &ev);  // vmax < 2^ev: p * vn * K3 * 2^(7 - ev) < 2^(7 + WS_SLACK)
-                const int nsig = 7 - ev;
-                if (__builtin_amdgcn_ballot_w64(fown != 1.f) != 0 || nsig != sig) {
-                    const float sf = ldexpf(1.f, nsig - sig);
-                    float fr[4];
-#pragma unroll
-                    for (int i = 0; i < 4; i++) fr[i] = __shfl(fown, (4 * g + i) & 7) * sf;  // O row m: head m % 8
-#pragma unroll
-                    for (int J = 0; J < 16; J++)
-#pragma unroll
-                        for (int i = 0; i < 4; i++) o[J][i] *= fr[i];
-                    lacc *= fown;
-                    xsum0 *= fown * sf; xsum1 *= fown * sf;
-                    mref = nref;
-                    sig = nsig;
-                }
-            }
-            // ---- P of both V halves = 2^(s - mref) * vn * K3 * 2^sig as fp16 hi (m16 < 8) / lo (m16 >= 8): row m16 of
-            // the P operand (head m16 % 8), each lane's 8 keys its own A operand (the P.V key order is the Q.K
-            // output order) ----
-            half8_t pa0, pa1;
-            {
-                const float vsc = ldexpf(1.f, sig) * TK3;
-                half8_t p0v, p1v;
-                float ls = 0.f, xs0 = 0.f, xs1 = 0.f;
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const float p = fast_exp2(sc[j] - mref);
-                    ls += p;
-                    const float x0 = p * (vn[j].x * vsc), x1 = p * (vn[j].y * vsc);
-                    xs0 += x0; xs1 += x1;
-                    const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
-                    p0v[j] = lo8 ? h0 : (_Float16)(x0 - (float)h0);
-                    p1v[j] = lo8 ? h1 : (_Float16)(x1 - (float)h1);
-                }
-                lacc += lo8 ? ls : 0.f;
-                xsum0 += xs0; xsum1 += xs1;
-                pa0 = p0v;
-                pa1 = p1v;
-            }
-            // ---- O^T += P . V over these 32 keys: dims < 128 (pc 0, 1) with the half-0 P, the rest with half 1 ----
-#pragma unroll
-            for (int pc = 0; pc < 4; pc++) {
-                const int rd = 16 * ((4 * pc + (m16 >> 2)) ^ (4 * g)) + 4 * (m16 & 3);
-                uint32_t r[8];
-#pragma unroll
-                for (int j = 0; j < 8; j++)
-                    r[j] = *reinterpret_cast<const uint32_t*>(Vc + (16 * (j >> 2) + 4 * g + (j & 3)) * AHD + rd);
-#pragma unroll
-                for (int jt = 0; jt < 4; jt++)
-                    o[4 * pc + jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pc < 2 ? pa0 : pa1, bsub8(r, jt),
-                                                                         o[4 * pc + jt], 0, 0, 0);
+                    for (int i = 0; i < 4; i++) o[J][i] *= fr[i];
+                lA *= fA;
+                lB *= fB;
+                xA0 *= fA * sf; xA1 *= fA * sf; xB0 *= fB * sf; xB1 *= fB * sf;
+                mA = nA;
+                mB = nB;
+                sig = nsig;
             }
         }
-        // ---- merge the four consumers: m, l per head, then O rows (hi + lo) scaled to the common maximum ----
-        const float l = sum_x32(sum_x16(lacc));
-        __syncthreads();  // every consumer is past its last chunk: the stages are free
-        if (lane < 8) { cm[wv][lane] = mref; cl[wv][lane] = l; }
-        __syncthreads();
-        float* Ow = reinterpret_cast<float*>(smem);  // [consumer][head][256]
-        const float un = ldexpf(1.f, -sig);
-        // O rows 4g + i: head (4g + i) % 8, hi for g < 2 and lo for g >= 2: lanes l and l + 32 hold the two parts
+        // ---- P of both V halves, fp16 hi + lo, into the P tiles: row 8 hl + h, column = key ----
+        {
+            const float vs0 = vn.x * ldexpf(1.f, sig) * TK3, vs1 = vn.y * ldexpf(1.f, sig) * TK3;
 #pragma unroll
-        for (int J = 0; J < 16; J++)
+            for (int hh = 0; hh < 2; hh++) {
+                const float p = fast_exp2((hh ? scB : scA) - (hh ? mB : mA));
+                const float x0 = p * vs0, x1 = p * vs1;
+                if (hh) { lB += p; xB0 += x0; xB1 += x1; } else { lA += p; xA0 += x0; xA1 += x1; }
+                const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+                _Float16* pr = reinterpret_cast<_Float16*>(Pt) + (g + 4 * hh) * WT_K + m16;
+                pr[0] = h0;
+                pr[8 * WT_K] = (_Float16)(x0 - (float)h0);
+                pr[16 * WT_K] = h1;
+                pr[24 * WT_K] = (_Float16)(x1 - (float)h1);
+            }
+        }
+        // P operand rows m16, keys 4g .. 4g + 3
+        const half4_t pa0 = *reinterpret_cast<const half4_t*>(Pt + (m16 * WT_K + 4 * g) * 2);
+        const half4_t pa1 = *reinterpret_cast<const half4_t*>(Pt + ((16 + m16) * WT_K + 4 * g) * 2);
+        // ---- V codes of the 4 keys, then O += P . V: block (h, b), operand half k = key 4g + k ----
+        uint32_t cd[4][4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) o[J][i] += __shfl_xor(o[J][i], 32);
-        // the V operands were (code + 128) * 2^-24: O = 2^24 o - 128 * sum(P * vn * K3 * 2^sig), per head and V half
-        const float xb0 = sum_x32(sum_x16(xsum0)) * VBIAS, xb1 = sum_x32(sum_x16(xsum1)) * VBIAS;
-        if (g < 2) {
+        for (int i = 0; i < 4; i++) v_codes16(cur.vw[i], cur.vx[i], cd[i]);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int h = 4 * g + i;
-                const float Mh = fmaxf(fmaxf(cm[0][h], cm[1][h]), fmaxf(cm[2][h], cm[3][h]));
-                const float f = ex2d(cm[wv][h], Mh) * un;
-                const float b0 = __shfl(xb0, h), b1 = __shfl(xb1, h);  // lane h: head h's sums (its hi lanes)
+        for (int h = 0; h < 2; h++)
 #pragma unroll
-                for (int pc = 0; pc < 4; pc++) {
-                    const float b = pc < 2 ? b0 : b1;
-                    *reinterpret_cast<float4*>(Ow + (wv * GQ + h) * AHD + 64 * pc + 4 * m16) =
-                        make_float4(fmaf(o[4 * pc][i], 16777216.f, -b) * f, fmaf(o[4 * pc + 1][i], 16777216.f, -b) * f,
-                                    fmaf(o[4 * pc + 2][i], 16777216.f, -b) * f, fmaf(o[4 * pc + 3][i], 16777216.f, -b) * f);
-                }
+            for (int b = 0; b < 8; b++) {
+                const int f = b & 3, by = 2 * h + (b >> 2);  // dim 8 m16 + b of half h: code 8h + b, word f, byte by
+                const uint32_t sel = (uint32_t)by | 0x0c00u | ((uint32_t)(4 + by) << 16) | 0x0c000000u;
+                typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+                const u32x2_t vb = {__builtin_amdgcn_perm(cd[1][f], cd[0][f], sel),
+                                    __builtin_amdgcn_perm(cd[3][f], cd[2][f], sel)};
+                o[8 * h + b] = __builtin_amdgcn_mfma_f32_16x16x16f16(h ? pa1 : pa0, __builtin_bit_cast(half4_t, vb),
+                                                                    o[8 * h + b], 0, 0, 0);
+            }
+        cur = nxt;
+    }
+    // ---- merge the eight wavefronts: m, l per head, then O rows (hi + lo) scaled to the common maximum ----
+    const float lAs = sum_row16(lA), lBs = sum_row16(lB);
+    // the V operands were (code + 128) * 2^-24: O = 2^24 o - 128 * sum(P * vn * K3 * 2^sig), per head and V half
+    const float bA0 = sum_row16(xA0) * VBIAS, bA1 = sum_row16(xA1) * VBIAS;
+    const float bB0 = sum_row16(xB0) * VBIAS, bB1 = sum_row16(xB1) * VBIAS;
+    if (m16 == 0) { cm[wv][g] = mA; cm[wv][g + 4] = mB; cl[wv][g] = lAs; cl[wv][g + 4] = lBs; }
+    __syncthreads();  // every wavefront is past its last step: the rings are free
+    float* Ow = reinterpret_cast<float*>(smem);  // [wavefront][head][256]
+    const float un = ldexpf(1.f, -sig);
+#pragma unroll
+    for (int J = 0; J < 16; J++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[J][i] += __shfl_xor(o[J][i], 32);  // lanes l, l + 32: the hi and lo rows
+    float b0[4], b1[4];  // row 4g + i is head 4 (g & 1) + i: its sums from lane 16 i (all lanes take part)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float a0 = __shfl(bA0, 16 * i), a1 = __shfl(bA1, 16 * i);
+        const float c0 = __shfl(bB0, 16 * i), c1 = __shfl(bB1, 16 * i);
+        b0[i] = (g & 1) ? c0 : a0;
+        b1[i] = (g & 1) ? c1 : a1;
+    }
+    if (g < 2) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int h = 4 * g + i;
+            float Mh = cm[0][h];
+#pragma unroll
+            for (int w = 1; w < WT_NW; w++) Mh = fmaxf(Mh, cm[w][h]);
+            const float f = ex2d(cm[wv][h], Mh) * un;
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++) {
+                const float b = hf ? b1[i] : b0[i];
+                float* dst = Ow + (wv * GQ + h) * AHD + 128 * hf + 8 * m16;
+                float r[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) r[k] = fmaf(o[8 * hf + k][i], 16777216.f, -b) * f;
+                *reinterpret_cast<float4*>(dst) = make_float4(r[0], r[1], r[2], r[3]);
+                *reinterpret_cast<float4*>(dst + 4) = make_float4(r[4], r[5], r[6], r[7]);
             }
         }
     }
     __syncthreads();
-    float* Om = reinterpret_cast<float*>(smem) + WS_NC * GQ * AHD;  // [head][256]: the merged acc, when rotating back
-    for (int it = tid; it < GQ * 64; it += 64 * (WS_NC + WS_NP)) {
-        const float* Ow = reinterpret_cast<const float*>(smem);
+    float* Om = reinterpret_cast<float*>(smem) + WT_NW * GQ * AHD;  // [head][256]: the merged acc, when rotating back
+    for (int it = tid; it < GQ * 64; it += 64 * WT_NW) {
         const int h = it >> 6, d4 = 4 * (it & 63);
         float4 a = *reinterpret_cast<const float4*>(Ow + h * AHD + d4);
 #pragma unroll
-        for (int w = 1; w < WS_NC; w++) {
+        for (int w = 1; w < WT_NW; w++) {
             const float4 b = *reinterpret_cast<const float4*>(Ow + (w * GQ + h) * AHD + d4);
             a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
         }
         if (rot) *reinterpret_cast<float4*>(Om + h * AHD + d4) = a;
         else *reinterpret_cast<float4*>(part_acc(part, tok, kvh * GQ + h, s, H, ns) + d4) = a;
         if ((it & 63) == 0) {
-            const float Mh = fmaxf(fmaxf(cm[0][h], cm[1][h]), fmaxf(cm[2][h], cm[3][h]));
+            float Mh = cm[0][h];
+#pragma unroll
+            for (int w = 1; w < WT_NW; w++) Mh = fmaxf(Mh, cm[w][h]);
+            float lsum = 0.f;
+#pragma unroll
+            for (int w = 0; w < WT_NW; w++) lsum += cl[w][h] * ex2d(cm[w][h], Mh);
             float* ml = part_ml(part, tok, kvh * GQ + h, s, H, ns, T);
             ml[0] = Mh;  // -inf when the token has no key in this split
-            ml[1] = cl[0][h] * ex2d(cm[0][h], Mh) + cl[1][h] * ex2d(cm[1][h], Mh) + cl[2][h] * ex2d(cm[2][h], Mh) +
-                    cl[3][h] * ex2d(cm[3][h], Mh);
+            ml[1] = lsum;
         }
     }
     if (rot) {
@@ -1148,11 +1159,11 @@ void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos
     if (kv.turbo) {
         static bool once = [] {
             MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_wst_kernel),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, WST_LDS));
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, WT_LDS));
             return true;
         }();
         (void)once;
-        hipLaunchKernelGGL(gqa_wst_kernel, dim3(KV * ns * T), dim3(64 * (WS_NC + WS_NP)), WST_LDS, st, qo, kv, H, pos_d,
+        hipLaunchKernelGGL(gqa_wst_kernel, dim3(KV * ns * T), dim3(64 * WT_NW), WT_LDS, st, qo, kv, H, pos_d,
                            max_t, part, T, ns, rot_out ? 1 : 0);
     } else {
         if (T == 1) {
