@@ -186,7 +186,9 @@ constexpr int W1_CH = 16 * WS_NC;                     // keys per chunk: 16 per 
 constexpr int W1_NS = 4;                              // stages: three chunks in flight, one being computed
 constexpr int W1_KB = W1_CH * AHD;                    // K rows of a stage; the V rows follow, then ks[64], vs[64]
 constexpr int W1_STAGE = ring_stage<W1_CH>();
-constexpr int W1_LDS = W1_NS * W1_STAGE;
+constexpr int W1_QT = W1_NS * W1_STAGE;              // query digit table: [digit 0, 1, 2][head][256] int8
+constexpr int W1_QS = W1_QT + 3 * GQ * AHD;             // the heads' score scales
+constexpr int W1_LDS = W1_QS + GQ * 4;
 static_assert(WS_NC * GQ * AHD * 4 <= W1_LDS, "the consumer merge fits in the stages");
 static_assert(W1_LDS <= 160 * 1024, "LDS");
 
@@ -210,42 +212,34 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws1_kernel(const 
     if (wv >= WS_NC) {
         ring_producer<W1_CH, W1_NS>(smem, kv, rbase, wv - WS_NC, lane, lo, first, nch);
     } else {
-        // ---- consumers. Query digits in registers: column m16 of the Q.K MFMA is head m16 / 2 (every head twice);
-        // lane (g, m16) holds dims 64 ks + 16 g .. +15 of it, the 4 lanes of a column together hold its 256 dims ----
-        int4_t_ qd[3][4];
-        float qs;
+        // ---- consumers. The query digits, once per workgroup: consumer w turns heads 2w, 2w + 1 (lane l: head
+        // 2w + l / 32, dims 8 (l % 32) .. + 7) into three signed base-256 digits of a 2^(22 - e) fixed point (|q| < 2^e
+        // over the head) in the digit table; after the first barrier every consumer takes its operands from it ----
         {
-            const float* qrow = qo + ((size_t)kvh * GQ + (m16 >> 1)) * AHD + 16 * g;
-            float4 qv4[16];
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-                for (int u = 0; u < 4; u++) qv4[4 * ks + u] = *reinterpret_cast<const float4*>(qrow + 64 * ks + 4 * u);
-            float qm = 0.f;
-#pragma unroll
-            for (int u = 0; u < 16; u++)
-                qm = fmaxf(fmaxf(qm, fmaxf(fabsf(qv4[u].x), fabsf(qv4[u].y))), fmaxf(fabsf(qv4[u].z), fabsf(qv4[u].w)));
-            qm = fmaxf(qm, __shfl_xor(qm, 16));
-            qm = fmaxf(qm, __shfl_xor(qm, 32));
+            const int h = 2 * wv + (lane >> 5), d0 = 8 * (lane & 31);
+            const float* qrow = qo + ((size_t)kvh * GQ + h) * AHD + d0;
+            const float4 qa = *reinterpret_cast<const float4*>(qrow), qb = *reinterpret_cast<const float4*>(qrow + 4);
+            float qm = fmaxf(fmaxf(fmaxf(fabsf(qa.x), fabsf(qa.y)), fmaxf(fabsf(qa.z), fabsf(qa.w))),
+                             fmaxf(fmaxf(fabsf(qb.x), fabsf(qb.y)), fmaxf(fabsf(qb.z), fabsf(qb.w))));
+            qm = max_x16(max_row16(qm));  // the 32 lanes of the head
             int e = 0;
             if (qm > 0.f) (void)frexpf(qm, &e);  // qm < 2^e
             const float up = ldexpf(1.f, 22 - e);
-            qs = ldexpf(1.f, e - 22) * SL2;
+            const float xv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+            int d[3][8];
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++)
+            for (int k = 0; k < 8; k++) digits3((int)__builtin_rintf(xv[k] * up), d[2][k], d[1][k], d[0][k]);
+            unsigned char* qt = smem + W1_QT + h * AHD + d0;
 #pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    const float4 x = qv4[4 * ks + u];
-                    int d[3][4];
-                    digits3((int)__builtin_rintf(x.x * up), d[2][0], d[1][0], d[0][0]);
-                    digits3((int)__builtin_rintf(x.y * up), d[2][1], d[1][1], d[0][1]);
-                    digits3((int)__builtin_rintf(x.z * up), d[2][2], d[1][2], d[0][2]);
-                    digits3((int)__builtin_rintf(x.w * up), d[2][3], d[1][3], d[0][3]);
-#pragma unroll
-                    for (int dig = 0; dig < 3; dig++)
-                        qd[dig][ks][u] = (int)pack_bytes(d[dig][0], d[dig][1], d[dig][2], d[dig][3]);
-                }
+            for (int dig = 0; dig < 3; dig++)
+                *reinterpret_cast<uint2*>(qt + dig * GQ * AHD) =
+                    make_uint2(pack_bytes(d[dig][0], d[dig][1], d[dig][2], d[dig][3]),
+                               pack_bytes(d[dig][4], d[dig][5], d[dig][6], d[dig][7]));
+            if ((lane & 31) == 0) reinterpret_cast<float*>(smem + W1_QS)[h] = ldexpf(1.f, e - 22) * SL2;
         }
+        // column m16 of the Q.K MFMA is head m16 / 2 (every head twice); lane (g, m16) holds dims 64 ks + 16 g .. + 15
+        int4_t_ qd[3][4];
+        float qs = 0.f;
         float4_t o[16];
 #pragma unroll
         for (int J = 0; J < 16; J++) o[J] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -253,7 +247,16 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws1_kernel(const 
         int sig = 0;
         const int kb = 16 * wv;  // this consumer's keys kb .. kb + 15 of every chunk
         for (int c = 0; c < nch; c++) {
-            __syncthreads();  // chunk c is in stage c % 4
+            __syncthreads();  // chunk c is in stage c % 4 (and, at c = 0, the digit table is complete)
+            if (c == 0) {
+#pragma unroll
+                for (int dig = 0; dig < 3; dig++)
+#pragma unroll
+                    for (int ks = 0; ks < 4; ks++)
+                        qd[dig][ks] = *reinterpret_cast<const int4_t_*>(smem + W1_QT + (dig * GQ + (m16 >> 1)) * AHD +
+                                                                        64 * ks + 16 * g);
+                qs = reinterpret_cast<const float*>(smem + W1_QS)[m16 >> 1];
+            }
             const int c0 = clo(c), ce = chi(c);
             if (c0 + kb >= ce) continue;
             const unsigned char* sb = smem + (c % W1_NS) * W1_STAGE;
@@ -736,13 +739,21 @@ __device__ __forceinline__ int4_t_ k_codes(uint2 x) {  // 16 nibbles -> the MFMA
 //     lane (g, n) decodes dims 8n .. 8n + 7 of both halves of keys 4g .. 4g + 3 straight from the raw rows (per key two
 //     16-bit words of low fields and two bytes of high bits): one v_perm LUT per 4 codes gives the codes biased by
 //     128, one v_perm per 2 codes the fp16-subnormal operand (as in the int8 kernels; the bias comes out at the end).
-constexpr int WT_NW = 8;                         // wavefronts
+#ifndef MOEX_WT_NW
+#define MOEX_WT_NW 8
+#define MOEX_WT_NS 4
+#endif
+#ifndef MOEX_WT_QREG
+#define MOEX_WT_QREG 1
+#endif
+constexpr int WT_NW = MOEX_WT_NW;                // wavefronts
 constexpr int WT_K = 16;                         // keys per wavefront and chunk
 constexpr int WT_CH = WT_K * WT_NW;              // keys per chunk
-constexpr int WT_NS = 4;                         // stages per wavefront
+constexpr int WT_NS = MOEX_WT_NS;                // stages per wavefront
 constexpr int WT_NRM = WT_K * TQ_KB;             // stage: K nibble rows at 0, then the norms (K pairs, V pairs)
-constexpr int WT_RV = WT_NRM + 2 * WT_K * 8;     // then the raw V rows
-constexpr int WT_STAGE = WT_RV + WT_K * TQ_VB;   // 3840 B
+constexpr int WT_RV = WT_NRM + 2 * WT_K * 8;     // then the raw V rows, at a 112-byte stride: the four rows that a
+constexpr int WT_VS = 112;                       // read spans (keys 4g + i, g = 0..3) start on distinct banks
+constexpr int WT_STAGE = WT_RV + WT_K * WT_VS;   // 4096 B
 constexpr int WT_PT = 2 * 16 * WT_K * 2;         // P tiles of a wavefront: two V halves of [16 rows][16 keys] fp16
 constexpr int WT_P0 = WT_NW * WT_NS * WT_STAGE;
 constexpr int WT_QT = WT_P0 + WT_NW * WT_PT;     // query digit table: [digit 2, 1, 0, zero][head][256] int8
@@ -750,7 +761,7 @@ constexpr int WT_QS = WT_QT + 4 * GQ * AHD;      // the heads' score scales
 constexpr int WT_LDS = WT_QS + GQ * 4;
 static_assert((WT_NW + 1) * GQ * AHD * 4 <= WT_P0, "the merge and the merged rows fit in the stages");
 static_assert(WT_LDS <= 160 * 1024, "LDS");
-static_assert(WT_NW == GQ, "one wavefront per head in the inverse rotation");
+static_assert(WT_NW >= GQ, "one wavefront per head for the query digits and the inverse rotation");
 
 // Sign tables of the inverse rotation (kernels.cuh:1123-1132, TQ_S1 / TQ_S2) as bit masks: bit j set = -1.
 constexpr uint32_t WS1[4] = {0xe46a0359u, 0x42f85949u, 0xa4c63bbbu, 0x49f250a9u};
@@ -824,10 +835,13 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
     };
     // five transfers per step: the 16 K rows (two of 8 rows; row r keeps 16-byte piece p in slot p ^ ((r / 2) % 8), so
     // the 8-byte reads of 16 rows at a 128-byte stride hit distinct banks), the norms (lanes 0-31 the K pairs, 32-63
-    // the V pairs) and the 1536 raw V bytes (1 KB, then 512 B from lanes 0-31); past the chunk's end keys are clamped
+    // the V pairs) and the raw V rows: 16-byte slot t (of 7 per row, the seventh a copy of the sixth) from row t / 7,
+    // piece min(t % 7, 5), by all lanes and then lanes 0-47; past the chunk's end keys are clamped
     const int kr0 = lane >> 3, kr1 = 8 + (lane >> 3);
     const uint32_t ko0 = kr0 * TQ_KB + 16 * ((lane & 7) ^ ((kr0 >> 1) & 7));
     const uint32_t ko1 = kr1 * TQ_KB + 16 * ((lane & 7) ^ ((kr1 >> 1) & 7));
+    const int vt1 = 64 + lane;
+    const uint32_t vo0 = (lane / 7) * TQ_VB + 16 * min(lane % 7, 5), vo1 = (vt1 / 7) * TQ_VB + 16 * min(vt1 % 7, 5);
     auto issue = [&](int j) {
         int k0, ke;
         keys(j, k0, ke);
@@ -839,18 +853,15 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
             dma16s(kb, ko0, st);
             dma16s(kb, ko1, st + 1024);
             dma4(nsrc + 2 * (size_t)k0 + (lane & 31), st + WT_NRM);
-            dma16s(vb, 16 * lane, st + WT_RV);
-            if (lane < 32) dma16s(vb, 1024 + 16 * lane, st + WT_RV + 1024);
+            dma16s(vb, vo0, st + WT_RV);
+            if (lane < 48) dma16s(vb, vo1, st + WT_RV + 1024);
         } else {
             dma16(Kg + (size_t)min(k0 + kr0, ke - 1) * TQ_KB + (ko0 - kr0 * TQ_KB), st);
             dma16(Kg + (size_t)min(k0 + kr1, ke - 1) * TQ_KB + (ko1 - kr1 * TQ_KB), st + 1024);
             dma4(nsrc + 2 * (size_t)min(k0 + ((lane & 31) >> 1), ke - 1) + (lane & 1), st + WT_NRM);
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const int b = 1024 * i + 16 * lane, r = b / TQ_VB;
-                if (i == 0 || lane < 32)
-                    dma16(Vg + (size_t)min(k0 + r, ke - 1) * TQ_VB + (b - r * TQ_VB), st + WT_RV + 1024 * i);
-            }
+            dma16(Vg + (size_t)min(k0 + lane / 7, ke - 1) * TQ_VB + (vo0 - (lane / 7) * TQ_VB), st + WT_RV);
+            if (lane < 48)
+                dma16(Vg + (size_t)min(k0 + vt1 / 7, ke - 1) * TQ_VB + (vo1 - (vt1 / 7) * TQ_VB), st + WT_RV + 1024);
         }
     };
     // step j's operands from its stage into registers: the K nibbles of key m16 (per MFMA ks), its norm pairs, and
@@ -873,7 +884,7 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             typedef unsigned short us2_t __attribute__((ext_vector_type(2)));
-            const unsigned char* row = st + WT_RV + (4 * g + i) * TQ_VB;
+            const unsigned char* row = st + WT_RV + (4 * g + i) * WT_VS;
             r.vw[i] = __builtin_bit_cast(uint32_t, us2_t{*reinterpret_cast<const unsigned short*>(row + 2 * m16),
                                                          *reinterpret_cast<const unsigned short*>(row + 32 + 2 * m16)});
             r.vx[i] = __builtin_bit_cast(uint32_t, us2_t{row[64 + m16], row[80 + m16]});
@@ -891,14 +902,10 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
     // ---- query digits, once per workgroup: wavefront w turns head w (lane l: dims 4l .. 4l + 3) into three signed
     // base-256 digits of a 2^(22 - e) fixed point (|q| < 2^e over the head) and writes them to the digit table in
     // the operand order: dim d at byte 16 (d / 16) + pos(d % 16), pos = the K codes' order {0,2,4,6, 1,3,5,7, 8,..} ----
-    {
+    if (wv < GQ) {
         const float4 q4 = *reinterpret_cast<const float4*>(qo + ((size_t)tok * H + kvh * GQ + wv) * AHD + 4 * lane);
         float qm = fmaxf(fmaxf(fabsf(q4.x), fabsf(q4.y)), fmaxf(fabsf(q4.z), fabsf(q4.w)));
         qm = max_x32(max_x16(max_row16(qm)));
-        // the first steps' transfers go out while the digits are formed (the query rows have arrived)
-#pragma unroll
-        for (int j = 0; j < WT_NS - 1; j++)
-            if (j < nst) issue(j);
         int e = 0;
         if (qm > 0.f) (void)frexpf(qm, &e);  // qm < 2^e
         const float up = ldexpf(1.f, 22 - e);
@@ -917,19 +924,23 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
         reinterpret_cast<uint32_t*>(qt + 3 * GQ * AHD)[lane] = 0u;  // the zero rows
         if (lane == 0) reinterpret_cast<float*>(smem + WT_QS)[wv] = ldexpf(1.f, e - 22) * (SL2 * TK4);
     }
+    // the first steps' transfers (the compiler's wait for the query rows above does not cover them)
+#pragma unroll
+    for (int j = 0; j < WT_NS - 1; j++)
+        if (j < nst) issue(j);
     __syncthreads();
     // the A operand of MFMA ks: lane (g, m16) holds the 16 bytes of dims 64 ks + 16 g .. + 15 of its row, digit m16 % 4
     // of head m16 / 4 (qx) and of head m16 / 4 + 4 (qy)
     const int dg = m16 & 3, hr = m16 >> 2;
+    const unsigned char* qtx = smem + WT_QT + (dg * GQ + hr) * AHD + 16 * g;  // head hr; head hr + 4 at + 4 * AHD
+#if MOEX_WT_QREG
     int4_t_ qx[4], qy[4];
-    {
-        const unsigned char* qt = smem + WT_QT + dg * GQ * AHD;
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            qx[ks] = *reinterpret_cast<const int4_t_*>(qt + hr * AHD + 64 * ks + 16 * g);
-            qy[ks] = *reinterpret_cast<const int4_t_*>(qt + (hr + 4) * AHD + 64 * ks + 16 * g);
-        }
+    for (int ks = 0; ks < 4; ks++) {
+        qx[ks] = *reinterpret_cast<const int4_t_*>(qtx + 64 * ks);
+        qy[ks] = *reinterpret_cast<const int4_t_*>(qtx + 4 * AHD + 64 * ks);
     }
+#endif
     const float qsA = reinterpret_cast<const float*>(smem + WT_QS)[g];
     const float qsB = reinterpret_cast<const float*>(smem + WT_QS)[g + 4];  // the lane's score heads g and g + 4
     float4_t o[16];  // o[8 h + b]: rows 4g .. 4g + 3 (hi rows for g < 2, lo rows for g >= 2), column m16: dim 128h + 8 m16 + b
@@ -940,14 +951,12 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
     float xA0 = 0.f, xA1 = 0.f, xB0 = 0.f, xB1 = 0.f;
     int sig = 0;
     unsigned char* Pt = smem + WT_P0 + wv * WT_PT;  // [V half][row 8 hl + h][16 keys] fp16
-    StepRegs cur;
-    if (nst > 0) {
-        wait_step(0, WT_NS - 2);
-        load_regs(0, cur);
-    }
     for (int j = 0; j < nst; j++) {
-        // step j + 3 goes to the stage of step j - 1, whose operands are in registers already
+        // step j + WT_NS - 1 goes to the stage of step j - 1, which this wavefront has read
         if (j + WT_NS - 1 < nst) issue(j + WT_NS - 1);
+        wait_step(j, WT_NS - 1);
+        StepRegs cur;
+        load_regs(j, cur);
         int k0, ke;
         keys(j, k0, ke);
         // ---- K codes and Q.K: [128-dim half], heads g (sx) and g + 4 (sy) against key m16 ----
@@ -956,14 +965,14 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             const int4_t_ b = k_codes(cur.nib[ks]);
-            sx[ks >> 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qx[ks], b, sx[ks >> 1], 0, 0, 0);
-            sy[ks >> 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qy[ks], b, sy[ks >> 1], 0, 0, 0);
-        }
-        // the next step's operands start on their way while this step computes
-        StepRegs nxt;
-        if (j + 1 < nst) {
-            wait_step(j + 1, WT_NS - 2);
-            load_regs(j + 1, nxt);
+#if MOEX_WT_QREG
+            const int4_t_ ax = qx[ks], ay = qy[ks];
+#else
+            const int4_t_ ax = *reinterpret_cast<const int4_t_*>(qtx + 64 * ks);
+            const int4_t_ ay = *reinterpret_cast<const int4_t_*>(qtx + 4 * AHD + 64 * ks);
+#endif
+            sx[ks >> 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, b, sx[ks >> 1], 0, 0, 0);
+            sy[ks >> 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ay, b, sy[ks >> 1], 0, 0, 0);
         }
         const float2 kn = cur.kn, vn = cur.vn;
         // ---- scores: per half d2 * 65536 + (d1 * 256 + d0), the latter exact in int32 (|d1 * 256 + d0| < 2^30) ----
@@ -1050,7 +1059,6 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
                 o[8 * h + b] = __builtin_amdgcn_mfma_f32_16x16x16f16(h ? pa1 : pa0, __builtin_bit_cast(half4_t, vb),
                                                                     o[8 * h + b], 0, 0, 0);
             }
-        cur = nxt;
     }
     // ---- merge the eight wavefronts: m, l per head, then O rows (hi + lo) scaled to the common maximum ----
     const float lAs = sum_row16(lA), lBs = sum_row16(lB);
@@ -1122,6 +1130,7 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
         // stage 64 in the lane), in the order of the reference's inverse: x S2, butterflies, / sqrt(128), x S1
         __syncthreads();
         const int h = wv;
+        if (h >= GQ) return;
         float* dst = part_acc(part, tok, kvh * GQ + h, s, H, ns);
 #pragma unroll
         for (int b = 0; b < 2; b++) {
