@@ -40,6 +40,8 @@ def main():
     ap.add_argument("--decode-only", action="store_true",
                     help="only the configs[2] and configs[3] decode timings (for counter runs); prints their JSON")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--config4-only", action="store_true",
+                    help="only the configs[4] prefill calls (for counter runs; prints no JSON line)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     a = ap.parse_args()
@@ -138,10 +140,10 @@ def main():
         M.attn_fa(qo, qg, c8, out, H, KV, pos_d, c8.max_t, LD, T, st)
 
     threads = cpu_threads()
-    want_cpu = not a.no_cpu and not a.decode_only
+    want_cpu = not a.no_cpu and not a.decode_only and not a.config4_only
     hc8 = host_cache(c8, n) if want_cpu else None
     qh, gh = (qo.cpu().numpy(), qg.cpu().numpy()) if want_cpu else (None, None)
-    if not a.decode_only:
+    if not a.decode_only and not a.config4_only:
         ms, wall_ms = time_steps(prefill, a.steps, a.warmup)
         tflops = flops_prefill(T, pos0) / (ms * 1e-3) / 1e12
         print(f"[bench] config1 int8 prefill T={T} pos0={pos0}: {ms:.3f} ms/step, {tflops:.1f} TFLOPS "
@@ -155,7 +157,7 @@ def main():
     extra = {}
     if not a.quick:
         # ---------------- config 0: pos0 = 0 ----------------
-        if not a.decode_only:
+        if not a.decode_only and not a.config4_only:
             pz = torch.tensor([0], dtype=torch.int32, device=dev)
             ms0, _ = time_steps(lambda: M.attn_fa(qo, qg, c8, out, H, KV, pz, c8.max_t, LD, T, st), 10, 3)
             extra["config0_prefill_int8"] = {"ms": round(ms0, 4),
@@ -169,11 +171,11 @@ def main():
         ctx = 90000
         NROT = 4  # 4 x 93.6 MB of KV > MALL
         rot = []
-        for i in range(NROT):
+        for i in range(0 if a.config4_only else NROT):
             c = M.DeviceKVCache(KV, ctx + 64, 0)
             fill_cache(c, ctx, seed=20 + i)
             rot.append(c)
-        for Tq in (1, 4):
+        for Tq in (() if a.config4_only else (1, 4)):
             ns = M.gqa_splits(Tq, KV, M.decode_splits(ctx))
             part = torch.empty(Tq * H * ns * (AHD + 2), device=dev)
             o1 = torch.empty((Tq, H, AHD), device=dev)
@@ -241,7 +243,7 @@ def main():
             M.attn_gqa_out(qo[:1], ct, H, KV, pd, ct.max_t, part, 1, ns, st)
             M.attn_combine(part, qg[:1], o1, H, ns, LD, 1, st)
 
-        t_td = time_rotating([tdec, lambda: flush_read.sum()], 20) * 2 - t_flush
+        t_td = time_rotating([tdec, lambda: flush_read.sum()], 1 if a.config4_only else 20) * 2 - t_flush
         tb = 2.0 * ctx * 240
         extra["config3_decode_turbo_262k"] = {"ns": ns, "us": round(t_td * 1e3, 2),
                                               "GBps": round(tb / (t_td * 1e-3) / 1e9, 1)}
@@ -265,6 +267,8 @@ def main():
         print(f"[bench] config4 prefill at 260096: turbo {ms_t:.2f} ms ({f4 / ms_t / 1e9:.0f} TFLOPS), "
               f"int8 {ms_i:.2f} ms ({f4 / ms_i / 1e9:.0f} TFLOPS)", flush=True)
         del ct
+        if a.config4_only:
+            return
         # ---------------- dense int8 projections either side of the attention ----------------
         dense = {}
         for nm, O_, I_ in (("qkv", H * 2 * AHD + 2 * KV * AHD, 2048), ("o_proj", 2048, H * AHD)):
