@@ -951,6 +951,31 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
     float xA0 = 0.f, xA1 = 0.f, xB0 = 0.f, xB1 = 0.f;
     int sig = 0;
     unsigned char* Pt = smem + WT_P0 + wv * WT_PT;  // [V half][row 8 hl + h][16 keys] fp16
+    // O += P . V of one step: block (h, b), operand half k = key 4g + k
+    auto pv = [&](const uint32_t (&cd)[4][4], const half4_t& pa0, const half4_t& pa1) {
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int b = 0; b < 8; b++) {
+                const int f = b & 3, by = 2 * h + (b >> 2);  // dim 8 m16 + b of half h: code 8h + b, word f, byte by
+                const uint32_t sel = (uint32_t)by | 0x0c00u | ((uint32_t)(4 + by) << 16) | 0x0c000000u;
+                typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+                const u32x2_t vb = {__builtin_amdgcn_perm(cd[1][f], cd[0][f], sel),
+                                    __builtin_amdgcn_perm(cd[3][f], cd[2][f], sel)};
+                o[8 * h + b] = __builtin_amdgcn_mfma_f32_16x16x16f16(h ? pa1 : pa0, __builtin_bit_cast(half4_t, vb),
+                                                                    o[8 * h + b], 0, 0, 0);
+            }
+    };
+    // P.V runs one step behind: step j's runs among step j + 1's K decode and Q.K (MFMA and VALU work of one
+    // wavefront overlap when interleaved), from its V codes and P kept in registers; before step 0 it adds zeros
+    uint32_t cdp[4][4];
+    half4_t pp0, pp1;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int f = 0; f < 4; f++) cdp[i][f] = 0x80808080u;
+#pragma unroll
+    for (int i = 0; i < 4; i++) pp0[i] = pp1[i] = (_Float16)0.f;
     for (int j = 0; j < nst; j++) {
         // step j + WT_NS - 1 goes to the stage of step j - 1, which this wavefront has read
         if (j + WT_NS - 1 < nst) issue(j + WT_NS - 1);
@@ -974,6 +999,7 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
             sx[ks >> 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, b, sx[ks >> 1], 0, 0, 0);
             sy[ks >> 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ay, b, sy[ks >> 1], 0, 0, 0);
         }
+        pv(cdp, pp0, pp1);  // step j - 1
         const float2 kn = cur.kn, vn = cur.vn;
         // ---- scores: per half d2 * 65536 + (d1 * 256 + d0), the latter exact in int32 (|d1 * 256 + d0| < 2^30) ----
         float scA, scB;
@@ -1040,26 +1066,13 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
                 pr[24 * WT_K] = (_Float16)(x1 - (float)h1);
             }
         }
-        // P operand rows m16, keys 4g .. 4g + 3
-        const half4_t pa0 = *reinterpret_cast<const half4_t*>(Pt + (m16 * WT_K + 4 * g) * 2);
-        const half4_t pa1 = *reinterpret_cast<const half4_t*>(Pt + ((16 + m16) * WT_K + 4 * g) * 2);
-        // ---- V codes of the 4 keys, then O += P . V: block (h, b), operand half k = key 4g + k ----
-        uint32_t cd[4][4];
+        // P operand rows m16, keys 4g .. 4g + 3, and the V codes of the 4 keys, for the next step's P.V
+        pp0 = *reinterpret_cast<const half4_t*>(Pt + (m16 * WT_K + 4 * g) * 2);
+        pp1 = *reinterpret_cast<const half4_t*>(Pt + ((16 + m16) * WT_K + 4 * g) * 2);
 #pragma unroll
-        for (int i = 0; i < 4; i++) v_codes16(cur.vw[i], cur.vx[i], cd[i]);
-#pragma unroll
-        for (int h = 0; h < 2; h++)
-#pragma unroll
-            for (int b = 0; b < 8; b++) {
-                const int f = b & 3, by = 2 * h + (b >> 2);  // dim 8 m16 + b of half h: code 8h + b, word f, byte by
-                const uint32_t sel = (uint32_t)by | 0x0c00u | ((uint32_t)(4 + by) << 16) | 0x0c000000u;
-                typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-                const u32x2_t vb = {__builtin_amdgcn_perm(cd[1][f], cd[0][f], sel),
-                                    __builtin_amdgcn_perm(cd[3][f], cd[2][f], sel)};
-                o[8 * h + b] = __builtin_amdgcn_mfma_f32_16x16x16f16(h ? pa1 : pa0, __builtin_bit_cast(half4_t, vb),
-                                                                    o[8 * h + b], 0, 0, 0);
-            }
+        for (int i = 0; i < 4; i++) v_codes16(cur.vw[i], cur.vx[i], cdp[i]);
     }
+    pv(cdp, pp0, pp1);  // the last step
     // ---- merge the eight wavefronts: m, l per head, then O rows (hi + lo) scaled to the common maximum ----
     const float lAs = sum_row16(lA), lBs = sum_row16(lB);
     // the V operands were (code + 128) * 2^-24: O = 2^24 o - 128 * sum(P * vn * K3 * 2^sig), per head and V half
