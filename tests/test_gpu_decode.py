@@ -123,6 +123,24 @@ def test_gqa_out_turbo(turbo_setup, pos0, T, ns):
     _check(f"gqa_out turbo ns={ns}", out.cpu().numpy(), qo, qg, hc, pos0, T)
 
 
+@pytest.mark.parametrize("pos0,T,ns", [(127, 1, 1), (128, 1, 1), (200, 1, 1), (2047, 3, 2), (39999, 1, 1),
+                                       (16383, 1, 7)])
+def test_gqa_turbo_steps(turbo_setup, pos0, T, ns):
+    """The turbo split kernel's key assignment: chunks of 128 keys, chunk 0 the short one, wavefront w taking keys
+    16w .. 16w + 15 of each chunk. 128 keys: one full chunk; 129: a one-key first chunk that seven wavefronts skip; 201:
+    a first chunk that ends inside wavefront 4's keys; one split over 40000 keys (313 chunks through each wavefront's
+    four-stage ring); a three-token window; splits of 2341 keys."""
+    import torch
+    import moex_amd as M
+    hc, dc, qo, qg = turbo_setup
+    part = torch.empty(T * H * ns * (AHD + 2), dtype=torch.float32, device="cuda")
+    out = torch.zeros((T, H, AHD), dtype=torch.float32, device="cuda")
+    M.attn_gqa_out(dev(qo[:T]), dc, H, KV, pos_tensor(pos0), dc.max_t, part, T, ns)
+    M.attn_combine(part, dev(qg[:T]), out, H, ns, LD, T)
+    torch.cuda.synchronize()
+    _check(f"gqa_out turbo steps ns={ns}", out.cpu().numpy(), qo, qg, hc, pos0, T)
+
+
 @pytest.mark.parametrize("pos0,T,ns", [(0, 1, 1), (1000, 2, 8)])
 def test_decode_heads_turbo(turbo_setup, pos0, T, ns):
     import torch
