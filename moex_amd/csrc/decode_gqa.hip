@@ -739,17 +739,10 @@ __device__ __forceinline__ int4_t_ k_codes(uint2 x) {  // 16 nibbles -> the MFMA
 //     lane (g, n) decodes dims 8n .. 8n + 7 of both halves of keys 4g .. 4g + 3 straight from the raw rows (per key two
 //     16-bit words of low fields and two bytes of high bits): one v_perm LUT per 4 codes gives the codes biased by
 //     128, one v_perm per 2 codes the fp16-subnormal operand (as in the int8 kernels; the bias comes out at the end).
-#ifndef MOEX_WT_NW
-#define MOEX_WT_NW 8
-#define MOEX_WT_NS 4
-#endif
-#ifndef MOEX_WT_QREG
-#define MOEX_WT_QREG 1
-#endif
-constexpr int WT_NW = MOEX_WT_NW;                // wavefronts
+constexpr int WT_NW = 8;                         // wavefronts
 constexpr int WT_K = 16;                         // keys per wavefront and chunk
 constexpr int WT_CH = WT_K * WT_NW;              // keys per chunk
-constexpr int WT_NS = MOEX_WT_NS;                // stages per wavefront
+constexpr int WT_NS = 4;                         // stages per wavefront
 constexpr int WT_NRM = WT_K * TQ_KB;             // stage: K nibble rows at 0, then the norms (K pairs, V pairs)
 constexpr int WT_RV = WT_NRM + 2 * WT_K * 8;     // then the raw V rows, at a 112-byte stride: the four rows that a
 constexpr int WT_VS = 112;                       // read spans (keys 4g + i, g = 0..3) start on distinct banks
@@ -761,7 +754,7 @@ constexpr int WT_QS = WT_QT + 4 * GQ * AHD;      // the heads' score scales
 constexpr int WT_LDS = WT_QS + GQ * 4;
 static_assert((WT_NW + 1) * GQ * AHD * 4 <= WT_P0, "the merge and the merged rows fit in the stages");
 static_assert(WT_LDS <= 160 * 1024, "LDS");
-static_assert(WT_NW >= GQ, "one wavefront per head for the query digits and the inverse rotation");
+static_assert(WT_NW == GQ, "one wavefront per head for the query digits and the inverse rotation");
 
 // Sign tables of the inverse rotation (kernels.cuh:1123-1132, TQ_S1 / TQ_S2) as bit masks: bit j set = -1.
 constexpr uint32_t WS1[4] = {0xe46a0359u, 0x42f85949u, 0xa4c63bbbu, 0x49f250a9u};
@@ -902,7 +895,7 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
     // ---- query digits, once per workgroup: wavefront w turns head w (lane l: dims 4l .. 4l + 3) into three signed
     // base-256 digits of a 2^(22 - e) fixed point (|q| < 2^e over the head) and writes them to the digit table in
     // the operand order: dim d at byte 16 (d / 16) + pos(d % 16), pos = the K codes' order {0,2,4,6, 1,3,5,7, 8,..} ----
-    if (wv < GQ) {
+    {
         const float4 q4 = *reinterpret_cast<const float4*>(qo + ((size_t)tok * H + kvh * GQ + wv) * AHD + 4 * lane);
         float qm = fmaxf(fmaxf(fabsf(q4.x), fabsf(q4.y)), fmaxf(fabsf(q4.z), fabsf(q4.w)));
         qm = max_x32(max_x16(max_row16(qm)));
@@ -932,15 +925,14 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
     // the A operand of MFMA ks: lane (g, m16) holds the 16 bytes of dims 64 ks + 16 g .. + 15 of its row, digit m16 % 4
     // of head m16 / 4 (qx) and of head m16 / 4 + 4 (qy)
     const int dg = m16 & 3, hr = m16 >> 2;
+    // (kept in registers: re-reading them from LDS every step measured 4 us slower)
     const unsigned char* qtx = smem + WT_QT + (dg * GQ + hr) * AHD + 16 * g;  // head hr; head hr + 4 at + 4 * AHD
-#if MOEX_WT_QREG
     int4_t_ qx[4], qy[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
         qx[ks] = *reinterpret_cast<const int4_t_*>(qtx + 64 * ks);
         qy[ks] = *reinterpret_cast<const int4_t_*>(qtx + 4 * AHD + 64 * ks);
     }
-#endif
     const float qsA = reinterpret_cast<const float*>(smem + WT_QS)[g];
     const float qsB = reinterpret_cast<const float*>(smem + WT_QS)[g + 4];  // the lane's score heads g and g + 4
     float4_t o[16];  // o[8 h + b]: rows 4g .. 4g + 3 (hi rows for g < 2, lo rows for g >= 2), column m16: dim 128h + 8 m16 + b
@@ -990,14 +982,8 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             const int4_t_ b = k_codes(cur.nib[ks]);
-#if MOEX_WT_QREG
-            const int4_t_ ax = qx[ks], ay = qy[ks];
-#else
-            const int4_t_ ax = *reinterpret_cast<const int4_t_*>(qtx + 64 * ks);
-            const int4_t_ ay = *reinterpret_cast<const int4_t_*>(qtx + 4 * AHD + 64 * ks);
-#endif
-            sx[ks >> 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, b, sx[ks >> 1], 0, 0, 0);
-            sy[ks >> 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ay, b, sy[ks >> 1], 0, 0, 0);
+            sx[ks >> 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qx[ks], b, sx[ks >> 1], 0, 0, 0);
+            sy[ks >> 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qy[ks], b, sy[ks >> 1], 0, 0, 0);
         }
         pv(cdp, pp0, pp1);  // step j - 1
         const float2 kn = cur.kn, vn = cur.vn;
@@ -1143,7 +1129,6 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
         // stage 64 in the lane), in the order of the reference's inverse: x S2, butterflies, / sqrt(128), x S1
         __syncthreads();
         const int h = wv;
-        if (h >= GQ) return;
         float* dst = part_acc(part, tok, kvh * GQ + h, s, H, ns);
 #pragma unroll
         for (int b = 0; b < 2; b++) {
