@@ -215,8 +215,16 @@ namespace {
 void decode_step(const float* q, const float* k, const float* v, const uint16_t* qn, const uint16_t* kn, float* qo,
                  moex_kv_cache kv, float* out, int H, int KV, const int* pos_d, int max_t, int rot, float theta,
                  float eps, int T, int ld, hipStream_t st, float* part, int ns, float* fa_scr, size_t fa_bytes) {
-    launch_qk_norm_rope(q, k, v, qn, kn, qo, kv, H, KV, pos_d, max_t, rot, theta, eps, ld, T, st);
     const int G = H / KV;
+    if (T == 1 && ns > 1 && G == GQ && !kv.turbo) {
+        // one int8 token: the split kernel runs the q/k front in its prologue (one launch fewer per step)
+        const FrontArgs fr{q, k, v, qn, kn, qo, skip_flag(), rot, theta, eps, ld};
+        ns = gqa_splits(T, KV, ns, false);
+        launch_gqa(qo, kv, H, KV, pos_d, max_t, part, T, ns, st, false, &fr);
+        launch_combine(part, q, out, H, ns, ld, T, st);
+        return;
+    }
+    launch_qk_norm_rope(q, k, v, qn, kn, qo, kv, H, KV, pos_d, max_t, rot, theta, eps, ld, T, st);
     const float* gate = kv.turbo ? nullptr : q;  // turbo: gated after the inverse rotation
     if (T > 2 && ns == 1 && G == GQ && (moex_fa_on() || kv.turbo) && moex_fa_supported()) {
         if (fa_scr) launch_fa_scratch(qo, gate, kv, out, H, KV, pos_d, max_t, ld, T, st, fa_scr, fa_bytes);

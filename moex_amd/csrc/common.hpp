@@ -69,6 +69,22 @@ __device__ __forceinline__ float* part_ml(float* part, int t, int h, int s, int 
     return part + (size_t)T * H * ns * AHD + (((size_t)t * H + h) * ns + s) * 2;
 }
 
+// The q/k front's inputs (attn_decode's q, k, v, qn, kn, qo, rot, theta, eps, ld) when a decode kernel runs the front
+// in its own prologue instead of after a separate qk_norm_rope launch, and the graph-fallback flag it honours.
+struct FrontArgs {
+    const float* q;
+    const float* k;
+    const float* v;
+    const uint16_t* qn;
+    const uint16_t* kn;
+    float* qo;
+    const int* skip;
+    int rot;
+    float theta;
+    float eps;
+    int ld;
+};
+
 }  // namespace moex
 
 // ---- internal launchers (each defined in its .hip file; argument checks happen in api.cpp) ----
@@ -88,8 +104,12 @@ void launch_set_skip(int v, hipStream_t st);
 int gqa_splits(int T, int KV, int ns, bool turbo);
 // rot_out (turbo caches): the partials come out rotated back to the output domain, for a gated combine with no
 // turbo_out after it
+// fr (int8, T = 1): the split kernel runs the q/k front itself (query rows, the new K/V row appended to the cache) and
+// writes qo; without it qo must hold the front's output already
 void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part, int T,
-                int ns, hipStream_t st, bool rot_out = false);
+                int ns, hipStream_t st, bool rot_out = false, const FrontArgs* fr = nullptr);
+// this device's graph-fallback flag (g_skip, kernels.cuh:46), for kernels of other files; nullptr if unavailable
+const int* skip_flag();
 void launch_fa(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d,
                int max_t, int ld, int T, hipStream_t st);
 // dense int8 projections (dense.hip)

@@ -5,7 +5,7 @@
 // consumer wavefronts compute), gqa_wsp_kernel for MTP-verify windows (token pairs on the same pipeline).
 // gqa_wst_kernel serves the TurboQuant cache, one token per workgroup, on eight symmetric wavefronts that each stream
 // and decode their own keys. The partial written per (token, head, split) is {m (log2 units), l, acc[256]}.
-#include "common.hpp"
+#include "front.hpp"
 
 namespace moex {
 
@@ -132,12 +132,34 @@ constexpr float WS_SLACK = 8.f;
 // that hands chunk c to the consumers (its stage held chunk c - 1, now consumed); the producers end each chunk with a
 // bare s_barrier, as __syncthreads would also wait for the chunks still in flight. Takes part in the nch + 2
 // barriers of the chunk loop and the consumer merge.
+// LDS transfers of 16 (4) bytes per active lane, lane l to lds + 16 l (4 l), written in inline asm: the compiler cannot
+// tell which LDS bytes a transfer writes and would make the wavefront's next LDS read wait for every transfer in
+// flight; the kernel waits for its own transfers with vm_wait. dma16s: wave-uniform base + per-lane 32-bit offset.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved: every other use of it in this kernel sets it first
+__device__ __forceinline__ void dma16(const void* g, const unsigned char* lds) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m) : "memory", "m0");
+}
+__device__ __forceinline__ void dma16s(const void* base, uint32_t off, const unsigned char* lds) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* g, const unsigned char* lds) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+template <int N> __device__ __forceinline__ void vm_wait() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
 template <int CH>
 constexpr int ring_stage() { return 2 * CH * AHD + 2 * CH * 4; }
 
+// chunk c of the ring into stage c % NS (the producers' transfers of it)
 template <int CH, int NS>
-__device__ __forceinline__ void ring_producer(unsigned char* smem, const moex_kv_cache& kv, size_t rbase, int pw,
-                                              int lane, int lo, int first, int nch) {
+__device__ __forceinline__ void ring_issue(unsigned char* smem, const moex_kv_cache& kv, size_t rbase, int pw, int lane,
+                                           int lo, int first, int c) {
     static_assert((CH == 64 || CH == 128) && NS >= 2 && NS <= 4, "ring shape");
     constexpr int KB = CH * AHD, STAGE = ring_stage<CH>(), NI = CH / 8;
     constexpr bool SC_ALL = CH == 128;
@@ -145,32 +167,58 @@ __device__ __forceinline__ void ring_producer(unsigned char* smem, const moex_kv
     const int8_t* src = (pw < 2 ? kv.k : kv.v) + rbase * AHD;
     const float* ssrc = (pw < 2 ? kv.ks : kv.vs) + rbase;
     const int r4 = lane >> 4, sl = lane & 15;
-    auto issue = [&](int c) {
-        const int c0 = c == 0 ? lo : lo + first + (c - 1) * CH, ce = c == 0 ? lo + first : lo + first + c * CH;
-        unsigned char* st = smem + (c % NS) * STAGE;
-        unsigned char* sb = st + (pw < 2 ? 0 : KB);
+    const int c0 = c == 0 ? lo : lo + first + (c - 1) * CH, ce = c == 0 ? lo + first : lo + first + c * CH;
+    unsigned char* st = smem + (c % NS) * STAGE;
+    unsigned char* sb = st + (pw < 2 ? 0 : KB);
 #pragma unroll
-        for (int u = 0; u < NI; u++) {
-            const int i = NI * (pw & 1) + u, r = 4 * i + r4;  // instruction i covers rows 4i .. 4i+3
-            const int piece = pw < 2 ? sl ^ (r & 15) : sl ^ (4 * (i & 3));
-            __builtin_amdgcn_global_load_lds((gptr_t)(src + (size_t)min(c0 + r, ce - 1) * AHD + 16 * piece),
-                                             (lptr_t)(sb + i * 1024), 16, 0, 0);
-        }
-        if (sc) {
-            const int k0 = SC_ALL ? 64 * (pw & 1) : 0;
-            __builtin_amdgcn_global_load_lds((gptr_t)(ssrc + min(c0 + k0 + lane, ce - 1)),
-                                             (lptr_t)(st + 2 * KB + (pw < 2 ? 0 : 4 * CH) + 4 * k0), 4, 0, 0);
-        }
-    };
-    for (int c = 0; c < NS - 1 && c < nch; c++) issue(c);
+    for (int u = 0; u < NI; u++) {
+        const int i = NI * (pw & 1) + u, r = 4 * i + r4;  // instruction i covers rows 4i .. 4i+3
+        const int piece = pw < 2 ? sl ^ (r & 15) : sl ^ (4 * (i & 3));
+        dma16(src + (size_t)min(c0 + r, ce - 1) * AHD + 16 * piece, sb + i * 1024);
+    }
+    if (sc) {
+        const int k0 = SC_ALL ? 64 * (pw & 1) : 0;
+        dma4(ssrc + min(c0 + k0 + lane, ce - 1), st + 2 * KB + (pw < 2 ? 0 : 4 * CH) + 4 * k0);
+    }
+}
+// the first NS - 1 chunks
+template <int CH, int NS>
+__device__ __forceinline__ void ring_first(unsigned char* smem, const moex_kv_cache& kv, size_t rbase, int pw, int lane,
+                                           int lo, int first, int nch) {
+    for (int c = 0; c < NS - 1 && c < nch; c++) ring_issue<CH, NS>(smem, kv, rbase, pw, lane, lo, first, c);
+}
+// issued: the first chunks went out already (ring_first). ppos >= 0: the cache row at position ppos was just formed
+// by this workgroup (patch: K row, V row, ks, vs in LDS) and may not have reached memory when its chunk was moved; the
+// producer that moved each part of that row overwrites it in the stage once the chunk has landed.
+template <int CH, int NS>
+__device__ __forceinline__ void ring_producer(unsigned char* smem, const moex_kv_cache& kv, size_t rbase, int pw,
+                                              int lane, int lo, int first, int nch, bool issued = false, int ppos = -1,
+                                              const unsigned char* patch = nullptr) {
+    constexpr int KB = CH * AHD, STAGE = ring_stage<CH>(), NI = CH / 8;
+    constexpr bool SC_ALL = CH == 128;
+    const bool sc = SC_ALL || !(pw & 1);
+    if (!issued) ring_first<CH, NS>(smem, kv, rbase, pw, lane, lo, first, nch);
     for (int c = 0; c < nch; c++) {
         // chunk c has landed when at most the chunks issued after it are in flight (NI or NI + 1 instructions each)
         const int after = min(nch - 1 - c, NS - 2);
-        if (after == 0) wait_vm<0>();
-        else if (sc) { if (after == 1) wait_vm<NI + 1>(); else wait_vm<2 * (NI + 1)>(); }
-        else { if (after == 1) wait_vm<NI>(); else wait_vm<2 * NI>(); }
+        if (after == 0) vm_wait<0>();
+        else if (sc) { if (after == 1) vm_wait<NI + 1>(); else vm_wait<2 * (NI + 1)>(); }
+        else { if (after == 1) vm_wait<NI>(); else vm_wait<2 * NI>(); }
+        const int c0 = c == 0 ? lo : lo + first + (c - 1) * CH, ce = c == 0 ? lo + first : lo + first + c * CH;
+        if (ppos >= c0 && ppos < ce) {
+            const int r = ppos - c0;
+            unsigned char* st = smem + (c % NS) * STAGE;
+            if ((r >> 2) / NI == (pw & 1) && lane < 16) {  // this producer moved the row's K (V) bytes
+                const int slot = pw < 2 ? lane ^ (r & 15) : lane ^ (4 * ((r >> 2) & 3));
+                *reinterpret_cast<uint4*>(st + (pw < 2 ? 0 : KB) + r * AHD + 16 * slot) =
+                    *reinterpret_cast<const uint4*>(patch + (pw < 2 ? 0 : AHD) + 16 * lane);
+            }
+            if (sc && lane == 0 && (SC_ALL ? r / 64 == (pw & 1) : true))
+                *reinterpret_cast<float*>(st + 2 * KB + (pw < 2 ? 0 : 4 * CH) + 4 * r) =
+                    reinterpret_cast<const float*>(patch + 2 * AHD)[pw < 2 ? 0 : 1];
+        }
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        if (c + NS - 1 < nch) issue(c + NS - 1);
+        if (c + NS - 1 < nch) ring_issue<CH, NS>(smem, kv, rbase, pw, lane, lo, first, c + NS - 1);
     }
     __syncthreads();
     __syncthreads();
@@ -188,15 +236,24 @@ constexpr int W1_KB = W1_CH * AHD;                    // K rows of a stage; the 
 constexpr int W1_STAGE = ring_stage<W1_CH>();
 constexpr int W1_QT = W1_NS * W1_STAGE;              // query digit table: [digit 0, 1, 2][head][256] int8
 constexpr int W1_QS = W1_QT + 3 * GQ * AHD;             // the heads' score scales
-constexpr int W1_LDS = W1_QS + GQ * 4;
+constexpr int W1_QO = W1_QS + GQ * 4;                   // the query rows formed in the prologue: [head][256] f32
+constexpr int W1_PT = W1_QO + GQ * AHD * 4;              // the new cache row formed there: K, V codes, ks, vs
+constexpr int W1_LDS = W1_PT + 2 * AHD + 16;
 static_assert(WS_NC * GQ * AHD * 4 <= W1_LDS, "the consumer merge fits in the stages");
 static_assert(W1_LDS <= 160 * 1024, "LDS");
 
+// fr.q != nullptr: attn_decode's q/k front runs in the prologue (as qk_norm_rope_kernel would, bit for bit): the
+// query rows of the group go to LDS (and to qo from split 0), and the split that holds position pos0 forms the new
+// K/V row, writes it to the cache and patches it into its stage (its chunk may have been moved before the row
+// reached memory). With the skip flag set it does neither and reads qo, as the attention kernels after a skipped
+// front would.
 __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws1_kernel(const float* __restrict__ qo, moex_kv_cache kv,
                                                                          int H, const int* __restrict__ pos_d,
-                                                                         int max_t, float* __restrict__ part, int ns) {
+                                                                         int max_t, float* __restrict__ part, int ns,
+                                                                         FrontArgs fr) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float cm[WS_NC][GQ], cl[WS_NC][GQ];
+    __shared__ float fsh[2][5 * AHD], fsh8[2][48];
     const int nb = gridDim.x, w_id = xcd_work_id(blockIdx.x, nb);
     const int s = w_id % ns, kvh = w_id / ns;
     const int pos0 = *pos_d, Tmax = pos0 + 1;
@@ -208,16 +265,58 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws1_kernel(const 
     auto chi = [&](int c) { return c == 0 ? lo + first : lo + first + c * W1_CH; };
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 4, m16 = lane & 15;
     const size_t rbase = (size_t)kvh * max_t;
+    // the producers' first chunks go out before the prologue (its barriers leave them in flight)
+    if (wv >= WS_NC) ring_first<W1_CH, W1_NS>(smem, kv, rbase, wv - WS_NC, lane, lo, first, nch);
+    const bool fused = fr.q && !(fr.skip && *fr.skip);
+    const bool app = fused && hi == Tmax && hi > lo;  // this split holds the new row pos0
+    const float* qtab = reinterpret_cast<const float*>(smem + W1_QO);
+    unsigned char* patch = smem + W1_PT;
+    if (fused) {
+        // ---- the front: two groups of 256 threads (thread d owns dim d), each with four query heads and the key row
+        // of the group (the same bits in both groups) in one pass ----
+        const int half = tid >> 8, d = tid & 255;
+        float x[5];
+#pragma unroll
+        for (int i = 0; i < 4; i++) x[i] = fr.q[(kvh * GQ + 4 * half + i) * 2 * AHD + d];
+        x[4] = fr.k[kvh * AHD + d];
+        const uint16_t* const w[5] = {fr.qn, fr.qn, fr.qn, fr.qn, fr.kn};
+        front::norm_rope_n<5, true>(x, w, d, pos0, fr.rot, fr.theta, fr.eps, fsh[half], fsh8[half]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int h = 4 * half + i;
+            reinterpret_cast<float*>(smem + W1_QO)[h * AHD + d] = x[i];
+            if (s == 0) fr.qo[(kvh * GQ + h) * AHD + d] = x[i];
+        }
+        if (app) {  // the new row: group 0 stores it
+            int8_t ck, cv;
+            float sk, sv;
+            front::quant_i8<true>(x[4], fr.v[kvh * AHD + d], fsh8[half] + 40, d, ck, cv, sk, sv);
+            if (half == 0) {
+                const size_t row = rbase + pos0;
+                kv.k[row * AHD + d] = ck;
+                kv.v[row * AHD + d] = cv;
+                reinterpret_cast<int8_t*>(patch)[d] = ck;
+                reinterpret_cast<int8_t*>(patch)[AHD + d] = cv;
+                if (d == 0) {
+                    kv.ks[row] = sk;
+                    kv.vs[row] = sv;
+                    reinterpret_cast<float*>(patch + 2 * AHD)[0] = sk;
+                    reinterpret_cast<float*>(patch + 2 * AHD)[1] = sv;
+                }
+            }
+        }
+        front::sync<true>();
+    }
 
     if (wv >= WS_NC) {
-        ring_producer<W1_CH, W1_NS>(smem, kv, rbase, wv - WS_NC, lane, lo, first, nch);
+        ring_producer<W1_CH, W1_NS>(smem, kv, rbase, wv - WS_NC, lane, lo, first, nch, true, app ? pos0 : -1, patch);
     } else {
         // ---- consumers. The query digits, once per workgroup: consumer w turns heads 2w, 2w + 1 (lane l: head
         // 2w + l / 32, dims 8 (l % 32) .. + 7) into three signed base-256 digits of a 2^(22 - e) fixed point (|q| < 2^e
         // over the head) in the digit table; after the first barrier every consumer takes its operands from it ----
         {
             const int h = 2 * wv + (lane >> 5), d0 = 8 * (lane & 31);
-            const float* qrow = qo + ((size_t)kvh * GQ + h) * AHD + d0;
+            const float* qrow = fused ? qtab + h * AHD + d0 : qo + ((size_t)kvh * GQ + h) * AHD + d0;
             const float4 qa = *reinterpret_cast<const float4*>(qrow), qb = *reinterpret_cast<const float4*>(qrow + 4);
             float qm = fmaxf(fmaxf(fmaxf(fabsf(qa.x), fabsf(qa.y)), fmaxf(fabsf(qa.z), fabsf(qa.w))),
                              fmaxf(fmaxf(fabsf(qb.x), fabsf(qb.y)), fmaxf(fabsf(qb.z), fabsf(qb.w))));
@@ -763,26 +862,6 @@ __device__ __forceinline__ float sgn(const uint32_t* m, int j, float x) {
     return (m[j >> 5] >> (j & 31)) & 1 ? -x : x;
 }
 
-// LDS transfers of 16 (4) bytes per active lane, lane l to lds + 16 l (4 l), written in inline asm: the compiler cannot
-// tell which LDS bytes a transfer writes and would make the wavefront's next LDS read wait for every transfer in
-// flight; the kernel waits for its own transfers with vm_wait. dma16s: wave-uniform base + per-lane 32-bit offset.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved: every other use of it in this kernel sets it first
-__device__ __forceinline__ void dma16(const void* g, const unsigned char* lds) {
-    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m) : "memory", "m0");
-}
-__device__ __forceinline__ void dma16s(const void* base, uint32_t off, const unsigned char* lds) {
-    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m)
-                 : "memory", "m0");
-}
-__device__ __forceinline__ void dma4(const void* g, const unsigned char* lds) {
-    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-template <int N> __device__ __forceinline__ void vm_wait() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
 
 // 16 V codes -> biased code bytes. w = 2-bit low fields (code c at bits 2c); x = high bits, codes 0-7 in bits 0-7 and
 // codes 8-15 in bits 16-23. Word f of the result holds codes f, 4 + f, 8 + f, 12 + f in bytes 0..3: byte i of
@@ -1162,7 +1241,7 @@ int gqa_splits(int T, int KV, int ns, bool turbo) {
 }
 
 void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part, int T,
-                int ns, hipStream_t st, bool rot_out) {
+                int ns, hipStream_t st, bool rot_out, const FrontArgs* fr) {
     if (kv.turbo) {
         static bool once = [] {
             MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_wst_kernel),
@@ -1181,7 +1260,7 @@ void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos
             }();
             (void)once;
             hipLaunchKernelGGL(gqa_ws1_kernel, dim3(KV * ns), dim3(64 * (WS_NC + WS_NP)), W1_LDS, st, qo, kv, H, pos_d,
-                               max_t, part, ns);
+                               max_t, part, ns, fr ? *fr : FrontArgs{});
         }
         else if (T == 2) launch_wsp<1>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
         else launch_wsp<2>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);

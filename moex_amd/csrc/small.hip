@@ -8,7 +8,8 @@
 // reference's warp tree is reproduced exactly. The WHT's stage 32 is a shuffle too (dims d and d^32 share a
 // wavefront); only stage 64 crosses wavefronts and goes through LDS.
 #pragma clang fp contract(off)
-#include "common.hpp"
+#include <mutex>
+#include "front.hpp"
 
 namespace moex {
 
@@ -33,17 +34,8 @@ constexpr float K4 = 0.241529f / 127.f, K3 = 0.190207f / 127.f;  // code scales 
 // graph-fallback flag (kernels.cuh:46, g_skip): nonzero -> qk_norm_rope / turbo_out return at once
 __device__ int g_skip;
 
-// ---- block reductions over a 256-thread block (4 wavefronts of 64) ----
-__device__ __forceinline__ float sum32(float v) {  // 32-lane xor tree (kernels.cuh:13-16)
-#pragma unroll
-    for (int o = 16; o; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
-__device__ __forceinline__ float max32(float v) {
-#pragma unroll
-    for (int o = 16; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
+// ---- block reductions over a 256-thread block (4 wavefronts of 64): the front's, thread d = threadIdx.x ----
+__device__ __forceinline__ float sum32(float v) { return front::sum32(v); }
 // sum over the thread's 128-value half: 32-lane trees, then ((s0 + s1) + s2) + s3 (kernels.cuh:1161-1169)
 __device__ __forceinline__ float half_sum(float v, float* sh8) {
     v = sum32(v);
@@ -54,26 +46,7 @@ __device__ __forceinline__ float half_sum(float v, float* sh8) {
     const int b = g & ~3;
     return ((sh8[b] + sh8[b + 1]) + sh8[b + 2]) + sh8[b + 3];
 }
-__device__ __forceinline__ float block_sum(float v, float* sh8) {
-    v = sum32(v);
-    const int g = threadIdx.x >> 5;
-    __syncthreads();
-    if ((threadIdx.x & 31) == 0) sh8[g] = v;
-    __syncthreads();
-    // the reference's second xor tree over the 8 partials (kernels.cuh:19-28): xor 4, then 2, then 1
-    return ((sh8[0] + sh8[4]) + (sh8[2] + sh8[6])) + ((sh8[1] + sh8[5]) + (sh8[3] + sh8[7]));
-}
-__device__ __forceinline__ float block_max(float v, float* sh8) {
-    v = max32(v);
-    const int g = threadIdx.x >> 5;
-    __syncthreads();
-    if ((threadIdx.x & 31) == 0) sh8[g] = v;
-    __syncthreads();
-    float m = sh8[0];
-#pragma unroll
-    for (int i = 1; i < 8; i++) m = fmaxf(m, sh8[i]);
-    return m;
-}
+__device__ __forceinline__ float block_sum(float v, float* sh8) { return front::block_sum(v, sh8, threadIdx.x); }
 
 // WHT of both 128-value halves of the block's row (kernels.cuh:1143-1159); dir 0 forward, 1 inverse.
 __device__ __forceinline__ float wht(float x, float* sh, int dir) {
@@ -130,11 +103,12 @@ __device__ __forceinline__ void append_row(float x, float vv, moex_kv_cache kv, 
         if (!(j & 7)) V[64 + b * 16 + j / 8] = (uint8_t)(hb >> (d & 63));
         if (j == 0) { kv.ks[row * 2 + b] = nk; kv.vs[row * 2 + b] = nv; }
     } else {  // int8 per row (kernels.cuh:1227-1235)
-        const float mk = block_max(fabsf(x), sh8), mv = block_max(fabsf(vv), sh8 + 8);
-        const float sk = mk > 0.f ? mk / 127.f : 1.f, sv = mv > 0.f ? mv / 127.f : 1.f;
+        int8_t ck, cv;
+        float sk, sv;
+        front::quant_i8(x, vv, sh8, d, ck, cv, sk, sv);
         const size_t o = row * AHD + d;
-        kv.k[o] = (int8_t)__builtin_rintf(x / sk);
-        kv.v[o] = (int8_t)__builtin_rintf(vv / sv);
+        kv.k[o] = ck;
+        kv.v[o] = cv;
         if (d == 0) { kv.ks[row] = sk; kv.vs[row] = sv; }
     }
 }
@@ -153,18 +127,7 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(
     q += (size_t)tok * ld; k += (size_t)tok * ld; v += (size_t)tok * ld; qo += (size_t)tok * H * AHD;
     const bool isq = hh < H;
     float x = isq ? q[hh * 2 * AHD + d] : k[(hh - H) * AHD + d];
-    const float r = rsqrtf(block_sum(x * x, sh8) / AHD + eps);
-    const float w = (float)__builtin_bit_cast(_Float16, (isq ? qn : kn)[d]);
-    x = x * r * (1.f + w);
-    t[d] = x;
-    __syncthreads();
-    const int h2 = rot / 2;
-    if (d < rot) {
-        const int j = d < h2 ? d : d - h2;
-        const float ang = (float)pos * powf(theta, -2.f * j / rot);
-        const float cs = cosf(ang), sn = sinf(ang);
-        x = d < h2 ? t[d] * cs - t[d + h2] * sn : t[d] * cs + t[d - h2] * sn;
-    }
+    x = front::norm_rope(x, isq ? qn : kn, d, pos, rot, theta, eps, t, sh8);
     if (isq) {
         const float y = kv.turbo ? wht(x, sh, 0) : x;  // turbo: the keys' rotation (the block is uniform)
         qo[hh * AHD + d] = y;
@@ -393,6 +356,20 @@ __global__ void __launch_bounds__(256) decode_heads_kernel(const float* __restri
         float* ml = part_ml(part, tok, h, sp, H, ns, gridDim.y);
         ml[0] = M; ml[1] = L;
     }
+}
+
+const int* skip_flag() {
+    static std::mutex mu;
+    static const int* ptr[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lk(mu);
+    if (!ptr[dev]) {  // first use on this device, which is current here
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_skip)) != hipSuccess) return nullptr;
+        ptr[dev] = static_cast<const int*>(p);
+    }
+    return ptr[dev];
 }
 
 __global__ void set_int_kernel(int* p, int v) { *p = v; }
