@@ -938,6 +938,10 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
     };
     // step j's operands from its stage into registers: the K nibbles of key m16 (per MFMA ks), its norm pairs, and
     // the raw V words of keys 4g .. 4g + 3 (dims 8 m16 .. 8 m16 + 7 of both halves)
+    // v_perm selectors: low fields of dims 8 m16 .. 8 m16 + 7 (bytes 2 (m16 % 2), +1 of each half's dword) into the
+    // two halves of vw; the high-bit byte m16 % 4 of each half's dword into bytes 0 and 2 of vx (bytes 1, 3 unused)
+    const uint32_t ow = 2 * (m16 & 1), ox = m16 & 3;
+    const uint32_t vsel_w = ow | (ow + 1) << 8 | (ow + 4) << 16 | (ow + 5) << 24, vsel_x = ox | (ox + 4) << 16;
     struct StepRegs {
         uint2 nib[4];
         float2 kn, vn;
@@ -953,13 +957,12 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
         }
         r.kn = *reinterpret_cast<const float2*>(st + WT_NRM + 8 * m16);
         r.vn = *reinterpret_cast<const float2*>(st + WT_NRM + 8 * WT_K + 8 * m16);
+        // whole dwords (two per read instruction), the lane's 16 bits / byte of each half picked by one v_perm
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            typedef unsigned short us2_t __attribute__((ext_vector_type(2)));
-            const unsigned char* row = st + WT_RV + (4 * g + i) * WT_VS;
-            r.vw[i] = __builtin_bit_cast(uint32_t, us2_t{*reinterpret_cast<const unsigned short*>(row + 2 * m16),
-                                                         *reinterpret_cast<const unsigned short*>(row + 32 + 2 * m16)});
-            r.vx[i] = __builtin_bit_cast(uint32_t, us2_t{row[64 + m16], row[80 + m16]});
+            const uint32_t* row = reinterpret_cast<const uint32_t*>(st + WT_RV + (4 * g + i) * WT_VS);
+            r.vw[i] = __builtin_amdgcn_perm(row[8 + (m16 >> 1)], row[m16 >> 1], vsel_w);
+            r.vx[i] = __builtin_amdgcn_perm(row[20 + (m16 >> 2)], row[16 + (m16 >> 2)], vsel_x);
         }
     };
     // step j has landed once at most 5 * min(a, nst - 1 - j) transfers are in flight (a = steps issued past it)
