@@ -159,62 +159,73 @@ __global__ void __launch_bounds__(256) turbo_out_kernel(float* __restrict__ out,
 }
 
 // attn_combine_k (kernels.cuh:1317-1329): merge ns partials {m (log2 units), l, acc[256]}.
-// Grid (H, T, DC): block (h, t, c) owns dims [c*DW, (c+1)*DW), DW = 256/DC; its 256 threads are DW dims x NG split
-// groups. Every thread merges its splits online (running max, no separate max pass) with 16 loads in flight, then the
-// NG groups are merged through LDS. One pass over the partials.
-constexpr int CDC = 16, CDW = AHD / CDC, CNG = 256 / CDW;
+// Grid (H, T, CDC): block (h, t, c) owns dims [64 c, 64 c + 64); its 256 threads are 16 dim quads (one float4 of acc
+// per split) x 16 split groups. A thread loads 8 of its splits at once, takes their maximum, then weighs them with
+// independent exponentials (no serial online chain); m and l are the same for the 16 threads of a group, so only
+// the group's acc goes through LDS. One pass over the partials.
+constexpr int CDC = AHD / 64, CNG = 16, CSB = 8;
 __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ part, const float* __restrict__ q_gate,
                                                       float* __restrict__ out, int H, int ns, int ld) {
-    __shared__ float sm[CNG][CDW], sl[CNG][CDW], sa[CNG][CDW];
+    __shared__ float sm[CNG], sl[CNG];
+    __shared__ float4 sa[CNG][16];
     const int tok = blockIdx.y, h = blockIdx.x, tid = threadIdx.x, T = gridDim.y;
     float* pp = const_cast<float*>(part);
-    const float* acc_rows = part_acc(pp, tok, h, 0, H, ns);
+    const float4* acc_rows = reinterpret_cast<const float4*>(part_acc(pp, tok, h, 0, H, ns) + 64 * blockIdx.z);
     const float2* ml = reinterpret_cast<const float2*>(part_ml(pp, tok, h, 0, H, ns, T));
-    const int dl = tid % CDW, gi = tid / CDW, d = blockIdx.z * CDW + dl;
+    const int dq = tid & 15, gi = tid >> 4;
     // the gate goes out with the partials rather than after the merge
-    const float gt = (q_gate && tid < CDW) ? q_gate[(size_t)tok * ld + h * 2 * AHD + AHD + d] : 0.f;
-    float mt = -INFINITY, lt = 0.f, at = 0.f;
-    for (int s0 = gi; s0 < ns; s0 += 16 * CNG) {
-        float2 q[16];
-        float a[16];
+    const float gt = (q_gate && tid < 64) ? q_gate[(size_t)tok * ld + h * 2 * AHD + AHD + 64 * blockIdx.z + tid] : 0.f;
+    float mt = -INFINITY, lt = 0.f;
+    float4 at = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = gi; s0 < ns; s0 += CSB * CNG) {
+        float2 q[CSB];
+        float4 a[CSB];
 #pragma unroll
-        for (int u = 0; u < 16; u++) {
+        for (int u = 0; u < CSB; u++) {
             const int s = s0 + u * CNG;
             if (s < ns) {
                 q[u] = ml[s];
-                a[u] = acc_rows[(size_t)s * AHD + d];
+                a[u] = acc_rows[(size_t)s * (AHD / 4) + dq];
             } else {
                 q[u] = make_float2(-INFINITY, 0.f);
-                a[u] = 0.f;
+                a[u] = make_float4(0.f, 0.f, 0.f, 0.f);
             }
         }
+        float mb = mt;
 #pragma unroll
-        for (int u = 0; u < 16; u++) {
-            if (q[u].y > 0.f) {  // empty splits (l = 0, m = -inf) contribute nothing
-                const float mn = fmaxf(mt, q[u].x);
-                const float f = fast_exp2(mt - mn), g = fast_exp2(q[u].x - mn);  // f = 0 while mt = -inf
-                lt = lt * f + q[u].y * g;
-                at = at * f + a[u] * g;
-                mt = mn;
-            }
+        for (int u = 0; u < CSB; u++)
+            if (q[u].y > 0.f) mb = fmaxf(mb, q[u].x);  // empty splits (l = 0, m = -inf) contribute nothing
+        if (mb == -INFINITY) continue;                  // nothing yet
+        const float f = fast_exp2(mt - mb);             // 0 while mt = -inf
+        lt *= f;
+        at.x *= f; at.y *= f; at.z *= f; at.w *= f;
+#pragma unroll
+        for (int u = 0; u < CSB; u++) {
+            const float g = q[u].y > 0.f ? fast_exp2(q[u].x - mb) : 0.f;
+            lt = fmaf(q[u].y, g, lt);
+            at.x = fmaf(a[u].x, g, at.x); at.y = fmaf(a[u].y, g, at.y);
+            at.z = fmaf(a[u].z, g, at.z); at.w = fmaf(a[u].w, g, at.w);
         }
+        mt = mb;
     }
-    sm[gi][dl] = mt; sl[gi][dl] = lt; sa[gi][dl] = at;
+    if (dq == 0) { sm[gi] = mt; sl[gi] = lt; }
+    sa[gi][dq] = at;
     __syncthreads();
-    if (tid >= CDW) return;
+    if (tid >= 64) return;
     float M = -INFINITY;
 #pragma unroll
-    for (int g = 0; g < CNG; g++) M = fmaxf(M, sm[g][tid]);  // split 0 is never empty: M is finite
+    for (int g = 0; g < CNG; g++) M = fmaxf(M, sm[g]);  // split 0 is never empty: M is finite
     float l = 0.f, acc = 0.f;
+    const float* saf = reinterpret_cast<const float*>(&sa[0][0]);
 #pragma unroll
     for (int g = 0; g < CNG; g++) {
-        const float f = fast_exp2(sm[g][tid] - M);
-        l += sl[g][tid] * f;
-        acc += sa[g][tid] * f;
+        const float f = fast_exp2(sm[g] - M);
+        l += sl[g] * f;
+        acc += saf[g * 64 + tid] * f;
     }
     float x = acc / l;
     if (q_gate) x = x / (1.f + __expf(-gt));
-    out[((size_t)tok * H + h) * AHD + d] = x;
+    out[((size_t)tok * H + h) * AHD + 64 * blockIdx.z + tid] = x;
 }
 
 // Per-query-head decode (the contract of attn_decode_k, kernels.cuh:1238-1315): any H / KV, int8 or turbo.
