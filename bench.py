@@ -213,19 +213,37 @@ def main():
             t_g = e0.elapsed_time(e1) / (10 * NG)
             del graph
             kv_bytes = 2.0 * ctx * 520
+            t_ad = None
+            if Tq == 1:
+                # the whole attn_decode step from the raw q/k/v row: at T = 1 the split kernel runs the q/k front and
+                # the append in its prologue. Each call rewrites row ctx - 1 of its cache with the same bytes.
+                LQ = LD + 2 * KV * AHD
+                qkv = torch.randn((1, LQ), generator=torch.Generator(device=dev).manual_seed(7), device=dev)
+                qn = torch.zeros(AHD, dtype=torch.int16, device=dev)
+                qo_ad = torch.empty((1, H, AHD), device=dev)
+                nsd = M.decode_splits(ctx)
+                part_ad = torch.empty(H * nsd * (AHD + 2), device=dev)
+
+                def adec(c):
+                    return lambda: M.attn_decode(qkv, qkv[:, LD:], qkv[:, LD + KV * AHD:], qn, qn, qo_ad, c, o1, H, KV,
+                                                 pd, c.max_t, 64, 1e7, 1e-6, 1, LQ, st, part_ad, nsd)
+                t_ad = time_rotating([adec(c) for c in rot], 200)
             dec[f"T{Tq}"] = {"ns": ns, "split_kernel_us": round(t_k * 1e3, 2), "with_combine_us": round(t_f * 1e3, 2),
                              "graph_step_us": round(t_g * 1e3, 2),
                              "GBps": round(kv_bytes / (t_f * 1e-3) / 1e9, 1),
                              "graph_GBps": round(kv_bytes / (t_g * 1e-3) / 1e9, 1),
                              "split_kernel_GBps": round(kv_bytes / (t_k * 1e-3) / 1e9, 1),
                              "hbm_frac": round(kv_bytes / (t_f * 1e-3) / 1e9 / PEAK_HBM, 4)}
+            if t_ad is not None:
+                dec[f"T{Tq}"]["attn_decode_us"] = round(t_ad * 1e3, 2)
             if want_cpu:
                 if Tq == 1:
                     hrot = host_cache(rot[0], ctx)
                 dec[f"T{Tq}"]["cpu"] = cpu_decode(hrot, qh[:Tq], gh[:Tq], ctx - Tq, Tq, kv_bytes, threads)
             print(f"[bench] config2 decode T={Tq} ctx={ctx} ns={ns}: {t_f * 1e3:.1f} us "
                   f"({dec[f'T{Tq}']['GBps']} GB/s; split kernel alone {t_k * 1e3:.1f} us; "
-                  f"graph-replayed step {t_g * 1e3:.1f} us = {dec[f'T{Tq}']['graph_GBps']} GB/s)", flush=True)
+                  f"graph-replayed step {t_g * 1e3:.1f} us = {dec[f'T{Tq}']['graph_GBps']} GB/s"
+                  + (f"; whole attn_decode step {t_ad * 1e3:.1f} us" if t_ad is not None else "") + ")", flush=True)
         del rot
         extra["config2_decode_int8_90k"] = dec
         # ---------------- config 1 depth comparison / config 4: turbo at 262k ----------------
