@@ -67,7 +67,9 @@ void moex_kv_free(moex_kv_cache kv);
  * all T K/V rows quantized into kv (int8, or turbo codes), the query written to qo [T][H][256] (turbo: rotated),
  * then attention over keys [0, pos+t] written gated to out [T][H][256].
  * Dispatch as the reference: T > 2 and ns == 1 -> prefill (FA; MOEX_FA=0 -> moex_attn_prefill for int8);
- * ns > 1 -> split-K GQA decode + combine (part: T*H*ns*(256+2) floats); else the per-head kernel. */
+ * ns > 1 -> split-K GQA decode + combine (part: T*H*ns*(256+2) floats); else the per-head kernel.
+ * int8, T == 1, ns > 1, H/KV == 8: the front and the append run inside the split kernel (two launches in all), with
+ * qo, the cache row and out bit-identical to the separate front's. */
 void moex_attn_decode(const float* q, const float* k, const float* v, const uint16_t* qn, const uint16_t* kn,
                       float* qo, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d, int max_t,
                       int rot, float theta, float eps, int T, int ld, void* stream, float* part, int ns);
