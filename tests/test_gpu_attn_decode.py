@@ -107,3 +107,47 @@ def test_skip_flag_and_soft_errors():
     finally:
         M.lib().moex_set_soft_error(None)
     assert slot.value == 1  # hipErrorInvalidValue
+
+
+def test_skip_flag_fused_front():
+    """With g_skip set, attn_decode's int8 T = 1 split-K step (whose split kernel runs the front and the append in
+    its prologue) appends nothing, leaves qo as it was and attends with that qo, as the reference's attention after
+    a skipped qk_norm_rope_k (kernels.cuh:1189) does: its output equals attn_gqa + attn_combine on the same qo, bit
+    for bit."""
+    import torch
+    import moex_amd as M
+    from tests.gpu_util import random_int8_cache, upload
+    pos, max_t = 3000, 3072
+    hc = random_int8_cache(max_t, seed=71)
+    dc = upload(hc)
+    rng = np.random.default_rng(72)
+    LQ = H * 2 * AHD + 2 * KV * AHD
+    qkv = dev(rng.standard_normal((1, LQ), dtype=np.float32))
+    qo0 = rng.standard_normal((1, H, AHD), dtype=np.float32)
+    qo = dev(qo0)
+    qn = torch.zeros(AHD, dtype=torch.int16, device="cuda")
+    ns = M.decode_splits(pos + 1)
+    assert ns > 1
+    part = torch.empty(H * ns * (AHD + 2), device="cuda")
+    out = torch.full((1, H, AHD), float("nan"), device="cuda")
+    M.set_skip(1)
+    try:
+        M.attn_decode(qkv, qkv[:, H * 2 * AHD:], qkv[:, H * 2 * AHD + KV * AHD:], qn, qn, qo, dc, out, H, KV,
+                      pos_tensor(pos), max_t, 64, 1e7, 1e-6, 1, LQ, None, part, ns)
+        torch.cuda.synchronize()
+    finally:
+        M.set_skip(0)
+        torch.cuda.synchronize()
+    after = download(dc)
+    for a, b, name in ((after.k, hc.k, "k"), (after.v, hc.v, "v"), (after.ks, hc.ks, "ks"), (after.vs, hc.vs, "vs")):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"cache {name} changed under the skip flag"
+    assert np.array_equal(qo.cpu().numpy(), qo0), "qo changed under the skip flag"
+    nsg = M.gqa_splits(1, KV, ns)
+    part2 = torch.empty(H * ns * (AHD + 2), device="cuda")
+    out2 = torch.full((1, H, AHD), float("nan"), device="cuda")
+    M.attn_gqa(qo, dc, H, KV, pos_tensor(pos), max_t, part2, 1, nsg)
+    M.attn_combine(part2, qkv, out2, H, nsg, LQ, 1)
+    torch.cuda.synchronize()
+    got, ref = out.cpu().numpy(), out2.cpu().numpy()
+    report("skip flag, fused front", ns=nsg, same=bool(np.array_equal(got, ref)))
+    assert np.all(np.isfinite(got)) and np.array_equal(got, ref)
