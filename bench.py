@@ -6,7 +6,8 @@ reference's flop count 4*H*D*T*(pos0 + T/2) (tests/test_fa.cu:137). A step = one
 cache) are resident in HBM before the timed region.
 
 Also reported (other configs of BASELINE.json, same JSON line): decode / MTP verify at 90k context (T=1, T=4;
-HBM GB/s over the 520 B/row KV, rotating over 4 caches that together exceed the MALL), TurboQuant decode at 262144, TurboQuant prefill at
+HBM GB/s over the 520 B/row KV, rotating over 4 caches that together exceed the MALL), TurboQuant decode at 262144 (rotating over 3 caches),
+TurboQuant prefill at
 260096..262143 and the int8 chunk at the same depth, and config 0 (pos0 = 0).
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--decode-only] [--no-cpu]
@@ -114,10 +115,10 @@ def main():
     def time_rotating(fns, steps):
         """Average time per call of fns[i % len(fns)] over `steps` back-to-back calls. Each fn reads its own KV
         cache and together they exceed the 256 MB MALL, so every call streams its cache from HBM; timing a loop
-        avoids the event overhead that dominates a single ~20 us launch."""
-        for f in fns:
-            f()
-        torch.cuda.synchronize()
+        avoids the event overhead that dominates a single ~20 us launch. The clocks are settled first: the
+        configs[2] lines follow the CPU baseline, which leaves the GPU idle for seconds, and the compute-bound T = 4
+        kernel measured 29.5 us instead of 24-25 us without this."""
+        settle(lambda: [f() for f in fns], ms=100.0)
         e0, e1 = ev(), ev()
         e0.record(st)
         for i in range(steps):
@@ -247,21 +248,27 @@ def main():
         del rot
         extra["config2_decode_int8_90k"] = dec
         # ---------------- config 1 depth comparison / config 4: turbo at 262k ----------------
-        flush_read = torch.ones(192 << 20, dtype=torch.float32, device=dev)  # 768 MB read between calls
-        t_flush = time_rotating([lambda: flush_read.sum()], 20)
-        ct = M.DeviceKVCache(KV, 262144 + 64, 1)
-        fill_cache(ct, 262144, seed=12)
+        # three turbo caches of 262144 keys (3 x 125.8 MB > the 256 MB MALL) rotate, so every decode call streams
+        # its KV from HBM, as the int8 caches above do; configs[4] uses the first
         ctx = 262144
+        cts = []
+        for i in range(1 if a.config4_only else 3):
+            c = M.DeviceKVCache(KV, ctx + 64, 1)
+            fill_cache(c, ctx, seed=12 + i)
+            cts.append(c)
+        ct = cts[0]
         ns = M.gqa_splits(1, KV, M.decode_splits(ctx), 1)
         part = torch.empty(H * ns * (AHD + 2), device=dev)
         o1 = torch.empty((1, H, AHD), device=dev)
         pd = torch.tensor([ctx - 1], dtype=torch.int32, device=dev)
 
-        def tdec():  # what attn_decode runs: partials rotated back in the split kernel, gated combine
-            M.attn_gqa_out(qo[:1], ct, H, KV, pd, ct.max_t, part, 1, ns, st)
-            M.attn_combine(part, qg[:1], o1, H, ns, LD, 1, st)
+        def tdec(c):  # what attn_decode runs: partials rotated back in the split kernel, gated combine
+            def f():
+                M.attn_gqa_out(qo[:1], c, H, KV, pd, c.max_t, part, 1, ns, st)
+                M.attn_combine(part, qg[:1], o1, H, ns, LD, 1, st)
+            return f
 
-        t_td = time_rotating([tdec, lambda: flush_read.sum()], 1 if a.config4_only else 20) * 2 - t_flush
+        t_td = time_rotating([tdec(c) for c in cts], 3 if a.config4_only else 90)
         tb = 2.0 * ctx * 240
         extra["config3_decode_turbo_262k"] = {"ns": ns, "us": round(t_td * 1e3, 2),
                                               "GBps": round(tb / (t_td * 1e-3) / 1e9, 1)}
@@ -284,7 +291,7 @@ def main():
                                                                      threads, full=False)
         print(f"[bench] config4 prefill at 260096: turbo {ms_t:.2f} ms ({f4 / ms_t / 1e9:.0f} TFLOPS), "
               f"int8 {ms_i:.2f} ms ({f4 / ms_i / 1e9:.0f} TFLOPS)", flush=True)
-        del ct
+        del ct, cts
         if a.config4_only:
             return
         # ---------------- dense int8 projections either side of the attention ----------------
