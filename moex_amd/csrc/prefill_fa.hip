@@ -277,6 +277,142 @@ __global__ void __launch_bounds__(256) fa_image_kernel(moex_kv_cache kv, const i
     }
 }
 
+// Tile image j of a kv head (src: its first image) -> the LDS buffer buf, by DMA wavefront pw (0..3): 1 KB pieces
+// pw, pw + 4, .. (10 for pw = 0, 9 for the others), leaving out the padding slots nobody reads.
+__device__ __forceinline__ void fa_issue_img(const unsigned char* src, int j, unsigned char* buf, int pw, int lane) {
+    constexpr int NP = (TILE_BYTES + 1023) / 1024;  // 37 pieces, the last one partial
+    static_assert(NP == 37 && TILE_BYTES % 16 == 0, "image pieces");
+    const unsigned char* g = src + (size_t)j * TILE_BYTES + 16 * lane;
+#pragma unroll
+    for (int u = 0; u < 10; u++) {
+        const int i = pw + 4 * u, sl = 64 * i + lane;  // 16-byte slot of the image
+        // padding: slot 32 of each 33-slot K row, slot 4 of each 5-slot V^T row, the spare scales, the end
+        const bool pad = sl < KT_BYTES / 16 ? sl % 33 == 32
+                         : sl < (KT_BYTES + VT_BYTES) / 16 ? (sl - KT_BYTES / 16) % 5 == 4
+                                                           : sl >= (KT_BYTES + VT_BYTES + SC_BYTES) / 16;
+        if (i < NP && !pad)
+            __builtin_amdgcn_global_load_lds((gptr_t)(g + i * 1024), (lptr_t)(buf + i * 1024), 16, 0, 0);
+    }
+}
+// The DMA wavefronts' wait for the first pair of a run of ntiles tiles issued back to back (the tiles after it are
+// still in flight: 10 transfers a tile for pw = 0, 9 for the others)
+__device__ __forceinline__ void fa_wait_first_pair(int ntiles, int pw) {
+    if (ntiles >= 4) { if (pw == 0) wait_vm<20>(); else wait_vm<18>(); }
+    else if (ntiles == 3) { if (pw == 0) wait_vm<10>(); else wait_vm<9>(); }
+    else wait_vm<0>();
+}
+
+// One key tile of a computing wavefront (32 query rows): S^T = K . Q^T, the lazily rescaled softmax and O^T += V^T . P^T.
+// Kt, Vt, scl: the tile's buffer in LDS; k0: its first key; first: the first tile this wavefront computes for its
+// rows (it sets m_ref, and each of its rows sees the tile's first key); prow: the last key the lane's row sees; wmin:
+// the last key the wavefront's first row sees (a tile reaching past it is a diagonal one).
+__device__ __forceinline__ void fa_tile(const _Float16* Kt, const _Float16* Vt, const float* scl, int k0, bool first,
+                                        int prow, int wmin, int r, int h32, const half8_t (&qf)[16],
+                                        float16_t (&o)[8], float& m_ref, float& l_run) {
+    const half2_t ones = half2_t{(_Float16)1.f, (_Float16)1.f};
+    float16_t sc;
+#pragma unroll
+    for (int i = 0; i < 16; i++) sc[i] = 0.f;
+    float4 kq[4];  // the score scales, read during the last Q.K MFMAs
+    {   // K operands read FA_KPF MFMAs ahead of their use (LDS latency)
+        const _Float16* krow = Kt + r * KST + 8 * h32;
+        half8_t ka[FA_KPF];
+#pragma unroll
+        for (int s = 0; s < FA_KPF; s++) ka[s] = *reinterpret_cast<const half8_t*>(krow + 16 * s);
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            const half8_t a = ka[s % FA_KPF];
+            if (s + FA_KPF < 16)
+                ka[s % FA_KPF] = *reinterpret_cast<const half8_t*>(krow + 16 * (s + FA_KPF));
+            if (s == 16 - 2) {
+#pragma unroll
+                for (int a4 = 0; a4 < 4; a4++) kq[a4] = *reinterpret_cast<const float4*>(scl + 8 * a4 + 4 * h32);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep each read FA_KPF MFMAs ahead of its use
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], sc, 0, 0, 0);
+        }
+    }
+    // scores relative to the row's reference maximum: t = s * scale - m_ref in one fma (tile 0 sets m_ref: key 0
+    // is unmasked in every row, so it is finite)
+    const float mneg = first ? 0.f : -m_ref;
+#pragma unroll
+    for (int a4 = 0; a4 < 4; a4++) {
+        sc[4 * a4] = fmaf(sc[4 * a4], kq[a4].x, mneg); sc[4 * a4 + 1] = fmaf(sc[4 * a4 + 1], kq[a4].y, mneg);
+        sc[4 * a4 + 2] = fmaf(sc[4 * a4 + 2], kq[a4].z, mneg); sc[4 * a4 + 3] = fmaf(sc[4 * a4 + 3], kq[a4].w, mneg);
+    }
+    if (k0 + BK - 1 > wmin) {  // a diagonal tile: causal mask per row
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            if (k0 + 8 * (i >> 2) + 4 * h32 + (i & 3) > prow) sc[i] = -INFINITY;
+    }
+    // ---- P^T (fp16) as B operands: MFMA m (keys 16m ..) takes S elements 8m .. 8m+7 ----
+    half8_t pf[2];
+    float ls = 0.f;
+    auto make_p = [&]() {
+        ls = 0.f;
+#pragma unroll
+        for (int m = 0; m < 2; m++)
+#pragma unroll
+            for (int jj = 0; jj < 8; jj += 2) {
+                const float p0 = fast_exp2(sc[8 * m + jj]), p1 = fast_exp2(sc[8 * m + jj + 1]);
+                const half2_t ph = half2_t{(_Float16)p0, (_Float16)p1};
+                pf[m][jj] = ph[0]; pf[m][jj + 1] = ph[1];
+                ls = __builtin_amdgcn_fdot2(ph, ones, ls, false);
+            }
+    };
+    auto row_max = [&]() {  // this lane's half of the row; the other half is in lane ^ 32
+        float mt = sc[0];
+#pragma unroll
+        for (int i = 1; i < 16; i++) mt = fmaxf(mt, sc[i]);
+        return mt;
+    };
+    if (first) {
+        float mt = row_max();
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        m_ref = mt;
+#pragma unroll
+        for (int i = 0; i < 16; i++) sc[i] -= mt;
+        make_p();
+    } else {
+        // lazy rescale: O and l are referenced to m_ref and move only when a row's maximum passes it by the
+        // slack. No score of a lane's half passes m_ref + slack while its probabilities sum to at most 2^slack,
+        // so the row maximum is needed only when some lane's sum exceeds that (or overflowed)
+        make_p();
+        if (__ballot(!(ls <= RESCALE_LSUM))) {
+            const float mt = row_max();
+            const float d = fmaxf(fmaxf(mt, __shfl_xor(mt, 32)), 0.f);
+            const float cf = fast_exp2(-d);
+#pragma unroll
+            for (int db = 0; db < 8; db++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) o[db][i] *= cf;
+            l_run *= cf;
+            m_ref += d;
+#pragma unroll
+            for (int i = 0; i < 16; i++) sc[i] -= d;
+            make_p();
+        }
+    }
+    l_run += ls;
+    // ---- O^T += V^T . P^T ----
+    {   // V^T operands read FA_KPF MFMAs ahead (MFMA q: dims 32*(q/2) + r, keys 16*(q%2) ..)
+        const _Float16* vrow = Vt + r * VST + 8 * h32;
+        half8_t va[FA_KPF];
+#pragma unroll
+        for (int q = 0; q < FA_KPF; q++) va[q] = *reinterpret_cast<const half8_t*>(vrow + 32 * (q >> 1) * VST + 16 * (q & 1));
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+            const half8_t a = va[q % FA_KPF];
+            if (q + FA_KPF < 16) {
+                const int qn = q + FA_KPF;
+                va[q % FA_KPF] = *reinterpret_cast<const half8_t*>(vrow + 32 * (qn >> 1) * VST + 16 * (qn & 1));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            o[q >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[q & 1], o[q >> 1], 0, 0, 0);
+        }
+    }
+}
+
 // Warp-specialised workgroup of 8 wavefronts. Wavefronts 0-3 compute (32 query rows each); wavefronts 4-7 fill the LDS
 // tile buffers. Each SIMD holds one wavefront of each kind, so the filling runs beside the other wavefront's MFMAs.
 //   IMG = false: the staging wavefronts load the next tiles' int8/turbo K and V and widen them (two buffers: during
@@ -322,29 +458,12 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
     if (threadIdx.x >= 256 && IMG) {
         // ---------------- DMA wavefronts: image j -> buffer j % 4, 1 KB pieces i = pw, pw + 4, .. ----------------
         const int pw = (threadIdx.x >> 6) - 4, lane = threadIdx.x & 63;
-        const unsigned char* src = img + (size_t)kvh * ntmax * TILE_BYTES + 16 * lane;
-        constexpr int NP = (TILE_BYTES + 1023) / 1024;  // 37 pieces, the last one partial
-        static_assert(NP == 37 && TILE_BYTES % 16 == 0, "image pieces");
-        auto issue = [&](int j) {
-            const unsigned char* g = src + (size_t)(ja + j) * TILE_BYTES;
-            unsigned char* l = smem + (j % NB) * TILE_BYTES;
-#pragma unroll
-            for (int u = 0; u < 10; u++) {
-                const int i = pw + 4 * u, sl = 64 * i + lane;  // 16-byte slot of the image
-                // padding: slot 32 of each 33-slot K row, slot 4 of each 5-slot V^T row, the spare scales, the end
-                const bool pad = sl < KT_BYTES / 16 ? sl % 33 == 32
-                                 : sl < (KT_BYTES + VT_BYTES) / 16 ? (sl - KT_BYTES / 16) % 5 == 4
-                                                                   : sl >= (KT_BYTES + VT_BYTES + SC_BYTES) / 16;
-                if (i < NP && !pad)
-                    __builtin_amdgcn_global_load_lds((gptr_t)(g + i * 1024), (lptr_t)(l + i * 1024), 16, 0, 0);
-            }
-        };
+        const unsigned char* src = img + (size_t)kvh * ntmax * TILE_BYTES;
+        auto issue = [&](int j) { fa_issue_img(src, ja + j, smem + (j % NB) * TILE_BYTES, pw, lane); };
         // piece counts per wavefront: 10 for pw = 0 (pieces 0, 4, .., 36), 9 for the others
         // pairs of tiles: pair p = tiles 2p, 2p + 1 in buffers 2 (p % 2), + 1; one barrier per pair
         for (int j = 0; j < 4 && j < ntiles; j++) issue(j);
-        if (ntiles >= 4) { if (pw == 0) wait_vm<20>(); else wait_vm<18>(); }
-        else if (ntiles == 3) { if (pw == 0) wait_vm<10>(); else wait_vm<9>(); }
-        else wait_vm<0>();
+        fa_wait_first_pair(ntiles, pw);
         asm volatile("s_barrier" ::: "memory");  // pair 0 is in buffers 0, 1
         const int np = (ntiles + 1) / 2;
         for (int p = 0; p < np; p++) {
@@ -424,7 +543,6 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
 #pragma unroll
         for (int i = 0; i < 16; i++) o[db][i] = 0.f;
     float m_ref = -INFINITY, l_run = 0.f;
-    const half2_t ones = half2_t{(_Float16)1.f, (_Float16)1.f};
     __syncthreads();
 
     // split: this wavefront's tiles of the piece, then barriers only while the others finish theirs (one loop with a
@@ -432,112 +550,8 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
     const int wt = max(0, min(ntiles, wtiles - ja));
     for (int j = 0; j < (SPLIT ? wt : ntiles); j++) {
         if (SPLIT || j < wtiles) {
-            const _Float16* Kt = reinterpret_cast<const _Float16*>(KBUF(j % NB));
-            const _Float16* Vt = reinterpret_cast<const _Float16*>(VBUF(j % NB));
-            const float* scl = SBUF(j % NB);
-            const int k0 = (ja + j) * BK;
-            // ---- S^T = K . Q^T: lane = (row r, key half h32), element i: key 8*(i/4) + 4*h32 + i%4 ----
-            float16_t sc;
-#pragma unroll
-            for (int i = 0; i < 16; i++) sc[i] = 0.f;
-            float4 kq[4];  // the score scales, read during the last Q.K MFMAs
-            {   // K operands read FA_KPF MFMAs ahead of their use (LDS latency)
-                const _Float16* krow = Kt + r * KST + 8 * h32;
-                half8_t ka[FA_KPF];
-#pragma unroll
-                for (int s = 0; s < FA_KPF; s++) ka[s] = *reinterpret_cast<const half8_t*>(krow + 16 * s);
-#pragma unroll
-                for (int s = 0; s < 16; s++) {
-                    const half8_t a = ka[s % FA_KPF];
-                    if (s + FA_KPF < 16)
-                        ka[s % FA_KPF] = *reinterpret_cast<const half8_t*>(krow + 16 * (s + FA_KPF));
-                    if (s == 16 - 2) {
-#pragma unroll
-                        for (int a4 = 0; a4 < 4; a4++) kq[a4] = *reinterpret_cast<const float4*>(scl + 8 * a4 + 4 * h32);
-                    }
-                    __builtin_amdgcn_sched_barrier(0);  // keep each read FA_KPF MFMAs ahead of its use
-                    sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], sc, 0, 0, 0);
-                }
-            }
-            // scores relative to the row's reference maximum: t = s * scale - m_ref in one fma (tile 0 sets m_ref: key 0
-            // is unmasked in every row, so it is finite)
-            const float mneg = j == 0 ? 0.f : -m_ref;
-#pragma unroll
-            for (int a4 = 0; a4 < 4; a4++) {
-                sc[4 * a4] = fmaf(sc[4 * a4], kq[a4].x, mneg); sc[4 * a4 + 1] = fmaf(sc[4 * a4 + 1], kq[a4].y, mneg);
-                sc[4 * a4 + 2] = fmaf(sc[4 * a4 + 2], kq[a4].z, mneg); sc[4 * a4 + 3] = fmaf(sc[4 * a4 + 3], kq[a4].w, mneg);
-            }
-            if (k0 + BK - 1 > wmin) {  // a diagonal tile: causal mask per row
-#pragma unroll
-                for (int i = 0; i < 16; i++)
-                    if (k0 + 8 * (i >> 2) + 4 * h32 + (i & 3) > prow) sc[i] = -INFINITY;
-            }
-            // ---- P^T (fp16) as B operands: MFMA m (keys 16m ..) takes S elements 8m .. 8m+7 ----
-            half8_t pf[2];
-            float ls = 0.f;
-            auto make_p = [&]() {
-                ls = 0.f;
-#pragma unroll
-                for (int m = 0; m < 2; m++)
-#pragma unroll
-                    for (int jj = 0; jj < 8; jj += 2) {
-                        const float p0 = fast_exp2(sc[8 * m + jj]), p1 = fast_exp2(sc[8 * m + jj + 1]);
-                        const half2_t ph = half2_t{(_Float16)p0, (_Float16)p1};
-                        pf[m][jj] = ph[0]; pf[m][jj + 1] = ph[1];
-                        ls = __builtin_amdgcn_fdot2(ph, ones, ls, false);
-                    }
-            };
-            auto row_max = [&]() {  // this lane's half of the row; the other half is in lane ^ 32
-                float mt = sc[0];
-#pragma unroll
-                for (int i = 1; i < 16; i++) mt = fmaxf(mt, sc[i]);
-                return mt;
-            };
-            if (j == 0) {
-                float mt = row_max();
-                mt = fmaxf(mt, __shfl_xor(mt, 32));
-                m_ref = mt;
-#pragma unroll
-                for (int i = 0; i < 16; i++) sc[i] -= mt;
-                make_p();
-            } else {
-                // lazy rescale: O and l are referenced to m_ref and move only when a row's maximum passes it by the
-                // slack. No score of a lane's half passes m_ref + slack while its probabilities sum to at most 2^slack,
-                // so the row maximum is needed only when some lane's sum exceeds that (or overflowed)
-                make_p();
-                if (__ballot(!(ls <= RESCALE_LSUM))) {
-                    const float mt = row_max();
-                    const float d = fmaxf(fmaxf(mt, __shfl_xor(mt, 32)), 0.f);
-                    const float cf = fast_exp2(-d);
-#pragma unroll
-                    for (int db = 0; db < 8; db++)
-#pragma unroll
-                        for (int i = 0; i < 16; i++) o[db][i] *= cf;
-                    l_run *= cf;
-                    m_ref += d;
-#pragma unroll
-                    for (int i = 0; i < 16; i++) sc[i] -= d;
-                    make_p();
-                }
-            }
-            l_run += ls;
-            // ---- O^T += V^T . P^T ----
-            {   // V^T operands read FA_KPF MFMAs ahead (MFMA q: dims 32*(q/2) + r, keys 16*(q%2) ..)
-                const _Float16* vrow = Vt + r * VST + 8 * h32;
-                half8_t va[FA_KPF];
-#pragma unroll
-                for (int q = 0; q < FA_KPF; q++) va[q] = *reinterpret_cast<const half8_t*>(vrow + 32 * (q >> 1) * VST + 16 * (q & 1));
-#pragma unroll
-                for (int q = 0; q < 16; q++) {
-                    const half8_t a = va[q % FA_KPF];
-                    if (q + FA_KPF < 16) {
-                        const int qn = q + FA_KPF;
-                        va[q % FA_KPF] = *reinterpret_cast<const half8_t*>(vrow + 32 * (qn >> 1) * VST + 16 * (qn & 1));
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-                    o[q >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[q & 1], o[q >> 1], 0, 0, 0);
-                }
-            }
+            fa_tile(reinterpret_cast<const _Float16*>(KBUF(j % NB)), reinterpret_cast<const _Float16*>(VBUF(j % NB)),
+                    SBUF(j % NB), (ja + j) * BK, j == 0, prow, wmin, r, h32, qf, o, m_ref, l_run);
         }
         if (!IMG || (j & 1) || j + 1 == ntiles) __syncthreads();
     }
