@@ -151,3 +151,42 @@ def test_skip_flag_fused_front():
     got, ref = out.cpu().numpy(), out2.cpu().numpy()
     report("skip flag, fused front", ns=nsg, same=bool(np.array_equal(got, ref)))
     assert np.all(np.isfinite(got)) and np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("pos,ns", [(0, 4), (1, 2), (63, 2), (64, 2), (65, 7), (255, 3), (256, 128), (3000, 128),
+                                    (5183, 5), (20480, 64), (89999, 128)])
+def test_fused_front_matches_three_launches(pos, ns):
+    """attn_decode's int8 T = 1 split step runs the q/k front and the append inside the split kernel; the same step
+    as three launches (qk_norm_rope, attn_gqa, attn_combine) must give the same qo, cache rows and output, bit for
+    bit. The positions put the new row alone in a split, alone in the short first chunk, at a chunk boundary and deep
+    in the cache, and (pos 0) leave most splits empty."""
+    import torch
+    import moex_amd as M
+    from tests.gpu_util import random_int8_cache, upload
+    max_t = max(pos + 1, 1024)
+    hc = random_int8_cache(max_t, seed=81)
+    da, db = upload(hc), upload(hc)
+    rng = np.random.default_rng(82 + pos)
+    LQ = H * 2 * AHD + 2 * KV * AHD
+    qkv = dev(rng.standard_normal((1, LQ), dtype=np.float32))
+    qn = dev((0.1 * rng.standard_normal(AHD)).astype(np.float16).view(np.int16))  # fp16 norm weights
+    kn = dev((0.1 * rng.standard_normal(AHD)).astype(np.float16).view(np.int16))
+    nsg = M.gqa_splits(1, KV, ns)
+    part = torch.empty(H * ns * (AHD + 2), device="cuda")
+    qa, qb = torch.full((1, H, AHD), float("nan"), device="cuda"), torch.full((1, H, AHD), float("nan"), device="cuda")
+    oa, ob = torch.full((1, H, AHD), float("nan"), device="cuda"), torch.full((1, H, AHD), float("nan"), device="cuda")
+    pd = pos_tensor(pos)
+    M.attn_decode(qkv, qkv[:, H * 2 * AHD:], qkv[:, H * 2 * AHD + KV * AHD:], qn, kn, qa, da, oa, H, KV, pd, max_t,
+                  64, 1e7, 1e-6, 1, LQ, None, part, ns)
+    M.qk_norm_rope(qkv, qkv[:, H * 2 * AHD:], qkv[:, H * 2 * AHD + KV * AHD:], qn, kn, qb, db, H, KV, pd, max_t,
+                   64, 1e7, 1e-6, LQ, 1)
+    M.attn_gqa(qb, db, H, KV, pd, max_t, part, 1, nsg)
+    M.attn_combine(part, qkv, ob, H, nsg, LQ, 1)
+    torch.cuda.synchronize()
+    ca, cb = download(da), download(db)
+    for x, y, name in ((ca.k, cb.k, "k"), (ca.v, cb.v, "v"), (ca.ks, cb.ks, "ks"), (ca.vs, cb.vs, "vs")):
+        assert np.array_equal(x.view(np.uint8), y.view(np.uint8)), f"cache {name} differs"
+    ga, gb = oa.cpu().numpy(), ob.cpu().numpy()
+    report("fused front vs three launches", pos=pos, ns=nsg, maxdiff=float(np.abs(ga - gb).max()))
+    assert np.array_equal(qa.cpu().numpy(), qb.cpu().numpy())
+    assert np.all(np.isfinite(ga)) and np.array_equal(ga, gb)
