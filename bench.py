@@ -214,29 +214,27 @@ def main():
             t_g = e0.elapsed_time(e1) / (10 * NG)
             del graph
             kv_bytes = 2.0 * ctx * 520
-            t_ad = None
-            if Tq == 1:
-                # the whole attn_decode step from the raw q/k/v row: at T = 1 the split kernel runs the q/k front and
-                # the append in its prologue. Each call rewrites row ctx - 1 of its cache with the same bytes.
-                LQ = LD + 2 * KV * AHD
-                qkv = torch.randn((1, LQ), generator=torch.Generator(device=dev).manual_seed(7), device=dev)
-                qn = torch.zeros(AHD, dtype=torch.int16, device=dev)
-                qo_ad = torch.empty((1, H, AHD), device=dev)
-                nsd = M.decode_splits(ctx)
-                part_ad = torch.empty(H * nsd * (AHD + 2), device=dev)
+            # the whole attn_decode step from the raw q/k/v rows (front, append, split kernel, combine; at T = 1
+            # the split kernel runs the front and the append in its prologue). Each call rewrites rows
+            # ctx - Tq .. ctx - 1 of its cache with the same bytes.
+            LQ = LD + 2 * KV * AHD
+            qkv = torch.randn((Tq, LQ), generator=torch.Generator(device=dev).manual_seed(7), device=dev)
+            qn = torch.zeros(AHD, dtype=torch.int16, device=dev)
+            qo_ad = torch.empty((Tq, H, AHD), device=dev)
+            nsd = M.decode_splits(ctx)
+            part_ad = torch.empty(Tq * H * nsd * (AHD + 2), device=dev)
 
-                def adec(c):
-                    return lambda: M.attn_decode(qkv, qkv[:, LD:], qkv[:, LD + KV * AHD:], qn, qn, qo_ad, c, o1, H, KV,
-                                                 pd, c.max_t, 64, 1e7, 1e-6, 1, LQ, st, part_ad, nsd)
-                t_ad = time_rotating([adec(c) for c in rot], 200)
+            def adec(c):
+                return lambda: M.attn_decode(qkv, qkv[:, LD:], qkv[:, LD + KV * AHD:], qn, qn, qo_ad, c, o1, H, KV,
+                                             pd, c.max_t, 64, 1e7, 1e-6, Tq, LQ, st, part_ad, nsd)
+            t_ad = time_rotating([adec(c) for c in rot], 200)
             dec[f"T{Tq}"] = {"ns": ns, "split_kernel_us": round(t_k * 1e3, 2), "with_combine_us": round(t_f * 1e3, 2),
                              "graph_step_us": round(t_g * 1e3, 2),
                              "GBps": round(kv_bytes / (t_f * 1e-3) / 1e9, 1),
                              "graph_GBps": round(kv_bytes / (t_g * 1e-3) / 1e9, 1),
                              "split_kernel_GBps": round(kv_bytes / (t_k * 1e-3) / 1e9, 1),
                              "hbm_frac": round(kv_bytes / (t_f * 1e-3) / 1e9 / PEAK_HBM, 4)}
-            if t_ad is not None:
-                dec[f"T{Tq}"]["attn_decode_us"] = round(t_ad * 1e3, 2)
+            dec[f"T{Tq}"]["attn_decode_us"] = round(t_ad * 1e3, 2)
             if want_cpu:
                 if Tq == 1:
                     hrot = host_cache(rot[0], ctx)
@@ -244,7 +242,7 @@ def main():
             print(f"[bench] config2 decode T={Tq} ctx={ctx} ns={ns}: {t_f * 1e3:.1f} us "
                   f"({dec[f'T{Tq}']['GBps']} GB/s; split kernel alone {t_k * 1e3:.1f} us; "
                   f"graph-replayed step {t_g * 1e3:.1f} us = {dec[f'T{Tq}']['graph_GBps']} GB/s"
-                  + (f"; whole attn_decode step {t_ad * 1e3:.1f} us" if t_ad is not None else "") + ")", flush=True)
+                  f"; whole attn_decode step {t_ad * 1e3:.1f} us)", flush=True)
         del rot
         extra["config2_decode_int8_90k"] = dec
         # ---------------- config 1 depth comparison / config 4: turbo at 262k ----------------
@@ -272,11 +270,27 @@ def main():
         tb = 2.0 * ctx * 240
         extra["config3_decode_turbo_262k"] = {"ns": ns, "us": round(t_td * 1e3, 2),
                                               "GBps": round(tb / (t_td * 1e-3) / 1e9, 1)}
+        if not a.config4_only:
+            # the whole attn_decode step from the raw q/k/v row: front (+ forward WHT, turbo append of row ctx - 1,
+            # the same bytes each call), split kernel, gated combine
+            LQ = LD + 2 * KV * AHD
+            qkv_t = torch.randn((1, LQ), generator=torch.Generator(device=dev).manual_seed(8), device=dev)
+            qn_t = torch.zeros(AHD, dtype=torch.int16, device=dev)
+            qo_t = torch.empty((1, H, AHD), device=dev)
+            nsd = M.decode_splits(ctx)
+            part_t = torch.empty(H * nsd * (AHD + 2), device=dev)
+
+            def tstep(c):
+                return lambda: M.attn_decode(qkv_t, qkv_t[:, LD:], qkv_t[:, LD + KV * AHD:], qn_t, qn_t, qo_t, c, o1, H,
+                                             KV, pd, c.max_t, 64, 1e7, 1e-6, 1, LQ, st, part_t, nsd)
+            extra["config3_decode_turbo_262k"]["attn_decode_us"] = round(time_rotating([tstep(c) for c in cts], 90) * 1e3, 2)
         hct = None
         if want_cpu:
             hct = host_cache(ct, ctx)
             extra["config3_decode_turbo_262k"]["cpu"] = cpu_decode(hct, qh[:1], gh[:1], ctx - 1, 1, tb, threads)
-        print(f"[bench] config3 turbo decode ctx={ctx}: {t_td * 1e3:.1f} us ({tb / t_td / 1e6:.0f} GB/s)", flush=True)
+        print(f"[bench] config3 turbo decode ctx={ctx}: {t_td * 1e3:.1f} us ({tb / t_td / 1e6:.0f} GB/s)"
+              + (f"; whole attn_decode step {extra['config3_decode_turbo_262k']['attn_decode_us']} us"
+                 if 'attn_decode_us' in extra['config3_decode_turbo_262k'] else ""), flush=True)
         if a.decode_only:
             print(json.dumps({"decode_only": True, **extra}), flush=True)
             return
