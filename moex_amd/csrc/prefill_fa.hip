@@ -462,6 +462,7 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
         auto issue = [&](int j) { fa_issue_img(src, ja + j, smem + (j % NB) * TILE_BYTES, pw, lane); };
         // piece counts per wavefront: 10 for pw = 0 (pieces 0, 4, .., 36), 9 for the others
         // pairs of tiles: pair p = tiles 2p, 2p + 1 in buffers 2 (p % 2), + 1; one barrier per pair
+        asm volatile("s_barrier" ::: "memory");  // the queries' reads are out ahead of the first images
         for (int j = 0; j < 4 && j < ntiles; j++) issue(j);
         fa_wait_first_pair(ntiles, pw);
         asm volatile("s_barrier" ::: "memory");  // pair 0 is in buffers 0, 1
@@ -529,10 +530,18 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
     half8_t qf[16];
     {
         const float* qrow = qo + ((size_t)(t0 + min(tokw, nt - 1)) * H + head) * AHD;
+        float4 qa[32];
 #pragma unroll
         for (int s = 0; s < 16; s++) {
             const float4* p4 = reinterpret_cast<const float4*>(qrow + 16 * s + 8 * h32);
-            const float4 a = p4[0], b = p4[1];
+            qa[2 * s] = p4[0];
+            qa[2 * s + 1] = p4[1];
+        }
+        // with tile images, the DMA wavefronts send the first images once these reads are out
+        if (IMG) asm volatile("s_barrier" ::: "memory");
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            const float4 a = qa[2 * s], b = qa[2 * s + 1];
             qf[s] = half8_t{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
                             (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
         }
