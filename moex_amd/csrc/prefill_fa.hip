@@ -1,12 +1,14 @@
 // FlashAttention-2 chunked causal GQA prefill on gfx950 (replaces attn_fa_k<TB>, kernels.cuh:1443-1728).
 //
+// int8 chunks of at most FA_GQA_MAXT tokens run on the split-K decode kernels instead (fa_plan).
 // Workgroup = (kv head, 16 query tokens) = 128 query rows (8 heads x 16 tokens) and 8 wavefronts:
 //   - wavefronts 4-7 fill LDS with key tiles of 32, widened to fp16: K as [key][dim] (row stride padded to 528 B:
 //     conflict-free reads with immediate offsets), V transposed as [dim][key] and already multiplied by its row scale
 //     (int8: vs; turbo: half norm * K3), so P enters the P.V product as plain fp16 probabilities. Turbo K is likewise
-//     multiplied by its half norm * K4; int8 K stays exact and its scale is applied to the fp32 score. For a chunk
-//     of at least 8 token tiles per kv head a pre-pass (fa_image_kernel) widens every tile once into a workspace and
-//     the wavefronts copy the images by DMA; for shorter chunks they load and widen each tile themselves;
+//     multiplied by its half norm * K4; int8 K stays exact and its scale is applied to the fp32 score. A pre-pass
+//     (fa_image_kernel) widens every tile once into a workspace and the wavefronts copy the images by DMA; without
+//     the workspace (MOEX_FA_IMAGES=0, an allocation that failed, the no-allocation entry point) they load and widen
+//     each tile themselves;
 //   - wavefronts 0-3 compute, 32 query rows each (wavefront w: tokens 4w .. 4w+3, row r = (token 4w + r/8,
 //     head r%8)): S^T = K . Q^T and O^T += V^T . P^T on v_mfma_f32_32x32x16_f16 with Q fp16 in registers. The 32x32
 //     D layout gives each lane one query row (lane % 32) and 16 keys. LDS operand reads are issued two MFMAs ahead
@@ -40,7 +42,7 @@ constexpr int SC_BYTES = BK * 4;            // per-key score scale
 // One tile buffer in LDS: widened K rows, scaled V^T, the score scales and a spare slot. A tile image in global memory
 // (the pre-pass output) holds the same bytes, so a DMA copies it as is.
 constexpr int TILE_BYTES = KT_BYTES + VT_BYTES + 2 * SC_BYTES;  // 37632 B
-constexpr int FA_IMG_TILES = 8;             // token tiles per kv head from which the tile-image path is used
+constexpr int FA_GQA_MAXT = 64;             // int8 chunks up to this many tokens run on the split-K decode kernels
 constexpr float SL2 = 0.0625f * 1.4426950408889634f;
 constexpr float TK4 = 0.241529f / 127.f, TK3 = 0.190207f / 127.f;
 constexpr int FA_KPF = 2;                   // LDS operand reads in flight ahead of the MFMAs
@@ -651,7 +653,7 @@ struct WsKey {
     int dev;
     hipStream_t st;
     int kind;  // 0: FA tile images, 1: FA partials of split token tiles, 2: fp16 GEMM activations,
-               // 3: GEMM K-split partials
+               // 3: GEMM K-split partials, 4: decode-kernel partials of short FA chunks
     bool operator<(const WsKey& o) const {
         return dev != o.dev ? dev < o.dev : st != o.st ? st < o.st : kind < o.kind;
     }
@@ -718,7 +720,17 @@ int fa_ncu() {
 struct FaPlan {
     int NT, ntmax, nsf;
     size_t part_bytes, img_bytes;
+    int gns;            // > 0: an int8 chunk this short runs on the split-K decode kernels with gns splits
+    size_t gqa_bytes;   // their partials
 };
+
+// Chunks of at most this many tokens (int8) run on the decode kernels (gqa_wsp_kernel per 4-token group, then the
+// combine) instead of the FA kernel, whose workgroups hold 16 tokens each and leave most of the chip idle on a short
+// chunk. MOEX_FA_GQA_MAXT=n sets the bound (0: never); it is read on every call.
+int fa_gqa_maxt() {
+    if (const char* e = std::getenv("MOEX_FA_GQA_MAXT")) return std::max(0, std::atoi(e));
+    return FA_GQA_MAXT;
+}
 
 FaPlan fa_plan(int H, int KV, int max_t, int T) {
     const int ncu = fa_ncu();
@@ -745,7 +757,17 @@ FaPlan fa_plan(int H, int KV, int max_t, int T) {
     }
     p.nsf = nsf;
     p.part_bytes = nsf > 1 ? (size_t)T * H * nsf * FP_ROW * sizeof(float) : 0;
-    p.img_bytes = NT >= FA_IMG_TILES ? (size_t)KV * p.ntmax * TILE_BYTES : 0;
+    // tile images for every chunk: measured faster than widening in the kernel at every chunk length and context
+    // (a 3-token chunk over 90 000 keys: 159 against 388 us for turbo). MOEX_FA_IMAGES=0 turns them off (read on
+    // every call), which saves the workspace and gives the same bits.
+    const char* ie = std::getenv("MOEX_FA_IMAGES");
+    p.img_bytes = !(ie && std::atoi(ie) == 0) ? (size_t)KV * p.ntmax * TILE_BYTES : 0;
+    p.gns = 0;
+    p.gqa_bytes = 0;
+    if (T <= fa_gqa_maxt() && H == KV * GQ) {
+        p.gns = gqa_splits(T, KV, moex_decode_splits(max_t), false);
+        p.gqa_bytes = (size_t)T * H * p.gns * (AHD + 2) * sizeof(float);
+    }
     return p;
 }
 
@@ -785,6 +807,14 @@ template <bool TB>
 void launch_fa_t(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d,
                  int max_t, int ld, int T, hipStream_t st) {
     const FaPlan p = fa_plan(H, KV, max_t, T);
+    if (!TB && p.gns > 0) {  // a short int8 chunk: split-K decode kernels and the gated combine
+        float* part = reinterpret_cast<float*>(stream_workspace(p.gqa_bytes, st, 4));
+        if (part) {
+            launch_gqa(qo, kv, H, KV, pos_d, max_t, part, T, p.gns, st);
+            launch_combine(part, q_gate, out, H, p.gns, ld, T, st);
+            return;
+        }
+    }
     float* fpart = p.part_bytes ? reinterpret_cast<float*>(stream_workspace(p.part_bytes, st, 1)) : nullptr;
     unsigned char* img = p.img_bytes ? stream_workspace(p.img_bytes, st, 0) : nullptr;
     launch_fa_bufs<TB>(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, st, p, img, fpart, fpart ? p.nsf : 1);
@@ -800,6 +830,11 @@ void launch_fa(const float* qo, const float* q_gate, moex_kv_cache kv, float* ou
 void launch_fa_scratch(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
                        const int* pos_d, int max_t, int ld, int T, hipStream_t st, float* scratch, size_t bytes) {
     const FaPlan p = fa_plan(H, KV, max_t, T);
+    if (!kv.turbo && p.gns > 0 && p.gqa_bytes <= bytes) {  // a short int8 chunk, as in launch_fa_t
+        launch_gqa(qo, kv, H, KV, pos_d, max_t, scratch, T, p.gns, st);
+        launch_combine(scratch, q_gate, out, H, p.gns, ld, T, st);
+        return;
+    }
     // the pieces' partial rows must fit the scratch: fewer pieces when they do not (no tile images: the staging
     // wavefronts widen every tile, which gives the same bits)
     const size_t per = (size_t)T * H * FP_ROW * sizeof(float);
@@ -813,7 +848,7 @@ void launch_fa_scratch(const float* qo, const float* q_gate, moex_kv_cache kv, f
 
 size_t fa_workspace_bytes(int H, int KV, int max_t, int T) {
     const FaPlan p = fa_plan(H, KV, max_t, T);
-    return p.part_bytes + p.img_bytes;
+    return std::max(p.part_bytes + p.img_bytes, p.gqa_bytes);  // (a turbo chunk takes the FA path)
 }
 
 }  // namespace moex

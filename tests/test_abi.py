@@ -81,14 +81,16 @@ def test_gqa_splits_policy():
 
 def test_attn_workspace_bytes():
     """The per-stream workspace one attn_fa call takes (for a VRAM audit beside kv_bytes): tile images of
-    KV * ceil(max_t / 32) * 37632 B for chunks of 128 tokens and more; partial rows of split token tiles for short
-    chunks (256 CUs: the fallback without a device, MI355X's count)."""
+    KV * ceil(max_t / 32) * 37632 B, plus partial rows of split token tiles for short chunks; for chunks of at most
+    64 tokens, at least the decode kernels' partials T * H * ns * 1032 B, which int8 chunks take instead (the count
+    covers turbo chunks, which take the FA path). 256 CUs: the fallback without a device, MI355X's count."""
     import moex_amd as M
     if not os.path.exists(M.LIB_PATH):
         pytest.skip("libmoex_attn.so not built")
     assert M.attn_workspace_bytes(16, 2, 34816, 2048) == 2 * 1088 * 37632          # configs[1]: images only
     assert M.attn_workspace_bytes(16, 2, 262144, 2048) == 2 * 8192 * 37632         # configs[4]: 617 MB
-    assert M.attn_workspace_bytes(16, 2, 40000, 64) == 64 * 16 * 32 * 1040         # 32 key pieces, no images
-    assert M.attn_workspace_bytes(16, 2, 64, 64) == 0                              # nothing to split
+    assert M.attn_workspace_bytes(16, 2, 40000, 64) == 2 * 1250 * 37632 + 64 * 16 * 32 * 1040  # 32 key pieces
+    assert M.attn_workspace_bytes(16, 2, 64, 64) == 64 * 16 * 1 * 1032                # decode kernels, 1 split
+    assert M.attn_workspace_bytes(16, 2, 40000, 256) == 2 * 1250 * 37632 + 256 * 16 * 16 * 1040  # 16 pieces
     assert M.attn_workspace_bytes(12, 2, 1000, 64) == 0                            # not a GQA-8 shape
     assert M.workspace_held() == 0

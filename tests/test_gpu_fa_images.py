@@ -1,9 +1,8 @@
 """attn_fa's two staging paths and its tile-image workspace.
 
-A chunk of 8 or more 16-token tiles per kv head (T >= 128) is widened once by the image pre-pass and copied into LDS
-by DMA; a shorter chunk is widened inside the FA kernel. The two paths feed the same bytes to the same arithmetic, so
-the rows two chunks have in common (same token tiles, same wavefronts, key splitting off) come out bit for bit the
-same. The workspace is per (device, stream) and grows with max_t; growing it, and a second stream, must not change a
+A chunk is widened once by the image pre-pass and copied into LDS by DMA; with MOEX_FA_IMAGES=0 the FA kernel widens
+each tile itself. The two paths feed the same bytes to the same arithmetic, so the rows two chunks have in common
+(same token tiles, same wavefronts, key splitting off) come out bit for bit the same. The workspace is per (device, stream) and grows with max_t; growing it, and a second stream, must not change a
 result.
 """
 import numpy as np
@@ -50,8 +49,9 @@ def test_image_path_matches_in_kernel_widening(data, turbo, pos0, monkeypatch):
     else:
         dc = upload(random_int8_cache(max_t, seed=4))
     gate = None if turbo else qg_d
-    img = _fa(dc, qo_d, gate, pos0, 128)      # 8 token tiles: tile images + DMA
-    ink = _fa(dc, qo_d, gate, pos0, 112)      # 7 token tiles: widened in the kernel
+    img = _fa(dc, qo_d, gate, pos0, 128)      # tile images + DMA
+    monkeypatch.setenv("MOEX_FA_IMAGES", "0")
+    ink = _fa(dc, qo_d, gate, pos0, 112)      # widened in the kernel
     report("fa image vs in-kernel", turbo=turbo, pos0=pos0, maxdiff=float(np.abs(img[:112] - ink).max()))
     assert np.all(np.isfinite(img))
     assert np.array_equal(img[:112], ink)

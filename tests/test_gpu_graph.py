@@ -129,11 +129,14 @@ def test_fa_images_and_dense_graph_replays():
         torch.cuda.synchronize()
 
 
-def test_fa_key_pieces_graph_new_position():
+@pytest.mark.parametrize("gqa_maxt", ["0", "64"])
+def test_fa_key_pieces_graph_new_position(gqa_maxt, monkeypatch):
     """A short chunk splits its token tiles' keys into pieces chosen on the device from pos_d: one captured attn_fa
-    (FA kernel + merge), replayed after the position changes, matches an eager call at each position bit for bit."""
+    (image pre-pass, FA kernel + merge), replayed after the position changes, matches an eager call at each position
+    bit for bit. The same for the decode kernels that run such a chunk by default (split kernel + combine)."""
     import torch
     import moex_amd as M
+    monkeypatch.setenv("MOEX_FA_GQA_MAXT", gqa_maxt)
     from tests.gpu_util import LD, random_int8_cache, upload
     rng = np.random.default_rng(23)
     dc = upload(random_int8_cache(12000, seed=24))

@@ -55,14 +55,38 @@ def test_fa_int8(setup, pos0, T):
     assert np.all(np.isfinite(o)) and np.all(np.abs(o).max(axis=-1) > 0)
 
 
+@pytest.mark.parametrize("pos0,T", [(32000, 64), (5000, 3), (34000, 17), (0, 37), (30000, 8)])
+def test_fa_short_chunks_on_decode_kernels(setup, pos0, T, monkeypatch):
+    """int8 chunks of at most 64 tokens run on the split-K decode kernels and the gated combine: the test_fa.cu gate,
+    and agreement with the FA kernel on the same chunk (MOEX_FA_GQA_MAXT=0) to the FA split tolerance."""
+    import torch
+    import moex_amd as M
+    hc, dc, qo, qg, qo_d, qg_d = setup
+    outs = {}
+    for maxt in ("64", "0"):
+        monkeypatch.setenv("MOEX_FA_GQA_MAXT", maxt)
+        out = torch.full((T, H, AHD), float("nan"), dtype=torch.float32, device="cuda")
+        M.attn_fa(qo_d, qg_d, dc, out, H, KV, pos_tensor(pos0), dc.max_t, LD, T)
+        torch.cuda.synchronize()
+        outs[maxt] = out.cpu().numpy()
+        assert np.all(np.isfinite(outs[maxt]))
+        _gate(f"fa int8 short, gqa bound {maxt}", outs[maxt], qo, qg, hc, pos0, T)
+    mag = float(np.abs(outs["0"]).max())
+    d = float(np.abs(outs["64"] - outs["0"]).max())
+    report("fa short: decode kernels vs FA kernel", pos0=pos0, T=T, maxdiff=d, mag=mag)
+    assert d <= 2e-3 * mag
+
+
 @pytest.mark.parametrize("pos0,T", [(32000, 64), (0, 1024), (5000, 3), (20000, 200), (34000, 17)])
 def test_fa_key_split(setup, pos0, T, monkeypatch):
     """Chunks whose token tiles leave the chip underfilled (KV x tiles < CUs) split each token tile's keys over
     several workgroups, merged by a second kernel: both results meet the gate, and they agree with the unsplit kernel
-    (MOEX_FA_SPLIT=1)."""
+    (MOEX_FA_SPLIT=1). The FA kernel also for the chunks of at most 64 tokens (MOEX_FA_GQA_MAXT=0), which by default
+    run on the decode kernels."""
     import torch
     import moex_amd as M
     hc, dc, qo, qg, qo_d, qg_d = setup
+    monkeypatch.setenv("MOEX_FA_GQA_MAXT", "0")
     outs = {}
     for cap in ("32", "1"):
         monkeypatch.setenv("MOEX_FA_SPLIT", cap)

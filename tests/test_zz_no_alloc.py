@@ -72,12 +72,13 @@ def test_noalloc_matches_attn_decode(turbo):
         assert np.all(np.isfinite(ob)) and same
 
 
-def test_noalloc_capped_pieces_and_rejection():
-    """T = 64 at 32000 would take 32 key pieces (34 MB of partials): the scratch (32 MiB) holds 31, so the result
-    is within the FA split tolerance (2e-3 of max |out|, as split vs unsplit). T*H*ns*1032 beyond the scratch is an
-    argument error that leaves out untouched."""
+def test_noalloc_capped_pieces_and_rejection(monkeypatch):
+    """T = 64 at 32000 on the FA kernel (MOEX_FA_GQA_MAXT=0) would take 32 key pieces (34 MB of partials): the
+    scratch (32 MiB) holds 31, so the result is within the FA split tolerance (2e-3 of max |out|, as split vs
+    unsplit). T*H*ns*1032 beyond the scratch is an argument error that leaves out untouched."""
     import torch
     import moex_amd as M
+    monkeypatch.setenv("MOEX_FA_GQA_MAXT", "0")
     max_t = 32064
     hc = random_int8_cache(max_t, seed=23)
     caches = [upload(hc), upload(hc)]
