@@ -14,10 +14,10 @@
  * bytes (MOEX_FA_IMAGES=0: none, the kernel widens each tile itself, same results, slower). A chunk whose token
  * tiles leave the chip underfilled (KV * ceil(T / 16) < CUs) may split each token tile's keys over several
  * workgroups, with a second workspace for their partial results, T * H * pieces * 1040 bytes (at most 32 pieces;
- * MOEX_FA_SPLIT=n caps them, 1 turns splitting off). An int8 chunk of at most 64 tokens (MOEX_FA_GQA_MAXT=n sets
- * the bound, 0 turns it off) runs on the split-K decode kernels and the combine instead, with a workspace of
- * T * H * ns * 1032 bytes for their partials (ns = moex_gqa_splits(T, KV, moex_decode_splits(max_t), 0)). The dense
- * GEMM (moex_dense.h) keeps two more. Each is one per (device, stream), allocated on first use with hipMalloc and grown
+ * MOEX_FA_SPLIT=n caps them, 1 turns splitting off). A chunk of at most 64 tokens (turbo: 16; MOEX_FA_GQA_MAXT=n
+ * sets the int8 bound to n and the turbo bound to n / 4, 0 turns it off) runs on the split-K decode kernels and the
+ * combine instead, with a workspace of T * H * ns * 1032 bytes for their partials (ns = moex_gqa_splits(T, KV,
+ * moex_decode_splits(max_t), turbo)). The dense GEMM (moex_dense.h) keeps two more. Each is one per (device, stream), allocated on first use with hipMalloc and grown
  * when a larger call comes. An outgrown buffer is not freed before the process ends, because a HIP graph captured
  * earlier may still replay into it. No workspace is allocated while the stream is being captured: a call that would
  * need to grow one reports hipErrorStreamCaptureUnsupported. So after one eager call of a given max_t and T on a

@@ -1,6 +1,6 @@
 // FlashAttention-2 chunked causal GQA prefill on gfx950 (replaces attn_fa_k<TB>, kernels.cuh:1443-1728).
 //
-// int8 chunks of at most FA_GQA_MAXT tokens run on the split-K decode kernels instead (fa_plan).
+// Chunks of at most FA_GQA_MAXT tokens (turbo: a quarter) run on the split-K decode kernels instead (fa_plan).
 // Workgroup = (kv head, 16 query tokens) = 128 query rows (8 heads x 16 tokens) and 8 wavefronts:
 //   - wavefronts 4-7 fill LDS with key tiles of 32, widened to fp16: K as [key][dim] (row stride padded to 528 B:
 //     conflict-free reads with immediate offsets), V transposed as [dim][key] and already multiplied by its row scale
@@ -42,7 +42,8 @@ constexpr int SC_BYTES = BK * 4;            // per-key score scale
 // One tile buffer in LDS: widened K rows, scaled V^T, the score scales and a spare slot. A tile image in global memory
 // (the pre-pass output) holds the same bytes, so a DMA copies it as is.
 constexpr int TILE_BYTES = KT_BYTES + VT_BYTES + 2 * SC_BYTES;  // 37632 B
-constexpr int FA_GQA_MAXT = 64;             // int8 chunks up to this many tokens run on the split-K decode kernels
+constexpr int FA_GQA_MAXT = 64;             // int8 chunks up to this many tokens (turbo: a quarter) run on the
+                                            // split-K decode kernels
 constexpr float SL2 = 0.0625f * 1.4426950408889634f;
 constexpr float TK4 = 0.241529f / 127.f, TK3 = 0.190207f / 127.f;
 constexpr int FA_KPF = 2;                   // LDS operand reads in flight ahead of the MFMAs
@@ -720,19 +721,21 @@ int fa_ncu() {
 struct FaPlan {
     int NT, ntmax, nsf;
     size_t part_bytes, img_bytes;
-    int gns;            // > 0: an int8 chunk this short runs on the split-K decode kernels with gns splits
+    int gns;            // > 0: a chunk this short runs on the split-K decode kernels with gns splits
     size_t gqa_bytes;   // their partials
 };
 
-// Chunks of at most this many tokens (int8) run on the decode kernels (gqa_wsp_kernel per 4-token group, then the
-// combine) instead of the FA kernel, whose workgroups hold 16 tokens each and leave most of the chip idle on a short
-// chunk. MOEX_FA_GQA_MAXT=n sets the bound (0: never); it is read on every call.
-int fa_gqa_maxt() {
-    if (const char* e = std::getenv("MOEX_FA_GQA_MAXT")) return std::max(0, std::atoi(e));
-    return FA_GQA_MAXT;
+// Chunks of at most this many tokens run on the decode kernels (int8: gqa_wsp_kernel per 4-token group; turbo:
+// gqa_wst_kernel per token; then the combine) instead of the FA kernel, whose workgroups hold 16 tokens each and
+// leave most of the chip idle on a short chunk. MOEX_FA_GQA_MAXT=n sets the int8 bound to n and the turbo bound to
+// n / 4 (0: never); it is read on every call.
+int fa_gqa_maxt(bool turbo) {
+    int n = FA_GQA_MAXT;
+    if (const char* e = std::getenv("MOEX_FA_GQA_MAXT")) n = std::max(0, std::atoi(e));
+    return turbo ? n / 4 : n;
 }
 
-FaPlan fa_plan(int H, int KV, int max_t, int T) {
+FaPlan fa_plan(int H, int KV, int max_t, int T, bool turbo) {
     const int ncu = fa_ncu();
     FaPlan p;
     p.NT = (T + FT - 1) / FT;
@@ -764,8 +767,8 @@ FaPlan fa_plan(int H, int KV, int max_t, int T) {
     p.img_bytes = !(ie && std::atoi(ie) == 0) ? (size_t)KV * p.ntmax * TILE_BYTES : 0;
     p.gns = 0;
     p.gqa_bytes = 0;
-    if (T <= fa_gqa_maxt() && H == KV * GQ) {
-        p.gns = gqa_splits(T, KV, moex_decode_splits(max_t), false);
+    if (T <= fa_gqa_maxt(turbo) && H == KV * GQ) {
+        p.gns = gqa_splits(T, KV, moex_decode_splits(max_t), turbo);
         p.gqa_bytes = (size_t)T * H * p.gns * (AHD + 2) * sizeof(float);
     }
     return p;
@@ -806,8 +809,9 @@ void launch_fa_bufs(const float* qo, const float* q_gate, moex_kv_cache kv, floa
 template <bool TB>
 void launch_fa_t(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d,
                  int max_t, int ld, int T, hipStream_t st) {
-    const FaPlan p = fa_plan(H, KV, max_t, T);
-    if (!TB && p.gns > 0) {  // a short int8 chunk: split-K decode kernels and the gated combine
+    const FaPlan p = fa_plan(H, KV, max_t, T, TB);
+    if (p.gns > 0) {  // a short chunk: split-K decode kernels and the gated combine (turbo: in the rotated domain, as
+                      // the FA kernel leaves it)
         float* part = reinterpret_cast<float*>(stream_workspace(p.gqa_bytes, st, 4));
         if (part) {
             launch_gqa(qo, kv, H, KV, pos_d, max_t, part, T, p.gns, st);
@@ -829,8 +833,8 @@ void launch_fa(const float* qo, const float* q_gate, moex_kv_cache kv, float* ou
 
 void launch_fa_scratch(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
                        const int* pos_d, int max_t, int ld, int T, hipStream_t st, float* scratch, size_t bytes) {
-    const FaPlan p = fa_plan(H, KV, max_t, T);
-    if (!kv.turbo && p.gns > 0 && p.gqa_bytes <= bytes) {  // a short int8 chunk, as in launch_fa_t
+    const FaPlan p = fa_plan(H, KV, max_t, T, kv.turbo != 0);
+    if (p.gns > 0 && p.gqa_bytes <= bytes) {  // a short chunk, as in launch_fa_t
         launch_gqa(qo, kv, H, KV, pos_d, max_t, scratch, T, p.gns, st);
         launch_combine(scratch, q_gate, out, H, p.gns, ld, T, st);
         return;
@@ -847,8 +851,13 @@ void launch_fa_scratch(const float* qo, const float* q_gate, moex_kv_cache kv, f
 }
 
 size_t fa_workspace_bytes(int H, int KV, int max_t, int T) {
-    const FaPlan p = fa_plan(H, KV, max_t, T);
-    return std::max(p.part_bytes + p.img_bytes, p.gqa_bytes);  // (a turbo chunk takes the FA path)
+    // the larger of the int8 and the turbo plan (the query does not name the cache format)
+    size_t b = 0;
+    for (bool tb : {false, true}) {
+        const FaPlan p = fa_plan(H, KV, max_t, T, tb);
+        b = std::max(b, p.gns > 0 ? p.gqa_bytes : p.part_bytes + p.img_bytes);
+    }
+    return b;
 }
 
 }  // namespace moex

@@ -139,11 +139,15 @@ def turbo_setup():
     return hc, dc, qo, qg, dev(qo), dev(qg)
 
 
-@pytest.mark.parametrize("pos0,T", [(0, 37), (5, 3), (1000, 100), (4096, 2048)])
-def test_fa_turbo(turbo_setup, pos0, T):
-    """No gate (turbo: attn_fa writes the rotated-domain output), then turbo_out -> the full turbo reference."""
+@pytest.mark.parametrize("gqa_maxt", ["64", "0"])
+@pytest.mark.parametrize("pos0,T", [(0, 37), (5, 3), (1000, 100), (4096, 2048), (6000, 16), (3000, 8)])
+def test_fa_turbo(turbo_setup, pos0, T, gqa_maxt, monkeypatch):
+    """No gate (turbo: attn_fa writes the rotated-domain output), then turbo_out -> the full turbo reference. Chunks
+    of at most 16 tokens run on the turbo split-K decode kernel by default (bound 64 / 4), on the FA kernel with
+    MOEX_FA_GQA_MAXT=0."""
     import torch
     import moex_amd as M
+    monkeypatch.setenv("MOEX_FA_GQA_MAXT", gqa_maxt)
     hc, dc, qo, qg, qo_d, qg_d = turbo_setup
     out = torch.zeros((T, H, AHD), dtype=torch.float32, device="cuda")
     M.attn_fa(qo_d, None, dc, out, H, KV, pos_tensor(pos0), dc.max_t, LD, T)
