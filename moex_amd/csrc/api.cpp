@@ -216,6 +216,20 @@ void decode_step(const float* q, const float* k, const float* v, const uint16_t*
                  moex_kv_cache kv, float* out, int H, int KV, const int* pos_d, int max_t, int rot, float theta,
                  float eps, int T, int ld, hipStream_t st, float* part, int ns, float* fa_scr, size_t fa_bytes) {
     const int G = H / KV;
+    if (ns == 1 && T <= 2 && G == GQ) {
+        // the reference's one-split path (attn_decode_k per query head, no partials): one workgroup per head and
+        // token leaves the chip idle (90 000 keys: 8.4 ms int8, 11.6 ms turbo). The split-K kernels take it with
+        // partials of the library's own (a workspace, or the no-allocation scratch); the per-head kernel only when
+        // that is not available.
+        const int n2 = gqa_splits(T, KV, moex_decode_splits(max_t), kv.turbo != 0);
+        const size_t need = (size_t)T * H * n2 * (AHD + 2) * sizeof(float);
+        float* w = fa_scr ? (need <= fa_bytes ? fa_scr : nullptr)
+                          : n2 > 1 ? reinterpret_cast<float*>(stream_workspace(need, st, 4)) : nullptr;
+        if (w) {
+            part = w;
+            ns = n2;
+        }
+    }
     if (T == 1 && ns > 1 && G == GQ && !kv.turbo) {
         // one int8 token: the split kernel runs the q/k front in its prologue (one launch fewer per step)
         const FrontArgs fr{q, k, v, qn, kn, qo, skip_flag(), rot, theta, eps, ld};

@@ -72,7 +72,7 @@ def test_attn_decode_paths():
     q1 = torch.empty((1, H, AHD), dtype=torch.float32, device="cuda")
     for cache, full in ((ct, b), (c8, a)):
         run(cache, d1, pos0 + T - 1, 1, ns, part, q1)   # GQA split + combine
-        run(cache, d2, pos0 + T - 1, 1, 1, None, q1)    # per-head kernel
+        run(cache, d2, pos0 + T - 1, 1, 1, None, q1)    # ns = 1: split-K with the library's own partials
         f = full[T - 1]
         e1 = float(np.abs(d1.cpu().numpy()[0] - f).max())
         e2 = float(np.abs(d2.cpu().numpy()[0] - f).max())
@@ -190,3 +190,33 @@ def test_fused_front_matches_three_launches(pos, ns):
     report("fused front vs three launches", pos=pos, ns=nsg, maxdiff=float(np.abs(ga - gb).max()))
     assert np.array_equal(qa.cpu().numpy(), qb.cpu().numpy())
     assert np.all(np.isfinite(ga)) and np.array_equal(ga, gb)
+
+
+@pytest.mark.parametrize("turbo", [0, 1])
+@pytest.mark.parametrize("T", [1, 2])
+def test_one_split_call_runs_split_k(turbo, T):
+    """attn_decode with ns = 1 (the reference's one-split path, no partials) runs the split-K kernels with partials
+    of the library's own, moex_gqa_splits(T, KV, moex_decode_splits(max_t)) splits: the same bits as a call that
+    passes those splits and a partial buffer."""
+    import torch
+    import moex_amd as M
+    LQ = H * 2 * AHD + 2 * KV * AHD
+    n = 20000
+    outs = []
+    for ns in (1, M.decode_splits(n + 64)):
+        c = M.DeviceKVCache(KV, n + 64, turbo)
+        g = torch.Generator(device="cuda").manual_seed(40)
+        k = torch.randn((n, KV * AHD), generator=g, device="cuda")
+        v = torch.randn((n, KV * AHD), generator=g, device="cuda")
+        M.kv_append(k, v, c, KV, pos_tensor(0), c.max_t, KV * AHD, n)
+        qkv = torch.randn((T, LQ), generator=g, device="cuda")
+        qn = torch.zeros(AHD, dtype=torch.int16, device="cuda")
+        qo = torch.empty((T, H, AHD), device="cuda")
+        out = torch.full((T, H, AHD), float("nan"), device="cuda")
+        part = torch.empty(T * H * ns * (AHD + 2), device="cuda") if ns > 1 else None
+        M.attn_decode(qkv, qkv[:, H * 2 * AHD:], qkv[:, H * 2 * AHD + KV * AHD:], qn, qn, qo, c, out, H, KV,
+                      pos_tensor(n), c.max_t, 64, 1e7, 1e-6, T, LQ, None, part, ns)
+        torch.cuda.synchronize()
+        outs.append(out.cpu().numpy())
+    report("attn_decode ns=1 vs splits", turbo=turbo, T=T, maxdiff=float(np.abs(outs[0] - outs[1]).max()))
+    assert np.all(np.isfinite(outs[0])) and np.array_equal(outs[0], outs[1])
