@@ -230,11 +230,12 @@ void decode_step(const float* q, const float* k, const float* v, const uint16_t*
             ns = n2;
         }
     }
-    if (T == 1 && ns > 1 && G == GQ && !kv.turbo) {
-        // one int8 token: the split kernel runs the q/k front in its prologue (one launch fewer per step)
+    if (T == 1 && ns > 1 && G == GQ) {
+        // one token: the split kernel runs the q/k front in its prologue (one launch fewer per step); turbo: its
+        // partials rotated back, so the combine gates them and no turbo_out follows
         const FrontArgs fr{q, k, v, qn, kn, qo, skip_flag(), rot, theta, eps, ld};
-        ns = gqa_splits(T, KV, ns, false);
-        launch_gqa(qo, kv, H, KV, pos_d, max_t, part, T, ns, st, false, &fr);
+        ns = gqa_splits(T, KV, ns, kv.turbo != 0);
+        launch_gqa(qo, kv, H, KV, pos_d, max_t, part, T, ns, st, kv.turbo != 0, &fr);
         launch_combine(part, q, out, H, ns, ld, T, st);
         return;
     }

@@ -855,6 +855,7 @@ constexpr int WT_QT = WT_P0 + WT_NW * WT_PT;     // query digit table: [digit 2,
 constexpr int WT_QS = WT_QT + 4 * GQ * AHD;      // the heads' score scales
 constexpr int WT_LDS = WT_QS + GQ * 4;
 static_assert((WT_NW + 1) * GQ * AHD * 4 <= WT_P0, "the merge and the merged rows fit in the stages");
+static_assert(WT_NW * WT_PT == GQ * AHD * 4, "the fused front's rotated queries: head w in wavefront w's P tile");
 static_assert(WT_LDS <= 160 * 1024, "LDS");
 static_assert(WT_NW == GQ, "one wavefront per head for the query digits and the inverse rotation");
 
@@ -883,7 +884,8 @@ __device__ __forceinline__ void v_codes16(uint32_t w, uint32_t x, uint32_t cd[4]
 // it commutes with the combine's weighted sum): the combine then gates it directly and no turbo_out launch follows.
 __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __restrict__ qo, moex_kv_cache kv, int H,
                                                                 const int* __restrict__ pos_d, int max_t,
-                                                                float* __restrict__ part, int T, int ns, int rot) {
+                                                                float* __restrict__ part, int T, int ns, int rot,
+                                                                FrontArgs fr) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float cm[WT_NW][GQ], cl[WT_NW][GQ];
     const int nb = gridDim.x, w_id = xcd_work_id(blockIdx.x, nb);
@@ -977,11 +979,45 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
         else vm_wait<0>();
     };
 
+    // ---- the front (T = 1, fr.q set, skip flag clear): the q/k RMSNorm + RoPE, the queries' forward rotation and,
+    // in the split that holds position pos0, the TurboQuant append of the new row, with qk_norm_rope_kernel's
+    // arithmetic (front.hpp). Two groups of 256 threads (thread d owns dim d), each with four query heads and the key
+    // row (the same bits in both; group 0 stores the row). Its scratch is the stage area, which no transfer writes
+    // yet; the rotated queries go to the P tiles, not used before the key loop. The stored row has left this
+    // workgroup's queue (vmcnt) before any transfer of it is issued. ----
+    const bool fused = fr.q && !(fr.skip && *fr.skip);
+    const float* qtab = reinterpret_cast<const float*>(smem + WT_P0);
+    if (fused) {
+        const int half = tid >> 8, d = tid & 255;
+        float* fsh = reinterpret_cast<float*>(smem) + half * 5 * AHD;
+        float* fsh8 = reinterpret_cast<float*>(smem) + 10 * AHD + half * 48;
+        float x[5];
+#pragma unroll
+        for (int i = 0; i < 4; i++) x[i] = fr.q[(kvh * GQ + 4 * half + i) * 2 * AHD + d];
+        x[4] = fr.k[kvh * AHD + d];
+        const uint16_t* const w[5] = {fr.qn, fr.qn, fr.qn, fr.qn, fr.kn};
+        front::norm_rope_n<5, true>(x, w, d, pos0, fr.rot, fr.theta, fr.eps, fsh, fsh8);
+        float y[4] = {x[0], x[1], x[2], x[3]};
+        front::wht_n<4, true>(y, fsh, 0, d);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int h = 4 * half + i;
+            reinterpret_cast<float*>(smem + WT_P0)[h * AHD + d] = y[i];
+            if (s == 0) fr.qo[(kvh * GQ + h) * AHD + d] = y[i];
+        }
+        if (hi == Tmax && hi > lo) {  // this split holds the new row
+            front::append_turbo<true>(x[4], fr.v[kvh * AHD + d], kv, rbase + pos0, fsh + 4 * AHD, fsh8 + 40, d,
+                                      half == 0);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        front::sync<true>();
+    }
     // ---- query digits, once per workgroup: wavefront w turns head w (lane l: dims 4l .. 4l + 3) into three signed
     // base-256 digits of a 2^(22 - e) fixed point (|q| < 2^e over the head) and writes them to the digit table in
     // the operand order: dim d at byte 16 (d / 16) + pos(d % 16), pos = the K codes' order {0,2,4,6, 1,3,5,7, 8,..} ----
     {
-        const float4 q4 = *reinterpret_cast<const float4*>(qo + ((size_t)tok * H + kvh * GQ + wv) * AHD + 4 * lane);
+        const float4 q4 = *reinterpret_cast<const float4*>(
+            fused ? qtab + wv * AHD + 4 * lane : qo + ((size_t)tok * H + kvh * GQ + wv) * AHD + 4 * lane);
         float qm = fmaxf(fmaxf(fabsf(q4.x), fabsf(q4.y)), fmaxf(fabsf(q4.z), fabsf(q4.w)));
         qm = max_x32(max_x16(max_row16(qm)));
         int e = 0;
@@ -1256,7 +1292,7 @@ void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos
         }();
         (void)once;
         hipLaunchKernelGGL(gqa_wst_kernel, dim3(KV * ns * T), dim3(64 * WT_NW), WT_LDS, st, qo, kv, H, pos_d,
-                           max_t, part, T, ns, rot_out ? 1 : 0);
+                           max_t, part, T, ns, rot_out ? 1 : 0, fr && T == 1 ? *fr : FrontArgs{});
     } else {
         if (T == 1) {
             static bool once = [] {

@@ -1,8 +1,9 @@
-// The q/k front's arithmetic (RMSNorm(1 + w), partial RoPE, the int8 quantizer) over a group of 256 threads in which
-// thread d owns dim d of one head row (kernels.cuh:13-41,1185-1236). qk_norm_rope_kernel runs it as a whole block;
-// the int8 T = 1 decode kernel runs it in its prologue as two groups of 256 (both calling the same barriers), so the
-// rows it appends and the query it scores are bit-identical to the front kernel's. The reductions keep the
-// reference's orders: the 32-lane xor tree of warp_sum and the second xor tree over the 8 partials of block_sum (an
+// The q/k front's arithmetic (RMSNorm(1 + w), partial RoPE, the int8 and TurboQuant quantizers, the WHT) over a group
+// of 256 threads in which thread d owns dim d of one head row (kernels.cuh:13-41,1141-1236). qk_norm_rope_kernel
+// runs it as a whole block; the T = 1 decode kernels (int8 and turbo) run it in their prologues as two groups of 256
+// (both calling the same barriers), so the rows they append and the queries they score are bit-identical to the
+// front kernel's. The reductions keep the reference's orders: the 32-lane xor tree of warp_sum, the second xor tree
+// over the 8 partials of block_sum and the in-order sum of the four 32-lane partials of each 128-value half (an
 // xor-shuffle with offset <= 16 never leaves its 32-lane half of a 64-wide wavefront). Every function turns FP
 // contraction off for its own body (the including file may allow it).
 #pragma once
@@ -123,6 +124,130 @@ __device__ __forceinline__ void quant_i8(float x, float vv, float* sh8, int d, i
     sv = mv > 0.f ? mv / 127.f : 1.f;
     ck = (int8_t)__builtin_rintf(x / sk);
     cv = (int8_t)__builtin_rintf(vv / sv);
+}
+
+
+// TurboQuant constants (kernels.cuh:1123-1139): sign tables, centroid codes, decision thresholds.
+static __constant__ float c_S1[128] = {
+    -1, 1, 1,-1,-1, 1,-1, 1,-1,-1, 1, 1, 1, 1, 1, 1, 1,-1, 1,-1, 1,-1,-1, 1, 1, 1,-1, 1, 1,-1,-1,-1,
+    -1, 1, 1,-1, 1, 1,-1, 1,-1, 1, 1,-1,-1, 1,-1, 1, 1, 1, 1,-1,-1,-1,-1,-1, 1,-1, 1, 1, 1, 1,-1, 1,
+    -1,-1, 1,-1,-1,-1, 1,-1,-1,-1, 1,-1,-1,-1, 1, 1, 1,-1,-1, 1, 1, 1,-1,-1, 1, 1,-1, 1, 1,-1, 1,-1,
+    -1, 1, 1,-1, 1,-1, 1,-1, 1, 1, 1, 1,-1, 1,-1, 1, 1,-1, 1, 1,-1,-1,-1,-1,-1, 1, 1,-1, 1, 1,-1, 1};
+static __constant__ float c_S2[128] = {
+     1, 1, 1, 1,-1, 1, 1,-1, 1,-1,-1,-1, 1,-1,-1,-1, 1, 1,-1,-1, 1,-1, 1,-1, 1,-1,-1, 1,-1, 1, 1, 1,
+     1, 1,-1,-1,-1, 1,-1,-1,-1,-1,-1,-1, 1, 1, 1,-1, 1,-1, 1, 1, 1,-1,-1, 1,-1,-1,-1,-1,-1,-1, 1, 1,
+     1,-1, 1,-1,-1,-1,-1, 1,-1, 1,-1, 1,-1,-1, 1, 1,-1, 1,-1, 1, 1,-1, 1,-1,-1,-1,-1, 1,-1,-1, 1,-1,
+     1,-1, 1, 1, 1,-1,-1, 1,-1, 1,-1, 1, 1,-1,-1, 1,-1, 1,-1, 1, 1,-1, 1,-1, 1,-1,-1,-1,-1,-1, 1,-1};
+static __constant__ int8_t c_I4[16] = {-127, -96, -75, -58, -44, -31, -18, -6, 6, 18, 31, 44, 58, 75, 96, 127};
+static __constant__ int8_t c_I3[8] = {-127, -79, -45, -14, 14, 45, 79, 127};
+static __constant__ float c_M4[15] = {-0.212203f, -0.162947f, -0.127026f, -0.097164f, -0.070671f, -0.046174f, -0.022824f, 0.f,
+                               0.022824f, 0.046174f, 0.070671f, 0.097164f, 0.127026f, 0.162947f, 0.212203f};
+static __constant__ float c_M3[7] = {-0.154496f, -0.092804f, -0.044243f, 0.f, 0.044243f, 0.092804f, 0.154496f};
+constexpr float K4 = 0.241529f / 127.f, K3 = 0.190207f / 127.f;  // code scales (kernels.cuh:1135)
+
+
+// sum over the thread's 128-value half: 32-lane trees, then ((s0 + s1) + s2) + s3 (kernels.cuh:1161-1169)
+template <bool BARE = false>
+__device__ __forceinline__ float half_sum(float v, float* sh8, int d) {
+#pragma clang fp contract(off)
+    v = sum32(v);
+    const int g = d >> 5;
+    sync<BARE>();
+    if ((d & 31) == 0) sh8[g] = v;
+    sync<BARE>();
+    const int b = g & ~3;
+    return ((sh8[b] + sh8[b + 1]) + sh8[b + 2]) + sh8[b + 3];
+}
+
+// WHT of both 128-value halves of the group's row (kernels.cuh:1143-1159); dir 0 forward, 1 inverse. Stages 1..32
+// are xor-shuffles within the wavefront; stage 64 (dims j and j ^ 64, different wavefronts) goes through sh.
+template <bool BARE = false>
+__device__ __forceinline__ float wht(float x, float* sh, int dir, int d) {
+#pragma clang fp contract(off)
+    const int j = d & 127;
+    float v = x * (dir ? c_S2[j] : c_S1[j]);
+#pragma unroll
+    for (int h = 1; h < 64; h <<= 1) {
+        const float o = __shfl_xor(v, h);
+        v = (d & h) ? o - v : v + o;
+    }
+    sync<BARE>();
+    sh[d] = v;
+    sync<BARE>();
+    const float a = sh[d & ~64], b = sh[d | 64];
+    v = (j & 64) ? a - b : a + b;
+    return v * 0.08838834764831845f * (dir ? c_S1[j] : c_S2[j]);
+}
+
+// wht of N rows at once (row i in x[i], its stage-64 exchange in sh + i AHD): one pair of barriers for all of them,
+// each row's arithmetic that of wht
+template <int N, bool BARE>
+__device__ __forceinline__ void wht_n(float (&x)[N], float* sh, int dir, int d) {
+#pragma clang fp contract(off)
+    const int j = d & 127;
+    float v[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        v[i] = x[i] * (dir ? c_S2[j] : c_S1[j]);
+#pragma unroll
+        for (int h = 1; h < 64; h <<= 1) {
+            const float o = __shfl_xor(v[i], h);
+            v[i] = (d & h) ? o - v[i] : v[i] + o;
+        }
+    }
+    sync<BARE>();
+#pragma unroll
+    for (int i = 0; i < N; i++) sh[i * AHD + d] = v[i];
+    sync<BARE>();
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const float a = sh[i * AHD + (d & ~64)], b = sh[i * AHD + (d | 64)];
+        x[i] = ((j & 64) ? a - b : a + b) * 0.08838834764831845f * (dir ? c_S1[j] : c_S2[j]);
+    }
+}
+
+// TurboQuant code of x (thread d of the row); norm_out = the half's corrected norm (kernels.cuh:1172-1183)
+template <int BITS, bool BARE = false>
+__device__ __forceinline__ int tq_quant(float x, float* sh, float* sh8, int d, float& norm_out) {
+#pragma clang fp contract(off)
+    const float n = sqrtf(half_sum<BARE>(x * x, sh8, d));
+    const float r = wht<BARE>(n > 1e-20f ? x / n : 0.f, sh, 0, d);
+    int idx = 0;
+    if (BITS == 4) {
+#pragma unroll
+        for (int i = 0; i < 15; i++) idx += r >= c_M4[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 7; i++) idx += r >= c_M3[i];
+    }
+    const float c = BITS == 4 ? (float)c_I4[idx] * K4 : (float)c_I3[idx] * K3;
+    const float rn = sqrtf(half_sum<BARE>(c * c, sh8, d));
+    norm_out = rn > 1e-20f ? n / rn : n;
+    return idx;
+}
+
+// TurboQuant quantize-append of one row (kernels.cuh:1210-1226): x = post-RoPE k of dim d, vv = raw v of dim d; K
+// 4-bit, V 3-bit codes packed as the reference packs them. Every thread of the group computes; store: this group
+// writes the cache row.
+template <bool BARE = false>
+__device__ __forceinline__ void append_turbo(float x, float vv, moex_kv_cache kv, size_t row, float* sh, float* sh8,
+                                             int d, bool store) {
+#pragma clang fp contract(off)
+    const int j = d & 127, b = d >> 7;
+    float nk, nv;
+    const int ik = tq_quant<4, BARE>(x, sh, sh8, d, nk);
+    const int iv = tq_quant<3, BARE>(vv, sh, sh8, d, nv);
+    uint8_t* K = reinterpret_cast<uint8_t*>(kv.k) + row * TQ_KB;
+    uint8_t* V = reinterpret_cast<uint8_t*>(kv.v) + row * TQ_VB;
+    const int ik1 = __shfl_down(ik, 1);
+    const int lo = iv & 3;
+    const int q4 = lo | (__shfl_down(lo, 1) << 2) | (__shfl_down(lo, 2) << 4) | (__shfl_down(lo, 3) << 6);
+    const unsigned long long hb = __ballot(iv & 4);
+    if (!store) return;
+    if (!(j & 1)) K[b * 64 + j / 2] = (uint8_t)(ik | (ik1 << 4));
+    if (!(j & 3)) V[b * 32 + j / 4] = (uint8_t)q4;
+    if (!(j & 7)) V[64 + b * 16 + j / 8] = (uint8_t)(hb >> (d & 63));
+    if (j == 0) { kv.ks[row * 2 + b] = nk; kv.vs[row * 2 + b] = nv; }
 }
 
 }  // namespace front

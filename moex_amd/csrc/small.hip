@@ -13,95 +13,22 @@
 
 namespace moex {
 
-// TurboQuant constants (kernels.cuh:1123-1139): sign tables, centroid codes, decision thresholds.
-__constant__ float c_S1[128] = {
-    -1, 1, 1,-1,-1, 1,-1, 1,-1,-1, 1, 1, 1, 1, 1, 1, 1,-1, 1,-1, 1,-1,-1, 1, 1, 1,-1, 1, 1,-1,-1,-1,
-    -1, 1, 1,-1, 1, 1,-1, 1,-1, 1, 1,-1,-1, 1,-1, 1, 1, 1, 1,-1,-1,-1,-1,-1, 1,-1, 1, 1, 1, 1,-1, 1,
-    -1,-1, 1,-1,-1,-1, 1,-1,-1,-1, 1,-1,-1,-1, 1, 1, 1,-1,-1, 1, 1, 1,-1,-1, 1, 1,-1, 1, 1,-1, 1,-1,
-    -1, 1, 1,-1, 1,-1, 1,-1, 1, 1, 1, 1,-1, 1,-1, 1, 1,-1, 1, 1,-1,-1,-1,-1,-1, 1, 1,-1, 1, 1,-1, 1};
-__constant__ float c_S2[128] = {
-     1, 1, 1, 1,-1, 1, 1,-1, 1,-1,-1,-1, 1,-1,-1,-1, 1, 1,-1,-1, 1,-1, 1,-1, 1,-1,-1, 1,-1, 1, 1, 1,
-     1, 1,-1,-1,-1, 1,-1,-1,-1,-1,-1,-1, 1, 1, 1,-1, 1,-1, 1, 1, 1,-1,-1, 1,-1,-1,-1,-1,-1,-1, 1, 1,
-     1,-1, 1,-1,-1,-1,-1, 1,-1, 1,-1, 1,-1,-1, 1, 1,-1, 1,-1, 1, 1,-1, 1,-1,-1,-1,-1, 1,-1,-1, 1,-1,
-     1,-1, 1, 1, 1,-1,-1, 1,-1, 1,-1, 1, 1,-1,-1, 1,-1, 1,-1, 1, 1,-1, 1,-1, 1,-1,-1,-1,-1,-1, 1,-1};
-__constant__ int8_t c_I4[16] = {-127, -96, -75, -58, -44, -31, -18, -6, 6, 18, 31, 44, 58, 75, 96, 127};
-__constant__ int8_t c_I3[8] = {-127, -79, -45, -14, 14, 45, 79, 127};
-__constant__ float c_M4[15] = {-0.212203f, -0.162947f, -0.127026f, -0.097164f, -0.070671f, -0.046174f, -0.022824f, 0.f,
-                               0.022824f, 0.046174f, 0.070671f, 0.097164f, 0.127026f, 0.162947f, 0.212203f};
-__constant__ float c_M3[7] = {-0.154496f, -0.092804f, -0.044243f, 0.f, 0.044243f, 0.092804f, 0.154496f};
-constexpr float K4 = 0.241529f / 127.f, K3 = 0.190207f / 127.f;  // code scales (kernels.cuh:1135)
-
 // graph-fallback flag (kernels.cuh:46, g_skip): nonzero -> qk_norm_rope / turbo_out return at once
 __device__ int g_skip;
 
-// ---- block reductions over a 256-thread block (4 wavefronts of 64): the front's, thread d = threadIdx.x ----
-__device__ __forceinline__ float sum32(float v) { return front::sum32(v); }
-// sum over the thread's 128-value half: 32-lane trees, then ((s0 + s1) + s2) + s3 (kernels.cuh:1161-1169)
-__device__ __forceinline__ float half_sum(float v, float* sh8) {
-    v = sum32(v);
-    const int g = threadIdx.x >> 5;
-    __syncthreads();
-    if ((threadIdx.x & 31) == 0) sh8[g] = v;
-    __syncthreads();
-    const int b = g & ~3;
-    return ((sh8[b] + sh8[b + 1]) + sh8[b + 2]) + sh8[b + 3];
-}
+// ---- the front's helpers over a 256-thread block (thread d = threadIdx.x owns dim d of the row) ----
+using front::c_I3;
+using front::c_I4;
+using front::K3;
+using front::K4;
 __device__ __forceinline__ float block_sum(float v, float* sh8) { return front::block_sum(v, sh8, threadIdx.x); }
-
-// WHT of both 128-value halves of the block's row (kernels.cuh:1143-1159); dir 0 forward, 1 inverse.
-__device__ __forceinline__ float wht(float x, float* sh, int dir) {
-    const int d = threadIdx.x, j = d & 127;
-    float v = x * (dir ? c_S2[j] : c_S1[j]);
-#pragma unroll
-    for (int h = 1; h < 64; h <<= 1) {  // stages 1..32: within the wavefront
-        const float o = __shfl_xor(v, h);
-        v = (d & h) ? o - v : v + o;
-    }
-    __syncthreads();
-    sh[d] = v;
-    __syncthreads();
-    const float a = sh[d & ~64], b = sh[d | 64];  // stage 64: dims j and j ^ 64 (different wavefronts)
-    v = (j & 64) ? a - b : a + b;
-    return v * 0.08838834764831845f * (dir ? c_S1[j] : c_S2[j]);
-}
-
-// TurboQuant code of x (thread d of the row); norm_out = the half's corrected norm (kernels.cuh:1172-1183)
-template <int BITS>
-__device__ __forceinline__ int tq_quant(float x, float* sh, float* sh8, float& norm_out) {
-    const float n = sqrtf(half_sum(x * x, sh8));
-    const float r = wht(n > 1e-20f ? x / n : 0.f, sh, 0);
-    int idx = 0;
-    if (BITS == 4) {
-#pragma unroll
-        for (int i = 0; i < 15; i++) idx += r >= c_M4[i];
-    } else {
-#pragma unroll
-        for (int i = 0; i < 7; i++) idx += r >= c_M3[i];
-    }
-    const float c = BITS == 4 ? (float)c_I4[idx] * K4 : (float)c_I3[idx] * K3;
-    const float rn = sqrtf(half_sum(c * c, sh8));
-    norm_out = rn > 1e-20f ? n / rn : n;
-    return idx;
-}
+__device__ __forceinline__ float wht(float x, float* sh, int dir) { return front::wht(x, sh, dir, threadIdx.x); }
 
 // Quantize-append of one (kv head, position) row: x = post-RoPE k of dim d, vv = raw v of dim d.
 __device__ __forceinline__ void append_row(float x, float vv, moex_kv_cache kv, size_t row, float* sh, float* sh8) {
     const int d = threadIdx.x;
     if (kv.turbo) {  // K 4-bit, V 3-bit (kernels.cuh:1210-1226)
-        const int j = d & 127, b = d >> 7;
-        float nk, nv;
-        const int ik = tq_quant<4>(x, sh, sh8, nk);
-        const int iv = tq_quant<3>(vv, sh, sh8, nv);
-        uint8_t* K = reinterpret_cast<uint8_t*>(kv.k) + row * TQ_KB;
-        uint8_t* V = reinterpret_cast<uint8_t*>(kv.v) + row * TQ_VB;
-        const int ik1 = __shfl_down(ik, 1);
-        if (!(j & 1)) K[b * 64 + j / 2] = (uint8_t)(ik | (ik1 << 4));
-        const int lo = iv & 3;
-        const int q4 = lo | (__shfl_down(lo, 1) << 2) | (__shfl_down(lo, 2) << 4) | (__shfl_down(lo, 3) << 6);
-        if (!(j & 3)) V[b * 32 + j / 4] = (uint8_t)q4;
-        const unsigned long long hb = __ballot(iv & 4);
-        if (!(j & 7)) V[64 + b * 16 + j / 8] = (uint8_t)(hb >> (d & 63));
-        if (j == 0) { kv.ks[row * 2 + b] = nk; kv.vs[row * 2 + b] = nv; }
+        front::append_turbo(x, vv, kv, row, sh, sh8, d, true);
     } else {  // int8 per row (kernels.cuh:1227-1235)
         int8_t ck, cv;
         float sk, sv;

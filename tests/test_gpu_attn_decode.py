@@ -109,17 +109,34 @@ def test_skip_flag_and_soft_errors():
     assert slot.value == 1  # hipErrorInvalidValue
 
 
-def test_skip_flag_fused_front():
-    """With g_skip set, attn_decode's int8 T = 1 split-K step (whose split kernel runs the front and the append in
-    its prologue) appends nothing, leaves qo as it was and attends with that qo, as the reference's attention after
-    a skipped qk_norm_rope_k (kernels.cuh:1189) does: its output equals attn_gqa + attn_combine on the same qo, bit
-    for bit."""
+def _caches(M, torch, turbo, max_t, seed, n=2):
+    """n caches with the same rows: int8 from the random int8 cache, turbo by appending the same random k / v rows"""
+    from tests.gpu_util import random_int8_cache, upload
+    if not turbo:
+        hc = random_int8_cache(max_t, seed=seed)
+        return hc, [upload(hc) for _ in range(n)]
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    k = torch.randn((max_t, KV * AHD), generator=g, device="cuda")
+    v = torch.randn((max_t, KV * AHD), generator=g, device="cuda")
+    cs = []
+    for _ in range(n):
+        c = M.DeviceKVCache(KV, max_t, 1)
+        M.kv_append(k, v, c, KV, pos_tensor(0), max_t, KV * AHD, max_t)
+        cs.append(c)
+    torch.cuda.synchronize()
+    return download(cs[0]), cs
+
+
+@pytest.mark.parametrize("turbo", [0, 1])
+def test_skip_flag_fused_front(turbo):
+    """With g_skip set, attn_decode's T = 1 split-K step (whose split kernel runs the front and the append in its
+    prologue) appends nothing, leaves qo as it was and attends with that qo, as the reference's attention after a
+    skipped qk_norm_rope_k (kernels.cuh:1189) does: its output equals the split kernel + attn_combine on the same qo,
+    bit for bit (turbo: the partials rotated back, as the step runs them)."""
     import torch
     import moex_amd as M
-    from tests.gpu_util import random_int8_cache, upload
     pos, max_t = 3000, 3072
-    hc = random_int8_cache(max_t, seed=71)
-    dc = upload(hc)
+    hc, (dc,) = _caches(M, torch, turbo, max_t, 71, 1)
     rng = np.random.default_rng(72)
     LQ = H * 2 * AHD + 2 * KV * AHD
     qkv = dev(rng.standard_normal((1, LQ), dtype=np.float32))
@@ -142,36 +159,35 @@ def test_skip_flag_fused_front():
     for a, b, name in ((after.k, hc.k, "k"), (after.v, hc.v, "v"), (after.ks, hc.ks, "ks"), (after.vs, hc.vs, "vs")):
         assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"cache {name} changed under the skip flag"
     assert np.array_equal(qo.cpu().numpy(), qo0), "qo changed under the skip flag"
-    nsg = M.gqa_splits(1, KV, ns)
+    nsg = M.gqa_splits(1, KV, ns, turbo)
     part2 = torch.empty(H * ns * (AHD + 2), device="cuda")
     out2 = torch.full((1, H, AHD), float("nan"), device="cuda")
-    M.attn_gqa(qo, dc, H, KV, pos_tensor(pos), max_t, part2, 1, nsg)
+    (M.attn_gqa_out if turbo else M.attn_gqa)(qo, dc, H, KV, pos_tensor(pos), max_t, part2, 1, nsg)
     M.attn_combine(part2, qkv, out2, H, nsg, LQ, 1)
     torch.cuda.synchronize()
     got, ref = out.cpu().numpy(), out2.cpu().numpy()
-    report("skip flag, fused front", ns=nsg, same=bool(np.array_equal(got, ref)))
+    report("skip flag, fused front", turbo=turbo, ns=nsg, same=bool(np.array_equal(got, ref)))
     assert np.all(np.isfinite(got)) and np.array_equal(got, ref)
 
 
+@pytest.mark.parametrize("turbo", [0, 1])
 @pytest.mark.parametrize("pos,ns", [(0, 4), (1, 2), (63, 2), (64, 2), (65, 7), (255, 3), (256, 128), (3000, 128),
                                     (5183, 5), (20480, 64), (89999, 128)])
-def test_fused_front_matches_three_launches(pos, ns):
-    """attn_decode's int8 T = 1 split step runs the q/k front and the append inside the split kernel; the same step
-    as three launches (qk_norm_rope, attn_gqa, attn_combine) must give the same qo, cache rows and output, bit for
-    bit. The positions put the new row alone in a split, alone in the short first chunk, at a chunk boundary and deep
-    in the cache, and (pos 0) leave most splits empty."""
+def test_fused_front_matches_three_launches(pos, ns, turbo):
+    """attn_decode's T = 1 split step runs the q/k front and the append inside the split kernel; the same step as
+    three launches (qk_norm_rope, the split kernel, attn_combine) must give the same qo, cache rows and output, bit
+    for bit. The positions put the new row alone in a split, alone in the short first chunk, at a chunk boundary and
+    deep in the cache, and (pos 0) leave most splits empty."""
     import torch
     import moex_amd as M
-    from tests.gpu_util import random_int8_cache, upload
     max_t = max(pos + 1, 1024)
-    hc = random_int8_cache(max_t, seed=81)
-    da, db = upload(hc), upload(hc)
+    hc, (da, db) = _caches(M, torch, turbo, max_t, 81)
     rng = np.random.default_rng(82 + pos)
     LQ = H * 2 * AHD + 2 * KV * AHD
     qkv = dev(rng.standard_normal((1, LQ), dtype=np.float32))
     qn = dev((0.1 * rng.standard_normal(AHD)).astype(np.float16).view(np.int16))  # fp16 norm weights
     kn = dev((0.1 * rng.standard_normal(AHD)).astype(np.float16).view(np.int16))
-    nsg = M.gqa_splits(1, KV, ns)
+    nsg = M.gqa_splits(1, KV, ns, turbo)
     part = torch.empty(H * ns * (AHD + 2), device="cuda")
     qa, qb = torch.full((1, H, AHD), float("nan"), device="cuda"), torch.full((1, H, AHD), float("nan"), device="cuda")
     oa, ob = torch.full((1, H, AHD), float("nan"), device="cuda"), torch.full((1, H, AHD), float("nan"), device="cuda")
@@ -180,14 +196,14 @@ def test_fused_front_matches_three_launches(pos, ns):
                   64, 1e7, 1e-6, 1, LQ, None, part, ns)
     M.qk_norm_rope(qkv, qkv[:, H * 2 * AHD:], qkv[:, H * 2 * AHD + KV * AHD:], qn, kn, qb, db, H, KV, pd, max_t,
                    64, 1e7, 1e-6, LQ, 1)
-    M.attn_gqa(qb, db, H, KV, pd, max_t, part, 1, nsg)
+    (M.attn_gqa_out if turbo else M.attn_gqa)(qb, db, H, KV, pd, max_t, part, 1, nsg)
     M.attn_combine(part, qkv, ob, H, nsg, LQ, 1)
     torch.cuda.synchronize()
     ca, cb = download(da), download(db)
     for x, y, name in ((ca.k, cb.k, "k"), (ca.v, cb.v, "v"), (ca.ks, cb.ks, "ks"), (ca.vs, cb.vs, "vs")):
         assert np.array_equal(x.view(np.uint8), y.view(np.uint8)), f"cache {name} differs"
     ga, gb = oa.cpu().numpy(), ob.cpu().numpy()
-    report("fused front vs three launches", pos=pos, ns=nsg, maxdiff=float(np.abs(ga - gb).max()))
+    report("fused front vs three launches", turbo=turbo, pos=pos, ns=nsg, maxdiff=float(np.abs(ga - gb).max()))
     assert np.array_equal(qa.cpu().numpy(), qb.cpu().numpy())
     assert np.all(np.isfinite(ga)) and np.array_equal(ga, gb)
 
