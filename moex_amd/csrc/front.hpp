@@ -250,5 +250,196 @@ __device__ __forceinline__ void append_turbo(float x, float vv, moex_kv_cache kv
     if (j == 0) { kv.ks[row * 2 + b] = nk; kv.vs[row * 2 + b] = nv; }
 }
 
+// ---- The same arithmetic on one wavefront per head row: lane l owns dims 4l .. 4l + 3 (x[i] = dim 4l + i), so a
+// workgroup of 256 threads serves four rows and needs no barrier. The reductions and the WHT reproduce the orders of
+// the 256-thread functions above exactly: a 32-lane warp of the reference (dims 32w .. 32w + 31) is lanes 8w .. 8w+7;
+// its xor tree pairs dims d and d ^ 16, ^ 8, ^ 4 across lanes (lane ^ 4, ^ 2, ^ 1) and d ^ 2, d ^ 1 inside the lane.
+namespace wave {
+
+// every dim gets its reference warp's sum (the 32-lane xor tree: offsets 16, 8, 4, 2, 1)
+__device__ __forceinline__ void sum32(float (&v)[4]) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int o = 4; o >= 1; o >>= 1)
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] += __shfl_xor(v[i], o);
+    float a[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) a[i] = v[i] + v[i ^ 2];
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = a[i] + a[i ^ 1];
+}
+// the 8 warp sums (warp w: lane 8w), wave-uniform
+__device__ __forceinline__ void warp_sums(const float (&v)[4], float (&s)[8]) {
+#pragma unroll
+    for (int w = 0; w < 8; w++) s[w] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[0]), 8 * w));
+}
+// block_sum over the row's 256 dims of v (per dim): the reference's second xor tree over the 8 warp sums
+__device__ __forceinline__ float block_sum(float (&v)[4]) {
+#pragma clang fp contract(off)
+    sum32(v);
+    float s[8];
+    warp_sums(v, s);
+    return ((s[0] + s[4]) + (s[2] + s[6])) + ((s[1] + s[5]) + (s[3] + s[7]));
+}
+// half_sum of the lane's 128-value half: ((s0 + s1) + s2) + s3 over the half's four warps
+__device__ __forceinline__ float half_sum(float (&v)[4], int lane) {
+#pragma clang fp contract(off)
+    sum32(v);
+    float s[8];
+    warp_sums(v, s);
+    const float h0 = ((s[0] + s[1]) + s[2]) + s[3], h1 = ((s[4] + s[5]) + s[6]) + s[7];
+    return lane < 32 ? h0 : h1;
+}
+__device__ __forceinline__ float row_max(const float (&v)[4]) {
+    float m = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    return m;
+}
+
+// norm_rope on the lane's 4 dims (rot % 8 == 0: a RoPE partner is 4 dims per lane away, same slot)
+__device__ __forceinline__ void norm_rope(float (&x)[4], const uint16_t* w, int lane, int pos, int rot, float theta,
+                                          float eps) {
+#pragma clang fp contract(off)
+    float sq[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) sq[i] = x[i] * x[i];
+    const float r = rsqrtf(block_sum(sq) / AHD + eps);
+    const uint2 wb = *reinterpret_cast<const uint2*>(w + 4 * lane);
+    const uint16_t wh[4] = {(uint16_t)(wb.x & 0xffffu), (uint16_t)(wb.x >> 16), (uint16_t)(wb.y & 0xffffu),
+                            (uint16_t)(wb.y >> 16)};
+#pragma unroll
+    for (int i = 0; i < 4; i++) x[i] = x[i] * r * (1.f + (float)__builtin_bit_cast(_Float16, wh[i]));
+    const int h2 = rot / 2, d0 = 4 * lane;
+    const int partner = d0 < h2 ? lane + h2 / 4 : lane - h2 / 4;
+    float px[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) px[i] = __shfl(x[i], partner & 63);
+    // the angles depend on j = d mod h2 only: lane t computes those of j = t and t + 64 (the same expression as the
+    // 256-thread function), the rotating lanes take theirs by shuffle
+    float ca = 1.f, sa = 0.f, cb = 1.f, sb = 0.f;
+    if (lane < h2) {
+        const float ang = (float)pos * powf(theta, -2.f * lane / rot);
+        ca = cosf(ang);
+        sa = sinf(ang);
+    }
+    if (lane + 64 < h2) {
+        const float ang = (float)pos * powf(theta, -2.f * (lane + 64) / rot);
+        cb = cosf(ang);
+        sb = sinf(ang);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int d = d0 + i, j = d < h2 ? d : d - h2;
+        const float c0 = __shfl(ca, j & 63), c1 = __shfl(cb, j & 63);  // every lane takes part in every shuffle
+        const float s0 = __shfl(sa, j & 63), s1 = __shfl(sb, j & 63);
+        const float cs = j < 64 ? c0 : c1, sn = j < 64 ? s0 : s1;
+        if (d < rot) x[i] = d < h2 ? x[i] * cs - px[i] * sn : x[i] * cs + px[i] * sn;
+    }
+}
+
+// wht of both 128-value halves of the row (dir 0 forward, 1 inverse)
+__device__ __forceinline__ void wht(float (&x)[4], int dir, int lane) {
+#pragma clang fp contract(off)
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int j = (4 * lane + i) & 127;
+        v[i] = x[i] * (dir ? c_S2[j] : c_S1[j]);
+    }
+#pragma unroll
+    for (int h = 1; h <= 2; h <<= 1) {  // stages 1, 2: inside the lane
+        float a[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) a[i] = (i & h) ? v[i ^ h] - v[i] : v[i] + v[i ^ h];
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = a[i];
+    }
+#pragma unroll
+    for (int h = 4; h <= 64; h <<= 1) {  // stages 4 .. 64: lane ^ h / 4
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float o = __shfl_xor(v[i], h / 4);
+            v[i] = ((4 * lane) & h) ? o - v[i] : v[i] + o;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int j = (4 * lane + i) & 127;
+        x[i] = v[i] * 0.08838834764831845f * (dir ? c_S1[j] : c_S2[j]);
+    }
+}
+
+// TurboQuant codes of the lane's 4 dims; norm_out = the lane's half's corrected norm
+template <int BITS>
+__device__ __forceinline__ void tq_quant(const float (&x)[4], int lane, int (&idx)[4], float& norm_out) {
+#pragma clang fp contract(off)
+    float sq[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) sq[i] = x[i] * x[i];
+    const float n = sqrtf(half_sum(sq, lane));
+    float r[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) r[i] = n > 1e-20f ? x[i] / n : 0.f;
+    wht(r, 0, lane);
+    float cc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        int k = 0;
+        if (BITS == 4) {
+#pragma unroll
+            for (int t = 0; t < 15; t++) k += r[i] >= c_M4[t];
+        } else {
+#pragma unroll
+            for (int t = 0; t < 7; t++) k += r[i] >= c_M3[t];
+        }
+        idx[i] = k;
+        const float c = BITS == 4 ? (float)c_I4[k] * K4 : (float)c_I3[k] * K3;
+        cc[i] = c * c;
+    }
+    const float rn = sqrtf(half_sum(cc, lane));
+    norm_out = rn > 1e-20f ? n / rn : n;
+}
+
+// quantize-append of one row (x: post-RoPE k, vv: raw v, the lane's 4 dims each), int8 or TurboQuant
+__device__ __forceinline__ void append(const float (&x)[4], const float (&vv)[4], moex_kv_cache kv, size_t row,
+                                       int lane) {
+#pragma clang fp contract(off)
+    if (kv.turbo) {
+        int ik[4], iv[4];
+        float nk, nv;
+        tq_quant<4>(x, lane, ik, nk);
+        tq_quant<3>(vv, lane, iv, nv);
+        const int b = lane >> 5, l = lane & 31;  // half, lane within it: dims 4l .. 4l + 3 of the half
+        uint8_t* K = reinterpret_cast<uint8_t*>(kv.k) + row * TQ_KB;
+        uint8_t* V = reinterpret_cast<uint8_t*>(kv.v) + row * TQ_VB;
+        const uint32_t kb = (uint32_t)(ik[0] | (ik[1] << 4)) | ((uint32_t)(ik[2] | (ik[3] << 4)) << 8);
+        *reinterpret_cast<uint16_t*>(K + b * 64 + 2 * l) = (uint16_t)kb;
+        V[b * 32 + l] = (uint8_t)((iv[0] & 3) | ((iv[1] & 3) << 2) | ((iv[2] & 3) << 4) | ((iv[3] & 3) << 6));
+        const int hb = ((iv[0] >> 2) & 1) | (((iv[1] >> 2) & 1) << 1) | (((iv[2] >> 2) & 1) << 2) | (((iv[3] >> 2) & 1) << 3);
+        const int hb1 = __shfl_down(hb, 1);
+        if (!(l & 1)) V[64 + b * 16 + l / 2] = (uint8_t)(hb | (hb1 << 4));
+        if (l == 0) { kv.ks[row * 2 + b] = nk; kv.vs[row * 2 + b] = nv; }
+    } else {
+        float ak[4], av[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) { ak[i] = fabsf(x[i]); av[i] = fabsf(vv[i]); }
+        const float mk = row_max(ak), mv = row_max(av);
+        const float sk = mk > 0.f ? mk / 127.f : 1.f, sv = mv > 0.f ? mv / 127.f : 1.f;
+        uint32_t ck = 0, cv = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            ck |= (uint32_t)(uint8_t)(int8_t)__builtin_rintf(x[i] / sk) << (8 * i);
+            cv |= (uint32_t)(uint8_t)(int8_t)__builtin_rintf(vv[i] / sv) << (8 * i);
+        }
+        *reinterpret_cast<uint32_t*>(kv.k + row * AHD + 4 * lane) = ck;
+        *reinterpret_cast<uint32_t*>(kv.v + row * AHD + 4 * lane) = cv;
+        if (lane == 0) { kv.ks[row] = sk; kv.vs[row] = sv; }
+    }
+}
+
+}  // namespace wave
+
 }  // namespace front
 }  // namespace moex

@@ -63,6 +63,43 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(
     }
 }
 
+// The same front on one wavefront per head row (front::wave, the same bits): rows r = token (H + KV) + head of the
+// chunk, four to a workgroup, no barrier. KV rows append (k normalized and rotated; v raw). Needs rot % 8 == 0.
+__global__ void __launch_bounds__(256) front_rows_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const uint16_t* __restrict__ qn, const uint16_t* __restrict__ kn, float* __restrict__ qo, moex_kv_cache kv,
+    int H, int KV, const int* __restrict__ pos_d, int max_t, int rot, float theta, float eps, int ld, int T) {
+    if (g_skip) return;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= T * (H + KV)) return;
+    const int tok = r / (H + KV), hh = r - tok * (H + KV), pos = *pos_d + tok;
+    q += (size_t)tok * ld; k += (size_t)tok * ld; v += (size_t)tok * ld;
+    const bool isq = hh < H;
+    const float4 x4 = *reinterpret_cast<const float4*>((isq ? q + hh * 2 * AHD : k + (hh - H) * AHD) + 4 * lane);
+    float x[4] = {x4.x, x4.y, x4.z, x4.w};
+    front::wave::norm_rope(x, isq ? qn : kn, lane, pos, rot, theta, eps);
+    if (isq) {
+        if (kv.turbo) front::wave::wht(x, 0, lane);  // the keys' rotation
+        *reinterpret_cast<float4*>(qo + ((size_t)tok * H + hh) * AHD + 4 * lane) = make_float4(x[0], x[1], x[2], x[3]);
+    } else {
+        const float4 v4 = *reinterpret_cast<const float4*>(v + (hh - H) * AHD + 4 * lane);
+        const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+        front::wave::append(x, vv, kv, (size_t)(hh - H) * max_t + pos, lane);
+    }
+}
+// Quantize-append only, one wavefront per row (rows r = token KV + kv head)
+__global__ void __launch_bounds__(256) append_rows_kernel(const float* __restrict__ k, const float* __restrict__ v,
+                                                          moex_kv_cache kv, int KV, const int* __restrict__ pos_d,
+                                                          int max_t, int ld, int T) {
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= T * KV) return;
+    const int tok = r / KV, kvh = r - tok * KV;
+    const size_t o = (size_t)tok * ld + kvh * AHD + 4 * lane;
+    const float4 k4 = *reinterpret_cast<const float4*>(k + o), v4 = *reinterpret_cast<const float4*>(v + o);
+    const float x[4] = {k4.x, k4.y, k4.z, k4.w}, vv[4] = {v4.x, v4.y, v4.z, v4.w};
+    front::wave::append(x, vv, kv, (size_t)kvh * max_t + *pos_d + tok, lane);
+}
+
 // Quantize-append only: grid (KV, T); k already normalized and rotated.
 __global__ void __launch_bounds__(256) kv_append_kernel(const float* __restrict__ k, const float* __restrict__ v,
                                                         moex_kv_cache kv, const int* __restrict__ pos_d, int max_t,
@@ -317,13 +354,24 @@ __global__ void set_skip_kernel(int v) { g_skip = v; }
 void launch_qk_norm_rope(const float* q, const float* k, const float* v, const uint16_t* qn, const uint16_t* kn,
                          float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, int rot,
                          float theta, float eps, int ld, int T, hipStream_t st) {
-    hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(H + KV, T), dim3(256), 0, st, q, k, v, qn, kn, qo, kv, H, KV, pos_d,
-                       max_t, rot, theta, eps, ld);
+    // the 16-byte row loads and the wavefront layout need 4-float aligned rows
+    const bool al = ld % 4 == 0 && ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)qo) % 16 == 0 &&
+                    ((uintptr_t)qn | (uintptr_t)kn) % 8 == 0;
+    if (rot % 8 == 0 && al)
+        hipLaunchKernelGGL(front_rows_kernel, dim3((T * (H + KV) + 3) / 4), dim3(256), 0, st, q, k, v, qn, kn, qo, kv,
+                           H, KV, pos_d, max_t, rot, theta, eps, ld, T);
+    else
+        hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(H + KV, T), dim3(256), 0, st, q, k, v, qn, kn, qo, kv, H, KV,
+                           pos_d, max_t, rot, theta, eps, ld);
     MOEX_LAUNCHED();
 }
 void launch_kv_append(const float* k, const float* v, moex_kv_cache kv, int KV, const int* pos_d, int max_t, int ld,
                       int T, hipStream_t st) {
-    hipLaunchKernelGGL(kv_append_kernel, dim3(KV, T), dim3(256), 0, st, k, v, kv, pos_d, max_t, ld);
+    if (ld % 4 == 0 && ((uintptr_t)k | (uintptr_t)v) % 16 == 0)
+        hipLaunchKernelGGL(append_rows_kernel, dim3((T * KV + 3) / 4), dim3(256), 0, st, k, v, kv, KV, pos_d, max_t, ld,
+                           T);
+    else
+        hipLaunchKernelGGL(kv_append_kernel, dim3(KV, T), dim3(256), 0, st, k, v, kv, pos_d, max_t, ld);
     MOEX_LAUNCHED();
 }
 void launch_turbo_out(float* out, const float* q_gate, int H, int ld, int T, hipStream_t st) {
