@@ -122,6 +122,22 @@ __global__ void __launch_bounds__(256) turbo_out_kernel(float* __restrict__ out,
     o[d] = x / (1.f + __expf(-q_gate[(size_t)tok * ld + h * 2 * AHD + AHD + d]));
 }
 
+// turbo_out_kernel on one wavefront per (token, head) row, four rows a workgroup (front::wave::wht: the same bits)
+__global__ void __launch_bounds__(256) turbo_out_rows_kernel(float* __restrict__ out, const float* __restrict__ q_gate,
+                                                             int H, int ld, int T) {
+    if (g_skip) return;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= T * H) return;
+    const int tok = r / H, h = r - tok * H;
+    float4* o4 = reinterpret_cast<float4*>(out + (size_t)r * AHD + 4 * lane);
+    const float4 a = *o4;
+    float x[4] = {a.x, a.y, a.z, a.w};
+    front::wave::wht(x, 1, lane);
+    const float4 g = *reinterpret_cast<const float4*>(q_gate + (size_t)tok * ld + h * 2 * AHD + AHD + 4 * lane);
+    *o4 = make_float4(x[0] / (1.f + __expf(-g.x)), x[1] / (1.f + __expf(-g.y)), x[2] / (1.f + __expf(-g.z)),
+                      x[3] / (1.f + __expf(-g.w)));
+}
+
 // attn_combine_k (kernels.cuh:1317-1329): merge ns partials {m (log2 units), l, acc[256]}.
 // Grid (H, T, CDC): block (h, t, c) owns dims [64 c, 64 c + 64); its 256 threads are 16 dim quads (one float4 of acc
 // per split) x 16 split groups. A thread loads 8 of its splits at once, takes their maximum, then weighs them with
@@ -375,7 +391,10 @@ void launch_kv_append(const float* k, const float* v, moex_kv_cache kv, int KV, 
     MOEX_LAUNCHED();
 }
 void launch_turbo_out(float* out, const float* q_gate, int H, int ld, int T, hipStream_t st) {
-    hipLaunchKernelGGL(turbo_out_kernel, dim3(H, T), dim3(256), 0, st, out, q_gate, H, ld);
+    if (ld % 4 == 0 && ((uintptr_t)out | (uintptr_t)q_gate) % 16 == 0)
+        hipLaunchKernelGGL(turbo_out_rows_kernel, dim3((T * H + 3) / 4), dim3(256), 0, st, out, q_gate, H, ld, T);
+    else
+        hipLaunchKernelGGL(turbo_out_kernel, dim3(H, T), dim3(256), 0, st, out, q_gate, H, ld);
     MOEX_LAUNCHED();
 }
 void launch_combine(const float* part, const float* q_gate, float* out, int H, int ns, int ld, int T, hipStream_t st) {

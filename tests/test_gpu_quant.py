@@ -124,3 +124,40 @@ def test_qk_norm_rope_front(turbo, pos0):
     assert np.array_equal(got.v[:, sl], ref.v[:, sl])  # V is not normalized: bit-exact
     assert np.allclose(got.ks[:, sl], ref.ks[:, sl], rtol=1e-5)
     assert np.array_equal(got.vs[:, sl].view(np.uint32), ref.vs[:, sl].view(np.uint32))
+
+
+@pytest.mark.parametrize("turbo", [0, 1])
+def test_wavefront_kernels_match_block_kernels(turbo):
+    """The one-wavefront-per-row kernels (front, append, turbo_out) against the 256-thread kernels that run when a row
+    is not 16-byte aligned (a buffer one float past an aligned one, same values): the same bits in qo, the cache and
+    the output."""
+    import torch
+    import moex_amd as M
+    T, pos0, max_t = 37, 900, 1024
+    LQ = H * 2 * AHD + 2 * KV * AHD
+    rng = np.random.default_rng(91)
+    qkv_h = rng.standard_normal((T, LQ), dtype=np.float32)
+    qn = dev((0.1 * rng.standard_normal(AHD)).astype(np.float16).view(np.int16))
+    kn = dev((0.1 * rng.standard_normal(AHD)).astype(np.float16).view(np.int16))
+    res = []
+    for off in (0, 1):  # 1: every row starts one float past a 16-byte boundary
+        buf = torch.zeros(T * LQ + 4, device="cuda")
+        qkv = buf[off:off + T * LQ].view(T, LQ)
+        qkv.copy_(torch.from_numpy(qkv_h))
+        qob = torch.zeros(T * H * AHD + 4, device="cuda")
+        qo = qob[off:off + T * H * AHD].view(T, H, AHD)
+        c = M.DeviceKVCache(KV, max_t, turbo)
+        M.qk_norm_rope(qkv, qkv[:, H * 2 * AHD:], qkv[:, H * 2 * AHD + KV * AHD:], qn, kn, qo, c, H, KV,
+                       pos_tensor(pos0), max_t, 64, 1e7, 1e-6, LQ, T)
+        M.kv_append(qkv[:, :KV * AHD], qkv[:, KV * AHD:2 * KV * AHD], c, KV, pos_tensor(0), max_t, LQ, T)
+        if turbo:
+            M.turbo_out(qo, qkv, H, LQ, T)
+        torch.cuda.synchronize()
+        hc = download(c)
+        res.append((qo.cpu().numpy().copy(), hc))
+    (qa, ca), (qb, cb) = res
+    assert np.array_equal(qa.view(np.uint32), qb.view(np.uint32))
+    rows = np.r_[0:T, pos0:pos0 + T]  # the rows the two calls wrote (the rest of a new cache is not initialised)
+    for x, y in ((ca.k, cb.k), (ca.v, cb.v), (ca.ks, cb.ks), (ca.vs, cb.vs)):
+        a, b = np.ascontiguousarray(x[:, rows]), np.ascontiguousarray(y[:, rows])
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
