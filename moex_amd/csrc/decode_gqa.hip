@@ -253,7 +253,6 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws1_kernel(const 
                                                                          FrontArgs fr) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float cm[WS_NC][GQ], cl[WS_NC][GQ];
-    __shared__ float fsh[2][5 * AHD], fsh8[2][48];
     const int nb = gridDim.x, w_id = xcd_work_id(blockIdx.x, nb);
     const int s = w_id % ns, kvh = w_id / ns;
     const int pos0 = *pos_d, Tmax = pos0 + 1;
@@ -274,37 +273,36 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws1_kernel(const 
     const float* qtab = reinterpret_cast<const float*>(smem + W1_QO);
     unsigned char* patch = smem + W1_PT;
     if (fused) {
-        // ---- the front: two groups of 256 threads (thread d owns dim d), each with four query heads and the key row
-        // of the group (the same bits in both groups) in one pass ----
-        const int half = tid >> 8, d = tid & 255;
-        float x[5];
-#pragma unroll
-        for (int i = 0; i < 4; i++) x[i] = fr.q[(kvh * GQ + 4 * half + i) * 2 * AHD + d];
-        x[4] = fr.k[kvh * AHD + d];
-        const uint16_t* const w[5] = {fr.qn, fr.qn, fr.qn, fr.qn, fr.kn};
-        front::norm_rope_n<5, true>(x, w, d, pos0, fr.rot, fr.theta, fr.eps, fsh[half], fsh8[half]);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int h = 4 * half + i;
-            reinterpret_cast<float*>(smem + W1_QO)[h * AHD + d] = x[i];
-            if (s == 0) fr.qo[(kvh * GQ + h) * AHD + d] = x[i];
+        // ---- the front, one wavefront per row (front::wave: the arithmetic of qk_norm_rope_kernel, no barrier):
+        // wavefront w forms query head w; in the split that holds pos0, wavefront 0 also forms the key row and the
+        // int8 codes of the new row, which go to the cache and to the patch ----
+        {
+            const float4 a = *reinterpret_cast<const float4*>(fr.q + (kvh * GQ + wv) * 2 * AHD + 4 * lane);
+            float x[4] = {a.x, a.y, a.z, a.w};
+            front::wave::norm_rope(x, fr.qn, lane, pos0, fr.rot, fr.theta, fr.eps);
+            const float4 y = make_float4(x[0], x[1], x[2], x[3]);
+            *reinterpret_cast<float4*>(smem + W1_QO + 4 * (wv * AHD + 4 * lane)) = y;
+            if (s == 0) *reinterpret_cast<float4*>(fr.qo + (kvh * GQ + wv) * AHD + 4 * lane) = y;
         }
-        if (app) {  // the new row: group 0 stores it
-            int8_t ck, cv;
+        if (app && wv == 0) {
+            const float4 a = *reinterpret_cast<const float4*>(fr.k + kvh * AHD + 4 * lane);
+            const float4 b = *reinterpret_cast<const float4*>(fr.v + kvh * AHD + 4 * lane);
+            float x[4] = {a.x, a.y, a.z, a.w};
+            const float vv[4] = {b.x, b.y, b.z, b.w};
+            front::wave::norm_rope(x, fr.kn, lane, pos0, fr.rot, fr.theta, fr.eps);
+            uint32_t ck, cv;
             float sk, sv;
-            front::quant_i8<true>(x[4], fr.v[kvh * AHD + d], fsh8[half] + 40, d, ck, cv, sk, sv);
-            if (half == 0) {
-                const size_t row = rbase + pos0;
-                kv.k[row * AHD + d] = ck;
-                kv.v[row * AHD + d] = cv;
-                reinterpret_cast<int8_t*>(patch)[d] = ck;
-                reinterpret_cast<int8_t*>(patch)[AHD + d] = cv;
-                if (d == 0) {
-                    kv.ks[row] = sk;
-                    kv.vs[row] = sv;
-                    reinterpret_cast<float*>(patch + 2 * AHD)[0] = sk;
-                    reinterpret_cast<float*>(patch + 2 * AHD)[1] = sv;
-                }
+            front::wave::quant_i8(x, vv, ck, cv, sk, sv);
+            const size_t row = rbase + pos0;
+            *reinterpret_cast<uint32_t*>(kv.k + row * AHD + 4 * lane) = ck;
+            *reinterpret_cast<uint32_t*>(kv.v + row * AHD + 4 * lane) = cv;
+            reinterpret_cast<uint32_t*>(patch)[lane] = ck;
+            reinterpret_cast<uint32_t*>(patch + AHD)[lane] = cv;
+            if (lane == 0) {
+                kv.ks[row] = sk;
+                kv.vs[row] = sv;
+                reinterpret_cast<float*>(patch + 2 * AHD)[0] = sk;
+                reinterpret_cast<float*>(patch + 2 * AHD)[1] = sv;
             }
         }
         front::sync<true>();
@@ -855,7 +853,6 @@ constexpr int WT_QT = WT_P0 + WT_NW * WT_PT;     // query digit table: [digit 2,
 constexpr int WT_QS = WT_QT + 4 * GQ * AHD;      // the heads' score scales
 constexpr int WT_LDS = WT_QS + GQ * 4;
 static_assert((WT_NW + 1) * GQ * AHD * 4 <= WT_P0, "the merge and the merged rows fit in the stages");
-static_assert(WT_NW * WT_PT == GQ * AHD * 4, "the fused front's rotated queries: head w in wavefront w's P tile");
 static_assert(WT_LDS <= 160 * 1024, "LDS");
 static_assert(WT_NW == GQ, "one wavefront per head for the query digits and the inverse rotation");
 
@@ -979,45 +976,38 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
         else vm_wait<0>();
     };
 
-    // ---- the front (T = 1, fr.q set, skip flag clear): the q/k RMSNorm + RoPE, the queries' forward rotation and,
-    // in the split that holds position pos0, the TurboQuant append of the new row, with qk_norm_rope_kernel's
-    // arithmetic (front.hpp). Two groups of 256 threads (thread d owns dim d), each with four query heads and the key
-    // row (the same bits in both; group 0 stores the row). Its scratch is the stage area, which no transfer writes
-    // yet; the rotated queries go to the P tiles, not used before the key loop. The stored row has left this
-    // workgroup's queue (vmcnt) before any transfer of it is issued. ----
+    // ---- the front (T = 1, fr.q set, skip flag clear), one wavefront per row (front::wave: the arithmetic of
+    // qk_norm_rope_kernel, no barrier): wavefront w forms query head w (RMSNorm, RoPE, the forward rotation) and keeps
+    // it for its query digits; in the split that holds pos0, wavefront 0 also forms the key row and appends the new
+    // row (TurboQuant), which leaves the queue (vmcnt) before a barrier that all transfers follow ----
     const bool fused = fr.q && !(fr.skip && *fr.skip);
-    const float* qtab = reinterpret_cast<const float*>(smem + WT_P0);
+    const bool app = fused && hi == Tmax && hi > lo;
+    float qf4[4];
     if (fused) {
-        const int half = tid >> 8, d = tid & 255;
-        float* fsh = reinterpret_cast<float*>(smem) + half * 5 * AHD;
-        float* fsh8 = reinterpret_cast<float*>(smem) + 10 * AHD + half * 48;
-        float x[5];
-#pragma unroll
-        for (int i = 0; i < 4; i++) x[i] = fr.q[(kvh * GQ + 4 * half + i) * 2 * AHD + d];
-        x[4] = fr.k[kvh * AHD + d];
-        const uint16_t* const w[5] = {fr.qn, fr.qn, fr.qn, fr.qn, fr.kn};
-        front::norm_rope_n<5, true>(x, w, d, pos0, fr.rot, fr.theta, fr.eps, fsh, fsh8);
-        float y[4] = {x[0], x[1], x[2], x[3]};
-        front::wht_n<4, true>(y, fsh, 0, d);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int h = 4 * half + i;
-            reinterpret_cast<float*>(smem + WT_P0)[h * AHD + d] = y[i];
-            if (s == 0) fr.qo[(kvh * GQ + h) * AHD + d] = y[i];
-        }
-        if (hi == Tmax && hi > lo) {  // this split holds the new row
-            front::append_turbo<true>(x[4], fr.v[kvh * AHD + d], kv, rbase + pos0, fsh + 4 * AHD, fsh8 + 40, d,
-                                      half == 0);
+        const float4 a = *reinterpret_cast<const float4*>(fr.q + (kvh * GQ + wv) * 2 * AHD + 4 * lane);
+        qf4[0] = a.x; qf4[1] = a.y; qf4[2] = a.z; qf4[3] = a.w;
+        front::wave::norm_rope(qf4, fr.qn, lane, pos0, fr.rot, fr.theta, fr.eps);
+        front::wave::wht(qf4, 0, lane);
+        if (s == 0)
+            *reinterpret_cast<float4*>(fr.qo + (kvh * GQ + wv) * AHD + 4 * lane) =
+                make_float4(qf4[0], qf4[1], qf4[2], qf4[3]);
+        if (app && wv == 0) {
+            const float4 k4 = *reinterpret_cast<const float4*>(fr.k + kvh * AHD + 4 * lane);
+            const float4 v4 = *reinterpret_cast<const float4*>(fr.v + kvh * AHD + 4 * lane);
+            float x[4] = {k4.x, k4.y, k4.z, k4.w};
+            const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+            front::wave::norm_rope(x, fr.kn, lane, pos0, fr.rot, fr.theta, fr.eps);
+            front::wave::append(x, vv, kv, rbase + pos0, lane);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
-        front::sync<true>();
     }
     // ---- query digits, once per workgroup: wavefront w turns head w (lane l: dims 4l .. 4l + 3) into three signed
     // base-256 digits of a 2^(22 - e) fixed point (|q| < 2^e over the head) and writes them to the digit table in
     // the operand order: dim d at byte 16 (d / 16) + pos(d % 16), pos = the K codes' order {0,2,4,6, 1,3,5,7, 8,..} ----
     {
-        const float4 q4 = *reinterpret_cast<const float4*>(
-            fused ? qtab + wv * AHD + 4 * lane : qo + ((size_t)tok * H + kvh * GQ + wv) * AHD + 4 * lane);
+        float4 q4;
+        if (fused) q4 = make_float4(qf4[0], qf4[1], qf4[2], qf4[3]);
+        else q4 = *reinterpret_cast<const float4*>(qo + ((size_t)tok * H + kvh * GQ + wv) * AHD + 4 * lane);
         float qm = fmaxf(fmaxf(fabsf(q4.x), fabsf(q4.y)), fmaxf(fabsf(q4.z), fabsf(q4.w)));
         qm = max_x32(max_x16(max_row16(qm)));
         int e = 0;
@@ -1038,7 +1028,9 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
         reinterpret_cast<uint32_t*>(qt + 3 * GQ * AHD)[lane] = 0u;  // the zero rows
         if (lane == 0) reinterpret_cast<float*>(smem + WT_QS)[wv] = ldexpf(1.f, e - 22) * (SL2 * TK4);
     }
-    // the first steps' transfers (the compiler's wait for the query rows above does not cover them)
+    // the first steps' transfers (the compiler's wait for the query rows above does not cover them); after the new
+    // row's stores, in the split that appends it
+    if (app) __syncthreads();
 #pragma unroll
     for (int j = 0; j < WT_NS - 1; j++)
         if (j < nst) issue(j);

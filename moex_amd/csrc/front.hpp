@@ -402,6 +402,24 @@ __device__ __forceinline__ void tq_quant(const float (&x)[4], int lane, int (&id
     norm_out = rn > 1e-20f ? n / rn : n;
 }
 
+// int8 codes of the lane's 4 dims of a k and a v row (byte i = dim 4l + i) and the rows' scales
+__device__ __forceinline__ void quant_i8(const float (&x)[4], const float (&vv)[4], uint32_t& ck, uint32_t& cv,
+                                         float& sk, float& sv) {
+#pragma clang fp contract(off)
+    float ak[4], av[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) { ak[i] = fabsf(x[i]); av[i] = fabsf(vv[i]); }
+    const float mk = row_max(ak), mv = row_max(av);
+    sk = mk > 0.f ? mk / 127.f : 1.f;
+    sv = mv > 0.f ? mv / 127.f : 1.f;
+    ck = cv = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        ck |= (uint32_t)(uint8_t)(int8_t)__builtin_rintf(x[i] / sk) << (8 * i);
+        cv |= (uint32_t)(uint8_t)(int8_t)__builtin_rintf(vv[i] / sv) << (8 * i);
+    }
+}
+
 // quantize-append of one row (x: post-RoPE k, vv: raw v, the lane's 4 dims each), int8 or TurboQuant
 __device__ __forceinline__ void append(const float (&x)[4], const float (&vv)[4], moex_kv_cache kv, size_t row,
                                        int lane) {
@@ -422,17 +440,9 @@ __device__ __forceinline__ void append(const float (&x)[4], const float (&vv)[4]
         if (!(l & 1)) V[64 + b * 16 + l / 2] = (uint8_t)(hb | (hb1 << 4));
         if (l == 0) { kv.ks[row * 2 + b] = nk; kv.vs[row * 2 + b] = nv; }
     } else {
-        float ak[4], av[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) { ak[i] = fabsf(x[i]); av[i] = fabsf(vv[i]); }
-        const float mk = row_max(ak), mv = row_max(av);
-        const float sk = mk > 0.f ? mk / 127.f : 1.f, sv = mv > 0.f ? mv / 127.f : 1.f;
-        uint32_t ck = 0, cv = 0;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            ck |= (uint32_t)(uint8_t)(int8_t)__builtin_rintf(x[i] / sk) << (8 * i);
-            cv |= (uint32_t)(uint8_t)(int8_t)__builtin_rintf(vv[i] / sv) << (8 * i);
-        }
+        uint32_t ck, cv;
+        float sk, sv;
+        quant_i8(x, vv, ck, cv, sk, sv);
         *reinterpret_cast<uint32_t*>(kv.k + row * AHD + 4 * lane) = ck;
         *reinterpret_cast<uint32_t*>(kv.v + row * AHD + 4 * lane) = cv;
         if (lane == 0) { kv.ks[row] = sk; kv.vs[row] = sv; }
