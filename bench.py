@@ -150,10 +150,15 @@ def main():
         print(f"[bench] config1 int8 prefill T={T} pos0={pos0}: {ms:.3f} ms/step, {tflops:.1f} TFLOPS "
               f"({100 * tflops / PEAK_F16:.1f}% of {PEAK_F16:.0f})", flush=True)
 
-    traffic = None
+    # HBM bytes per call from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes over this same call (counters
+    # cannot be read inside this run); the file names the kernel source it was recorded on
+    traffic, traffic_src = None, None
     tf = os.path.join(ROOT, "profiles", "fa_prefill_int8_c1_traffic.json")
     if os.path.exists(tf):
-        traffic = json.load(open(tf)).get("bytes_per_launch")
+        tj = json.load(open(tf))
+        traffic = tj.get("bytes_per_launch")
+        traffic_src = ("profiles/fa_prefill_int8_c1_traffic.json (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; recorded on "
+                       f"{tj.get('recorded_on', 'an earlier build')})")
 
     extra = {}
     if not a.quick:
@@ -295,11 +300,17 @@ def main():
             print(json.dumps({"decode_only": True, **extra}), flush=True)
             return
         p4 = torch.tensor([260096], dtype=torch.int32, device=dev)
-        ms_t, _ = time_steps(lambda: M.attn_fa(qo, None, ct, out, H, KV, p4, ct.max_t, LD, T, st), 3, 1)
-        ms_i, _ = time_steps(lambda: M.attn_fa(qo, qg, c8, out, H, KV, p4, c8.max_t, LD, T, st), 3, 1)
+
+        def turbo_chunk():  # a complete turbo step: FA in the rotated domain, then the inverse WHT and the gate
+            M.attn_fa(qo, None, ct, out, H, KV, p4, ct.max_t, LD, T, st)
+            M.turbo_out(out, qg, H, LD, T, st)
+        n4 = 3 if a.config4_only else 10
+        ms_t, _ = time_steps(turbo_chunk, n4, 2)
+        ms_i, _ = time_steps(lambda: M.attn_fa(qo, qg, c8, out, H, KV, p4, c8.max_t, LD, T, st), n4, 2)
         f4 = flops_prefill(T, 260096)
         extra["config4_prefill_260k"] = {"turbo_ms": round(ms_t, 3), "turbo_tflops": round(f4 / ms_t / 1e9, 1),
-                                         "int8_ms": round(ms_i, 3), "int8_tflops": round(f4 / ms_i / 1e9, 1)}
+                                         "int8_ms": round(ms_i, 3), "int8_tflops": round(f4 / ms_i / 1e9, 1),
+                                         "steps": n4, "turbo_step": "attn_fa + turbo_out"}
         if want_cpu:
             extra["config4_prefill_260k"]["cpu_turbo"] = cpu_prefill(hct, qh, gh, 260096, T,
                                                                      threads, full=False)
@@ -356,7 +367,7 @@ def main():
                                "keys), H=16, KV=2, head_dim=256, sigmoid-gated", "global_batch": 1, "seq_len": n,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_F16, "unit": "TFLOP/s",
-                     "frac": round(tflops / PEAK_F16, 4), "traffic": traffic},
+                     "frac": round(tflops / PEAK_F16, 4), "traffic": traffic, "traffic_source": traffic_src},
         "cpu_baseline": cpu,
         "wall_ms_per_step": round(wall_ms, 4),
     }

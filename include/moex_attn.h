@@ -17,11 +17,15 @@
  * MOEX_FA_SPLIT=n caps them, 1 turns splitting off). A chunk of at most 64 tokens (turbo: 16; MOEX_FA_GQA_MAXT=n
  * sets the int8 bound to n and the turbo bound to n / 4, 0 turns it off) runs on the split-K decode kernels and the
  * combine instead, with a workspace of T * H * ns * 1032 bytes for their partials (ns = moex_gqa_splits(T, KV,
- * moex_decode_splits(max_t), turbo)). The dense GEMM (moex_dense.h) keeps two more. Each is one per (device, stream), allocated on first use with hipMalloc and grown
+ * moex_decode_splits(max_t), turbo)). moex_attn_decode with ns == 1 and T <= 2 (the reference's one-split call) runs
+ * the split-K kernels too, with its partials in a workspace of T * H * n2 * 1032 bytes (n2 = moex_gqa_splits(T, KV,
+ * moex_decode_splits(max_t), turbo); none when n2 == 1). The dense GEMM (moex_dense.h) keeps two more. Each is one per (device, stream), allocated on first use with hipMalloc and grown
  * when a larger call comes. An outgrown buffer is not freed before the process ends, because a HIP graph captured
  * earlier may still replay into it. No workspace is allocated while the stream is being captured: a call that would
  * need to grow one reports hipErrorStreamCaptureUnsupported. So after one eager call of a given max_t and T on a
- * stream, the same call can be captured into a HIP graph. A graph's replays use the capturing stream's workspaces:
+ * stream, the same call can be captured into a HIP graph. The one exception is the one-split decode step above: while
+ * its workspace does not exist yet it is captured with the per-head kernel of the reference (no partials, no
+ * allocation, no error), so it can be captured first time as the reference's can. A graph's replays use the capturing stream's workspaces:
  * replays and eager calls that overlap in time on different streams race on them. moex_attn_workspace_bytes gives
  * the bytes one call needs, moex_workspace_held the bytes held now (for a VRAM audit next to moex_kv_bytes).
  *
@@ -70,7 +74,9 @@ void moex_kv_free(moex_kv_cache kv);
  * all T K/V rows quantized into kv (int8, or turbo codes), the query written to qo [T][H][256] (turbo: rotated),
  * then attention over keys [0, pos+t] written gated to out [T][H][256].
  * Dispatch as the reference: T > 2 and ns == 1 -> prefill (FA; MOEX_FA=0 -> moex_attn_prefill for int8);
- * ns > 1 -> split-K GQA decode + combine (part: T*H*ns*(256+2) floats); else the per-head kernel.
+ * ns > 1 -> split-K GQA decode + combine (part: T*H*ns*(256+2) floats); ns == 1 with T <= 2 and H/KV == 8 -> the
+ * same split-K kernels with partials in the library's per-stream workspace (the per-head kernel of the reference
+ * only under a first-time capture or when one split would do); otherwise the per-head kernel.
  * int8, T == 1, ns > 1, H/KV == 8: the front and the append run inside the split kernel (two launches in all), with
  * qo, the cache row and out bit-identical to the separate front's. */
 void moex_attn_decode(const float* q, const float* k, const float* v, const uint16_t* qn, const uint16_t* kn,
@@ -153,8 +159,8 @@ int moex_decode_splits(int n_ctx);
  * cache with KV heads (turbo != 0 for a turbo cache): at most ns. A caller that launches moex_attn_gqa and
  * moex_attn_combine itself passes this value to both. No counterpart in the reference. */
 int moex_gqa_splits(int T, int KV, int ns, int turbo);
-/* Workspace bytes one moex_attn_fa (or moex_attn_decode prefill) call with these sizes takes on its stream: tile
- * images plus the partials of split token tiles. No counterpart in the reference (its attn_fa_k needs none); for the
+/* Workspace bytes one moex_attn_fa or moex_attn_decode call with these sizes takes on its stream: tile images plus
+ * the partials of split token tiles, or for T <= 2 the partials of the one-split decode step. No counterpart in the reference (its attn_fa_k needs none); for the
  * engine's VRAM audit (moex.cu:960) beside moex_kv_bytes. */
 size_t moex_attn_workspace_bytes(int H, int KV, int max_t, int T);
 /* Bytes the library's per-stream workspaces hold now, on every device and stream, outgrown buffers included. No

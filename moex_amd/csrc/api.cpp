@@ -5,6 +5,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
 #include "common.hpp"
 
 namespace moex {
@@ -31,6 +32,12 @@ static bool arg_fail(const char* what) {
 #define MOEX_REQUIRE(cond, what) do { if (!(cond)) { arg_fail(what); return; } } while (0)
 
 static inline hipStream_t S(void* st) { return reinterpret_cast<hipStream_t>(st); }
+
+size_t decode_ns1_workspace_bytes(int H, int KV, int max_t, int T, bool turbo) {
+    if (T > 2 || H != KV * GQ) return 0;
+    const int n2 = gqa_splits(T, KV, moex_decode_splits(max_t), turbo);
+    return n2 > 1 ? (size_t)T * H * n2 * (AHD + 2) * sizeof(float) : 0;
+}
 
 }  // namespace moex
 
@@ -127,6 +134,9 @@ void moex_gemm_i8(const int8_t* q, const float* s, const float* X, float* Y, int
 
 size_t moex_attn_workspace_bytes(int H, int KV, int max_t, int T) {
     if (!(KV > 0 && H == KV * GQ && T > 0 && max_t > 0)) return 0;
+    if (T <= 2)  // a one-split attn_decode step (attn_fa of T <= 2 takes the same workspace kind, never more)
+        return std::max({fa_workspace_bytes(H, KV, max_t, T), decode_ns1_workspace_bytes(H, KV, max_t, T, false),
+                         decode_ns1_workspace_bytes(H, KV, max_t, T, true)});
     return fa_workspace_bytes(H, KV, max_t, T);
 }
 
@@ -219,12 +229,14 @@ void decode_step(const float* q, const float* k, const float* v, const uint16_t*
     if (ns == 1 && T <= 2 && G == GQ) {
         // the reference's one-split path (attn_decode_k per query head, no partials): one workgroup per head and
         // token leaves the chip idle (90 000 keys: 8.4 ms int8, 11.6 ms turbo). The split-K kernels take it with
-        // partials of the library's own (a workspace, or the no-allocation scratch); the per-head kernel only when
-        // that is not available.
+        // partials of the library's own (a workspace, or the no-allocation scratch). The per-head kernel runs when
+        // that is not available: one split, no allocation possible, or the stream is being captured before an eager
+        // call made the workspace (quietly: the reference's path allocates nothing and captures first time).
+        const size_t need = decode_ns1_workspace_bytes(H, KV, max_t, T, kv.turbo != 0);
         const int n2 = gqa_splits(T, KV, moex_decode_splits(max_t), kv.turbo != 0);
-        const size_t need = (size_t)T * H * n2 * (AHD + 2) * sizeof(float);
-        float* w = fa_scr ? (need <= fa_bytes ? fa_scr : nullptr)
-                          : n2 > 1 ? reinterpret_cast<float*>(stream_workspace(need, st, 4)) : nullptr;
+        float* w = !need ? nullptr
+                   : fa_scr ? (need <= fa_bytes ? fa_scr : nullptr)
+                            : reinterpret_cast<float*>(stream_workspace(need, st, 4, true));
         if (w) {
             part = w;
             ns = n2;

@@ -115,9 +115,12 @@ void launch_fa(const float* qo, const float* q_gate, moex_kv_cache kv, float* ou
 // dense int8 projections (dense.hip)
 void launch_quantize_rows_i8(const uint16_t* W, int8_t* q, float* s, int O, int I, hipStream_t st);
 void launch_gemv_i8(const int8_t* q, const float* s, const float* x, float* y, int NT, int I, int O, hipStream_t st);
-// Device memory kept per (device, stream, kind) until the process ends, grown on demand (a call that grows it first
-// waits for the stream). nullptr if it cannot be allocated.
-unsigned char* stream_workspace(size_t need, hipStream_t st, int kind);
+// Device memory kept per (device, stream, kind) until the process ends, grown on demand. nullptr if it cannot be
+// allocated; during stream capture a workspace that would have to grow is not allocated and nullptr is returned,
+// reported as hipErrorStreamCaptureUnsupported unless quiet (the caller then takes a path that needs none).
+unsigned char* stream_workspace(size_t need, hipStream_t st, int kind, bool quiet = false);
+// workspace bytes of a one-split attn_decode step of T <= 2 tokens (its split-K partials), 0 when it takes none
+size_t decode_ns1_workspace_bytes(int H, int KV, int max_t, int T, bool turbo);
 // bytes the workspaces hold on every device and stream, outgrown buffers included
 size_t stream_workspace_bytes();
 // attn_fa that allocates nothing: no tile images, the key pieces' partials in the given scratch (fewer pieces if they

@@ -665,7 +665,7 @@ size_t g_ws_retired = 0;  // bytes of outgrown buffers kept alive for captured g
 
 }  // namespace
 
-unsigned char* stream_workspace(size_t need, hipStream_t st, int kind) {
+unsigned char* stream_workspace(size_t need, hipStream_t st, int kind, bool quiet) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
     std::lock_guard<std::mutex> lk(g_ws_mu);
@@ -673,7 +673,7 @@ unsigned char* stream_workspace(size_t need, hipStream_t st, int kind) {
     if (w.second >= need) return w.first;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
-        report(hipErrorStreamCaptureUnsupported, __FILE__, __LINE__);
+        if (!quiet) report(hipErrorStreamCaptureUnsupported, __FILE__, __LINE__);
         return nullptr;
     }
     const size_t want = std::max(need, w.second + w.second / 2);

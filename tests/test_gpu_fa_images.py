@@ -50,10 +50,14 @@ def test_image_path_matches_in_kernel_widening(data, turbo, pos0, monkeypatch):
         dc = upload(random_int8_cache(max_t, seed=4))
     gate = None if turbo else qg_d
     img = _fa(dc, qo_d, gate, pos0, 128)      # tile images + DMA
+    img2 = _fa(dc, qo_d, gate, pos0, 128)     # the same call again: each path is deterministic
     monkeypatch.setenv("MOEX_FA_IMAGES", "0")
     ink = _fa(dc, qo_d, gate, pos0, 112)      # widened in the kernel
-    report("fa image vs in-kernel", turbo=turbo, pos0=pos0, maxdiff=float(np.abs(img[:112] - ink).max()))
+    ink2 = _fa(dc, qo_d, gate, pos0, 112)
+    report("fa image vs in-kernel", turbo=turbo, pos0=pos0, maxdiff=float(np.abs(img[:112] - ink).max()),
+           img_repeat=bool(np.array_equal(img, img2)), ink_repeat=bool(np.array_equal(ink, ink2)))
     assert np.all(np.isfinite(img))
+    assert np.array_equal(img, img2) and np.array_equal(ink, ink2)
     assert np.array_equal(img[:112], ink)
 
 

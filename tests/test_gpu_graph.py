@@ -165,3 +165,61 @@ def test_fa_key_pieces_graph_new_position(gqa_maxt, monkeypatch):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out_g, eager[p0]), p0
+
+
+@pytest.mark.parametrize("turbo", [0, 1])
+@pytest.mark.parametrize("T", [1, 2])
+def test_one_split_decode_captured_first(turbo, T):
+    """attn_decode with ns = 1 and T <= 2 (the reference's one-split call, kernels.cuh:1861-1863, which allocates
+    nothing) captured as the first call on a fresh stream with no soft-error slot: the capture takes the per-head
+    kernel instead of a workspace it may not allocate, reports nothing, and every replay (position advanced, new rows
+    copied in between) matches the fp64 oracle at 1e-4 of max |out|. An eager call on that stream afterwards runs the
+    split-K kernels with a new workspace; the graph keeps replaying correctly."""
+    import torch
+    import moex_amd as M
+    from oracle import oracle as orc
+    from tests.gpu_util import download
+    LQ = H * 2 * AHD + 2 * KV * AHD
+    ctx, base = 2048, 1500
+    c = M.DeviceKVCache(KV, ctx, turbo)
+    g = torch.Generator(device="cuda").manual_seed(31 + T + 2 * turbo)
+    kv = torch.randn((base, 2 * KV * AHD), generator=g, device="cuda")
+    M.kv_append(kv[:, :KV * AHD], kv[:, KV * AHD:], c, KV, torch.zeros(1, dtype=torch.int32, device="cuda"), ctx,
+                2 * KV * AHD, base)
+    qn = torch.zeros(AHD, dtype=torch.int16, device="cuda")
+    qkv = torch.zeros((T, LQ), device="cuda")
+    qo = torch.empty((T, H, AHD), device="cuda")
+    out = torch.empty((T, H, AHD), device="cuda")
+    pos = torch.zeros(1, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    held = M.lib().moex_workspace_held()
+    st = torch.cuda.Stream()
+
+    def step():
+        M.attn_decode(qkv, qkv[:, H * 2 * AHD:], qkv[:, H * 2 * AHD + KV * AHD:], qn, qn, qo, c, out, H, KV, pos, ctx,
+                      64, 1e7, 1e-6, T, LQ, st, None, 1)
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        step()
+    torch.cuda.synchronize()
+    assert M.lib().moex_workspace_held() == held  # nothing allocated under capture
+    for i in range(4):
+        p = base + T * i
+        qkv.copy_(torch.randn((T, LQ), generator=g, device="cuda"))
+        M.set_int(pos, p)
+        torch.cuda.synchronize()
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        if i == 2:  # an eager step on the capturing stream: split-K with its own workspace, then the graph again
+            with torch.cuda.stream(st):
+                step()
+            st.synchronize()
+        hc = download(c)
+        rows = [(t, h) for t in range(T) for h in range(H)]
+        ref = orc.attn_rows_f64(qo.cpu().numpy(), qkv.cpu().numpy(), LQ, H, hc, p, rows).reshape(T, H, AHD)
+        got = out.cpu().numpy()
+        err, mag = float(np.abs(got - ref).max()), float(np.abs(ref).max())
+        print(f"one-split capture turbo={turbo} T={T} replay {i}: err={err:.3e} mag={mag:.3e}", flush=True)
+        assert np.all(np.isfinite(got)) and err <= 1e-4 * mag, i

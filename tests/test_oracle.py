@@ -310,3 +310,76 @@ def test_dense_exact_product(orc):
     y16 = orc.dense_i8_fp16x(q, s, x)
     ref16 = (x.astype(np.float16).astype(np.float64) @ q.T.astype(np.float64)) * s.astype(np.float64)
     assert np.abs(y16 - ref16).max() <= 1e-12 * np.abs(ref16).max()
+
+
+def _fa_emul_2key(q, k, ks, v, vs, round_q=True, round_p=True):
+    """numpy restatement of the precision model for one row over the keys given (one 64-key tile): fp32 score
+    s = float32(q16 . k) * (ks * sl2), base-2 softmax against the tile max in fp32, P * vs rounded to fp16."""
+    sl2 = np.float32(np.float32(1.0 / 16.0) * np.float32(1.4426950408889634))
+    qq = q.astype(np.float16).astype(np.float64) if round_q else q.astype(np.float64)
+    s = np.array([np.float32(np.float32(qq @ kj.astype(np.float64)) * np.float32(np.float32(ksj) * sl2))
+                  for kj, ksj in zip(k, ks)], np.float32)
+    e = np.exp2((s - s.max()).astype(np.float32)).astype(np.float32)
+    pv = (e * vs.astype(np.float32)).astype(np.float32)
+    if round_p:
+        pv = pv.astype(np.float16).astype(np.float32)
+    o = (pv.astype(np.float64)[:, None] * v.astype(np.float64)).sum(0)
+    return o.astype(np.float32).astype(np.float64) / float(e.astype(np.float32).sum(dtype=np.float32))
+
+
+def _one_head_cache(orc, k, ks, v, vs):
+    c = orc.HostCache(1, len(k), 0)
+    c.k[0], c.ks[0], c.v[0], c.vs[0] = k, ks, v, vs
+    return c
+
+
+def test_fa_precision_model_single_key(orc):
+    """fp16-exact Q and V scale, one visible key: softmax weight 1, no rounding left, so the precision model equals
+    the fp64 reference (and the closed form v * vs) to 1e-12."""
+    rng = np.random.default_rng(12)
+    q = rng.standard_normal(AHD).astype(np.float16).astype(np.float32)
+    k = rng.integers(-127, 128, (1, AHD)).astype(np.int8)
+    v = rng.integers(-127, 128, (1, AHD)).astype(np.int8)
+    ks = np.array([0.0123], np.float32)
+    vs = np.array([np.float16(0.0371)], np.float32)
+    c = _one_head_cache(orc, k, ks, v, vs)
+    qo = q.reshape(1, 1, AHD)
+    a = orc.attn_rows_f64(qo, None, 2 * AHD, 1, c, 0, [(0, 0)])[0]
+    b = orc.attn_rows_fa_emul(qo, None, 2 * AHD, 1, c, 0, [(0, 0)])[0]
+    assert np.allclose(b, a, rtol=1e-12, atol=0)
+    assert np.allclose(b, v[0].astype(np.float64) * float(vs[0]), rtol=1e-12, atol=0)
+
+
+def test_fa_precision_model_rounding_points(orc):
+    """Two keys whose rounding effects are known: the model equals the numpy restatement to 1e-6, and the same
+    restatement with the P * vs rounding (or the Q rounding) dropped differs from it by far more, so a model that
+    lost either rounding fails here."""
+    # P * vs rounding: fp16-exact Q; key 1 scores about 1 below key 0 (weight ~1/2), P * vs1 not fp16-exact
+    q = np.zeros(AHD, np.float32); q[0] = 1.0
+    k = np.zeros((2, AHD), np.int8); k[0, 0] = 64; k[1, 0] = 0
+    sl2 = np.float32(np.float32(1.0 / 16.0) * np.float32(1.4426950408889634))
+    ks = np.array([1.0 / (64 * float(sl2)), 0.02], np.float32)   # s0 ~ 1, s1 = 0
+    v = np.full((2, AHD), 100, np.int8); v[1] = -77
+    vs = np.array([2.0 ** -16, 1.3e-5], np.float32)   # 0.5 * vs1 lands among the fp16 subnormals (spacing 2^-24)
+    c = _one_head_cache(orc, k, ks, v, vs)
+    qo = q.reshape(1, 1, AHD)
+    got = orc.attn_rows_fa_emul(qo, None, 2 * AHD, 1, c, 1, [(0, 0)])[0]
+    want = _fa_emul_2key(q, k, ks, v, vs)
+    loose = _fa_emul_2key(q, k, ks, v, vs, round_p=False)
+    tol = 1e-6 * np.abs(want).max()
+    assert np.abs(got - want).max() <= tol
+    assert np.abs(got - loose).max() > 50 * tol
+    # Q rounding: every dim of q is 1 + 2^-12 (rounds to 1 in fp16) against a full key of 127s
+    q = np.full(AHD, 1.0 + 2.0 ** -12, np.float32)
+    k = np.zeros((2, AHD), np.int8); k[0] = 127
+    ks = np.array([3.0 / (256 * 127 * float(sl2)), 0.02], np.float32)   # s0 ~ 3, s1 = 0
+    v = np.full((2, AHD), 50, np.int8); v[1] = -120
+    vs = np.array([np.float16(0.25), np.float16(0.125)], np.float32)
+    c = _one_head_cache(orc, k, ks, v, vs)
+    qo = q.reshape(1, 1, AHD)
+    got = orc.attn_rows_fa_emul(qo, None, 2 * AHD, 1, c, 1, [(0, 0)])[0]
+    want = _fa_emul_2key(q, k, ks, v, vs)
+    loose = _fa_emul_2key(q, k, ks, v, vs, round_q=False)
+    tol = 1e-6 * np.abs(want).max()
+    assert np.abs(got - want).max() <= tol
+    assert np.abs(got - loose).max() > 20 * tol
