@@ -416,6 +416,154 @@ __device__ __forceinline__ void fa_tile(const _Float16* Kt, const _Float16* Vt, 
     }
 }
 
+// What a block does: up to two segments, each a token tile over key tiles [ja, ja + ntiles), and what its epilogue
+// writes: the output rows, a piece's partial rows for fa_merge_kernel, or its half of a pair (merged in the kernel).
+enum { FA_MODE_ONE = 0, FA_MODE_SPLIT = 1, FA_MODE_PAIR = 2 };
+enum { FA_EPI_OUT = 0, FA_EPI_PIECE = 1, FA_EPI_PAIR = 2 };
+struct FaSeg {
+    int tile, ja, ntiles, epi;
+};
+__host__ __device__ inline int fa_ntiles(int t, int pos0, int T) {  // key tiles token tile t sees
+    return (pos0 + (FT * (t + 1) < T ? FT * (t + 1) : T) + BK - 1) / BK;
+}
+
+// Pairs (full grids): token tile t's work grows with t, so one block per tile leaves the chip waiting for the last
+// tiles (at pos0 = 0 the heaviest has twice the average). Pair q = tiles NT - 1 - q (heavy) and q (light), both of one
+// kv head, goes to two blocks on one XCD: block 0 takes key tiles [0, s) of the heavy tile, block 1 the light tile and
+// then key tiles [s, n) of the heavy one, s chosen so both do about half of the pair. The heavy tile's halves merge in
+// the kernel (fa_pair_merge). A pair whose halves would differ by less than FA_PAIR_MIN tiles is not split; an odd
+// tile count leaves the middle tile to one block.
+constexpr int FA_PAIR_MIN = 4;
+constexpr int FA_PAIR_SLOT = 64 * 128 + 128;  // floats per wavefront half: O (lane-interleaved float4s), {m, l} per lane
+__device__ __forceinline__ bool fa_pair_block(int b, int KV, int NT, int& kvh, int& q, int& role) {
+    if (8 % KV == 0) {  // blocks b and b + 8 run on one XCD: the two blocks of a pair
+        const int xpk = 8 / KV, x = b & 7, i = b >> 3;
+        kvh = x / xpk;
+        q = (i >> 1) * xpk + x % xpk;
+        role = i & 1;
+    } else {
+        const int per = 2 * ((NT + 1) / 2);
+        kvh = b / per;
+        q = (b % per) >> 1;
+        role = b & 1;
+        if (kvh >= KV) return false;
+    }
+    return q < NT / 2 || (q == NT / 2 && (NT & 1) && role == 0);
+}
+__host__ inline int fa_pair_grid(int KV, int T) {
+    const int nq = ((T + FT - 1) / FT + 1) / 2;
+    if (8 % KV == 0) { const int xpk = 8 / KV; return 16 * ((nq + xpk - 1) / xpk); }
+    return KV * 2 * nq;
+}
+__device__ __forceinline__ int fa_pair_segs(int q, int role, int pos0, int T, int NT, int pmin, FaSeg (&sg)[2]) {
+    if (q == NT / 2) {  // the middle tile of an odd count
+        sg[0] = FaSeg{q, 0, fa_ntiles(q, pos0, T), FA_EPI_OUT};
+        return 1;
+    }
+    const int tH = NT - 1 - q, nH = fa_ntiles(tH, pos0, T), nL = fa_ntiles(q, pos0, T);
+    // block 1's part starts at or below every row's last key, so each row sees keys in both parts
+    const int s = min((nH + nL + 1) / 2, (pos0 + FT * tH) / BK);
+    if (s < 1 || nH - s < pmin) {
+        sg[0] = role ? FaSeg{q, 0, nL, FA_EPI_OUT} : FaSeg{tH, 0, nH, FA_EPI_OUT};
+        return 1;
+    }
+    if (role == 0) {
+        sg[0] = FaSeg{tH, 0, s, FA_EPI_PAIR};
+        return 1;
+    }
+    sg[0] = FaSeg{tH, s, nH - s, FA_EPI_PAIR};
+    sg[1] = FaSeg{q, 0, nL, FA_EPI_OUT};
+    return 2;
+}
+
+// The pair merge, per computing wavefront (32 rows, the same rows in both blocks). Its arrival counter pcnt[2 slot]
+// is even when a launch starts (zeroed at allocation, +2 per launch); the first arrival stores its {O, m, l} with
+// agent-scope stores, waits for them to complete and marks pcnt[2 slot + 1] with the count the second arrival will
+// have seen. The second arrival waits for that mark (the first is past its arrival, so it is running and the wait
+// ends; it is bounded all the same), loads the partner's half the same way and merges. The merge is symmetric in
+// the two halves, so the bits do not depend on which block arrives first. Returns true in the merging wavefront.
+__device__ __forceinline__ bool fa_pair_merge(float* __restrict__ pbuf, unsigned* __restrict__ pcnt, int slot, int lane,
+                                              float16_t (&o)[8], float m_ref, float& l_run) {
+    // products rounded before the sum (no fma contraction), so the merge is symmetric in the two halves
+#pragma clang fp contract(off)
+    unsigned* cnt = pcnt + 2 * slot;
+    unsigned old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(pbuf + (size_t)slot * FA_PAIR_SLOT, 0, FA_PAIR_SLOT * 4, 0x00020000);
+    constexpr int SC1 = 16;  // agent-scope accesses (the partner may run on another XCD)
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    typedef float f2v __attribute__((ext_vector_type(2)));
+    if (!(old & 1)) {
+#pragma unroll
+        for (int db = 0; db < 8; db++)
+#pragma unroll
+            for (int a4 = 0; a4 < 4; a4++)
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    f4v{o[db][4 * a4], o[db][4 * a4 + 1], o[db][4 * a4 + 2], o[db][4 * a4 + 3]}, rs,
+                    ((4 * db + a4) * 64 + lane) * 16, 0, SC1);
+        __builtin_amdgcn_raw_buffer_store_b64(f2v{m_ref, l_run}, rs, 64 * 128 * 4 + lane * 8, 0, SC1);
+        __builtin_amdgcn_s_waitcnt(0);  // the stores have completed
+        if (lane == 0) __hip_atomic_store(cnt + 1, old + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return false;
+    }
+    for (int it = 0; it < (1 << 22); it++) {
+        const unsigned mark = __builtin_amdgcn_readfirstlane(__hip_atomic_load(cnt + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        if (mark == old) break;
+        __builtin_amdgcn_s_sleep(4);
+    }
+    const f2v ml = __builtin_amdgcn_raw_buffer_load_b64(rs, 64 * 128 * 4 + lane * 8, 0, SC1);
+    const float M = fmaxf(m_ref, ml.x), ca = fast_exp2(ml.x - M), cb = fast_exp2(m_ref - M);
+    l_run = ml.y * ca + l_run * cb;
+#pragma unroll
+    for (int db = 0; db < 8; db++)
+#pragma unroll
+        for (int a4 = 0; a4 < 4; a4++) {
+            const f4v pa = __builtin_amdgcn_raw_buffer_load_b128(rs, ((4 * db + a4) * 64 + lane) * 16, 0, SC1);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                o[db][4 * a4 + e] = pa[e] * ca + o[db][4 * a4 + e] * cb;
+        }
+    return true;
+}
+
+// The lane's output row: O / l * sigmoid(gate) (the gate by the hardware reciprocal: 1 ulp; the output's tolerance
+// is fp16-level)
+__device__ __forceinline__ void fa_write_out(const float16_t (&o)[8], float l_run, float* __restrict__ out,
+                                             const float* __restrict__ q_gate, size_t t, int head, int H, int ld,
+                                             int h32) {
+    const float il = 1.f / l_run;
+    float* orow = out + (t * H + head) * AHD;
+    const float* grow = q_gate ? q_gate + t * ld + head * 2 * AHD + AHD : nullptr;
+    // the gate row is loaded a dims block ahead of its use (loads issued one by one behind the stores would each
+    // wait for the memory round trip)
+    float4 gc[4], gn[4];
+    if (grow)
+#pragma unroll
+        for (int a4 = 0; a4 < 4; a4++) gc[a4] = *reinterpret_cast<const float4*>(grow + 8 * a4 + 4 * h32);
+#pragma unroll
+    for (int db = 0; db < 8; db++) {
+        if (grow && db + 1 < 8)
+#pragma unroll
+            for (int a4 = 0; a4 < 4; a4++)
+                gn[a4] = *reinterpret_cast<const float4*>(grow + 32 * (db + 1) + 8 * a4 + 4 * h32);
+#pragma unroll
+        for (int a4 = 0; a4 < 4; a4++) {
+            const int d = 32 * db + 8 * a4 + 4 * h32;
+            float4 res = make_float4(o[db][4 * a4] * il, o[db][4 * a4 + 1] * il, o[db][4 * a4 + 2] * il, o[db][4 * a4 + 3] * il);
+            if (grow) {
+                const float4 g = gc[a4];
+                res.x *= __builtin_amdgcn_rcpf(1.f + __expf(-g.x)); res.y *= __builtin_amdgcn_rcpf(1.f + __expf(-g.y));
+                res.z *= __builtin_amdgcn_rcpf(1.f + __expf(-g.z)); res.w *= __builtin_amdgcn_rcpf(1.f + __expf(-g.w));
+            }
+            *reinterpret_cast<float4*>(orow + d) = res;
+        }
+#pragma unroll
+        for (int a4 = 0; a4 < 4; a4++) gc[a4] = gn[a4];
+    }
+}
+
 // Warp-specialised workgroup of 8 wavefronts. Wavefronts 0-3 compute (32 query rows each); wavefronts 4-7 fill the LDS
 // tile buffers. Each SIMD holds one wavefront of each kind, so the filling runs beside the other wavefront's MFMAs.
 //   IMG = false: the staging wavefronts load the next tiles' int8/turbo K and V and widen them (two buffers: during
@@ -424,24 +572,27 @@ __device__ __forceinline__ void fa_tile(const _Float16* Kt, const _Float16* Vt, 
 //   IMG = true: the tiles were widened by fa_image_kernel; the staging wavefronts only copy images by DMA into four
 //   buffers (two pairs of tiles: one computed while the next lands, one barrier per pair), leaving out the padding
 //   slots nobody reads.
-template <bool TB, bool IMG, bool SPLIT>
+template <bool TB, bool IMG, int MODE>
 __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restrict__ qo, const float* __restrict__ q_gate,
                                                             moex_kv_cache kv, const unsigned char* __restrict__ img,
                                                             int ntmax, float* __restrict__ out, int H, int KV,
                                                             const int* __restrict__ pos_d, int max_t, int ld, int T,
-                                                            float* __restrict__ fpart, int nsf, int ncu) {
+                                                            float* __restrict__ fpart, int nsf, int ncu,
+                                                            unsigned* __restrict__ pcnt) {
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr int NB = IMG ? 4 : 2;
 #define KBUF(i) (smem + (i) * TILE_BYTES)
 #define VBUF(i) (smem + (i) * TILE_BYTES + KT_BYTES)
 #define SBUF(i) (reinterpret_cast<float*>(smem + (i) * TILE_BYTES + KT_BYTES + VT_BYTES))
     const int NT = (T + FT - 1) / FT, pos0 = *pos_d;
-    int kvh, tile, piece = 0, nsp = 1;
-    if (SPLIT) {
+    // the block's segments (at most two): token tile, key tiles [ja, ja + ntiles), what the epilogue does
+    FaSeg sg[2];
+    int kvh, nseg = 1, piece = 0, pslot = 0;
+    if (MODE == FA_MODE_SPLIT) {
         // block b takes the b-th piece, pieces listed heaviest token tile first, so the blocks left without one are
         // the last ones dispatched (a queued block waits for a whole CU's LDS even when it has nothing to do)
         const int w = fa_piece_w(pos0, T, KV, NT, ncu);
-        int b = blockIdx.x;
+        int b = blockIdx.x, tile, nsp = 1;
         for (tile = NT - 1; tile >= 0; tile--) {
             nsp = fa_pieces(tile, pos0, T, nsf, w);
             if (b < KV * nsp) break;
@@ -450,160 +601,179 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
         if (tile < 0) return;
         kvh = b % KV;
         piece = b / KV;
-    } else if (!map_block(blockIdx.x, KV, NT, kvh, tile)) {
-        return;
+        const int nall = fa_ntiles(tile, pos0, T), ja = piece * nall / nsp;
+        sg[0] = FaSeg{tile, ja, (piece + 1) * nall / nsp - ja, nsp > 1 ? FA_EPI_PIECE : FA_EPI_OUT};
+    } else if (MODE == FA_MODE_PAIR) {
+        int q, role;
+        if (!fa_pair_block(blockIdx.x, KV, NT, kvh, q, role)) return;
+        nseg = fa_pair_segs(q, role, pos0, T, NT, nsf, sg);  // nsf: the pair minimum
+        pslot = (kvh * (NT / 2) + q) * 4;
+    } else {
+        int tile;
+        if (!map_block(blockIdx.x, KV, NT, kvh, tile)) return;
+        sg[0] = FaSeg{tile, 0, fa_ntiles(tile, pos0, T), FA_EPI_OUT};
     }
-    const int t0 = tile * FT, nt = min(FT, T - t0), hi = pos0 + t0 + nt;  // keys [0, hi)
     const size_t rbase = (size_t)kvh * max_t;
-    const int nall = (hi + BK - 1) / BK, ja = SPLIT ? piece * nall / nsp : 0;  // this piece: key tiles [ja, ja + ntiles)
-    const int ntiles = SPLIT ? (piece + 1) * nall / nsp - ja : nall;
 
     if (threadIdx.x >= 256 && IMG) {
         // ---------------- DMA wavefronts: image j -> buffer j % 4, 1 KB pieces i = pw, pw + 4, .. ----------------
         const int pw = (threadIdx.x >> 6) - 4, lane = threadIdx.x & 63;
         const unsigned char* src = img + (size_t)kvh * ntmax * TILE_BYTES;
-        auto issue = [&](int j) { fa_issue_img(src, ja + j, smem + (j % NB) * TILE_BYTES, pw, lane); };
-        // piece counts per wavefront: 10 for pw = 0 (pieces 0, 4, .., 36), 9 for the others
-        // pairs of tiles: pair p = tiles 2p, 2p + 1 in buffers 2 (p % 2), + 1; one barrier per pair
-        asm volatile("s_barrier" ::: "memory");  // the queries' reads are out ahead of the first images
-        for (int j = 0; j < 4 && j < ntiles; j++) issue(j);
-        fa_wait_first_pair(ntiles, pw);
-        asm volatile("s_barrier" ::: "memory");  // pair 0 is in buffers 0, 1
-        const int np = (ntiles + 1) / 2;
-        for (int p = 0; p < np; p++) {
-            wait_vm<0>();                            // pair p + 1 has landed
-            asm volatile("s_barrier" ::: "memory");  // every computing wavefront is past pair p
-            if (2 * p + 4 < ntiles) issue(2 * p + 4);
-            if (2 * p + 5 < ntiles) issue(2 * p + 5);
+        for (int g = 0; g < nseg; g++) {
+            const int ja = __builtin_amdgcn_readfirstlane(sg[g].ja), ntiles = __builtin_amdgcn_readfirstlane(sg[g].ntiles);
+            auto issue = [&](int j) { fa_issue_img(src, ja + j, smem + (j % NB) * TILE_BYTES, pw, lane); };
+            // piece counts per wavefront: 10 for pw = 0 (pieces 0, 4, .., 36), 9 for the others
+            // pairs of tiles: pair p = tiles 2p, 2p + 1 in buffers 2 (p % 2), + 1; one barrier per pair
+            asm volatile("s_barrier" ::: "memory");  // the queries' reads are out ahead of the first images
+            for (int j = 0; j < 4 && j < ntiles; j++) issue(j);
+            fa_wait_first_pair(ntiles, pw);
+            asm volatile("s_barrier" ::: "memory");  // pair 0 is in buffers 0, 1
+            const int np = (ntiles + 1) / 2;
+            for (int p = 0; p < np; p++) {
+                wait_vm<0>();                            // pair p + 1 has landed
+                asm volatile("s_barrier" ::: "memory");  // every computing wavefront is past pair p
+                if (2 * p + 4 < ntiles) issue(2 * p + 4);
+                if (2 * p + 5 < ntiles) issue(2 * p + 5);
+            }
         }
         return;
     }
     if (threadIdx.x >= 256) {
         // ---------------- staging wavefronts ----------------
         const int tid = threadIdx.x - 256;
-        StageK sk;
-        StageV sv;
-        const int ka = ja * BK;
-        load_k<TB>(sk, kv, rbase, ka, hi, tid);
-        load_v<TB>(sv, kv, rbase, ka, hi, tid);
-        store_k<TB>(sk, KBUF(0), SBUF(0), SBUF(0) + BK, ka, hi, tid);
-        store_v<TB>(sv, VBUF(0), ka, hi, tid);
-        if (ntiles > 1) {
-            load_k<TB>(sk, kv, rbase, ka + BK, hi, tid);
-            load_v<TB>(sv, kv, rbase, ka + BK, hi, tid);
-        }
-        __syncthreads();
-        for (int j = 0; j < ntiles; j++) {
-            const int k1 = ka + (j + 1) * BK, b = (j + 1) & 1;
-            if (j + 1 < ntiles) {
-                if (k1 + BK <= hi) {
-                    store_k<TB, true>(sk, KBUF(b), SBUF(b), SBUF(b) + BK, k1, hi, tid);
-                    store_v<TB, true>(sv, VBUF(b), k1, hi, tid);
-                } else {
-                    store_k<TB>(sk, KBUF(b), SBUF(b), SBUF(b) + BK, k1, hi, tid);
-                    store_v<TB>(sv, VBUF(b), k1, hi, tid);
-                }
+        for (int g = 0; g < nseg; g++) {
+            const int ntiles = __builtin_amdgcn_readfirstlane(sg[g].ntiles), ka = __builtin_amdgcn_readfirstlane(sg[g].ja) * BK;
+            const int hi = pos0 + min(FT * (__builtin_amdgcn_readfirstlane(sg[g].tile) + 1), T);
+            StageK sk;
+            StageV sv;
+            load_k<TB>(sk, kv, rbase, ka, hi, tid);
+            load_v<TB>(sv, kv, rbase, ka, hi, tid);
+            store_k<TB>(sk, KBUF(0), SBUF(0), SBUF(0) + BK, ka, hi, tid);
+            store_v<TB>(sv, VBUF(0), ka, hi, tid);
+            if (ntiles > 1) {
+                load_k<TB>(sk, kv, rbase, ka + BK, hi, tid);
+                load_v<TB>(sv, kv, rbase, ka + BK, hi, tid);
             }
-            if (j + 2 < ntiles) {
-                const int k2 = k1 + BK;
-                if (k2 + BK <= hi) {
-                    load_k<TB, true>(sk, kv, rbase, k2, hi, tid);
-                    load_v<TB, true>(sv, kv, rbase, k2, hi, tid);
-                } else {
-                    load_k<TB>(sk, kv, rbase, k2, hi, tid);
-                    load_v<TB>(sv, kv, rbase, k2, hi, tid);
+            __syncthreads();
+            for (int j = 0; j < ntiles; j++) {
+                const int k1 = ka + (j + 1) * BK, b = (j + 1) & 1;
+                if (j + 1 < ntiles) {
+                    if (k1 + BK <= hi) {
+                        store_k<TB, true>(sk, KBUF(b), SBUF(b), SBUF(b) + BK, k1, hi, tid);
+                        store_v<TB, true>(sv, VBUF(b), k1, hi, tid);
+                    } else {
+                        store_k<TB>(sk, KBUF(b), SBUF(b), SBUF(b) + BK, k1, hi, tid);
+                        store_v<TB>(sv, VBUF(b), k1, hi, tid);
+                    }
                 }
+                if (j + 2 < ntiles) {
+                    const int k2 = k1 + BK;
+                    if (k2 + BK <= hi) {
+                        load_k<TB, true>(sk, kv, rbase, k2, hi, tid);
+                        load_v<TB, true>(sv, kv, rbase, k2, hi, tid);
+                    } else {
+                        load_k<TB>(sk, kv, rbase, k2, hi, tid);
+                        load_v<TB>(sv, kv, rbase, k2, hi, tid);
+                    }
+                }
+                // tile j + 1 is in LDS; tile j + 2 stays in flight into registers (__syncthreads would wait for it)
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
             }
-            // tile j + 1 is in LDS; tile j + 2 stays in flight into registers (__syncthreads would wait for it)
-            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         }
         return;
     }
 
     // ---------------- computing wavefronts ----------------
     __builtin_amdgcn_s_setprio(2);  // ahead of the staging wavefronts at the SIMD's issue arbiter
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h32 = lane >> 5, r = lane & 31;
-    const int tokw = 4 * w + (r >> 3), head = kvh * GQ + (r & 7);                     // this lane's row
-    const int prow = min(pos0 + t0 + tokw, hi - 1);                                     // its last visible key
-    const int wmin = min(pos0 + t0 + 4 * w, hi - 1);                                    // the wavefront's first row
-    const int wmax = min(pos0 + t0 + 4 * w + 3, hi - 1);                                // ... and its last key
-    const int wtiles = wmax / BK + 1;  // tiles this wavefront computes
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), h32 = lane >> 5, r = lane & 31;
+    constexpr bool PIECEWISE = MODE != FA_MODE_ONE;
+    auto segment = [&](const FaSeg& sgc) {
+        // wave-uniform (the segment table may sit in scratch; its values would otherwise be taken as divergent)
+        const int tile = __builtin_amdgcn_readfirstlane(sgc.tile), ja = __builtin_amdgcn_readfirstlane(sgc.ja);
+        const int epi = __builtin_amdgcn_readfirstlane(sgc.epi);
+        int ntiles = __builtin_amdgcn_readfirstlane(sgc.ntiles);
+        const int t0 = tile * FT, nt = min(FT, T - t0), hi = pos0 + t0 + nt;  // keys [0, hi)
+        if (MODE == FA_MODE_ONE) ntiles = (hi + BK - 1) / BK;
+        const int tokw = 4 * w + (r >> 3), head = kvh * GQ + (r & 7);                     // this lane's row
+        const int prow = min(pos0 + t0 + tokw, hi - 1);                                     // its last visible key
+        const int wmin = min(pos0 + t0 + 4 * w, hi - 1);                                    // the wavefront's first row
+        const int wmax = min(pos0 + t0 + 4 * w + 3, hi - 1);                                // ... and its last key
+        const int wtiles = wmax / BK + 1;  // tiles this wavefront computes
 
-    // Q row (fp16) as B operands: MFMA s covers dims 16s + 8*h32 + 0..7
-    half8_t qf[16];
-    {
-        const float* qrow = qo + ((size_t)(t0 + min(tokw, nt - 1)) * H + head) * AHD;
-        float4 qa[32];
+        // Q row (fp16) as B operands: MFMA s covers dims 16s + 8*h32 + 0..7
+        half8_t qf[16];
+        {
+            const float* qrow = qo + ((size_t)(t0 + min(tokw, nt - 1)) * H + head) * AHD;
+            float4 qa[32];
 #pragma unroll
-        for (int s = 0; s < 16; s++) {
-            const float4* p4 = reinterpret_cast<const float4*>(qrow + 16 * s + 8 * h32);
-            qa[2 * s] = p4[0];
-            qa[2 * s + 1] = p4[1];
+            for (int s = 0; s < 16; s++) {
+                const float4* p4 = reinterpret_cast<const float4*>(qrow + 16 * s + 8 * h32);
+                qa[2 * s] = p4[0];
+                qa[2 * s + 1] = p4[1];
+            }
+            // with tile images, the DMA wavefronts send the first images once these reads are out
+            if (IMG) asm volatile("s_barrier" ::: "memory");
+#pragma unroll
+            for (int s = 0; s < 16; s++) {
+                const float4 a = qa[2 * s], b = qa[2 * s + 1];
+                qf[s] = half8_t{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
+                                (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
+            }
         }
-        // with tile images, the DMA wavefronts send the first images once these reads are out
-        if (IMG) asm volatile("s_barrier" ::: "memory");
-#pragma unroll
-        for (int s = 0; s < 16; s++) {
-            const float4 a = qa[2 * s], b = qa[2 * s + 1];
-            qf[s] = half8_t{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
-                            (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
-        }
-    }
-    float16_t o[8];
-#pragma unroll
-    for (int db = 0; db < 8; db++)
-#pragma unroll
-        for (int i = 0; i < 16; i++) o[db][i] = 0.f;
-    float m_ref = -INFINITY, l_run = 0.f;
-    __syncthreads();
-
-    // split: this wavefront's tiles of the piece, then barriers only while the others finish theirs (one loop with a
-    // per-tile test makes the compiler spill once the trip count is not the tile count)
-    const int wt = max(0, min(ntiles, wtiles - ja));
-    for (int j = 0; j < (SPLIT ? wt : ntiles); j++) {
-        if (SPLIT || j < wtiles) {
-            fa_tile(reinterpret_cast<const _Float16*>(KBUF(j % NB)), reinterpret_cast<const _Float16*>(VBUF(j % NB)),
-                    SBUF(j % NB), (ja + j) * BK, j == 0, prow, wmin, r, h32, qf, o, m_ref, l_run);
-        }
-        if (!IMG || (j & 1) || j + 1 == ntiles) __syncthreads();
-    }
-    if (SPLIT)
-        for (int j = wt; j < ntiles; j++)
-            if (!IMG || (j & 1) || j + 1 == ntiles) __syncthreads();
-#undef KBUF
-#undef VBUF
-#undef SBUF
-    // ---- epilogue: O / l * sigmoid(gate), or this piece's {O, m, l} for the merge ----
-    l_run += __shfl_xor(l_run, 32);
-    if (tokw >= nt) return;
-    const size_t t = (size_t)(t0 + tokw);
-    if (SPLIT && nsp > 1) {
-        float* prow = fpart + ((t * H + head) * nsf + piece) * FP_ROW;
+        float16_t o[8];
 #pragma unroll
         for (int db = 0; db < 8; db++)
 #pragma unroll
-            for (int a4 = 0; a4 < 4; a4++)
-                *reinterpret_cast<float4*>(prow + 32 * db + 8 * a4 + 4 * h32) =
-                    make_float4(o[db][4 * a4], o[db][4 * a4 + 1], o[db][4 * a4 + 2], o[db][4 * a4 + 3]);
-        if (h32 == 0) *reinterpret_cast<float2*>(prow + AHD) = make_float2(m_ref, l_run);
-        return;
-    }
-    const float il = 1.f / l_run;
-    float* orow = out + (t * H + head) * AHD;
-    const float* grow = q_gate ? q_gate + t * ld + head * 2 * AHD + AHD : nullptr;
-#pragma unroll
-    for (int db = 0; db < 8; db++)
-#pragma unroll
-        for (int a4 = 0; a4 < 4; a4++) {
-            const int d = 32 * db + 8 * a4 + 4 * h32;
-            float4 res = make_float4(o[db][4 * a4] * il, o[db][4 * a4 + 1] * il, o[db][4 * a4 + 2] * il, o[db][4 * a4 + 3] * il);
-            if (grow) {  // sigmoid(g) by the hardware reciprocal (1 ulp; the output's tolerance is fp16-level)
-                const float4 g = *reinterpret_cast<const float4*>(grow + d);
-                res.x *= __builtin_amdgcn_rcpf(1.f + __expf(-g.x)); res.y *= __builtin_amdgcn_rcpf(1.f + __expf(-g.y));
-                res.z *= __builtin_amdgcn_rcpf(1.f + __expf(-g.z)); res.w *= __builtin_amdgcn_rcpf(1.f + __expf(-g.w));
+            for (int i = 0; i < 16; i++) o[db][i] = 0.f;
+        float m_ref = -INFINITY, l_run = 0.f;
+        __syncthreads();
+
+        // pieces: this wavefront's tiles of the piece, then barriers only while the others finish theirs (one loop
+        // with a per-tile test makes the compiler spill once the trip count is not the tile count)
+        const int wt = max(0, min(ntiles, wtiles - ja));
+        for (int j = 0; j < (PIECEWISE ? wt : ntiles); j++) {
+            if (PIECEWISE || j < wtiles) {
+                fa_tile(reinterpret_cast<const _Float16*>(KBUF(j % NB)), reinterpret_cast<const _Float16*>(VBUF(j % NB)),
+                        SBUF(j % NB), (ja + j) * BK, j == 0, prow, wmin, r, h32, qf, o, m_ref, l_run);
             }
-            *reinterpret_cast<float4*>(orow + d) = res;
+            if (!IMG || (j & 1) || j + 1 == ntiles) __syncthreads();
         }
+        if (PIECEWISE)
+            for (int j = wt; j < ntiles; j++)
+                if (!IMG || (j & 1) || j + 1 == ntiles) __syncthreads();
+
+        // ---- epilogue: O / l * sigmoid(gate), this piece's {O, m, l} for the merge kernel, or the pair merge ----
+        l_run += __shfl_xor(l_run, 32);
+        const size_t t = (size_t)(t0 + tokw);
+        if (MODE == FA_MODE_SPLIT && epi == FA_EPI_PIECE) {
+            if (tokw < nt) {
+                float* pr = fpart + ((t * H + head) * nsf + piece) * FP_ROW;
+#pragma unroll
+                for (int db = 0; db < 8; db++)
+#pragma unroll
+                    for (int a4 = 0; a4 < 4; a4++)
+                        *reinterpret_cast<float4*>(pr + 32 * db + 8 * a4 + 4 * h32) =
+                            make_float4(o[db][4 * a4], o[db][4 * a4 + 1], o[db][4 * a4 + 2], o[db][4 * a4 + 3]);
+                if (h32 == 0) *reinterpret_cast<float2*>(pr + AHD) = make_float2(m_ref, l_run);
+            }
+            return;
+        }
+        if (MODE == FA_MODE_PAIR && epi == FA_EPI_PAIR) {
+            // the two blocks of a pair hold keys [0, s) and [s, n) of this token tile for the same rows; the one that
+            // finishes last merges, so neither waits for a block that may not have started
+            if (!fa_pair_merge(fpart, pcnt, pslot + w, lane, o, m_ref, l_run)) return;
+        }
+        if (tokw < nt) fa_write_out(o, l_run, out, q_gate, t, head, H, ld, h32);
+    };
+    if (MODE == FA_MODE_PAIR) {  // one copy of the segment's code: a second inlined copy ran 1.5x slower per tile
+#pragma nounroll
+        for (int g = 0; g < nseg; g++) segment(sg[g]);
+    } else {
+        segment(sg[0]);
+    }
+#undef KBUF
+#undef VBUF
+#undef SBUF
 }
 
 // Merge of the key pieces of the token tiles that fa_prefill_kernel split: out = sum_s O_s 2^(m_s - M) /
@@ -654,7 +824,8 @@ struct WsKey {
     int dev;
     hipStream_t st;
     int kind;  // 0: FA tile images, 1: FA partials of split token tiles, 2: fp16 GEMM activations,
-               // 3: GEMM K-split partials, 4: decode-kernel partials of short FA chunks
+               // 3: GEMM K-split partials, 4: decode-kernel partials of short FA chunks, 5: FA pair arrival
+               // counters (zeroed when allocated)
     bool operator<(const WsKey& o) const {
         return dev != o.dev ? dev < o.dev : st != o.st ? st < o.st : kind < o.kind;
     }
@@ -682,6 +853,11 @@ unsigned char* stream_workspace(size_t need, hipStream_t st, int kind, bool quie
         (void)hipGetLastError();  // out of memory: the caller takes a path without it, or reports the error
         return nullptr;
     }
+    if (kind == 5 && hipMemsetAsync(p, 0, want, st) != hipSuccess) {  // counters start even (never during capture)
+        (void)hipGetLastError();
+        (void)hipFree(p);
+        return nullptr;
+    }
     if (w.first) g_ws_retired += w.second;  // kept, not freed (see above)
     w = {static_cast<unsigned char*>(p), want};
     return w.first;
@@ -695,10 +871,10 @@ size_t stream_workspace_bytes() {
 }
 
 namespace {
-template <bool TB, bool IMG, bool SPLIT>
+template <bool TB, bool IMG, int MODE>
 void set_lds() {
     static bool once = [] {
-        MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(fa_prefill_kernel<TB, IMG, SPLIT>),
+        MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(fa_prefill_kernel<TB, IMG, MODE>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (IMG ? 4 : 2) * TILE_BYTES));
         return true;
     }();
@@ -720,7 +896,8 @@ int fa_ncu() {
 // (the device picks the actual count from pos0), the bytes of their partial rows, and the bytes of the tile images.
 struct FaPlan {
     int NT, ntmax, nsf;
-    size_t part_bytes, img_bytes;
+    bool pair;          // full grid: pairs of token tiles (fa_pair_segs), their halves merged in the kernel
+    size_t part_bytes, img_bytes, cnt_bytes;
     int gns;            // > 0: a chunk this short runs on the split-K decode kernels with gns splits
     size_t gqa_bytes;   // their partials
 };
@@ -760,6 +937,17 @@ FaPlan fa_plan(int H, int KV, int max_t, int T, bool turbo) {
     }
     p.nsf = nsf;
     p.part_bytes = nsf > 1 ? (size_t)T * H * nsf * FP_ROW * sizeof(float) : 0;
+    // pairs: MOEX_FA_PAIR=0 turns them off (read on every call)
+    const char* pe = std::getenv("MOEX_FA_PAIR");
+    // (one wave of workgroups: with more, one tile per workgroup heaviest first already balances the waves and
+    // measured faster, 4096 tokens at pos0 = 0: 158 against 178 us)
+    p.pair = nsf == 1 && NT >= 2 && KV * NT <= ncu && !(pe && std::atoi(pe) == 0);
+    p.cnt_bytes = 0;
+    if (p.pair) {
+        const size_t slots = (size_t)KV * (NT / 2) * 4;
+        p.part_bytes = slots * FA_PAIR_SLOT * sizeof(float);
+        p.cnt_bytes = slots * 2 * sizeof(unsigned);
+    }
     // tile images for every chunk: measured faster than widening in the kernel at every chunk length and context
     // (a 3-token chunk over 90 000 keys: 159 against 388 us for turbo). MOEX_FA_IMAGES=0 turns them off (read on
     // every call), which saves the workspace and gives the same bits.
@@ -779,24 +967,35 @@ FaPlan fa_plan(int H, int KV, int max_t, int T, bool turbo) {
 template <bool TB>
 void launch_fa_bufs(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
                     const int* pos_d, int max_t, int ld, int T, hipStream_t st, const FaPlan& p, unsigned char* img,
-                    float* fpart, int nsf) {
-    const int ncu = fa_ncu(), NT = p.NT, ntmax = p.ntmax, nb = fa_grid(KV, T);
+                    float* fpart, int nsf, unsigned* pcnt) {
+    const int ncu = fa_ncu(), ntmax = p.ntmax;
     if (nsf > 1 && !fpart) nsf = 1;
+    const bool pair = nsf == 1 && p.pair && fpart && pcnt;
     if (img) {
         hipLaunchKernelGGL(fa_image_kernel<TB>, dim3(ntmax, KV), dim3(256), 0, st, kv, pos_d, T, max_t, ntmax, img);
         MOEX_LAUNCHED();
     }
     // a split launch has KV x tiles x nsf blocks: the pieces of every tile, the rest exit at once
-    const dim3 grid(nsf > 1 ? KV * NT * nsf : nb);
+    const int mode = nsf > 1 ? FA_MODE_SPLIT : pair ? FA_MODE_PAIR : FA_MODE_ONE;
+    int pmin = FA_PAIR_MIN;  // MOEX_FA_PAIR_MIN=n: split a pair's heavy tile only when its second half has n tiles
+    if (const char* e = std::getenv("MOEX_FA_PAIR_MIN")) pmin = std::max(1, std::atoi(e));
+    const dim3 grid(mode == FA_MODE_SPLIT ? KV * p.NT * nsf : mode == FA_MODE_PAIR ? fa_pair_grid(KV, T) : fa_grid(KV, T));
     const size_t lds = (img ? 4 : 2) * TILE_BYTES;
-#define FA_LAUNCH(IMG_, SPLIT_)                                                                                        \
+#define FA_LAUNCH(IMG_, MODE_)                                                                                         \
     do {                                                                                                               \
-        set_lds<TB, IMG_, SPLIT_>();                                                                                   \
-        hipLaunchKernelGGL((fa_prefill_kernel<TB, IMG_, SPLIT_>), grid, dim3(512), lds, st, qo, q_gate, kv, img, ntmax, \
-                           out, H, KV, pos_d, max_t, ld, T, fpart, nsf, ncu);                                          \
+        set_lds<TB, IMG_, MODE_>();                                                                                    \
+        hipLaunchKernelGGL((fa_prefill_kernel<TB, IMG_, MODE_>), grid, dim3(512), lds, st, qo, q_gate, kv, img, ntmax,  \
+                           out, H, KV, pos_d, max_t, ld, T, fpart, mode == FA_MODE_PAIR ? pmin : nsf, ncu, pcnt);      \
     } while (0)
-    if (img) { if (nsf > 1) FA_LAUNCH(true, true); else FA_LAUNCH(true, false); }
-    else { if (nsf > 1) FA_LAUNCH(false, true); else FA_LAUNCH(false, false); }
+    if (img) {
+        if (mode == FA_MODE_SPLIT) FA_LAUNCH(true, FA_MODE_SPLIT);
+        else if (mode == FA_MODE_PAIR) FA_LAUNCH(true, FA_MODE_PAIR);
+        else FA_LAUNCH(true, FA_MODE_ONE);
+    } else {
+        if (mode == FA_MODE_SPLIT) FA_LAUNCH(false, FA_MODE_SPLIT);
+        else if (mode == FA_MODE_PAIR) FA_LAUNCH(false, FA_MODE_PAIR);
+        else FA_LAUNCH(false, FA_MODE_ONE);
+    }
 #undef FA_LAUNCH
     MOEX_LAUNCHED();
     if (nsf > 1) {
@@ -820,8 +1019,9 @@ void launch_fa_t(const float* qo, const float* q_gate, moex_kv_cache kv, float* 
         }
     }
     float* fpart = p.part_bytes ? reinterpret_cast<float*>(stream_workspace(p.part_bytes, st, 1)) : nullptr;
+    unsigned* pcnt = p.cnt_bytes ? reinterpret_cast<unsigned*>(stream_workspace(p.cnt_bytes, st, 5)) : nullptr;
     unsigned char* img = p.img_bytes ? stream_workspace(p.img_bytes, st, 0) : nullptr;
-    launch_fa_bufs<TB>(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, st, p, img, fpart, fpart ? p.nsf : 1);
+    launch_fa_bufs<TB>(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, st, p, img, fpart, fpart ? p.nsf : 1, pcnt);
 }
 }  // namespace
 
@@ -846,8 +1046,9 @@ void launch_fa_scratch(const float* qo, const float* q_gate, moex_kv_cache kv, f
     if (nsf > 1 && per * nsf > bytes) nsf = (int)std::min<size_t>(nsf, bytes / per);
     if (nsf < 2) nsf = 1;
     float* fpart = nsf > 1 ? scratch : nullptr;
-    if (kv.turbo) launch_fa_bufs<true>(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, st, p, nullptr, fpart, nsf);
-    else launch_fa_bufs<false>(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, st, p, nullptr, fpart, nsf);
+    // full grids run one block per token tile here (pairs need arrival counters that persist across calls)
+    if (kv.turbo) launch_fa_bufs<true>(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, st, p, nullptr, fpart, nsf, nullptr);
+    else launch_fa_bufs<false>(qo, q_gate, kv, out, H, KV, pos_d, max_t, ld, T, st, p, nullptr, fpart, nsf, nullptr);
 }
 
 size_t fa_workspace_bytes(int H, int KV, int max_t, int T) {
@@ -855,7 +1056,7 @@ size_t fa_workspace_bytes(int H, int KV, int max_t, int T) {
     size_t b = 0;
     for (bool tb : {false, true}) {
         const FaPlan p = fa_plan(H, KV, max_t, T, tb);
-        b = std::max(b, p.gns > 0 ? p.gqa_bytes : p.part_bytes + p.img_bytes);
+        b = std::max(b, p.gns > 0 ? p.gqa_bytes : p.part_bytes + p.img_bytes + p.cnt_bytes);
     }
     return b;
 }

@@ -83,12 +83,15 @@ def test_attn_workspace_bytes():
     """The per-stream workspace one attn_fa call takes (for a VRAM audit beside kv_bytes): tile images of
     KV * ceil(max_t / 32) * 37632 B, plus partial rows of split token tiles for short chunks; for chunks of at most
     64 tokens, at least the decode kernels' partials T * H * ns * 1032 B, which int8 chunks take instead (the count
-    covers turbo chunks, which take the FA path). 256 CUs: the fallback without a device, MI355X's count."""
+    covers turbo chunks, which take the FA path); full grids add the halves of their paired token tiles,
+    KV * (tiles / 2) * 4 wavefront slots of 33280 B, and 8 B of arrival counters per slot. 256 CUs: the fallback
+    without a device, MI355X's count."""
     import moex_amd as M
     if not os.path.exists(M.LIB_PATH):
         pytest.skip("libmoex_attn.so not built")
-    assert M.attn_workspace_bytes(16, 2, 34816, 2048) == 2 * 1088 * 37632          # configs[1]: images only
-    assert M.attn_workspace_bytes(16, 2, 262144, 2048) == 2 * 8192 * 37632         # configs[4]: 617 MB
+    pairs = 2 * 64 * 4 * (33280 + 8)                                                # 2048 tokens: 128 tiles
+    assert M.attn_workspace_bytes(16, 2, 34816, 2048) == 2 * 1088 * 37632 + pairs  # configs[1]
+    assert M.attn_workspace_bytes(16, 2, 262144, 2048) == 2 * 8192 * 37632 + pairs  # configs[4]: 617 MB
     assert M.attn_workspace_bytes(16, 2, 40000, 64) == 2 * 1250 * 37632 + 64 * 16 * 32 * 1040  # 32 key pieces
     assert M.attn_workspace_bytes(16, 2, 64, 64) == 64 * 16 * 1 * 1032                # decode kernels, 1 split
     assert M.attn_workspace_bytes(16, 2, 40000, 256) == 2 * 1250 * 37632 + 256 * 16 * 16 * 1040  # 16 pieces
