@@ -14,7 +14,11 @@
  * bytes (MOEX_FA_IMAGES=0: none, the kernel widens each tile itself, same results, slower). A chunk whose token
  * tiles leave the chip underfilled (KV * ceil(T / 16) < CUs) may split each token tile's keys over several
  * workgroups, with a second workspace for their partial results, T * H * pieces * 1040 bytes (at most 32 pieces;
- * MOEX_FA_SPLIT=n caps them, 1 turns splitting off). A chunk of at most 64 tokens (turbo: 16; MOEX_FA_GQA_MAXT=n
+ * MOEX_FA_SPLIT=n caps them, 1 turns splitting off). A chunk whose token tiles fill the chip once (KV * ceil(T / 16)
+ * <= CUs, not split, e.g. 2048 tokens) runs its token tiles in heavy/light pairs on two workgroups each, the heavy
+ * tile's two halves merged in the kernel: a workspace of KV * (ceil(T / 16) / 2) * 4 * 33280 bytes for one half's
+ * partial rows and one of 8 bytes per such slot for arrival counters (zeroed when allocated; MOEX_FA_PAIR=0 turns
+ * pairs off). A chunk of at most 64 tokens (turbo: 16; MOEX_FA_GQA_MAXT=n
  * sets the int8 bound to n and the turbo bound to n / 4, 0 turns it off) runs on the split-K decode kernels and the
  * combine instead, with a workspace of T * H * ns * 1032 bytes for their partials (ns = moex_gqa_splits(T, KV,
  * moex_decode_splits(max_t), turbo)). moex_attn_decode with ns == 1 and T <= 2 (the reference's one-split call) runs
@@ -88,7 +92,9 @@ void moex_attn_decode(const float* q, const float* k, const float* v, const uint
  * (T*H*ns*(256+2) floats) live in a device array of the library, MOEX_NOALLOC_SCRATCH_BYTES per GPU, held from the
  * library's load until the process ends; a larger T*H*ns is rejected (argument error). The prefill branch (T > 2,
  * ns == 1) runs FA without tile images (the same bits) and puts its key pieces' partials in that array, with fewer
- * pieces when they would not fit (results then within the FA tolerance of moex_attn_decode, not bit-identical).
+ * pieces when they would not fit (results then within the FA tolerance of moex_attn_decode, not bit-identical), and
+ * runs full one-wave grids one token tile per workgroup, without the pairs of moex_attn_fa (within the FA tolerance
+ * of moex_attn_decode there, not bit-identical).
  * Calls nothing that allocates. Every call on a GPU shares that GPU's array: calls that overlap in time on one GPU
  * (different streams, or a replayed graph beside an eager call) race on it. */
 #define MOEX_NOALLOC_SCRATCH_BYTES (32u << 20)
