@@ -43,6 +43,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--config4-only", action="store_true",
                     help="only the configs[4] prefill calls (for counter runs; prints no JSON line)")
+    ap.add_argument("--config0-only", action="store_true",
+                    help="only the configs[0] prefill calls (pos0 = 0; for counter runs; prints no JSON line)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     a = ap.parse_args()
@@ -141,6 +143,12 @@ def main():
         M.attn_fa(qo, qg, c8, out, H, KV, pos_d, c8.max_t, LD, T, st)
 
     threads = cpu_threads()
+    if a.config0_only:
+        pz = torch.tensor([0], dtype=torch.int32, device=dev)
+        ms0, _ = time_steps(lambda: M.attn_fa(qo, qg, c8, out, H, KV, pz, c8.max_t, LD, T, st), a.steps, a.warmup)
+        print(f"[bench] config0 int8 prefill pos0=0: {ms0:.4f} ms, {flops_prefill(T, 0) / ms0 / 1e9:.1f} TFLOPS",
+              flush=True)
+        return
     want_cpu = not a.no_cpu and not a.decode_only and not a.config4_only
     hc8 = host_cache(c8, n) if want_cpu else None
     qh, gh = (qo.cpu().numpy(), qg.cpu().numpy()) if want_cpu else (None, None)
