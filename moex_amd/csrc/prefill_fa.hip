@@ -86,6 +86,15 @@ struct StageV {
 };
 __device__ __forceinline__ int vkey(int tid, int i) { return 16 * (tid >> 7) + 4 * ((tid >> 6) & 1) + (i & 3) + 8 * (i >> 2); }
 
+// A scale product that is converted to fp16 later goes through r32 (rounded to fp32 first, then to fp16): otherwise
+// the compiler may fuse the product and the conversion into one v_fma_mixlo (one rounding) in one kernel and not in
+// another, and the tile images and the in-kernel widening must hold the same bytes (measured: one turbo half norm in
+// 8192 came out one fp16 ulp apart between two kernels that inline the same code)
+__device__ __forceinline__ float r32(float x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
 // FULL: every key of the tile exists (no clamping / masking)
 template <bool TB, bool FULL = false>
 __device__ __forceinline__ void load_k(StageK& S, moex_kv_cache kv, size_t rbase, int k0, int hi, int tid) {
@@ -128,7 +137,7 @@ __device__ __forceinline__ void load_v(StageV& S, moex_kv_cache kv, size_t rbase
             const uint8_t* vp = reinterpret_cast<const uint8_t*>(kv.v) + row * TQ_VB;
             const int b = dg >> 5;
             S.v[i] = (uint32_t)vp[b * 32 + (dg & 31)] | ((uint32_t)vp[64 + b * 16 + ((dg & 31) >> 1)] << 8);
-            S.vs[i] = kv.vs[row * 2 + b] * TK3;
+            S.vs[i] = r32(kv.vs[row * 2 + b] * TK3);
         } else {
             S.v[i] = *reinterpret_cast<const uint32_t*>(kv.v + row * AHD + dg * 4);
             S.vs[i] = kv.vs[row];
@@ -144,7 +153,8 @@ __device__ __forceinline__ void store_k(const StageK& S, unsigned char* kbuf, fl
     const bool ok = k0 + key < hi;
     uint32_t w[BK / 2];  // BK halves
     if (TB) {  // BK nibbles -> biased codes -> fp16, times the half norm * K4
-        const half2_t sc = half2_t{(_Float16)(S.kn * TK4), (_Float16)(S.kn * TK4)};
+        const _Float16 sch = (_Float16)r32(S.kn * TK4);
+        const half2_t sc = half2_t{sch, sch};
 #pragma unroll
         for (int i = 0; i < BK / 8; i++) {
             const uint4 u = S.k[i >> 2];
