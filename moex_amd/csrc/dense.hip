@@ -144,41 +144,48 @@ __global__ void __launch_bounds__(64 * GV_WAVES) gemv_kernel(const int8_t* __res
 }
 
 // The same product when every wavefront has at most one row group and one load step (rounds = 1, a part of at most
-// 64 * GV_U chunks: the attention's qkv and o shapes). Without loops the first weights can go out before the input
-// rows are copied into LDS by DMA, so the two memory round trips overlap. Same sum order as gemv_kernel.
-template <int NT>
+// 64 * GV_U chunks: the attention's qkv and o shapes). Without loops every load goes out at the start; each lane reads
+// its inputs straight from L2, so the products wait only for their own rows. Same sum order as gemv_kernel.
+template <int NT, int R>
 __global__ void __launch_bounds__(64 * GV_WAVES) gemv1_kernel(const int8_t* __restrict__ q, const float* __restrict__ s,
                                                               const float* __restrict__ x, float* __restrict__ y, int I,
                                                               int O, int KS) {
     constexpr int GV_U = gv_u<NT>();
-    extern __shared__ __align__(16) float xs[];  // [NT][I], then the partial sums [GV_WAVES][NT][GV_R]
-    float* red = xs + NT * I;
+    extern __shared__ __align__(16) float red[];  // the partial sums [GV_WAVES][NT][R] (R weight rows a group)
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nb = gridDim.x;
-    const int ngroups = (O + GV_R - 1) / GV_R;
+    const int ngroups = (O + R - 1) / R;
     const int part = wv % KS, slice = I / 16 / KS, cb = part * slice, ce = cb + slice;
     const int g = blockIdx.x + nb * (wv / KS);
     const bool on = g < ngroups;
-    u32x4 w[GV_U][GV_R];
+    // the lane's 16 inputs of each row of x first (read from L2 by every wavefront of this part; no LDS copy and no
+    // barrier before the products), then the weights, so the products of the first weight rows start while the
+    // later rows are still arriving
+    float4 xv[GV_U][NT][4];
+#pragma unroll
+    for (int u = 0; u < GV_U; u++) {
+        if (cb + 64 * u >= ce) continue;  // a step past the part (wave-uniform): nothing to load
+        const int c = min(cb + 64 * u + lane, I / 16 - 1);
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int d = 0; d < 4; d++) xv[u][t][d] = reinterpret_cast<const float4*>(x + (size_t)t * I)[4 * c + d];
+    }
+    u32x4 w[GV_U][R];
 #pragma unroll
     for (int u = 0; u < GV_U; u++)
 #pragma unroll
-        for (int r = 0; r < GV_R; r++) {
-            const u32x4* row = reinterpret_cast<const u32x4*>(q + (size_t)min(min(g, ngroups - 1) * GV_R + r, O - 1) * I);
+        for (int r = 0; r < R; r++) {
+            const u32x4* row = reinterpret_cast<const u32x4*>(q + (size_t)min(min(g, ngroups - 1) * R + r, O - 1) * I);
             const int c = cb + 64 * u + lane;
             w[u][r] = on && c < ce ? __builtin_nontemporal_load(row + c) : u32x4{0u, 0u, 0u, 0u};
         }
     // the row scale of this lane's output, loaded now so that its round trip overlaps the weights'
-    const float so = s[min(min(g, ngroups - 1) * GV_R + lane % GV_R, O - 1)];
-    for (int i = wv; i < NT * I * 4 / 1024; i += GV_WAVES)  // NT * I * 4 is a multiple of 1 KB (I % 512 == 0)
-        __builtin_amdgcn_global_load_lds((gptr_t)(reinterpret_cast<const char*>(x) + i * 1024 + 16 * lane),
-                                         (lptr_t)(reinterpret_cast<char*>(xs) + i * 1024), 16, 0, 0);
-    wait_vm<0>();
-    __syncthreads();  // the input rows have landed
-    float acc[NT][GV_R];
+    const float so = s[min(min(g, ngroups - 1) * R + lane % R, O - 1)];
+    float acc[NT][R];
 #pragma unroll
     for (int t = 0; t < NT; t++)
 #pragma unroll
-        for (int r = 0; r < GV_R; r++) acc[t][r] = 0.f;
+        for (int r = 0; r < R; r++) acc[t][r] = 0.f;
 #pragma unroll
     for (int u = 0; u < GV_U; u++) {
         const int c = cb + 64 * u + lane;
@@ -187,14 +194,14 @@ __global__ void __launch_bounds__(64 * GV_WAVES) gemv1_kernel(const int8_t* __re
         for (int t = 0; t < NT; t++) {
 #pragma unroll
             for (int d = 0; d < 4; d++) {
-                const float4 xv = reinterpret_cast<const float4*>(xs + t * I)[4 * c + d];
+                const float4 xq = xv[u][t][d];
 #pragma unroll
-                for (int r = 0; r < GV_R; r++) {
+                for (int r = 0; r < R; r++) {
                     const uint32_t wd = w[u][r][d];
-                    acc[t][r] += (float)(int8_t)(wd) * xv.x;
-                    acc[t][r] += (float)(int8_t)(wd >> 8) * xv.y;
-                    acc[t][r] += (float)(int8_t)(wd >> 16) * xv.z;
-                    acc[t][r] += (float)(int8_t)(wd >> 24) * xv.w;
+                    acc[t][r] += (float)(int8_t)(wd) * xq.x;
+                    acc[t][r] += (float)(int8_t)(wd >> 8) * xq.y;
+                    acc[t][r] += (float)(int8_t)(wd >> 16) * xq.z;
+                    acc[t][r] += (float)(int8_t)(wd >> 24) * xq.w;
                 }
             }
         }
@@ -202,15 +209,15 @@ __global__ void __launch_bounds__(64 * GV_WAVES) gemv1_kernel(const int8_t* __re
 #pragma unroll
     for (int t = 0; t < NT; t++)
 #pragma unroll
-        for (int r = 0; r < GV_R; r++) {
+        for (int r = 0; r < R; r++) {
             const float v = wave_sum(acc[t][r]);
-            if (lane == 0) red[(wv * NT + t) * GV_R + r] = v;
+            if (lane == 0) red[(wv * NT + t) * R + r] = v;
         }
     __syncthreads();
-    if (on && part == 0 && lane < NT * GV_R) {
-        const int t = lane / GV_R, r = lane % GV_R, o = g * GV_R + r;
-        float v = red[(wv * NT + t) * GV_R + r];
-        for (int p = 1; p < KS; p++) v += red[((wv + p) * NT + t) * GV_R + r];
+    if (on && part == 0 && lane < NT * R) {
+        const int t = lane / R, r = lane % R, o = g * R + r;
+        float v = red[(wv * NT + t) * R + r];
+        for (int p = 1; p < KS; p++) v += red[((wv + p) * NT + t) * R + r];
         if (o < O) y[(size_t)t * O + o] = v * so;
     }
 }
@@ -463,13 +470,14 @@ void launch_gemv_t(const int8_t* q, const float* s, const float* x, float* y, in
     const size_t lds = (size_t)NT * I * 4 + GV_WAVES * NT * GV_R * 4;
     const bool one = groups <= nb * (GV_WAVES / ks) && I / 16 / ks <= 64 * gv_u<NT>();
     if (one) {
-        static bool once1 = [] {
-            MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gemv1_kernel<NT>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-            return true;
-        }();
-        (void)once1;
-        hipLaunchKernelGGL(gemv1_kernel<NT>, dim3(nb), dim3(64 * GV_WAVES), lds, st, q, s, x, y, I, O, ks);
+        // groups of 4 rows when groups of 8 would leave half the wavefronts without work (o_proj): every wavefront
+        // then has work, half as much, and the sums are the same (a row's sum order does not depend on the group)
+        if ((O + 3) / 4 * ks <= nb * GV_WAVES && groups * ks * 2 <= nb * GV_WAVES)
+            hipLaunchKernelGGL((gemv1_kernel<NT, 4>), dim3(nb), dim3(64 * GV_WAVES), (size_t)GV_WAVES * NT * 4 * 4, st,
+                               q, s, x, y, I, O, ks);
+        else
+            hipLaunchKernelGGL((gemv1_kernel<NT, GV_R>), dim3(nb), dim3(64 * GV_WAVES), (size_t)GV_WAVES * NT * GV_R * 4,
+                               st, q, s, x, y, I, O, ks);
     } else {
         hipLaunchKernelGGL(gemv_kernel<NT>, dim3(nb), dim3(64 * GV_WAVES), lds, st, q, s, x, y, I, O, ks);
     }
