@@ -1,10 +1,11 @@
 /*
- * moex_dense.h -- C ABI of the MI355X (gfx950) dense int8 projections on either side of moex's attention: the fused
+ * moex_dense.h -- C ABI of the MI355X (gfx950) dense projections on either side of moex's attention: the fused
  * qkv projection that writes the q / gate / k / v rows attn_decode reads (moex.cu:1084,1395; [LQ = 9216][D = 2048])
  * and the o projection of its output (moex.cu:1086,1399; [D = 2048][AH*AHD = 4096]).
  *
  * The weights are the reference's default form of these matrices (struct Mat with q and s, kernels.cuh:186-196):
- * int8 [O][I] row-major plus one fp32 scale per row, y = s[o] * (q[o,:] . x). Every entry point replaces one function
+ * int8 [O][I] row-major plus one fp32 scale per row, y = s[o] * (q[o,:] . x); moex_gemv / moex_gemm take the
+ * matrix in any of the reference's forms (int8, int4 gs64, int6 gs64, fp16). Every entry point replaces one function
  * of src/kernels.cuh, cited on its declaration, with the reference's argument order. All pointers are device pointers;
  * stream is an opaque hipStream_t (NULL = the default stream). Nothing allocates or synchronizes, except moex_gemm_i8
  * with S > 8: it rounds X to fp16 into a per-(device, stream) workspace of S * I * 2 bytes, allocated on first use
@@ -34,6 +35,45 @@ void moex_gemv_i8(const int8_t* q, const float* s, const float* x, float* y, int
  * weights exact, fp32 accumulation, the row scale applied last), as gemm_i8_k (kernels.cuh:250-337).
  * I % 512 == 0 for S <= 8, I % 32 == 0 for S > 8. */
 void moex_gemm_i8(const int8_t* q, const float* s, const float* X, float* Y, int S, int I, int O, void* stream);
+
+/* ---- the other weight forms of a dense matrix (struct Mat, kernels.cuh:186-196) ----
+ * A matrix is held in exactly one form, the first non-NULL of q4, q6, q, f16 (the reference's order of tests):
+ *   f16       fp16 [O][I] (binary16 bit patterns);
+ *   q, s      int8 [O][I] + fp32 row scales [O] (as above);
+ *   q4, s     int4 gs64: [O][I/2] bytes, weight i of a row in bits 4 (i % 2) of byte i / 2 (low nibble first), two's
+ *             complement, and fp32 scales [O][I/64], one per 64 inputs: w = q * s;
+ *   q6, q6h, s  int6 gs64: the low 4 bits in q6 as q4's nibbles, the high 2 bits in q6h [O][I/4] at bits 2 (i % 4) of
+ *             byte i / 4, u = low | high << 4 in [0, 63], w = (u - 32) * s, s [O][I/64]. */
+typedef struct moex_mat {
+    const uint16_t* f16;
+    const int8_t* q;
+    const float* s;
+    const uint8_t* q4;
+    const uint8_t* q6;
+    const uint8_t* q6h;
+} moex_mat;
+
+/* quantize_rows_q4_k<<<O, 64>>>(W, q4, s, I) (kernels.cuh:576-590): per 64-input group scale = absmax / 7 (1 for a
+ * zero group), q = round-half-even(w / scale) clamped to [-8, 7]. I % 64 == 0. Bit-exact. */
+void moex_quantize_rows_q4(const uint16_t* W, uint8_t* q4, float* s, int O, int I, void* stream);
+
+/* quantize_rows_q6_k<<<O, 64>>>(W, q6, q6h, s, I) (kernels.cuh:552-573): scale = group absmax / 31 (1 for a zero
+ * group), u = round-half-even(w / scale) clamped to [-32, 31], + 32. I % 64 == 0. Bit-exact. */
+void moex_quantize_rows_q6(const uint16_t* W, uint8_t* q6, uint8_t* q6h, float* s, int O, int I, void* stream);
+
+/* gemv(m, x, y, I, O, st) (kernels.cuh:214-219): y [O] = W . x with fp32 sums for any form of m (int8 as
+ * moex_gemv_i8; int4 and int6 sum each 32-input unit, then scale it, as gemv_q4_k / gemv_q6_k, :486-550; fp16 as
+ * gemv_f16_k, :68-93). I % 64 == 0 (int4, int6), I % 32 == 0 (fp16), int8 as moex_gemv_i8. */
+void moex_gemv(const moex_mat* m, const float* x, float* y, int I, int O, void* stream);
+
+/* gemm(m, X, Y, S, I, O, st) (kernels.cuh:339-369): Y [S][O] = X [S][I] . W^T with the reference's choice of path:
+ *   int8: moex_gemm_i8;
+ *   int6 with S <= 8: one GEMV pass for all S rows, each row bit-identical to moex_gemv of that row;
+ *   int4 and fp16 with S <= 2: moex_gemv row by row;
+ *   otherwise the fp16 MFMA GEMM: activations rounded to fp16, int4 / int6 weights times their group scale rounded
+ *   to fp16 (fp16 weights as stored), fp32 accumulation (gemm_wmma_k :225-248, gemm_i8_k<true> :250-337).
+ * The GEMM takes the per-stream activation workspace of moex_gemm_i8 (S * I * 2 bytes). */
+void moex_gemm(const moex_mat* m, const float* X, float* Y, int S, int I, int O, void* stream);
 
 #ifdef __cplusplus
 }

@@ -16,6 +16,16 @@ AHD = 256
 TQ_KB, TQ_VB = 128, 96
 
 
+class Mat(ctypes.Structure):
+    """struct Mat (kernels.cuh:186-196) as moex_mat (include/moex_dense.h): one of f16; q, s (int8, row scales);
+    q4, s (int4 gs64); q6, q6h, s (int6 gs64). Fields take torch tensors or device addresses."""
+    _fields_ = [("f16", ctypes.c_void_p), ("q", ctypes.c_void_p), ("s", ctypes.c_void_p), ("q4", ctypes.c_void_p),
+                ("q6", ctypes.c_void_p), ("q6h", ctypes.c_void_p)]
+
+    def __init__(self, f16=None, q=None, s=None, q4=None, q6=None, q6h=None):
+        super().__init__(_p(f16), _p(q), _p(s), _p(q4), _p(q6), _p(q6h))
+
+
 class KVCache(ctypes.Structure):
     """struct KVCache (kernels.cuh:1121): int8 *k, *v; float *ks, *vs; int turbo."""
     _fields_ = [("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("ks", ctypes.c_void_p), ("vs", ctypes.c_void_p),
@@ -71,6 +81,10 @@ def lib():
     L.moex_quantize_rows_i8.argtypes = [vp, vp, vp, i, i, vp]
     L.moex_gemv_i8.argtypes = [vp, vp, vp, vp, i, i, vp]
     L.moex_gemm_i8.argtypes = [vp, vp, vp, vp, i, i, i, vp]
+    L.moex_quantize_rows_q4.argtypes = [vp, vp, vp, i, i, vp]
+    L.moex_quantize_rows_q6.argtypes = [vp, vp, vp, vp, i, i, vp]
+    L.moex_gemv.argtypes = [ctypes.POINTER(Mat), vp, vp, i, i, vp]
+    L.moex_gemm.argtypes = [ctypes.POINTER(Mat), vp, vp, i, i, i, vp]
     _lib = L
     return L
 
@@ -80,7 +94,8 @@ EXPORTS = ["moex_kv_alloc", "moex_kv_bytes", "moex_kv_free", "moex_attn_decode",
            "moex_turbo_out", "moex_set_int", "moex_set_soft_error", "moex_set_skip", "moex_fa_on",
            "moex_fa_supported", "moex_decode_splits", "moex_gqa_splits", "moex_version",
            "moex_attn_workspace_bytes", "moex_workspace_held",
-           "moex_quantize_rows_i8", "moex_gemv_i8", "moex_gemm_i8"]
+           "moex_quantize_rows_i8", "moex_gemv_i8", "moex_gemm_i8", "moex_quantize_rows_q4", "moex_quantize_rows_q6",
+           "moex_gemv", "moex_gemm"]
 
 
 def _p(x):
@@ -248,3 +263,24 @@ def gemv_i8(q, s, x, y, I, O, st=None):
 def gemm_i8(q, s, X, Y, S, I, O, st=None):
     """gemm(Mat{q, s}, X, Y, S, I, O) (kernels.cuh:339-350): S <= 8 one GEMV pass, else the fp16 MFMA GEMM."""
     lib().moex_gemm_i8(_p(q), _p(s), _p(X), _p(Y), S, I, O, _s(st))
+
+
+def quantize_rows_q4(W, q4, s, O, I, st=None):
+    """quantize_rows_q4_k (kernels.cuh:576-590): fp16 W [O][I] -> int4 gs64 q4 [O][I/2] + fp32 s [O][I/64]."""
+    lib().moex_quantize_rows_q4(_p(W), _p(q4), _p(s), O, I, _s(st))
+
+
+def quantize_rows_q6(W, q6, q6h, s, O, I, st=None):
+    """quantize_rows_q6_k (kernels.cuh:552-573): fp16 W [O][I] -> int6 gs64 planes q6 [O][I/2], q6h [O][I/4] + s."""
+    lib().moex_quantize_rows_q6(_p(W), _p(q6), _p(q6h), _p(s), O, I, _s(st))
+
+
+def gemv(m, x, y, I, O, st=None):
+    """gemv(const Mat&, x, y, I, O) (kernels.cuh:214-219) for a Mat in any form."""
+    lib().moex_gemv(ctypes.byref(m), _p(x), _p(y), I, O, _s(st))
+
+
+def gemm(m, X, Y, S, I, O, st=None):
+    """gemm(const Mat&, X, Y, S, I, O) (kernels.cuh:339-369) for a Mat in any form."""
+    lib().moex_gemm(ctypes.byref(m), _p(X), _p(Y), S, I, O, _s(st))
+

@@ -132,6 +132,56 @@ void moex_gemm_i8(const int8_t* q, const float* s, const float* X, float* Y, int
     launch_gemm_i8(q, s, X, Y, S_, I, O, S(stream));
 }
 
+void moex_quantize_rows_q4(const uint16_t* W, uint8_t* q4, float* s, int O, int I, void* stream) {
+    MOEX_REQUIRE(O > 0 && I > 0 && I % 64 == 0, "quantize_rows_q4 needs I % 64 == 0");
+    launch_quantize_rows_gs64(W, q4, nullptr, s, O, I, false, S(stream));
+}
+
+void moex_quantize_rows_q6(const uint16_t* W, uint8_t* q6, uint8_t* q6h, float* s, int O, int I, void* stream) {
+    MOEX_REQUIRE(O > 0 && I > 0 && I % 64 == 0, "quantize_rows_q6 needs I % 64 == 0");
+    launch_quantize_rows_gs64(W, q6, q6h, s, O, I, true, S(stream));
+}
+
+namespace {
+// the form a Mat is held in, tested in the reference's order (kernels.cuh:214-219): int4, int6, int8, fp16
+bool mat_ok(const moex_mat* m, int I) {
+    if (!m) return false;
+    if (m->q4) return m->s && I % 64 == 0;
+    if (m->q6) return m->q6h && m->s && I % 64 == 0;
+    if (m->q) return m->s != nullptr;
+    return m->f16 && I % 32 == 0;
+}
+}  // namespace
+
+void moex_gemv(const moex_mat* m, const float* x, float* y, int I, int O, void* stream) {
+    MOEX_REQUIRE(O > 0 && I > 0 && mat_ok(m, I), "gemv needs one form of the matrix (int4 / int6: I % 64 == 0 and "
+                                                  "scales; fp16: I % 32 == 0)");
+    if (!m->q4 && !m->q6 && m->q) {
+        moex_gemv_i8(m->q, m->s, x, y, I, O, stream);
+        return;
+    }
+    launch_gemv_mat(*m, x, y, 1, I, O, S(stream));
+}
+
+void moex_gemm(const moex_mat* m, const float* X, float* Y, int S_, int I, int O, void* stream) {
+    MOEX_REQUIRE(O > 0 && I > 0 && S_ > 0 && mat_ok(m, I), "gemm needs one form of the matrix (int4 / int6: "
+                                                            "I % 64 == 0 and scales; fp16: I % 32 == 0)");
+    if (!m->q4 && !m->q6 && m->q) {  // kernels.cuh:340-349, 366
+        moex_gemm_i8(m->q, m->s, X, Y, S_, I, O, stream);
+        return;
+    }
+    if (m->q6 && !m->q4 && S_ <= 8) {  // :350-357, 360: one GEMV pass for the rows
+        launch_gemv_mat(*m, X, Y, S_, I, O, S(stream));
+        return;
+    }
+    if (S_ <= 2) {  // :358-362: the GEMV row by row
+        launch_gemv_mat(*m, X, Y, S_, I, O, S(stream));
+        return;
+    }
+    MOEX_REQUIRE(I % 32 == 0, "gemm needs I % 32 == 0");
+    launch_gemm_mat(*m, X, Y, S_, I, O, S(stream));
+}
+
 size_t moex_attn_workspace_bytes(int H, int KV, int max_t, int T) {
     if (!(KV > 0 && H == KV * GQ && T > 0 && max_t > 0)) return 0;
     if (T <= 2)  // a one-split attn_decode step (attn_fa of T <= 2 takes the same workspace kind, never more)

@@ -133,6 +133,12 @@ float* noalloc_scratch();
 // the most workspace bytes one attn_fa call with these sizes takes on its stream
 size_t fa_workspace_bytes(int H, int KV, int max_t, int T);
 void launch_gemm_i8(const int8_t* q, const float* s, const float* X, float* Y, int S, int I, int O, hipStream_t st);
+// the other weight forms (dense.hip): int4 / int6 gs64 quantizers, the GEMV (NT rows, int6 in one pass, the others a
+// launch per row) and the fp16 MFMA GEMM
+void launch_quantize_rows_gs64(const uint16_t* W, uint8_t* q, uint8_t* qh, float* s, int O, int I, bool six,
+                               hipStream_t st);
+void launch_gemv_mat(const moex_mat& m, const float* x, float* y, int NT, int I, int O, hipStream_t st);
+void launch_gemm_mat(const moex_mat& m, const float* X, float* Y, int S, int I, int O, hipStream_t st);
 void launch_prefill_k7p(const float* qo, const float* q_gate, moex_kv_cache kv, float* out, int H, int KV,
                         const int* pos_d, int max_t, int ld, int T, hipStream_t st);
 }  // namespace moex

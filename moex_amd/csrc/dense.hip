@@ -1,5 +1,7 @@
-// Dense int8 projections on gfx950: the attention's qkv and o projections in their default form, int8 weights with a
-// per-row scale (replaces quantize_rows_i8_k, gemv_i8 and gemm_i8_k / gemm(), kernels.cuh:98-156,250-337).
+// Dense projections on gfx950: the attention's qkv and o projections in their default form, int8 weights with a
+// per-row scale (replaces quantize_rows_i8_k, gemv_i8 and gemm_i8_k / gemm(), kernels.cuh:98-156,250-337), and the
+// reference's other matrix forms, int4 / int6 with a scale per 64 inputs and fp16 (quantize_rows_q4_k / _q6_k,
+// gemv_q4_k / gemv_q6_k / gemv_f16_k, gemm_wmma_k, gemm_i8_k<true>: kernels.cuh:68-93,225-337,486-590).
 //
 //   quantize_rows_kernel   fp16 [O][I] -> int8 [O][I] + scale absmax/127 per row (bit-exact: IEEE divide, rint).
 //   gemv_kernel<NT>        y[t][o] = s[o] * sum_i q[o][i] x[t][i] for NT <= 8 rows of x, fp32 sums. HBM-bound on the
@@ -17,6 +19,11 @@
 //                          are read into one L2).
 //   gemm_ws_kernel         The same product and sum order with split roles: 4 wavefronts widen the next K step into
 //                          LDS while 4 run the MFMAs of this one. Used when the grid fits the chip in one pass.
+//   quantize_gs64_kernel   fp16 rows -> int4 / int6 codes + a scale per 64-input group (bit-exact).
+//   gemv_mat_kernel        the GEMV of the int4 / int6 / fp16 forms: a lane per 32-weight unit of R rows, each unit
+//                          summed in order and scaled, wavefront and part sums as gemv_kernel.
+//   gemm_kernel<form>      the same tiled MFMA GEMM for every form: the staging widens int4 / int6 weights times
+//                          their group scale to fp16 (or copies fp16 weights) where int8 is widened exactly.
 #include <algorithm>
 #include "common.hpp"
 
@@ -226,9 +233,70 @@ __global__ void __launch_bounds__(64 * GV_WAVES) gemv1_kernel(const int8_t* __re
 constexpr int GM_BM = 128, GM_BN = 128, GM_BK = 32;
 constexpr int GM_LD = GM_BK + 8;  // halves per LDS row (80 B: conflict-free 16-byte operand reads)
 
-__global__ void __launch_bounds__(256, 3) gemm_kernel(const int8_t* __restrict__ W, const float* __restrict__ s,
-                                                   const _Float16* __restrict__ X, float* __restrict__ Y, int S, int I,
-                                                   int O) {
+// The weight forms of a dense matrix (struct Mat, kernels.cuh:186-196): int8 with a row scale, int4 and int6 with a
+// scale per 64 inputs (gs64), fp16.
+enum { MF_I8 = 0, MF_Q4 = 1, MF_Q6 = 2, MF_F16 = 3 };
+
+// A product rounded to fp32 before anything else rounds it: without the barrier the compiler may fuse a multiply
+// with its fp16 conversion (v_fma_mix*), one rounding instead of the reference's two.
+__device__ __forceinline__ float r32(float x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+// 16 weights of one row at k .. k + 15 (k % 16 == 0) -> 8 dwords of fp16 pairs, as the reference's GEMMs widen them:
+// int8 exactly (row scale applied after the sums); int4 / int6 times the group scale in fp32, then rounded to fp16
+// (kernels.cuh:276-279, 313-317: __float2half / __floats2half2_rn of (float)v * s); fp16 as stored.
+struct WStage {
+    uint4 a;      // int8: 16 codes; int4 / int6: .x, .y the 16 low nibbles; fp16: halves 0-7
+    uint4 b;      // fp16: halves 8-15
+    uint32_t h;   // int6: the 16 high 2-bit fields
+    float sc;     // int4 / int6: the group scale
+};
+template <int FMT>
+__device__ __forceinline__ void wstage_load(WStage& w, const void* W, const uint8_t* Wh, const float* s, size_t row,
+                                            int I, int k) {
+    if constexpr (FMT == MF_I8) {
+        w.a = *reinterpret_cast<const uint4*>(reinterpret_cast<const int8_t*>(W) + row * I + k);
+    } else if constexpr (FMT == MF_F16) {
+        const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(W) + row * I + k);
+        w.a = p[0];
+        w.b = p[1];
+    } else {
+        const uint2 lo = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(W) + row * (I / 2) + k / 2);
+        w.a = make_uint4(lo.x, lo.y, 0u, 0u);
+        if constexpr (FMT == MF_Q6) w.h = *reinterpret_cast<const uint32_t*>(Wh + row * (I / 4) + k / 4);
+        w.sc = s[row * (I / 64) + k / 64];
+    }
+}
+template <int FMT>
+__device__ __forceinline__ void wstage_widen(const WStage& w, bool ok, uint32_t (&h)[8]) {
+    if constexpr (FMT == MF_I8) {
+        i8x4_to_h4(ok ? w.a.x : 0u, h[0], h[1]);
+        i8x4_to_h4(ok ? w.a.y : 0u, h[2], h[3]);
+        i8x4_to_h4(ok ? w.a.z : 0u, h[4], h[5]);
+        i8x4_to_h4(ok ? w.a.w : 0u, h[6], h[7]);
+    } else if constexpr (FMT == MF_F16) {
+        h[0] = ok ? w.a.x : 0u; h[1] = ok ? w.a.y : 0u; h[2] = ok ? w.a.z : 0u; h[3] = ok ? w.a.w : 0u;
+        h[4] = ok ? w.b.x : 0u; h[5] = ok ? w.b.y : 0u; h[6] = ok ? w.b.z : 0u; h[7] = ok ? w.b.w : 0u;
+    } else {
+        float v[16];
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const uint32_t nib = ((e < 8 ? w.a.x : w.a.y) >> (4 * (e & 7))) & 15u;
+            int q;
+            if constexpr (FMT == MF_Q4) q = (int)nib - (int)((nib & 8u) << 1);       // two's complement nibble
+            else q = (int)(nib | (((w.h >> (2 * e)) & 3u) << 4)) - 32;               // 6-bit code, offset 32
+            v[e] = r32((float)q * w.sc);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) h[i] = ok ? h22u(half2_t{(_Float16)v[2 * i], (_Float16)v[2 * i + 1]}) : 0u;
+    }
+}
+
+template <int FMT>
+__global__ void __launch_bounds__(256, 3) gemm_kernel(const void* __restrict__ W, const uint8_t* __restrict__ Wh,
+                                                   const float* __restrict__ s, const _Float16* __restrict__ X,
+                                                   float* __restrict__ Y, int S, int I, int O) {
     __shared__ __align__(16) _Float16 lds[2][2][GM_BM * GM_LD];  // [buffer][W, X][row][k]
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r = lane & 31, h32 = lane >> 5;
     // XCD-aware order (block b runs on XCD b % 8): with the token tiles a multiple of 8, XCD x takes token tiles
@@ -248,21 +316,18 @@ __global__ void __launch_bounds__(256, 3) gemm_kernel(const int8_t* __restrict__
     // staging: thread tid owns 16 weights (row tid/2, k 16*(tid%2)) and 16 activations (token tid/2, same k)
     const int sr = tid >> 1, sk = (tid & 1) * 16;
     const bool wok = o0 + sr < O, xok = s0 + sr < S;
-    const int8_t* wp = W + (size_t)min(o0 + sr, O - 1) * I + sk;
+    const size_t wrow = (size_t)min(o0 + sr, O - 1);
     const _Float16* xp = X + (size_t)min(s0 + sr, S - 1) * I + sk;
-    uint4 wreg;
+    WStage wreg;
     uint4 xreg[2];
     auto load = [&](int k0) {
-        wreg = *reinterpret_cast<const uint4*>(wp + k0);
+        wstage_load<FMT>(wreg, W, Wh, s, wrow, I, k0 + sk);
 #pragma unroll
         for (int j = 0; j < 2; j++) xreg[j] = reinterpret_cast<const uint4*>(xp + k0)[j];
     };
     auto store = [&](int b) {
         uint32_t h[8];
-        i8x4_to_h4(wok ? wreg.x : 0u, h[0], h[1]);
-        i8x4_to_h4(wok ? wreg.y : 0u, h[2], h[3]);
-        i8x4_to_h4(wok ? wreg.z : 0u, h[4], h[5]);
-        i8x4_to_h4(wok ? wreg.w : 0u, h[6], h[7]);
+        wstage_widen<FMT>(wreg, wok, h);
         uint4* wd = reinterpret_cast<uint4*>(&lds[b][0][sr * GM_LD + sk]);
         wd[0] = make_uint4(h[0], h[1], h[2], h[3]);
         wd[1] = make_uint4(h[4], h[5], h[6], h[7]);
@@ -310,13 +375,13 @@ __global__ void __launch_bounds__(256, 3) gemm_kernel(const int8_t* __restrict__
     for (int i = 0; i < 2; i++) {
         const int o = o0 + wo + 32 * i + r;
         if (o >= O) continue;
-        const float so = s[o];
+        const float so = FMT == MF_I8 ? s[o] : 1.f;  // the group scales are in the widened weights
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const int t = s0 + ws + 32 * j + 8 * (e >> 2) + 4 * h32 + (e & 3);
-                if (t < S) Y[(size_t)t * O + o] = acc[i][j][e] * so;
+                if (t < S) Y[(size_t)t * O + o] = FMT == MF_I8 ? acc[i][j][e] * so : acc[i][j][e];
             }
     }
 }
@@ -484,6 +549,187 @@ void launch_gemv_t(const int8_t* q, const float* s, const float* x, float* y, in
     MOEX_LAUNCHED();
 }
 
+// ---- int4 / int6 gs64 quantizers (quantize_rows_q4_k, quantize_rows_q6_k: kernels.cuh:552-590) ----
+// A workgroup per row; each wavefront takes 64-weight groups g = w, w + 4, .., a lane per weight. Scale = group absmax
+// / 7 (int4) or / 31 (int6), 1 for an all-zero group; codes round-half-even(w / scale) clamped to [-8, 7] /
+// [-32, 31] (int6 stored + 32). Packing: weight i's nibble at bits 4 (i % 2) of byte i / 2 of the row's low plane
+// (low nibble first); int6 adds its high 2 bits at bits 2 (i % 4) of byte i / 4 of the high plane. The lanes OR their
+// fields together across 8 (nibbles) or 16 (2-bit fields) lanes and one lane writes the dword.
+template <bool SIX>
+__global__ void __launch_bounds__(256) quantize_gs64_kernel(const uint16_t* __restrict__ W, uint8_t* __restrict__ q,
+                                                            uint8_t* __restrict__ qh, float* __restrict__ s, int I) {
+    const size_t row = blockIdx.x;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, G = I / 64;
+    const _Float16* wr = reinterpret_cast<const _Float16*>(W) + row * I;
+    for (int g = wv; g < G; g += 4) {
+        const float w = (float)wr[g * 64 + lane];
+        float m = fabsf(w);
+#pragma unroll
+        for (int o = 32; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const float sc = m > 0.f ? m / (SIX ? 31.f : 7.f) : 1.f;
+        uint32_t lo, hi = 0;
+        if (SIX) {
+            const uint32_t u = (uint32_t)((int)fminf(31.f, fmaxf(-32.f, __builtin_rintf(w / sc))) + 32);
+            lo = (u & 15u) << (4 * (lane & 7));
+            hi = (u >> 4) << (2 * (lane & 15));
+        } else {
+            const int v = max(-8, min(7, (int)__builtin_rintf(w / sc)));
+            lo = ((uint32_t)v & 15u) << (4 * (lane & 7));
+        }
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) lo |= __shfl_xor(lo, o);
+        if ((lane & 7) == 0) reinterpret_cast<uint32_t*>(q + row * (I / 2) + g * 32)[lane >> 3] = lo;
+        if (SIX) {
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) hi |= __shfl_xor(hi, o);
+            if ((lane & 15) == 0) reinterpret_cast<uint32_t*>(qh + row * (I / 4) + g * 16)[lane >> 4] = hi;
+        }
+        if (lane == 0) s[row * G + g] = sc;
+    }
+}
+
+// ---- GEMV of the int4 / int6 / fp16 forms (gemv_q4_k, gemv_q6_k, gemv_f16_k: kernels.cuh:68-93,486-550) ----
+// y[t][o] = sum over the row's 32-weight units c of (sum_k w[o][32c + k] x[t][32c + k]) * scale[o][c / 2] (fp16: no
+// scale), fp32 sums. Layout as gemv_kernel: a wavefront takes R rows over the KS-th part of the row's units, a lane
+// per unit (16 B of int4, 16 + 8 B of int6, 64 B of fp16 a row), reads its 32 inputs per row of x from L2, sums the
+// unit in k order, and the KS parts of a row are added in LDS in part order. KS and R depend on O, I and the form
+// only, so every row of a multi-row call is bit-identical to the same row alone.
+template <int FMT>
+struct MatUnit {
+    uint4 a[FMT == MF_F16 ? 4 : 1];
+    uint2 h;  // int6 high fields
+    float sc;
+};
+template <int FMT>
+__device__ __forceinline__ void mat_unit_load(MatUnit<FMT>& u, const uint8_t* W, const uint8_t* Wh, const float* s,
+                                              size_t row, int I, int c) {
+    if constexpr (FMT == MF_F16) {
+        const u32x4* p = reinterpret_cast<const u32x4*>(W + (row * I + 32 * (size_t)c) * 2);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const u32x4 v = __builtin_nontemporal_load(p + i);
+            u.a[i] = make_uint4(v[0], v[1], v[2], v[3]);
+        }
+    } else {
+        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(W + row * (I / 2)) + c);
+        u.a[0] = make_uint4(v[0], v[1], v[2], v[3]);
+        if constexpr (FMT == MF_Q6) u.h = reinterpret_cast<const uint2*>(Wh + row * (I / 4))[c];
+        u.sc = s[row * (I / 64) + c / 2];
+    }
+}
+template <int FMT>
+__device__ __forceinline__ float mat_unit_dot(const MatUnit<FMT>& u, const float4 (&x)[8]) {
+    float d = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const float xv[4] = {x[j].x, x[j].y, x[j].z, x[j].w};
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            const int k = 4 * j + n;
+            float w;
+            if constexpr (FMT == MF_F16) {
+                const uint4& q = u.a[k / 8];
+                const uint32_t d2 = ((k / 2) & 3) == 0 ? q.x : ((k / 2) & 3) == 1 ? q.y : ((k / 2) & 3) == 2 ? q.z : q.w;
+                w = (float)u2h2(d2)[k & 1];
+            } else {
+                const uint32_t dw = k < 8 ? u.a[0].x : k < 16 ? u.a[0].y : k < 24 ? u.a[0].z : u.a[0].w;
+                if constexpr (FMT == MF_Q4) {
+                    w = (float)(int)__builtin_amdgcn_sbfe(dw, 4 * (k & 7), 4);  // the signed nibble (the builtin returns it as unsigned)
+                } else {
+                    const uint32_t hb = ((k < 16 ? u.h.x : u.h.y) >> (2 * (k & 15))) & 3u;
+                    w = (float)((int)(((dw >> (4 * (k & 7))) & 15u) | (hb << 4)) - 32);
+                }
+            }
+            d = fmaf(w, xv[n], d);
+        }
+    }
+    return FMT == MF_F16 ? d : d * u.sc;
+}
+constexpr int GM_WAVES = 8;
+template <int FMT, int NT, int R>
+__global__ void __launch_bounds__(64 * GM_WAVES) gemv_mat_kernel(const uint8_t* __restrict__ W,
+                                                                 const uint8_t* __restrict__ Wh,
+                                                                 const float* __restrict__ s,
+                                                                 const float* __restrict__ x, float* __restrict__ y,
+                                                                 int I, int O, int KS) {
+    __shared__ float red[GM_WAVES][NT][R];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nb = gridDim.x;
+    const int U = I / 32, ngroups = (O + R - 1) / R, gpr = GM_WAVES / KS;
+    const int rounds = (ngroups + nb * gpr - 1) / (nb * gpr);
+    const int part = wv % KS, slice = U / KS, cb = part * slice, ce = cb + slice;
+    for (int j = 0; j < rounds; j++) {
+        const int g = blockIdx.x + nb * (wv / KS + j * gpr);
+        if (g < ngroups) {
+            float acc[NT][R];
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+#pragma unroll
+                for (int r = 0; r < R; r++) acc[t][r] = 0.f;
+            for (int c = cb + lane; c < ce; c += 64) {
+                MatUnit<FMT> u[R];
+#pragma unroll
+                for (int r = 0; r < R; r++) mat_unit_load<FMT>(u[r], W, Wh, s, (size_t)min(g * R + r, O - 1), I, c);
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    float4 xv[8];
+                    const float4* xp = reinterpret_cast<const float4*>(x + (size_t)t * I + 32 * (size_t)c);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) xv[i] = xp[i];
+#pragma unroll
+                    for (int r = 0; r < R; r++) acc[t][r] += mat_unit_dot<FMT>(u[r], xv);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const float v = wave_sum(acc[t][r]);
+                    if (lane == 0) red[wv][t][r] = v;
+                }
+        }
+        __syncthreads();
+        if (g < ngroups && part == 0 && lane < NT * R) {
+            const int t = lane / R, r = lane % R, o = g * R + r;
+            float v = red[wv][t][r];
+            for (int p = 1; p < KS; p++) v += red[wv + p][t][r];
+            if (o < O) y[(size_t)t * O + o] = v;
+        }
+        __syncthreads();  // the partial sums are read before the next round writes them
+    }
+}
+
+int dense_cus() {
+    static const int cus = [] {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            return v;
+        return 256;
+    }();
+    return cus;
+}
+
+template <int FMT, int NT>
+void launch_gemv_mat_t(const uint8_t* W, const uint8_t* Wh, const float* s, const float* x, float* y, int I, int O,
+                       hipStream_t st) {
+    // parts of at least one unit a lane, split while the wavefronts do not yet fill the chip's 8 slots per CU; then
+    // rows per wavefront: 4, fewer while the grid would leave CUs without a workgroup
+    const int U = I / 32, cus = dense_cus();
+    int ks = 1;
+    while (ks < GM_WAVES && (O + 3) / 4 * ks < GM_WAVES * cus && U % (2 * ks) == 0 && U / (2 * ks) >= 64) ks *= 2;
+    const int gpr = GM_WAVES / ks;
+    int R = 4;
+    while (R > 1 && ((O + R - 1) / R + gpr - 1) / gpr < cus) R /= 2;
+    const int nb = std::min(cus, ((O + R - 1) / R + gpr - 1) / gpr);
+    if (R == 4)
+        hipLaunchKernelGGL((gemv_mat_kernel<FMT, NT, 4>), dim3(nb), dim3(64 * GM_WAVES), 0, st, W, Wh, s, x, y, I, O, ks);
+    else if (R == 2)
+        hipLaunchKernelGGL((gemv_mat_kernel<FMT, NT, 2>), dim3(nb), dim3(64 * GM_WAVES), 0, st, W, Wh, s, x, y, I, O, ks);
+    else
+        hipLaunchKernelGGL((gemv_mat_kernel<FMT, NT, 1>), dim3(nb), dim3(64 * GM_WAVES), 0, st, W, Wh, s, x, y, I, O, ks);
+    MOEX_LAUNCHED();
+}
+
 }  // namespace
 
 void launch_quantize_rows_i8(const uint16_t* W, int8_t* q, float* s, int O, int I, hipStream_t st) {
@@ -533,7 +779,53 @@ void launch_gemm_i8(const int8_t* q, const float* s, const float* X, float* Y, i
             hipLaunchKernelGGL(gemm_reduce_kernel, dim3(1024), dim3(256), 0, st, part, s, Y, S, O, nks);
         }
     } else
-        hipLaunchKernelGGL(gemm_kernel, dim3(blocks), dim3(256), 0, st, q, s, Xh, Y, S, I, O);
+        hipLaunchKernelGGL(gemm_kernel<MF_I8>, dim3(blocks), dim3(256), 0, st, q, nullptr, s, Xh, Y, S, I, O);
+    MOEX_LAUNCHED();
+}
+
+void launch_quantize_rows_gs64(const uint16_t* W, uint8_t* q, uint8_t* qh, float* s, int O, int I, bool six,
+                               hipStream_t st) {
+    if (six) hipLaunchKernelGGL(quantize_gs64_kernel<true>, dim3(O), dim3(256), 0, st, W, q, qh, s, I);
+    else hipLaunchKernelGGL(quantize_gs64_kernel<false>, dim3(O), dim3(256), 0, st, W, q, qh, s, I);
+    MOEX_LAUNCHED();
+}
+
+void launch_gemv_mat(const moex_mat& m, const float* x, float* y, int NT, int I, int O, hipStream_t st) {
+    if (m.q4) {
+        for (int t = 0; t < NT; t++)
+            launch_gemv_mat_t<MF_Q4, 1>(m.q4, nullptr, m.s, x + (size_t)t * I, y + (size_t)t * O, I, O, st);
+    } else if (m.q6) {
+        switch (NT) {
+            case 1: launch_gemv_mat_t<MF_Q6, 1>(m.q6, m.q6h, m.s, x, y, I, O, st); break;
+            case 2: launch_gemv_mat_t<MF_Q6, 2>(m.q6, m.q6h, m.s, x, y, I, O, st); break;
+            case 3: launch_gemv_mat_t<MF_Q6, 3>(m.q6, m.q6h, m.s, x, y, I, O, st); break;
+            case 4: launch_gemv_mat_t<MF_Q6, 4>(m.q6, m.q6h, m.s, x, y, I, O, st); break;
+            case 5: launch_gemv_mat_t<MF_Q6, 5>(m.q6, m.q6h, m.s, x, y, I, O, st); break;
+            case 6: launch_gemv_mat_t<MF_Q6, 6>(m.q6, m.q6h, m.s, x, y, I, O, st); break;
+            case 7: launch_gemv_mat_t<MF_Q6, 7>(m.q6, m.q6h, m.s, x, y, I, O, st); break;
+            default: launch_gemv_mat_t<MF_Q6, 8>(m.q6, m.q6h, m.s, x, y, I, O, st); break;
+        }
+    } else {
+        const uint8_t* W = reinterpret_cast<const uint8_t*>(m.f16);
+        for (int t = 0; t < NT; t++)
+            launch_gemv_mat_t<MF_F16, 1>(W, nullptr, nullptr, x + (size_t)t * I, y + (size_t)t * O, I, O, st);
+    }
+}
+
+void launch_gemm_mat(const moex_mat& m, const float* X, float* Y, int S, int I, int O, hipStream_t st) {
+    const size_t n4 = (size_t)S * I / 4;  // I % 32 == 0
+    _Float16* Xh = reinterpret_cast<_Float16*>(stream_workspace(n4 * 8, st, 2));
+    if (!Xh) {
+        report(hipErrorOutOfMemory, __FILE__, __LINE__);
+        return;
+    }
+    hipLaunchKernelGGL(round_f16_kernel, dim3((unsigned)std::min<size_t>((n4 + 255) / 256, 4096)), dim3(256), 0, st,
+                       reinterpret_cast<const float4*>(X), reinterpret_cast<uint2*>(Xh), n4);
+    MOEX_LAUNCHED();
+    const dim3 grid(((O + GM_BM - 1) / GM_BM) * ((S + GM_BN - 1) / GM_BN));
+    if (m.q4) hipLaunchKernelGGL(gemm_kernel<MF_Q4>, grid, dim3(256), 0, st, m.q4, nullptr, m.s, Xh, Y, S, I, O);
+    else if (m.q6) hipLaunchKernelGGL(gemm_kernel<MF_Q6>, grid, dim3(256), 0, st, m.q6, m.q6h, m.s, Xh, Y, S, I, O);
+    else hipLaunchKernelGGL(gemm_kernel<MF_F16>, grid, dim3(256), 0, st, m.f16, nullptr, nullptr, Xh, Y, S, I, O);
     MOEX_LAUNCHED();
 }
 

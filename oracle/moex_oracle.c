@@ -31,6 +31,13 @@
  *                          numpy's float64 matmul in tests/test_oracle.py.
  *   orc_dense_i8_fp16x     not a parity target: the precision model of the prefill GEMM (activations rounded to
  *                          fp16, kernels.cuh:250,306-307), used to bound the reference kernel's error.
+ *   orc_quantize_rows_q4/q6  pinned: closed form (group absmax, IEEE divide, round-half-even, clamp, packing),
+ *                          checked in tests/test_oracle.py on constructed ties and known packed bytes, and against
+ *                          numpy's rint on random rows.
+ *   orc_dense_mat_f64      pinned: the exact product of the dequantized weights (q * scale, fp16 as stored) in fp64,
+ *                          checked against numpy's float64 matmul of independently unpacked weights.
+ *   orc_dense_mat_fp16x    not a parity target: the precision model of the int4 / int6 / fp16 GEMMs (weights
+ *                          fp16(fp32(q * scale)), activations fp16, kernels.cuh:276-279,306-307,313-317).
  */
 #include <math.h>
 #include <stdint.h>
@@ -431,5 +438,87 @@ void orc_dense_i8_fp16x(const int8_t* q, const float* s, const float* x, long S,
             double a = 0;
             for (long i = 0; i < I; i++) a += (double)q[o * I + i] * orc_round_f16(x[t * I + i]);
             y[t * O + o] = a * s[o];
+        }
+}
+
+/* ---- the other dense forms (struct Mat, kernels.cuh:186-196): int4 gs64, int6 gs64, fp16 ---- */
+
+/* quantize_rows_q4_k (kernels.cuh:576-590): per 64-input group scale = absmax / 7 (1 for a zero group),
+ * q = clamp(round-half-even(w / scale), -8, 7); weight i in bits 4 (i % 2) of byte i / 2 (low nibble first). */
+void orc_quantize_rows_q4(const uint16_t* W, long O, long I, uint8_t* q, float* s) {
+    memset(q, 0, (size_t)O * (I / 2));
+    for (long o = 0; o < O; o++)
+        for (long g = 0; g < I / 64; g++) {
+            const uint16_t* w = W + o * I + g * 64;
+            float m = 0.f;
+            for (int i = 0; i < 64; i++) { const float a = fabsf(h2f(w[i])); if (a > m) m = a; }
+            const float sc = m > 0.f ? m / 7.f : 1.f;
+            for (int i = 0; i < 64; i++) {
+                int v = (int)rintf(h2f(w[i]) / sc);
+                v = v < -8 ? -8 : v > 7 ? 7 : v;
+                q[o * (I / 2) + (g * 64 + i) / 2] |= (uint8_t)((v & 15) << (4 * (i & 1)));
+            }
+            s[o * (I / 64) + g] = sc;
+        }
+}
+
+/* quantize_rows_q6_k (kernels.cuh:552-573): scale = group absmax / 31 (1 for a zero group), u = clamp(round-half-
+ * even(w / scale), -32, 31) + 32; the low 4 bits in q as q4's nibbles, the high 2 bits at bits 2 (i % 4) of byte
+ * i / 4 of qh. */
+void orc_quantize_rows_q6(const uint16_t* W, long O, long I, uint8_t* q, uint8_t* qh, float* s) {
+    memset(q, 0, (size_t)O * (I / 2));
+    memset(qh, 0, (size_t)O * (I / 4));
+    for (long o = 0; o < O; o++)
+        for (long g = 0; g < I / 64; g++) {
+            const uint16_t* w = W + o * I + g * 64;
+            float m = 0.f;
+            for (int i = 0; i < 64; i++) { const float a = fabsf(h2f(w[i])); if (a > m) m = a; }
+            const float sc = m > 0.f ? m / 31.f : 1.f;
+            for (int i = 0; i < 64; i++) {
+                const int u = (int)fminf(31.f, fmaxf(-32.f, rintf(h2f(w[i]) / sc))) + 32;
+                const long k = g * 64 + i;
+                q[o * (I / 2) + k / 2] |= (uint8_t)((u & 15) << (4 * (i & 1)));
+                qh[o * (I / 4) + k / 4] |= (uint8_t)((u >> 4) << (2 * (i & 3)));
+            }
+            s[o * (I / 64) + g] = sc;
+        }
+}
+
+/* weight i of row o of a matrix in form fmt (1: int4 gs64, 2: int6 gs64, 3: fp16) as its integer code times the
+ * group scale (the exact value, fp64) */
+static double mat_w(int fmt, const void* w, const uint8_t* wh, const float* s, long I, long o, long i) {
+    if (fmt == 3) return h2f(((const uint16_t*)w)[o * I + i]);
+    const uint8_t b = ((const uint8_t*)w)[o * (I / 2) + i / 2];
+    const int nib = (b >> (4 * (i & 1))) & 15;
+    int v;
+    if (fmt == 1) v = nib >= 8 ? nib - 16 : nib;
+    else v = (nib | (((wh[o * (I / 4) + i / 4] >> (2 * (i & 3))) & 3) << 4)) - 32;
+    return (double)v * (double)s[o * (I / 64) + i / 64];
+}
+
+/* y[t][o] = sum_i w[o][i] * x[t][i] with the exact weights, fp64 (tests/test_kernels.cu:415-423: the reference's
+ * "exact int4 math" of gemv_q4). */
+void orc_dense_mat_f64(int fmt, const void* w, const uint8_t* wh, const float* s, const float* x, long S, long I,
+                       long O, double* y) {
+    for (long t = 0; t < S; t++)
+        for (long o = 0; o < O; o++) {
+            double a = 0;
+            for (long i = 0; i < I; i++) a += mat_w(fmt, w, wh, s, I, o, i) * x[t * I + i];
+            y[t * O + o] = a;
+        }
+}
+
+/* The GEMMs' rounding points: an int4 / int6 weight is q * scale in fp32, then fp16 (kernels.cuh:276-279,
+ * 313-317); fp16 weights as stored; activations rounded to fp16 (:306-307); exact sums in fp64. */
+void orc_dense_mat_fp16x(int fmt, const void* w, const uint8_t* wh, const float* s, const float* x, long S, long I,
+                         long O, double* y) {
+    for (long t = 0; t < S; t++)
+        for (long o = 0; o < O; o++) {
+            double a = 0;
+            for (long i = 0; i < I; i++) {
+                const float wf = fmt == 3 ? (float)mat_w(fmt, w, wh, s, I, o, i) : orc_round_f16((float)mat_w(fmt, w, wh, s, I, o, i));
+                a += (double)wf * orc_round_f16(x[t * I + i]);
+            }
+            y[t * O + o] = a;
         }
 }

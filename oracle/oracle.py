@@ -54,6 +54,11 @@ def lib():
         L.orc_quantize_rows_i8.argtypes = [_u16p, c.c_long, c.c_long, _i8p, _f32p]
         L.orc_dense_i8_f64.argtypes = [_i8p, _f32p, _f32p, c.c_long, c.c_long, c.c_long, _f64p]
         L.orc_dense_i8_fp16x.argtypes = [_i8p, _f32p, _f32p, c.c_long, c.c_long, c.c_long, _f64p]
+        L.orc_quantize_rows_q4.argtypes = [_u16p, c.c_long, c.c_long, _u8p, _f32p]
+        L.orc_quantize_rows_q6.argtypes = [_u16p, c.c_long, c.c_long, _u8p, _u8p, _f32p]
+        mat_args = [c.c_int, c.c_void_p, c.c_void_p, _f32p, _f32p, c.c_long, c.c_long, c.c_long, _f64p]
+        L.orc_dense_mat_f64.argtypes = mat_args
+        L.orc_dense_mat_fp16x.argtypes = mat_args
         _lib = L
     return _lib
 
@@ -187,3 +192,50 @@ def dense_i8_fp16x(q, s, x):
     y = np.zeros((S, O), np.float64)
     lib().orc_dense_i8_fp16x(q.reshape(-1), s, x.reshape(-1), S, I, O, y.reshape(-1))
     return y
+
+
+# ---- the other dense forms (struct Mat, kernels.cuh:186-196) ----
+MAT_Q4, MAT_Q6, MAT_F16 = 1, 2, 3
+
+
+def quantize_rows_q4(w16):
+    """quantize_rows_q4_k (kernels.cuh:576-590): fp16 [O][I] -> (uint8 [O][I/2] nibbles, float32 [O][I/64] scales)."""
+    w16 = np.ascontiguousarray(w16, np.float16)
+    O, I = w16.shape
+    q = np.zeros((O, I // 2), np.uint8); s = np.zeros((O, I // 64), np.float32)
+    lib().orc_quantize_rows_q4(w16.view(np.uint16).reshape(-1), O, I, q.reshape(-1), s.reshape(-1))
+    return q, s
+
+
+def quantize_rows_q6(w16):
+    """quantize_rows_q6_k (kernels.cuh:552-573): fp16 [O][I] -> (low plane [O][I/2], high plane [O][I/4], scales)."""
+    w16 = np.ascontiguousarray(w16, np.float16)
+    O, I = w16.shape
+    q = np.zeros((O, I // 2), np.uint8); qh = np.zeros((O, I // 4), np.uint8); s = np.zeros((O, I // 64), np.float32)
+    lib().orc_quantize_rows_q6(w16.view(np.uint16).reshape(-1), O, I, q.reshape(-1), qh.reshape(-1), s.reshape(-1))
+    return q, qh, s
+
+
+def _mat_call(fn, fmt, w, wh, s, x):
+    x = np.ascontiguousarray(x, np.float32)
+    S, I = x.shape
+    w = np.ascontiguousarray(w)
+    O = w.shape[0]
+    if fmt == MAT_F16:
+        w = w.view(np.uint16)
+        s = np.zeros(1, np.float32)
+    s = np.ascontiguousarray(s, np.float32).reshape(-1)
+    wh = None if wh is None else np.ascontiguousarray(wh, np.uint8)
+    y = np.zeros((S, O), np.float64)
+    fn(fmt, w.ctypes.data, None if wh is None else wh.ctypes.data, s, x.reshape(-1), S, I, O, y.reshape(-1))
+    return y
+
+
+def dense_mat_f64(fmt, w, wh, s, x):
+    """y [S][O] = W . x with the exact weights (code * group scale, or fp16), fp64 sums."""
+    return _mat_call(lib().orc_dense_mat_f64, fmt, w, wh, s, x)
+
+
+def dense_mat_fp16x(fmt, w, wh, s, x):
+    """The int4 / int6 / fp16 GEMMs' precision model: weights fp16(fp32(code * scale)), activations fp16."""
+    return _mat_call(lib().orc_dense_mat_fp16x, fmt, w, wh, s, x)

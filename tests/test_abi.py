@@ -49,7 +49,8 @@ def test_kv_bytes_formula():
 def test_python_mirror_keeps_reference_names():
     import moex_amd
     for n in ("attn_decode", "attn_fa", "attn_prefill", "kv_alloc", "kv_bytes", "attn_gqa", "attn_combine",
-              "attn_decode_heads", "turbo_out", "qk_norm_rope", "kv_append", "set_int"):
+              "attn_decode_heads", "turbo_out", "qk_norm_rope", "kv_append", "set_int", "gemv", "gemm",
+              "quantize_rows_q4", "quantize_rows_q6"):
         assert callable(getattr(moex_amd, n))
 
 

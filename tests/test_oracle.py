@@ -383,3 +383,110 @@ def test_fa_precision_model_rounding_points(orc):
     tol = 1e-6 * np.abs(want).max()
     assert np.abs(got - want).max() <= tol
     assert np.abs(got - loose).max() > 20 * tol
+
+
+# ---- the other dense forms (kernels.cuh:186-196 Mat; :552-590 quantize_rows_q6_k / q4_k; :486-550 the GEMVs) ----
+def _unpack_q4(q, I):
+    """numpy: two's complement nibbles, weight 2j in the low nibble of byte j"""
+    lo = (q & 15).astype(np.int16); hi = (q >> 4).astype(np.int16)
+    v = np.stack([lo, hi], -1).reshape(q.shape[0], I)
+    return np.where(v >= 8, v - 16, v)
+
+
+def _unpack_q6(q, qh, I):
+    lo = np.stack([q & 15, q >> 4], -1).reshape(q.shape[0], I).astype(np.int16)
+    hi = np.stack([(qh >> (2 * k)) & 3 for k in range(4)], -1).reshape(q.shape[0], I).astype(np.int16)
+    return (lo | (hi << 4)) - 32
+
+
+def test_quantize_q4_known_bytes_and_ties(orc):
+    """A group whose scale is exactly 1 (absmax 7): codes are the weights themselves, .5 quotients round to even,
+    and the packed bytes are known by hand (low nibble first, two's complement)."""
+    w = np.zeros((1, 128), np.float16)
+    w[0, :8] = [7, -7, 1, 2, 0.5, 1.5, -2.5, -0.5]
+    q, s = orc.quantize_rows_q4(w)
+    assert s[0, 0] == 1.0 and s[0, 1] == 1.0                      # the second group is all zero: scale 1
+    assert list(q[0, :4]) == [0x97, 0x21, 0x20, 0x0E]             # (7, -7), (1, 2), (0, 2), (-2, 0)
+    assert np.all(q[0, 4:] == 0)
+
+
+def test_quantize_q6_known_bytes_and_ties(orc):
+    """Scale exactly 1 (absmax 31): u = round-half-even(w) + 32, so -30.5 -> u = 2; low nibbles as q4's, high 2-bit
+    fields at bits 2 (i % 4) of byte i / 4; the zero weights of the group are u = 32 (high field 2)."""
+    w = np.zeros((1, 64), np.float16)
+    w[0, :6] = [31, -31, 1.5, -2.5, 16, -30.5]                     # u = 63, 1, 34, 30, 48, 2
+    q, qh, s = orc.quantize_rows_q6(w)
+    assert s[0, 0] == 1.0
+    assert list(q[0, :4]) == [0x1F, 0xE2, 0x20, 0x00]
+    assert list(qh[0, :3]) == [0x63, 0xA3, 0xAA]
+
+
+@pytest.mark.parametrize("six", [False, True])
+def test_quantize_gs64_random(orc, six):
+    """Random rows over a range of magnitudes, a zero group and an fp16-extreme group: the scale is the group absmax
+    / 7 (/ 31), every code is round-half-even of the binary32 quotient within the clamp, and dequantized weights lie
+    within half a scale of the input."""
+    rng = np.random.default_rng(33)
+    w = (rng.standard_normal((24, 256)) * np.geomspace(1e-4, 30, 24)[:, None]).astype(np.float16)
+    w[2, 64:128] = 0
+    w[3, :64] = np.float16(65504); w[3, 1] = np.float16(-65504)
+    qm = 31 if six else 7
+    if six:
+        q, qh, s = orc.quantize_rows_q6(w)
+        v = _unpack_q6(q, qh, 256)
+    else:
+        q, s = orc.quantize_rows_q4(w)
+        v = _unpack_q4(q, 256)
+    wf = w.astype(np.float32).reshape(24, 4, 64)
+    m = np.abs(wf).max(-1)
+    sc = np.where(m > 0, m / np.float32(qm), np.float32(1)).astype(np.float32)
+    assert np.array_equal(s.view(np.uint32), sc.view(np.uint32))
+    ref = np.clip(np.rint(wf / sc[..., None]), -qm - 1, qm).astype(np.int16).reshape(24, 256)
+    assert np.array_equal(v, ref)
+    assert np.all(np.abs(v.reshape(24, 4, 64)).max(-1)[m > 0] == qm)  # the absmax weight takes the top code
+    err = np.abs(v.reshape(24, 4, 64) * sc[..., None].astype(np.float64) - wf.astype(np.float64))
+    assert np.all(err <= sc[..., None] * 0.5000001)
+
+
+@pytest.mark.parametrize("fmt", ["q4", "q6", "f16"])
+def test_dense_mat_exact_product(orc, fmt):
+    """The exact product equals numpy's float64 matmul of independently unpacked weights; a matrix with a single
+    non-zero weight gives that weight times x; the GEMM model equals the exact product when weights and inputs are
+    fp16-exact and differs from it by rounding x alone otherwise."""
+    rng = np.random.default_rng(34)
+    O, I = 29, 256
+    w16 = (rng.standard_normal((O, I)) * 0.1).astype(np.float16)
+    x = rng.standard_normal((3, I)).astype(np.float32)
+    if fmt == "q4":
+        q, s = orc.quantize_rows_q4(w16); wh = None; F = orc.MAT_Q4
+        wd = _unpack_q4(q, I) * np.repeat(s.astype(np.float64), 64, 1)
+    elif fmt == "q6":
+        q, wh, s = orc.quantize_rows_q6(w16); F = orc.MAT_Q6
+        wd = _unpack_q6(q, wh, I) * np.repeat(s.astype(np.float64), 64, 1)
+    else:
+        q, wh, s, F = w16, None, None, orc.MAT_F16
+        wd = w16.astype(np.float64)
+    y = orc.dense_mat_f64(F, q, wh, s, x)
+    ref = x.astype(np.float64) @ wd.T
+    assert np.abs(y - ref).max() <= 1e-12 * np.abs(ref).max()
+    # the GEMM precision model: fp16(fp32(code * scale)) and fp16(x)
+    w32 = wd.astype(np.float32)
+    w16m = w32 if fmt == "f16" else w32.astype(np.float16).astype(np.float64)
+    ref16 = x.astype(np.float16).astype(np.float64) @ np.asarray(w16m, np.float64).T
+    y16 = orc.dense_mat_fp16x(F, q, wh, s, x)
+    assert np.abs(y16 - ref16).max() <= 1e-12 * np.abs(ref16).max()
+    xh = x.astype(np.float16).astype(np.float32)
+    if fmt == "f16":  # fp16 weights and fp16-exact inputs: the model is the exact product
+        assert np.abs(orc.dense_mat_fp16x(F, q, wh, s, xh) - orc.dense_mat_f64(F, q, wh, s, xh)).max() == 0
+    assert np.abs(y16 - y).max() > 0  # rounding x is not a no-op on these inputs
+
+
+def test_dense_mat_single_weight(orc):
+    """One non-zero int4 weight (code 3 at input 70 of row 5, group scale 0.25): y[5] = 0.75 x[70], all else 0."""
+    O, I = 8, 128
+    q = np.zeros((O, I // 2), np.uint8)
+    q[5, 35] = 0x03                                   # input 70: the low nibble of byte 35
+    s = np.full((O, I // 64), 0.25, np.float32)
+    x = np.arange(1, I + 1, dtype=np.float32)[None]
+    y = orc.dense_mat_f64(orc.MAT_Q4, q, None, s, x)
+    assert y[0, 5] == 0.75 * 71 and np.count_nonzero(y) == 1
