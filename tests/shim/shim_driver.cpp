@@ -3,10 +3,23 @@
 // for a prefill chunk (T = T0, ns = 1 -> FA), attn_fa on the same queries, then attn_decode for one token with split
 // partials (ns > 1). Inputs come from files the test wrote, outputs go to files the test checks against the oracle.
 //   shim_driver <dir> <turbo> <T0> <ns>
+// Dense mode drives the dense projections' shim with the reference's struct Mat (kernels.cuh:186-196): fp16 rows
+// from a file, quantized to int4 and int6 through the library, then gemv and gemm (S rows) for each form.
+//   shim_driver <dir> dense <O> <I> <S>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <vector>
 #include "attn_moex_amd.h"
+// the reference's dense matrix (kernels.cuh:186-196), which the dense shim converts
+struct Mat {
+    const half* f16 = nullptr;
+    const int8_t* q = nullptr;
+    const float* s = nullptr;
+    const uint8_t* q4 = nullptr;
+    const uint8_t *q6 = nullptr, *q6h = nullptr;
+};
+#include "dense_moex_amd.h"
 
 #define HC(x) do { hipError_t e = (x); if (e != hipSuccess) { fprintf(stderr, "%s: %s\n", #x, hipGetErrorString(e)); exit(2); } } while (0)
 
@@ -41,7 +54,47 @@ static void from_dev(const char* dir, const char* name, const void* d, size_t n)
     spit(dir, name, h.data(), n);
 }
 
+static int dense_main(const char* dir, int O, int I, int S) {
+    std::vector<char> wh = slurp(dir, "w16.bin"), xh = slurp(dir, "x.bin");
+    const half* w = to_dev<half>(wh);
+    const float* X = to_dev<float>(xh);
+    uint8_t *q4, *q6, *q6h;
+    float *s4, *s6, *y, *Y;
+    HC(hipMalloc(&q4, (size_t)O * I / 2));
+    HC(hipMalloc(&q6, (size_t)O * I / 2));
+    HC(hipMalloc(&q6h, (size_t)O * I / 4));
+    HC(hipMalloc(&s4, (size_t)O * (I / 64) * 4));
+    HC(hipMalloc(&s6, (size_t)O * (I / 64) * 4));
+    HC(hipMalloc(&y, (size_t)O * 4));
+    HC(hipMalloc(&Y, (size_t)S * O * 4));
+    moex_quantize_rows_q4(reinterpret_cast<const uint16_t*>(w), q4, s4, O, I, nullptr);
+    moex_quantize_rows_q6(reinterpret_cast<const uint16_t*>(w), q6, q6h, s6, O, I, nullptr);
+    Mat m[3];
+    m[0].q4 = q4; m[0].s = s4;
+    m[1].q6 = q6; m[1].q6h = q6h; m[1].s = s6;
+    m[2].f16 = w;
+    const char* names[3] = {"q4", "q6", "f16"};
+    for (int f = 0; f < 3; f++) {
+        gemv(m[f], X, y, I, O);
+        gemm(m[f], X, Y, S, I, O);
+        HC(hipDeviceSynchronize());
+        char n[64];
+        snprintf(n, sizeof n, "y_%s.bin", names[f]);
+        from_dev(dir, n, y, (size_t)O * 4);
+        snprintf(n, sizeof n, "Y_%s.bin", names[f]);
+        from_dev(dir, n, Y, (size_t)S * O * 4);
+    }
+    from_dev(dir, "q4.bin", q4, (size_t)O * I / 2);
+    from_dev(dir, "s4.bin", s4, (size_t)O * (I / 64) * 4);
+    from_dev(dir, "q6.bin", q6, (size_t)O * I / 2);
+    from_dev(dir, "q6h.bin", q6h, (size_t)O * I / 4);
+    from_dev(dir, "s6.bin", s6, (size_t)O * (I / 64) * 4);
+    printf("dense shim ok\n");
+    return 0;
+}
+
 int main(int argc, char** argv) {
+    if (argc == 6 && !strcmp(argv[2], "dense")) return dense_main(argv[1], atoi(argv[3]), atoi(argv[4]), atoi(argv[5]));
     if (argc != 5) { fprintf(stderr, "usage: shim_driver dir turbo T0 ns\n"); return 2; }
     const char* dir = argv[1];
     const int turbo = atoi(argv[2]), T0 = atoi(argv[3]), ns = atoi(argv[4]);

@@ -71,3 +71,37 @@ def test_shim_drives_the_library(tmp_path, turbo):
     err, mag = float(np.abs(do[0] - ref).max()), float(np.abs(ref).max())
     report("shim decode", turbo=turbo, err=err, mag=mag)
     assert err <= 1e-4 * mag
+
+
+@pytest.mark.gpu
+def test_shim_dense_forms(tmp_path):
+    """The dense projections' shim block of INTEGRATION.md with the reference's struct Mat: int4 and int6 quantized
+    through the library (bit-exact against the oracle), then gemv (1 row) and gemm (16 rows, the MFMA GEMM) for the
+    int4, int6 and fp16 forms, against the exact product (K11: 1e-5) and the GEMM's precision model (1e-5)."""
+    assert os.path.exists(DRIVER), "tests/shim/shim_driver is not built (run __graft_entry__.build())"
+    O, I, S = 1000, 512, 16
+    rng = np.random.default_rng(52)
+    w = (rng.standard_normal((O, I)) * 0.05).astype(np.float16)
+    x = rng.standard_normal((S, I)).astype(np.float32)
+    w.tofile(tmp_path / "w16.bin")
+    x.tofile(tmp_path / "x.bin")
+    r = subprocess.run([DRIVER, str(tmp_path), "dense", str(O), str(I), str(S)], capture_output=True, text=True,
+                       timeout=120)
+    print(r.stdout, r.stderr, flush=True)
+    assert r.returncode == 0
+    rd = lambda n, t, *s: np.fromfile(tmp_path / n, t).reshape(s)
+    q4, s4 = orc.quantize_rows_q4(w)
+    q6, q6h, s6 = orc.quantize_rows_q6(w)
+    assert np.array_equal(rd("q4.bin", np.uint8, O, I // 2), q4)
+    assert np.array_equal(rd("s4.bin", np.float32, O, I // 64), s4)
+    assert np.array_equal(rd("q6.bin", np.uint8, O, I // 2), q6) and np.array_equal(rd("q6h.bin", np.uint8, O, I // 4), q6h)
+    assert np.array_equal(rd("s6.bin", np.float32, O, I // 64), s6)
+    forms = {"q4": (orc.MAT_Q4, q4, None, s4), "q6": (orc.MAT_Q6, q6, q6h, s6), "f16": (orc.MAT_F16, w, None, None)}
+    for nm, (F, a, b, c) in forms.items():
+        y, Y = rd(f"y_{nm}.bin", np.float32, O), rd(f"Y_{nm}.bin", np.float32, S, O)
+        ref = orc.dense_mat_f64(F, a, b, c, x[:1])[0]
+        model = orc.dense_mat_fp16x(F, a, b, c, x)
+        e1 = float(np.abs(y - ref).max() / np.abs(ref).max())
+        e2 = float(np.abs(Y - model).max() / np.abs(model).max())
+        report("dense shim", form=nm, rel_gemv=e1, rel_gemm=e2)
+        assert e1 < 1e-5 and e2 < 1e-5
