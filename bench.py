@@ -356,6 +356,32 @@ def main():
             print(f"[bench] dense {nm} int8 [{O_}x{I_}]: GEMV 1 row {ent['gemv_1row_us']} us "
                   f"({ent['gemv_1row_GBps']} GB/s), 2 rows {ent['gemv_2row_us']} us; prefill GEMM S={T} "
                   f"{ms_g:.3f} ms ({ent['gemm_2048_tflops']} TFLOPS)", flush=True)
+            # the other forms of struct Mat (kernels.cuh:186-196) on the same shape: the one-row GEMV through moex_gemv
+            for fm, bpw in (("int4", 0.5), ("int6", 0.75), ("f16", 2.0)):
+                nrot_f = int(600e6 // (O_ * I_ * bpw)) + 1
+                mats = []
+                for k in range(nrot_f):
+                    w16 = (torch.randn((O_, I_), generator=g, device=dev) * 0.02).half()
+                    if fm == "f16":
+                        mats.append((M.Mat(f16=w16), w16))
+                        continue
+                    q4 = torch.empty((O_, I_ // 2), dtype=torch.uint8, device=dev)
+                    s4 = torch.empty((O_, I_ // 64), dtype=torch.float32, device=dev)
+                    if fm == "int4":
+                        M.quantize_rows_q4(w16, q4, s4, O_, I_, st)
+                        mats.append((M.Mat(q4=q4, s=s4), q4, s4))
+                    else:
+                        q6h = torch.empty((O_, I_ // 4), dtype=torch.uint8, device=dev)
+                        M.quantize_rows_q6(w16, q4, q6h, s4, O_, I_, st)
+                        mats.append((M.Mat(q6=q4, q6h=q6h, s=s4), q4, q6h, s4))
+                xd1 = torch.randn((1, I_), generator=g, device=dev)
+                yd1 = torch.empty((1, O_), device=dev)
+                t_f = time_rotating([lambda m=m: M.gemv(m[0], xd1, yd1, I_, O_, st) for m in mats], 200)
+                ent[f"gemv_{fm}_1row_us"] = round(t_f * 1e3, 2)
+                ent[f"gemv_{fm}_1row_GBps"] = round(O_ * I_ * bpw / (t_f * 1e-3) / 1e9, 1)
+                del mats
+            print(f"[bench] dense {nm} other forms, GEMV 1 row: int4 {ent['gemv_int4_1row_us']} us, int6 "
+                  f"{ent['gemv_int6_1row_us']} us, fp16 {ent['gemv_f16_1row_us']} us", flush=True)
             del ws
         extra["dense_int8_projections"] = dense
 
