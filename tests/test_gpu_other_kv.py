@@ -1,4 +1,4 @@
-"""The GQA-8 kernels at kv head counts other than the bench's 2 (H = 8 KV): 1, 3 and 4 kv heads.
+"""The GQA-8 kernels at kv head counts other than the bench's 2 (H = 8 KV): 1, 3, 4 and 8 kv heads.
 
 attn_fa (kernels.cuh:1443-1728) and the split-K decode (attn_gqa_k + attn_combine_k, :1744-1844, :1317-1329) map
 work to workgroups by kv head: the FA grid puts each kv head on 8 / KV of the eight XCDs when KV divides 8 (a plain
@@ -30,7 +30,7 @@ def _setup(KV, max_t, T, seed):
 # (KV, pos0, T): KV x token tiles <= 256 with >= 2 tiles -> heavy/light pairs; short -> key splits; long -> one
 # workgroup per token tile (two waves of the chip)
 FA_CASES = [(1, 0, 4096), (1, 3000, 1000), (4, 0, 1024), (4, 700, 130), (3, 0, 1360), (3, 2000, 64), (4, 0, 2048),
-            (1, 5000, 17)]
+            (1, 5000, 17), (8, 0, 512), (8, 1000, 2048)]
 
 
 @pytest.mark.parametrize("KV,pos0,T", FA_CASES)
@@ -54,7 +54,8 @@ def test_fa_other_kv(KV, pos0, T, monkeypatch):
     assert e_new <= 2.0 * e_ref + 1e-3 * mag
 
 
-@pytest.mark.parametrize("KV,pos,T", [(1, 20000, 1), (4, 20000, 1), (3, 9000, 1), (1, 20000, 4), (4, 5000, 2)])
+@pytest.mark.parametrize("KV,pos,T", [(1, 20000, 1), (4, 20000, 1), (3, 9000, 1), (1, 20000, 4), (4, 5000, 2),
+                                      (8, 20000, 1), (8, 3000, 4)])
 def test_decode_other_kv(KV, pos, T):
     """Split-K decode over KV x splits workgroups, then the gated combine; T query tokens at positions pos .. pos+T-1
     (each sees its own prefix)."""
