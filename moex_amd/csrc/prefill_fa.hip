@@ -439,11 +439,13 @@ __host__ __device__ inline int fa_ntiles(int t, int pos0, int T) {  // key tiles
 
 // Pairs (full grids): token tile t's work grows with t, so one block per tile leaves the chip waiting for the last
 // tiles (at pos0 = 0 the heaviest has twice the average). Pair q = tiles NT - 1 - q (heavy) and q (light), both of one
-// kv head, goes to two blocks on one XCD: block 0 takes key tiles [0, s) of the heavy tile, block 1 the light tile and
-// then key tiles [s, n) of the heavy one, s chosen so both do about half of the pair. The heavy tile's halves merge in
+// kv head, goes to two blocks on one XCD: block 0 takes key tiles [0, s) of the heavy tile, block 1 key tiles [s, n) of
+// the heavy one and then the light tile, s chosen so both take about as long (block 1 gives up FA_PAIR_EXTRA tiles for
+// its second segment). The heavy tile's halves merge in
 // the kernel (fa_pair_merge). A pair whose halves would differ by less than FA_PAIR_MIN tiles is not split; an odd
 // tile count leaves the middle tile to one block.
 constexpr int FA_PAIR_MIN = 4;
+constexpr int FA_PAIR_EXTRA = 5;  // key tiles the second block of a pair gives up for its second segment (see fa_pair_segs)
 constexpr int FA_PAIR_SLOT = 64 * 128 + 128;  // floats per wavefront half: O (lane-interleaved float4s), {m, l} per lane
 __device__ __forceinline__ bool fa_pair_block(int b, int KV, int NT, int& kvh, int& q, int& role) {
     if (8 % KV == 0) {  // blocks b and b + 8 run on one XCD: the two blocks of a pair
@@ -465,14 +467,18 @@ __host__ inline int fa_pair_grid(int KV, int T) {
     if (8 % KV == 0) { const int xpk = 8 / KV; return 16 * ((nq + xpk - 1) / xpk); }
     return KV * 2 * nq;
 }
-__device__ __forceinline__ int fa_pair_segs(int q, int role, int pos0, int T, int NT, int pmin, FaSeg (&sg)[2]) {
+// pk packs the pair parameters: bits 0-7 the minimum tiles of the heavy tile's second part, 8-15 the second block's
+// extra cost in tiles (its second segment's queries, epilogue and output)
+__device__ __forceinline__ int fa_pair_segs(int q, int role, int pos0, int T, int NT, int pk, FaSeg (&sg)[2]) {
+    const int pmin = pk & 255, extra = (pk >> 8) & 255;
     if (q == NT / 2) {  // the middle tile of an odd count
         sg[0] = FaSeg{q, 0, fa_ntiles(q, pos0, T), FA_EPI_OUT};
         return 1;
     }
     const int tH = NT - 1 - q, nH = fa_ntiles(tH, pos0, T), nL = fa_ntiles(q, pos0, T);
     // block 1's part starts at or below every row's last key, so each row sees keys in both parts
-    const int s = min((nH + nL + 1) / 2, (pos0 + FT * tH) / BK);
+    // equal time, not equal tiles: block 0 runs s tiles, block 1 the other nH + nL - s plus its extra
+    const int s = min((nH + nL + extra + 1) / 2, (pos0 + FT * tH) / BK);
     if (s < 1 || nH - s < pmin) {
         sg[0] = role ? FaSeg{q, 0, nL, FA_EPI_OUT} : FaSeg{tH, 0, nH, FA_EPI_OUT};
         return 1;
@@ -616,7 +622,7 @@ __global__ void __launch_bounds__(512, 1) fa_prefill_kernel(const float* __restr
     } else if (MODE == FA_MODE_PAIR) {
         int q, role;
         if (!fa_pair_block(blockIdx.x, KV, NT, kvh, q, role)) return;
-        nseg = fa_pair_segs(q, role, pos0, T, NT, nsf, sg);  // nsf: the pair minimum
+        nseg = fa_pair_segs(q, role, pos0, T, NT, nsf, sg);  // nsf: the packed pair parameters
         pslot = (kvh * (NT / 2) + q) * 4;
     } else {
         int tile;
@@ -988,14 +994,19 @@ void launch_fa_bufs(const float* qo, const float* q_gate, moex_kv_cache kv, floa
     // a split launch has KV x tiles x nsf blocks: the pieces of every tile, the rest exit at once
     const int mode = nsf > 1 ? FA_MODE_SPLIT : pair ? FA_MODE_PAIR : FA_MODE_ONE;
     int pmin = FA_PAIR_MIN;  // MOEX_FA_PAIR_MIN=n: split a pair's heavy tile only when its second half has n tiles
-    if (const char* e = std::getenv("MOEX_FA_PAIR_MIN")) pmin = std::max(1, std::atoi(e));
+    if (const char* e = std::getenv("MOEX_FA_PAIR_MIN")) pmin = std::max(1, std::min(255, std::atoi(e)));
+    // the second block of a pair also loads its light tile's queries and writes its output: it takes FA_PAIR_EXTRA
+    // fewer key tiles (MOEX_FA_PAIR_EXTRA=n overrides; measured on 2048-token chunks: at pos0 = 0 59.4 -> 58.2 us, at 32768 -0.4 %)
+    int pextra = FA_PAIR_EXTRA;
+    if (const char* e = std::getenv("MOEX_FA_PAIR_EXTRA")) pextra = std::max(0, std::min(255, std::atoi(e)));
+    const int pk = pmin | (pextra << 8);
     const dim3 grid(mode == FA_MODE_SPLIT ? KV * p.NT * nsf : mode == FA_MODE_PAIR ? fa_pair_grid(KV, T) : fa_grid(KV, T));
     const size_t lds = (img ? 4 : 2) * TILE_BYTES;
 #define FA_LAUNCH(IMG_, MODE_)                                                                                         \
     do {                                                                                                               \
         set_lds<TB, IMG_, MODE_>();                                                                                    \
         hipLaunchKernelGGL((fa_prefill_kernel<TB, IMG_, MODE_>), grid, dim3(512), lds, st, qo, q_gate, kv, img, ntmax,  \
-                           out, H, KV, pos_d, max_t, ld, T, fpart, mode == FA_MODE_PAIR ? pmin : nsf, ncu, pcnt);      \
+                           out, H, KV, pos_d, max_t, ld, T, fpart, mode == FA_MODE_PAIR ? pk : nsf, ncu, pcnt);       \
     } while (0)
     if (img) {
         if (mode == FA_MODE_SPLIT) FA_LAUNCH(true, FA_MODE_SPLIT);
