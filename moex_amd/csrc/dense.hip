@@ -398,22 +398,24 @@ __global__ void __launch_bounds__(256) round_f16_kernel(const float4* __restrict
 constexpr int GEMM_WS_MAX_BLOCKS = 512;  // 2 workgroups x 256 CUs
 constexpr int GEMM_MIN_KSTEPS = 16;        // K steps of a split, at least
 
-// Sum of the K splits of gemm_ws_kernel, in split order (deterministic), times the row scale.
+// Sum of the K splits of gemm_ws_kernel, in split order (deterministic), times the row scale (int8; s = nullptr: none).
 __global__ void __launch_bounds__(256) gemm_reduce_kernel(const float* __restrict__ part, const float* __restrict__ s,
                                                           float* __restrict__ Y, int S, int O, int nks) {
     const size_t n = (size_t)S * O;
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
         float a = 0.f;
         for (int k = 0; k < nks; k++) a += part[k * n + i];
-        Y[i] = a * s[i % O];
+        Y[i] = s ? a * s[i % O] : a;  // no row scale for the group-scaled forms
     }
 }
 
 // Warp-specialised variant: wavefronts 4-7 load and widen the next K step into the other LDS buffer while
 // wavefronts 0-3 run the MFMAs of this one (one barrier per K step), so the staging VALU work runs beside the MFMAs.
-__global__ void __launch_bounds__(512, 2) gemm_ws_kernel(const int8_t* __restrict__ W, const float* __restrict__ s,
-                                                         const _Float16* __restrict__ X, float* __restrict__ Y, int S, int I,
-                                                         int O, int nks, float* __restrict__ part) {
+template <int FMT>
+__global__ void __launch_bounds__(512, 2) gemm_ws_kernel(const void* __restrict__ W, const uint8_t* __restrict__ Wh,
+                                                         const float* __restrict__ s, const _Float16* __restrict__ X,
+                                                         float* __restrict__ Y, int S, int I, int O, int nks,
+                                                         float* __restrict__ part) {
     __shared__ __align__(16) _Float16 lds[2][2][GM_BM * GM_LD];  // [buffer][W, X][row][k]
     const int nO = (O + GM_BM - 1) / GM_BM, nS = (S + GM_BN - 1) / GM_BN, tiles = nO * nS;
     const int ks = blockIdx.x / tiles, bid = blockIdx.x % tiles;  // K split ks of tile bid (nks = 1: no split)
@@ -432,21 +434,18 @@ __global__ void __launch_bounds__(512, 2) gemm_ws_kernel(const int8_t* __restric
         // ---- staging: thread t owns 16 weights (row t/2, k 16*(t%2)) and 16 activations (token t/2, same k) ----
         const int tid = threadIdx.x - 256, sr = tid >> 1, sk = (tid & 1) * 16;
         const bool wok = o0 + sr < O, xok = s0 + sr < S;
-        const int8_t* wp = W + (size_t)min(o0 + sr, O - 1) * I + kb * GM_BK + sk;
+        const size_t wrow = (size_t)min(o0 + sr, O - 1);
         const _Float16* xp = X + (size_t)min(s0 + sr, S - 1) * I + kb * GM_BK + sk;
-        uint4 wreg;
+        WStage wreg;
         uint4 xreg[2];
         auto load = [&](int k0) {
-            wreg = *reinterpret_cast<const uint4*>(wp + k0);
+            wstage_load<FMT>(wreg, W, Wh, s, wrow, I, kb * GM_BK + k0 + sk);
 #pragma unroll
             for (int j = 0; j < 2; j++) xreg[j] = reinterpret_cast<const uint4*>(xp + k0)[j];
         };
         auto store = [&](int b) {
             uint32_t h[8];
-            i8x4_to_h4(wok ? wreg.x : 0u, h[0], h[1]);
-            i8x4_to_h4(wok ? wreg.y : 0u, h[2], h[3]);
-            i8x4_to_h4(wok ? wreg.z : 0u, h[4], h[5]);
-            i8x4_to_h4(wok ? wreg.w : 0u, h[6], h[7]);
+            wstage_widen<FMT>(wreg, wok, h);
             uint4* wd = reinterpret_cast<uint4*>(&lds[b][0][sr * GM_LD + sk]);
             wd[0] = make_uint4(h[0], h[1], h[2], h[3]);
             wd[1] = make_uint4(h[4], h[5], h[6], h[7]);
@@ -500,7 +499,7 @@ __global__ void __launch_bounds__(512, 2) gemm_ws_kernel(const int8_t* __restric
     for (int i = 0; i < 2; i++) {
         const int o = o0 + wo + 32 * i + r;
         if (o >= O) continue;
-        const float so = nks > 1 ? 1.f : s[o];  // a K split leaves the scale to the reduction
+        const float so = nks > 1 || FMT != MF_I8 ? 1.f : s[o];  // a K split leaves the scale to the reduction
         float* Yo = nks > 1 ? part + (size_t)ks * S * O : Y;
 #pragma unroll
         for (int j = 0; j < 2; j++)
@@ -773,7 +772,8 @@ void launch_gemm_i8(const int8_t* q, const float* s, const float* X, float* Y, i
             part = reinterpret_cast<float*>(stream_workspace((size_t)nks * S * O * sizeof(float), st, 3));
             if (!part) nks = 1;
         }
-        hipLaunchKernelGGL(gemm_ws_kernel, dim3(blocks * nks), dim3(512), 0, st, q, s, Xh, Y, S, I, O, nks, part);
+        hipLaunchKernelGGL(gemm_ws_kernel<MF_I8>, dim3(blocks * nks), dim3(512), 0, st, q, nullptr, s, Xh, Y, S, I, O, nks,
+                           part);
         if (nks > 1) {
             MOEX_LAUNCHED();
             hipLaunchKernelGGL(gemm_reduce_kernel, dim3(1024), dim3(256), 0, st, part, s, Y, S, O, nks);
@@ -822,10 +822,34 @@ void launch_gemm_mat(const moex_mat& m, const float* X, float* Y, int S, int I, 
     hipLaunchKernelGGL(round_f16_kernel, dim3((unsigned)std::min<size_t>((n4 + 255) / 256, 4096)), dim3(256), 0, st,
                        reinterpret_cast<const float4*>(X), reinterpret_cast<uint2*>(Xh), n4);
     MOEX_LAUNCHED();
-    const dim3 grid(((O + GM_BM - 1) / GM_BM) * ((S + GM_BN - 1) / GM_BN));
-    if (m.q4) hipLaunchKernelGGL(gemm_kernel<MF_Q4>, grid, dim3(256), 0, st, m.q4, nullptr, m.s, Xh, Y, S, I, O);
-    else if (m.q6) hipLaunchKernelGGL(gemm_kernel<MF_Q6>, grid, dim3(256), 0, st, m.q6, m.q6h, m.s, Xh, Y, S, I, O);
-    else hipLaunchKernelGGL(gemm_kernel<MF_F16>, grid, dim3(256), 0, st, m.f16, nullptr, nullptr, Xh, Y, S, I, O);
+    // the int8 GEMM's choice of kernel and K split (launch_gemm_i8); the group scales are in the widened weights, so
+    // the split's reduction applies none
+    const int blocks = ((O + GM_BM - 1) / GM_BM) * ((S + GM_BN - 1) / GM_BN);
+    const void* W = m.q4 ? static_cast<const void*>(m.q4) : m.q6 ? static_cast<const void*>(m.q6)
+                                                                 : static_cast<const void*>(m.f16);
+    const uint8_t* Wh = m.q4 ? nullptr : m.q6h;
+    const float* sg = m.q4 || m.q6 ? m.s : nullptr;
+    if (blocks <= GEMM_WS_MAX_BLOCKS) {
+        int nks = 2 * blocks >= GEMM_WS_MAX_BLOCKS ? 1 : std::max(1, std::min(GEMM_WS_MAX_BLOCKS / blocks, I / GM_BK / GEMM_MIN_KSTEPS));
+        float* part = nullptr;
+        if (nks > 1) {
+            part = reinterpret_cast<float*>(stream_workspace((size_t)nks * S * O * sizeof(float), st, 3));
+            if (!part) nks = 1;
+        }
+        if (m.q4) hipLaunchKernelGGL(gemm_ws_kernel<MF_Q4>, dim3(blocks * nks), dim3(512), 0, st, W, Wh, sg, Xh, Y, S, I, O, nks, part);
+        else if (m.q6) hipLaunchKernelGGL(gemm_ws_kernel<MF_Q6>, dim3(blocks * nks), dim3(512), 0, st, W, Wh, sg, Xh, Y, S, I, O, nks, part);
+        else hipLaunchKernelGGL(gemm_ws_kernel<MF_F16>, dim3(blocks * nks), dim3(512), 0, st, W, Wh, sg, Xh, Y, S, I, O, nks, part);
+        if (nks > 1) {
+            MOEX_LAUNCHED();
+            hipLaunchKernelGGL(gemm_reduce_kernel, dim3(1024), dim3(256), 0, st, part, nullptr, Y, S, O, nks);
+        }
+    } else if (m.q4) {
+        hipLaunchKernelGGL(gemm_kernel<MF_Q4>, dim3(blocks), dim3(256), 0, st, W, Wh, sg, Xh, Y, S, I, O);
+    } else if (m.q6) {
+        hipLaunchKernelGGL(gemm_kernel<MF_Q6>, dim3(blocks), dim3(256), 0, st, W, Wh, sg, Xh, Y, S, I, O);
+    } else {
+        hipLaunchKernelGGL(gemm_kernel<MF_F16>, dim3(blocks), dim3(256), 0, st, W, Wh, sg, Xh, Y, S, I, O);
+    }
     MOEX_LAUNCHED();
 }
 
