@@ -7,10 +7,12 @@
  * int8 [O][I] row-major plus one fp32 scale per row, y = s[o] * (q[o,:] . x); moex_gemv / moex_gemm take the
  * matrix in any of the reference's forms (int8, int4 gs64, int6 gs64, fp16). Every entry point replaces one function
  * of src/kernels.cuh, cited on its declaration, with the reference's argument order. All pointers are device pointers;
- * stream is an opaque hipStream_t (NULL = the default stream). Nothing allocates or synchronizes, except moex_gemm_i8
- * with S > 8: it rounds X to fp16 into a per-(device, stream) workspace of S * I * 2 bytes, allocated on first use
- * and grown (after waiting for the stream) for a larger S * I, kept until the process ends. Errors are reported
- * as in moex_attn.h (print and exit(1), or the soft-error slot).
+ * stream is an opaque hipStream_t (NULL = the default stream). Nothing allocates or synchronizes, except the MFMA
+ * GEMM (moex_gemm_i8 with S > 8, moex_gemm when it takes the GEMM): it rounds X to fp16 into a per-(device, stream)
+ * workspace of S * I * 2 bytes and, when its tile grid is short of one workgroup per CU, splits K and keeps the fp32
+ * partial sums in a second one (nks * S * O * 4 bytes, nks <= 512 / tiles). Both are allocated on first use and
+ * grown (after waiting for the stream) for larger sizes, kept until the process ends. Errors are reported as in
+ * moex_attn.h (print and exit(1), or the soft-error slot).
  */
 #ifndef MOEX_DENSE_H
 #define MOEX_DENSE_H
@@ -72,7 +74,7 @@ void moex_gemv(const moex_mat* m, const float* x, float* y, int I, int O, void* 
  *   int4 and fp16 with S <= 2: moex_gemv row by row;
  *   otherwise the fp16 MFMA GEMM: activations rounded to fp16, int4 / int6 weights times their group scale rounded
  *   to fp16 (fp16 weights as stored), fp32 accumulation (gemm_wmma_k :225-248, gemm_i8_k<true> :250-337).
- * The GEMM takes the per-stream activation workspace of moex_gemm_i8 (S * I * 2 bytes). */
+ * The GEMM takes the per-stream workspaces of moex_gemm_i8 (see the top of this file). */
 void moex_gemm(const moex_mat* m, const float* X, float* Y, int S, int I, int O, void* stream);
 
 #ifdef __cplusplus
