@@ -129,6 +129,53 @@ def test_fa_images_and_dense_graph_replays():
         torch.cuda.synchronize()
 
 
+def test_dense_forms_graph_replays():
+    """The int4 / int6 / fp16 matrix forms captured on a stream after one eager call (which allocates the GEMM's
+    workspaces): int4 GEMV, int6 four-row GEMV pass, fp16 GEMM with a K split and int4 GEMM, every replay bit-identical
+    to the eager outputs, with eager work in between."""
+    import torch
+    import moex_amd as M
+    rng = np.random.default_rng(19)
+    O, I = 2048, 1024
+    w16 = torch.from_numpy((rng.standard_normal((O, I)) * 0.02).astype(np.float16)).cuda()
+    q4 = torch.empty((O, I // 2), dtype=torch.uint8, device="cuda")
+    s4 = torch.empty((O, I // 64), dtype=torch.float32, device="cuda")
+    q6 = torch.empty_like(q4)
+    q6h = torch.empty((O, I // 4), dtype=torch.uint8, device="cuda")
+    s6 = torch.empty_like(s4)
+    M.quantize_rows_q4(w16, q4, s4, O, I)
+    M.quantize_rows_q6(w16, q6, q6h, s6, O, I)
+    m4, m6, mf = M.Mat(q4=q4, s=s4), M.Mat(q6=q6, q6h=q6h, s=s6), M.Mat(f16=w16)
+    x = torch.randn((64, I), device="cuda")
+    st = torch.cuda.Stream()
+
+    def run(ys):
+        M.gemv(m4, x[0], ys[0], I, O, st)
+        M.gemm(m6, x[:4], ys[1], 4, I, O, st)
+        M.gemm(mf, x[:16], ys[2], 16, I, O, st)   # 16 tiles: K split over workgroups, summed by a second kernel
+        M.gemm(m4, x, ys[3], 64, I, O, st)
+
+    shapes = [(O,), (4, O), (16, O), (64, O)]
+    ye = [torch.empty(sh, device="cuda") for sh in shapes]
+    torch.cuda.synchronize()
+    with torch.cuda.stream(st):
+        run(ye)
+    st.synchronize()
+    yg = [torch.zeros_like(y) for y in ye]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        run(yg)
+    torch.cuda.synchronize()
+    for i in range(3):
+        for y in yg:
+            y.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(yg, ye)), i
+        x.mul_(1.0)
+        torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("gqa_maxt", ["0", "64"])
 def test_fa_key_pieces_graph_new_position(gqa_maxt, monkeypatch):
     """A short chunk splits its token tiles' keys into pieces chosen on the device from pos_d: one captured attn_fa
