@@ -20,11 +20,12 @@
 //   gemm_ws_kernel         The same product and sum order with split roles: 4 wavefronts widen the next K step into
 //                          LDS while 4 run the MFMAs of this one. Used when the grid fits the chip in one pass.
 //   quantize_gs64_kernel   fp16 rows -> int4 / int6 codes + a scale per 64-input group (bit-exact).
-//   gemv_mat_kernel        the GEMV of the int4 / int6 / fp16 forms: a lane per 32-weight unit of R rows, each unit
+//   gemv_mat_kernel        the GEMV of the int4 / int6 / fp16 forms: a lane per 16-weight unit of R rows, each unit
 //                          summed in order and scaled, wavefront and part sums as gemv_kernel.
 //   gemm_kernel<form>      the same tiled MFMA GEMM for every form: the staging widens int4 / int6 weights times
 //                          their group scale to fp16 (or copies fp16 weights) where int8 is widened exactly.
 #include <algorithm>
+#include <cstdlib>
 #include "common.hpp"
 
 namespace moex {
@@ -588,39 +589,40 @@ __global__ void __launch_bounds__(256) quantize_gs64_kernel(const uint16_t* __re
 }
 
 // ---- GEMV of the int4 / int6 / fp16 forms (gemv_q4_k, gemv_q6_k, gemv_f16_k: kernels.cuh:68-93,486-550) ----
-// y[t][o] = sum over the row's 32-weight units c of (sum_k w[o][32c + k] x[t][32c + k]) * scale[o][c / 2] (fp16: no
+// y[t][o] = sum over the row's 16-weight units c of (sum_k w[o][16c + k] x[t][16c + k]) * scale[o][c / 4] (fp16: no
 // scale), fp32 sums. Layout as gemv_kernel: a wavefront takes R rows over the KS-th part of the row's units, a lane
-// per unit (16 B of int4, 16 + 8 B of int6, 64 B of fp16 a row), reads its 32 inputs per row of x from L2, sums the
+// per unit (8 B of int4, 8 + 4 B of int6, 32 B of fp16 a row), reads its 16 inputs per row of x from L2, sums the
 // unit in k order, and the KS parts of a row are added in LDS in part order. KS and R depend on O, I and the form
 // only, so every row of a multi-row call is bit-identical to the same row alone.
 template <int FMT>
 struct MatUnit {
-    uint4 a[FMT == MF_F16 ? 4 : 1];
-    uint2 h;  // int6 high fields
+    uint4 a[FMT == MF_F16 ? 2 : 1];  // int4 / int6: .x, .y the 16 low nibbles; fp16: 16 halves
+    uint32_t h;                      // int6: the 16 high 2-bit fields
     float sc;
 };
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 template <int FMT>
 __device__ __forceinline__ void mat_unit_load(MatUnit<FMT>& u, const uint8_t* W, const uint8_t* Wh, const float* s,
                                               size_t row, int I, int c) {
     if constexpr (FMT == MF_F16) {
-        const u32x4* p = reinterpret_cast<const u32x4*>(W + (row * I + 32 * (size_t)c) * 2);
+        const u32x4* p = reinterpret_cast<const u32x4*>(W + (row * I + 16 * (size_t)c) * 2);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < 2; i++) {
             const u32x4 v = __builtin_nontemporal_load(p + i);
             u.a[i] = make_uint4(v[0], v[1], v[2], v[3]);
         }
     } else {
-        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(W + row * (I / 2)) + c);
-        u.a[0] = make_uint4(v[0], v[1], v[2], v[3]);
-        if constexpr (FMT == MF_Q6) u.h = reinterpret_cast<const uint2*>(Wh + row * (I / 4))[c];
-        u.sc = s[row * (I / 64) + c / 2];
+        const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(W + row * (I / 2)) + c);
+        u.a[0] = make_uint4(v[0], v[1], 0u, 0u);
+        if constexpr (FMT == MF_Q6) u.h = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(Wh + row * (I / 4)) + c);
+        u.sc = s[row * (I / 64) + c / 4];
     }
 }
 template <int FMT>
-__device__ __forceinline__ float mat_unit_dot(const MatUnit<FMT>& u, const float4 (&x)[8]) {
+__device__ __forceinline__ float mat_unit_dot(const MatUnit<FMT>& u, const float4 (&x)[4]) {
     float d = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
+    for (int j = 0; j < 4; j++) {
         const float xv[4] = {x[j].x, x[j].y, x[j].z, x[j].w};
 #pragma unroll
         for (int n = 0; n < 4; n++) {
@@ -631,11 +633,11 @@ __device__ __forceinline__ float mat_unit_dot(const MatUnit<FMT>& u, const float
                 const uint32_t d2 = ((k / 2) & 3) == 0 ? q.x : ((k / 2) & 3) == 1 ? q.y : ((k / 2) & 3) == 2 ? q.z : q.w;
                 w = (float)u2h2(d2)[k & 1];
             } else {
-                const uint32_t dw = k < 8 ? u.a[0].x : k < 16 ? u.a[0].y : k < 24 ? u.a[0].z : u.a[0].w;
+                const uint32_t dw = k < 8 ? u.a[0].x : u.a[0].y;
                 if constexpr (FMT == MF_Q4) {
                     w = (float)(int)__builtin_amdgcn_sbfe(dw, 4 * (k & 7), 4);  // the signed nibble (the builtin returns it as unsigned)
                 } else {
-                    const uint32_t hb = ((k < 16 ? u.h.x : u.h.y) >> (2 * (k & 15))) & 3u;
+                    const uint32_t hb = (u.h >> (2 * k)) & 3u;
                     w = (float)((int)(((dw >> (4 * (k & 7))) & 15u) | (hb << 4)) - 32);
                 }
             }
@@ -653,7 +655,7 @@ __global__ void __launch_bounds__(64 * GM_WAVES) gemv_mat_kernel(const uint8_t* 
                                                                  int I, int O, int KS) {
     __shared__ float red[GM_WAVES][NT][R];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nb = gridDim.x;
-    const int U = I / 32, ngroups = (O + R - 1) / R, gpr = GM_WAVES / KS;
+    const int U = I / 16, ngroups = (O + R - 1) / R, gpr = GM_WAVES / KS;
     const int rounds = (ngroups + nb * gpr - 1) / (nb * gpr);
     const int part = wv % KS, slice = U / KS, cb = part * slice, ce = cb + slice;
     for (int j = 0; j < rounds; j++) {
@@ -670,10 +672,10 @@ __global__ void __launch_bounds__(64 * GM_WAVES) gemv_mat_kernel(const uint8_t* 
                 for (int r = 0; r < R; r++) mat_unit_load<FMT>(u[r], W, Wh, s, (size_t)min(g * R + r, O - 1), I, c);
 #pragma unroll
                 for (int t = 0; t < NT; t++) {
-                    float4 xv[8];
-                    const float4* xp = reinterpret_cast<const float4*>(x + (size_t)t * I + 32 * (size_t)c);
+                    float4 xv[4];
+                    const float4* xp = reinterpret_cast<const float4*>(x + (size_t)t * I + 16 * (size_t)c);
 #pragma unroll
-                    for (int i = 0; i < 8; i++) xv[i] = xp[i];
+                    for (int i = 0; i < 4; i++) xv[i] = xp[i];
 #pragma unroll
                     for (int r = 0; r < R; r++) acc[t][r] += mat_unit_dot<FMT>(u[r], xv);
                 }
@@ -711,15 +713,16 @@ int dense_cus() {
 template <int FMT, int NT>
 void launch_gemv_mat_t(const uint8_t* W, const uint8_t* Wh, const float* s, const float* x, float* y, int I, int O,
                        hipStream_t st) {
-    // parts of at least one unit a lane, split while the wavefronts do not yet fill the chip's 8 slots per CU; then
-    // rows per wavefront: 4, fewer while the grid would leave CUs without a workgroup
-    const int U = I / 32, cus = dense_cus();
+    // parts of at least 64 units (one load step a lane wherever I allows: a second, dependent step cost the qkv
+    // shape 8.4 -> 6.4 us for int4); rows per wavefront: 4, fewer while the grid would leave CUs without a
+    // workgroup; up to two workgroups per CU at once before the kernel loops over further rounds
+    const int U = I / 16, cus = dense_cus();
     int ks = 1;
-    while (ks < GM_WAVES && (O + 3) / 4 * ks < GM_WAVES * cus && U % (2 * ks) == 0 && U / (2 * ks) >= 64) ks *= 2;
+    while (ks < GM_WAVES && U % (2 * ks) == 0 && U / (2 * ks) >= 64) ks *= 2;
     const int gpr = GM_WAVES / ks;
     int R = 4;
     while (R > 1 && ((O + R - 1) / R + gpr - 1) / gpr < cus) R /= 2;
-    const int nb = std::min(cus, ((O + R - 1) / R + gpr - 1) / gpr);
+    const int nb = std::min(2 * cus, ((O + R - 1) / R + gpr - 1) / gpr);
     if (R == 4)
         hipLaunchKernelGGL((gemv_mat_kernel<FMT, NT, 4>), dim3(nb), dim3(64 * GM_WAVES), 0, st, W, Wh, s, x, y, I, O, ks);
     else if (R == 2)
