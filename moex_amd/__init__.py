@@ -18,7 +18,8 @@ TQ_KB, TQ_VB = 128, 96
 
 class Mat(ctypes.Structure):
     """struct Mat (kernels.cuh:186-196) as moex_mat (include/moex_dense.h): one of f16; q, s (int8, row scales);
-    q4, s (int4 gs64); q6, q6h, s (int6 gs64). Fields take torch tensors or device addresses."""
+    q4, s (int4 gs64); q6, q6h, s (int6 gs64). Fields take torch tensors or device addresses; the struct holds the
+    addresses only, so the caller keeps the tensors alive while it is used."""
     _fields_ = [("f16", ctypes.c_void_p), ("q", ctypes.c_void_p), ("s", ctypes.c_void_p), ("q4", ctypes.c_void_p),
                 ("q6", ctypes.c_void_p), ("q6h", ctypes.c_void_p)]
 
