@@ -898,6 +898,9 @@ void set_lds() {
 }
 
 int fa_ncu() {
+    // MOEX_FA_CUS=n plans the FA grids as for a chip of n CUs (read on every call; the grids stay correct for any n:
+    // tests use it to reach layouts this chip's count does not, such as a pair grid with an odd number of tiles)
+    if (const char* e = std::getenv("MOEX_FA_CUS")) return std::max(8, std::atoi(e));
     static const int ncu = [] {
         int dev = 0, v = 0;
         if (hipGetDevice(&dev) == hipSuccess &&

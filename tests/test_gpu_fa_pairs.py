@@ -121,3 +121,25 @@ def test_pairs_graph_replays(setup):
         assert np.array_equal(out.cpu().numpy(), ref), f"replay {i} differs"
         eager = _fa(dc, qo_d[:T], qg_d[:T], pos0, T, st)
         assert np.array_equal(eager, ref)
+
+
+@pytest.mark.parametrize("cus,pos0,T", [(254, 500, 2030), (254, 0, 2024), (250, 3000, 2000)])
+def test_pairs_odd_tile_count(setup, cus, pos0, T, monkeypatch):
+    """A pair grid with an odd number of token tiles leaves the middle tile to one workgroup alone. At 2 kv heads
+    and 256 CUs no chunk gets there (a pair grid needs 2 x tiles = the CU count), so the grids are planned as for a
+    chip of `cus` CUs (MOEX_FA_CUS): 127 or 125 tiles a kv head. Gate and agreement with one tile per workgroup."""
+    hc, dc, qo, qg, qo_d, qg_d = setup
+    monkeypatch.setenv("MOEX_FA_CUS", str(cus))
+    monkeypatch.setenv("MOEX_FA_PAIR", "1")
+    a = _fa(dc, qo_d[:T], qg_d[:T], pos0, T)
+    assert np.array_equal(a, _fa(dc, qo_d[:T], qg_d[:T], pos0, T)), "repeated pair calls differ"
+    monkeypatch.setenv("MOEX_FA_PAIR", "0")
+    one = _fa(dc, qo_d[:T], qg_d[:T], pos0, T)
+    _gate("fa pairs, odd tile count", a, qo, qg, hc, pos0, T)
+    mag = float(np.abs(one).max())
+    d = float(np.abs(a - one).max())
+    report("fa odd pairs vs one tile per workgroup", cus=cus, pos0=pos0, T=T, maxdiff=d, mag=mag)
+    assert np.all(np.isfinite(a)) and d <= 2e-3 * mag
+    # the middle tile's rows run alone, the same arithmetic as one tile per workgroup
+    mid = ((T + 15) // 16) // 2
+    assert np.array_equal(a[16 * mid:16 * mid + 16], one[16 * mid:16 * mid + 16])
