@@ -121,3 +121,28 @@ def test_turbo_other_kv(KV, pos0, T):
     e = float(np.abs(od.cpu().numpy()[0] - refd).max())
     report("decode turbo other kv", KV=KV, pos=pos, ns=ns, err=e, mag=float(np.abs(refd).max()))
     assert e <= 1e-4 * float(np.abs(refd).max())
+
+
+@pytest.mark.parametrize("KV,cus,T", [(3, 255, 1360), (3, 258, 1376), (1, 255, 4080)])
+def test_pairs_other_kv(KV, cus, T, monkeypatch):
+    """Pair grids at kv head counts whose layout the chip's CU count does not reach (planned as for `cus` CUs,
+    MOEX_FA_CUS): 3 kv heads take the plain block order (3 does not divide the 8 XCDs), odd tile counts leave a middle
+    tile alone. The test_fa.cu:114 gate against the oracle."""
+    import torch
+    import moex_amd as M
+    monkeypatch.setenv("MOEX_FA_CUS", str(cus))
+    pos0 = 100
+    H, ld, hc, dc, qo, qg = _setup(KV, pos0 + T + 40, T, seed=90 + KV + T)
+    out = torch.full((T, H, AHD), float("nan"), dtype=torch.float32, device="cuda")
+    M.attn_fa(dev(qo), dev(qg), dc, out, H, KV, pos_tensor(pos0), dc.max_t, ld, T)
+    torch.cuda.synchronize()
+    o = out.cpu().numpy()
+    assert np.all(np.isfinite(o))
+    rows = sample_rows(T, range(H))
+    ref = orc.attn_rows_f64(qo, qg, ld, H, hc, pos0, rows)
+    emu = orc.attn_rows_fa_emul(qo, qg, ld, H, hc, pos0, rows)
+    got = np.stack([o[t, h] for t, h in rows])
+    mag = float(np.abs(ref).max())
+    e_new, e_ref = float(np.abs(got - ref).max()), float(np.abs(emu - ref).max())
+    report("fa pairs other kv", KV=KV, cus=cus, T=T, e_new=e_new, e_ref=e_ref, mag=mag)
+    assert e_new <= 2.0 * e_ref + 1e-3 * mag
