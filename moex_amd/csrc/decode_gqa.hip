@@ -247,6 +247,9 @@ static_assert(W1_LDS <= 160 * 1024, "LDS");
 // K/V row, writes it to the cache and patches it into its stage (its chunk may have been moved before the row
 // reached memory). With the skip flag set it does neither and reads qo, as the attention kernels after a skipped
 // front would.
+// FR: launched with the front's arguments (a separate instance, so that the kernel without the front keeps its own
+// code and registers)
+template <bool FR>
 __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws1_kernel(const float* __restrict__ qo, moex_kv_cache kv,
                                                                          int H, const int* __restrict__ pos_d,
                                                                          int max_t, float* __restrict__ part, int ns,
@@ -264,49 +267,66 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_ws1_kernel(const 
     auto chi = [&](int c) { return c == 0 ? lo + first : lo + first + c * W1_CH; };
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 4, m16 = lane & 15;
     const size_t rbase = (size_t)kvh * max_t;
-    const bool fused = fr.q && !(fr.skip && *fr.skip);
-    // the producers' first chunks go out at once when the queries are read from qo; with the front in the prologue
-    // they go out after it: its row reads would otherwise queue behind ~25 MB of chunk transfers (measured: the step
-    // 0.3-0.4 us faster, although the transfers start later)
+    const bool fused = FR && fr.q && !(fr.skip && *fr.skip);
+    // the producers' first chunks go out at once when the queries are read from qo. With the front in the prologue
+    // the consumers form it, two query heads each (and wavefront 0 the new row), and the chunks go out once the
+    // consumers have issued all of their row reads (a barrier between the two), so those reads are not queued behind
+    // ~25 MB of chunk transfers while the front's arithmetic runs beside the chunks' flight
     if (wv >= WS_NC && !fused) ring_first<W1_CH, W1_NS>(smem, kv, rbase, wv - WS_NC, lane, lo, first, nch);
     const bool app = fused && hi == Tmax && hi > lo;  // this split holds the new row pos0
     const float* qtab = reinterpret_cast<const float*>(smem + W1_QO);
     unsigned char* patch = smem + W1_PT;
     if (fused) {
-        // ---- the front, one wavefront per row (front::wave: the arithmetic of qk_norm_rope_kernel, no barrier):
-        // wavefront w forms query head w; in the split that holds pos0, wavefront 0 also forms the key row and the
-        // int8 codes of the new row, which go to the cache and to the patch ----
-        {
-            const float4 a = *reinterpret_cast<const float4*>(fr.q + (kvh * GQ + wv) * 2 * AHD + 4 * lane);
-            float x[4] = {a.x, a.y, a.z, a.w};
-            front::wave::norm_rope(x, fr.qn, lane, pos0, fr.rot, fr.theta, fr.eps);
-            const float4 y = make_float4(x[0], x[1], x[2], x[3]);
-            *reinterpret_cast<float4*>(smem + W1_QO + 4 * (wv * AHD + 4 * lane)) = y;
-            if (s == 0) *reinterpret_cast<float4*>(fr.qo + (kvh * GQ + wv) * AHD + 4 * lane) = y;
+        float4 qa[2], ka, va;
+        uint2 wq, wk;
+        if (wv < WS_NC) {
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                qa[j] = *reinterpret_cast<const float4*>(fr.q + (kvh * GQ + 2 * wv + j) * 2 * AHD + 4 * lane);
+            wq = *reinterpret_cast<const uint2*>(fr.qn + 4 * lane);
+            if (app && wv == 0) {
+                ka = *reinterpret_cast<const float4*>(fr.k + kvh * AHD + 4 * lane);
+                va = *reinterpret_cast<const float4*>(fr.v + kvh * AHD + 4 * lane);
+                wk = *reinterpret_cast<const uint2*>(fr.kn + 4 * lane);
+            }
         }
-        if (app && wv == 0) {
-            const float4 a = *reinterpret_cast<const float4*>(fr.k + kvh * AHD + 4 * lane);
-            const float4 b = *reinterpret_cast<const float4*>(fr.v + kvh * AHD + 4 * lane);
-            float x[4] = {a.x, a.y, a.z, a.w};
-            const float vv[4] = {b.x, b.y, b.z, b.w};
-            front::wave::norm_rope(x, fr.kn, lane, pos0, fr.rot, fr.theta, fr.eps);
-            uint32_t ck, cv;
-            float sk, sv;
-            front::wave::quant_i8(x, vv, ck, cv, sk, sv);
-            const size_t row = rbase + pos0;
-            *reinterpret_cast<uint32_t*>(kv.k + row * AHD + 4 * lane) = ck;
-            *reinterpret_cast<uint32_t*>(kv.v + row * AHD + 4 * lane) = cv;
-            reinterpret_cast<uint32_t*>(patch)[lane] = ck;
-            reinterpret_cast<uint32_t*>(patch + AHD)[lane] = cv;
-            if (lane == 0) {
-                kv.ks[row] = sk;
-                kv.vs[row] = sv;
-                reinterpret_cast<float*>(patch + 2 * AHD)[0] = sk;
-                reinterpret_cast<float*>(patch + 2 * AHD)[1] = sv;
+        asm volatile("s_barrier" ::: "memory");  // the consumers' row reads are issued
+        if (wv >= WS_NC) {
+            ring_first<W1_CH, W1_NS>(smem, kv, rbase, wv - WS_NC, lane, lo, first, nch);
+        } else {
+            // ---- the front (front::wave: the arithmetic of qk_norm_rope_kernel): consumer w forms query heads
+            // 2w, 2w + 1; in the split that holds pos0, consumer 0 also forms the key row and the int8 codes of the
+            // new row, which go to the cache and to the patch ----
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int h = 2 * wv + j;
+                float x[4] = {qa[j].x, qa[j].y, qa[j].z, qa[j].w};
+                front::wave::norm_rope(x, wq, lane, pos0, fr.rot, fr.theta, fr.eps);
+                const float4 y = make_float4(x[0], x[1], x[2], x[3]);
+                *reinterpret_cast<float4*>(smem + W1_QO + 4 * (h * AHD + 4 * lane)) = y;
+                if (s == 0) *reinterpret_cast<float4*>(fr.qo + (kvh * GQ + h) * AHD + 4 * lane) = y;
+            }
+            if (app && wv == 0) {
+                float x[4] = {ka.x, ka.y, ka.z, ka.w};
+                const float vv[4] = {va.x, va.y, va.z, va.w};
+                front::wave::norm_rope(x, wk, lane, pos0, fr.rot, fr.theta, fr.eps);
+                uint32_t ck, cv;
+                float sk, sv;
+                front::wave::quant_i8(x, vv, ck, cv, sk, sv);
+                const size_t row = rbase + pos0;
+                *reinterpret_cast<uint32_t*>(kv.k + row * AHD + 4 * lane) = ck;
+                *reinterpret_cast<uint32_t*>(kv.v + row * AHD + 4 * lane) = cv;
+                reinterpret_cast<uint32_t*>(patch)[lane] = ck;
+                reinterpret_cast<uint32_t*>(patch + AHD)[lane] = cv;
+                if (lane == 0) {
+                    kv.ks[row] = sk;
+                    kv.vs[row] = sv;
+                    reinterpret_cast<float*>(patch + 2 * AHD)[0] = sk;
+                    reinterpret_cast<float*>(patch + 2 * AHD)[1] = sv;
+                }
             }
         }
         front::sync<true>();
-        if (wv >= WS_NC) ring_first<W1_CH, W1_NS>(smem, kv, rbase, wv - WS_NC, lane, lo, first, nch);
     }
 
     if (wv >= WS_NC) {
@@ -1288,13 +1308,19 @@ void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos
     } else {
         if (T == 1) {
             static bool once = [] {
-                MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_ws1_kernel),
+                MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_ws1_kernel<true>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, W1_LDS));
+                MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_ws1_kernel<false>),
                                             hipFuncAttributeMaxDynamicSharedMemorySize, W1_LDS));
                 return true;
             }();
             (void)once;
-            hipLaunchKernelGGL(gqa_ws1_kernel, dim3(KV * ns), dim3(64 * (WS_NC + WS_NP)), W1_LDS, st, qo, kv, H, pos_d,
-                               max_t, part, ns, fr ? *fr : FrontArgs{});
+            if (fr && fr->q)
+                hipLaunchKernelGGL(gqa_ws1_kernel<true>, dim3(KV * ns), dim3(64 * (WS_NC + WS_NP)), W1_LDS, st, qo, kv, H,
+                                   pos_d, max_t, part, ns, *fr);
+            else
+                hipLaunchKernelGGL(gqa_ws1_kernel<false>, dim3(KV * ns), dim3(64 * (WS_NC + WS_NP)), W1_LDS, st, qo, kv, H,
+                                   pos_d, max_t, part, ns, FrontArgs{});
         }
         else if (T == 2) launch_wsp<1>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
         else launch_wsp<2>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);

@@ -298,15 +298,14 @@ __device__ __forceinline__ float row_max(const float (&v)[4]) {
     return m;
 }
 
-// norm_rope on the lane's 4 dims (rot % 8 == 0: a RoPE partner is 4 dims per lane away, same slot)
-__device__ __forceinline__ void norm_rope(float (&x)[4], const uint16_t* w, int lane, int pos, int rot, float theta,
-                                          float eps) {
+// norm_rope on the lane's 4 dims (rot % 8 == 0: a RoPE partner is 4 dims per lane away, same slot); wb: the lane's 4
+// fp16 norm weights (w + 4 lane), loaded by the caller
+__device__ __forceinline__ void norm_rope(float (&x)[4], uint2 wb, int lane, int pos, int rot, float theta, float eps) {
 #pragma clang fp contract(off)
     float sq[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) sq[i] = x[i] * x[i];
     const float r = rsqrtf(block_sum(sq) / AHD + eps);
-    const uint2 wb = *reinterpret_cast<const uint2*>(w + 4 * lane);
     const uint16_t wh[4] = {(uint16_t)(wb.x & 0xffffu), (uint16_t)(wb.x >> 16), (uint16_t)(wb.y & 0xffffu),
                             (uint16_t)(wb.y >> 16)};
 #pragma unroll
@@ -337,6 +336,10 @@ __device__ __forceinline__ void norm_rope(float (&x)[4], const uint16_t* w, int 
         const float cs = j < 64 ? c0 : c1, sn = j < 64 ? s0 : s1;
         if (d < rot) x[i] = d < h2 ? x[i] * cs - px[i] * sn : x[i] * cs + px[i] * sn;
     }
+}
+__device__ __forceinline__ void norm_rope(float (&x)[4], const uint16_t* w, int lane, int pos, int rot, float theta,
+                                          float eps) {
+    norm_rope(x, *reinterpret_cast<const uint2*>(w + 4 * lane), lane, pos, rot, theta, eps);
 }
 
 // wht of both 128-value halves of the row (dir 0 forward, 1 inverse)
