@@ -264,29 +264,33 @@ int fa_grid(int KV, int T) {
 }
 }  // namespace
 
-// Tile images: one workgroup widens one 32-key tile of one kv head (keys past pos0 + T zeroed) into its LDS image,
-// with the staging wavefronts' code. The prefill kernel then copies images into LDS by DMA, so each tile is widened
-// once instead of once per token tile.
+// Tile images: a workgroup widens 32-key tiles j = blockIdx.x, + gridDim.x, .. of one kv head (keys past pos0 + T
+// zeroed) into their images, with the staging wavefronts' code. The prefill kernel then copies images into LDS by DMA,
+// so each tile is widened once instead of once per token tile. The grid is sized from the cache (the chunk's end is a
+// device value) but capped: a cache of 262 144 positions would otherwise launch 8 194 workgroups per kv head, most
+// of them for tiles past the chunk's end, and their dispatch alone took microseconds.
 template <bool TB>
 __global__ void __launch_bounds__(256) fa_image_kernel(moex_kv_cache kv, const int* __restrict__ pos_d, int T, int max_t,
                                                        int ntmax, unsigned char* __restrict__ img) {
-    const int j = blockIdx.x, kvh = blockIdx.y, hi = *pos_d + T, k0 = j * BK, tid = threadIdx.x;
-    if (k0 >= hi) return;
+    const int kvh = blockIdx.y, hi = *pos_d + T, tid = threadIdx.x;
     const size_t rbase = (size_t)kvh * max_t;
-    unsigned char* t = img + ((size_t)kvh * ntmax + j) * TILE_BYTES;
-    float* sc = reinterpret_cast<float*>(t + KT_BYTES + VT_BYTES);
-    StageK sk;
-    StageV sv;
-    if (k0 + BK <= hi) {
-        load_k<TB, true>(sk, kv, rbase, k0, hi, tid);
-        load_v<TB, true>(sv, kv, rbase, k0, hi, tid);
-        store_k<TB, true>(sk, t, sc, sc + BK, k0, hi, tid);
-        store_v<TB, true>(sv, t + KT_BYTES, k0, hi, tid);
-    } else {
-        load_k<TB>(sk, kv, rbase, k0, hi, tid);
-        load_v<TB>(sv, kv, rbase, k0, hi, tid);
-        store_k<TB>(sk, t, sc, sc + BK, k0, hi, tid);
-        store_v<TB>(sv, t + KT_BYTES, k0, hi, tid);
+    for (int j = blockIdx.x; j < ntmax && j * BK < hi; j += gridDim.x) {
+        const int k0 = j * BK;
+        unsigned char* t = img + ((size_t)kvh * ntmax + j) * TILE_BYTES;
+        float* sc = reinterpret_cast<float*>(t + KT_BYTES + VT_BYTES);
+        StageK sk;
+        StageV sv;
+        if (k0 + BK <= hi) {
+            load_k<TB, true>(sk, kv, rbase, k0, hi, tid);
+            load_v<TB, true>(sv, kv, rbase, k0, hi, tid);
+            store_k<TB, true>(sk, t, sc, sc + BK, k0, hi, tid);
+            store_v<TB, true>(sv, t + KT_BYTES, k0, hi, tid);
+        } else {
+            load_k<TB>(sk, kv, rbase, k0, hi, tid);
+            load_v<TB>(sv, kv, rbase, k0, hi, tid);
+            store_k<TB>(sk, t, sc, sc + BK, k0, hi, tid);
+            store_v<TB>(sv, t + KT_BYTES, k0, hi, tid);
+        }
     }
 }
 
@@ -991,7 +995,12 @@ void launch_fa_bufs(const float* qo, const float* q_gate, moex_kv_cache kv, floa
     if (nsf > 1 && !fpart) nsf = 1;
     const bool pair = nsf == 1 && p.pair && fpart && pcnt;
     if (img) {
-        hipLaunchKernelGGL(fa_image_kernel<TB>, dim3(ntmax, KV), dim3(256), 0, st, kv, pos_d, T, max_t, ntmax, img);
+        // workgroups per kv head: every tile of the cache, at most 16 per CU over the kv heads (MOEX_FA_IMG_WG=n:
+        // n per CU, read on every call)
+        int wpc = 16;
+        if (const char* e = std::getenv("MOEX_FA_IMG_WG")) wpc = std::max(1, std::atoi(e));
+        const int gx = std::max(1, std::min(ntmax, wpc * ncu / KV));
+        hipLaunchKernelGGL(fa_image_kernel<TB>, dim3(gx, KV), dim3(256), 0, st, kv, pos_d, T, max_t, ntmax, img);
         MOEX_LAUNCHED();
     }
     // a split launch has KV x tiles x nsf blocks: the pieces of every tile, the rest exit at once

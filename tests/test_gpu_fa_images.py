@@ -81,3 +81,18 @@ def test_workspace_growth_and_streams(data):
     report("fa workspace", maxdiff_ab=float(np.abs(a - b).max()), maxdiff_ad=float(np.abs(a - d).max()))
     assert np.all(np.isfinite(a))
     assert np.array_equal(a, b) and np.array_equal(a, c) and np.array_equal(a, d)
+
+
+@pytest.mark.parametrize("wg", ["1", "3"])
+def test_image_grid_loops(data, wg, monkeypatch):
+    """The pre-pass grid is capped (MOEX_FA_IMG_WG workgroups per CU over the kv heads) and each workgroup loops over
+    tiles: with 1 or 3 per CU the workgroups widen up to 5 of the chunk's 632 tiles per kv head each, which must give
+    the bytes of the default grid (one tile per workgroup here)."""
+    qo_d, qg_d = data
+    dc = upload(random_int8_cache(20400, seed=12))
+    pos0, T = 20000, 200
+    ref = _fa(dc, qo_d, qg_d, pos0, T)
+    monkeypatch.setenv("MOEX_FA_IMG_WG", wg)
+    got = _fa(dc, qo_d, qg_d, pos0, T)
+    report("fa image grid", wg=wg, maxdiff=float(np.abs(got - ref).max()))
+    assert np.all(np.isfinite(got)) and np.array_equal(got, ref)
