@@ -77,12 +77,12 @@ constexpr int TPK = 256 / BK;               // threads per K row; each owns BK d
 struct StageK {
     uint4 k[BK / 16];  // int8: BK bytes of key t/TPK (dims BK*(t%TPK) ..); turbo: the first BK/32 hold its nibbles
     float kn;          // turbo: the half norm of those dims
-    float ks;          // thread < BK: score scale of key t (int8: ks * sl2, turbo: sl2)
+    float ks;          // int8: the row scale of key k0 + t % BK (times sl2 when stored); turbo: unused
 };
 // V: thread t stages dims 4*(t%64) .. +3 of the 8 keys 16m + 4h + {0..3, 8..11} with m = t/128, h = (t/64)%2
 struct StageV {
     uint32_t v[8];     // int8: 4 bytes of each key; turbo: low byte | high byte << 8
-    float vs[8];       // scales of those keys (turbo: half norm * K3 of the thread's dims)
+    float vs[8];       // scales of those keys (turbo: the half norm of the thread's dims, times K3 when stored)
 };
 __device__ __forceinline__ int vkey(int tid, int i) { return 16 * (tid >> 7) + 4 * ((tid >> 6) & 1) + (i & 3) + 8 * (i >> 2); }
 
@@ -110,9 +110,10 @@ __device__ __forceinline__ void load_k(StageK& S, moex_kv_cache kv, size_t rbase
 #pragma unroll
         for (int i = 0; i < BK / 16; i++) S.k[i] = p[i];
     }
-    {   // every thread loads a scale (branch-free); threads < BK own key tid's
+    if (!TB) {  // every thread loads a scale (branch-free); threads < BK own key tid's. The loaded values are
+                // only scaled when stored, so a load's first use is its store
         const int tt = k0 + (tid & (BK - 1));
-        S.ks = TB ? SL2 : kv.ks[rbase + (FULL || tt < hi ? tt : hi - 1)] * SL2;
+        S.ks = kv.ks[rbase + (FULL || tt < hi ? tt : hi - 1)];
     }
 }
 
@@ -137,7 +138,7 @@ __device__ __forceinline__ void load_v(StageV& S, moex_kv_cache kv, size_t rbase
             const uint8_t* vp = reinterpret_cast<const uint8_t*>(kv.v) + row * TQ_VB;
             const int b = dg >> 5;
             S.v[i] = (uint32_t)vp[b * 32 + (dg & 31)] | ((uint32_t)vp[64 + b * 16 + ((dg & 31) >> 1)] << 8);
-            S.vs[i] = r32(kv.vs[row * 2 + b] * TK3);
+            S.vs[i] = kv.vs[row * 2 + b];
         } else {
             S.v[i] = *reinterpret_cast<const uint32_t*>(kv.v + row * AHD + dg * 4);
             S.vs[i] = kv.vs[row];
@@ -184,7 +185,7 @@ __device__ __forceinline__ void store_k(const StageK& S, unsigned char* kbuf, fl
         *reinterpret_cast<uint4*>(Kt + key * KST + ((BK / 8) * c + q) * 8) = make_uint4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
     // threads >= BK write their copy to the spare slot (branch-free)
     float* dst = tid < BK ? sbuf + tid : spare + (tid & (BK - 1));
-    *dst = FULL || k0 + (tid & (BK - 1)) < hi ? S.ks : 0.f;
+    *dst = FULL || k0 + (tid & (BK - 1)) < hi ? (TB ? SL2 : S.ks * SL2) : 0.f;
 }
 
 template <bool TB, bool FULL = false>
@@ -209,7 +210,9 @@ __device__ __forceinline__ void store_v(const StageV& S, unsigned char* vbuf, in
     // per dim e: the 8 keys -> fp16 times the key's scale, one 16-byte write at V^T position 16m + 8h
     half2_t vsc[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) vsc[i] = half2_t{(_Float16)S.vs[2 * i], (_Float16)S.vs[2 * i + 1]};
+    for (int i = 0; i < 4; i++)
+        vsc[i] = TB ? half2_t{(_Float16)r32(S.vs[2 * i] * TK3), (_Float16)r32(S.vs[2 * i + 1] * TK3)}
+                    : half2_t{(_Float16)S.vs[2 * i], (_Float16)S.vs[2 * i + 1]};
     uint32_t ca[4], cb[4];
     tr4x4(r[0], r[1], r[2], r[3], ca);
     tr4x4(r[4], r[5], r[6], r[7], cb);
