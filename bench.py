@@ -47,6 +47,9 @@ def main():
                     help="only the configs[0] prefill calls (pos0 = 0; for counter runs; prints no JSON line)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--mfma-calib", action="store_true",
+                    help="only time a library fp16 GEMM (torch.matmul, 8192^3) on random and on all-zero data: the "
+                         "rate the chip sustains under dense MFMA load, for reading the FA kernel's roofline")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (the attention path of a batch-1 engine); "
@@ -66,6 +69,27 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_calib_bytes_each_way": src.numel() * 4, "launches": 5}))
+        return
+    if a.mfma_calib:
+        n = 8192
+        g = torch.Generator(device=dev).manual_seed(3)
+        res = {}
+        for name, fill in (("random", True), ("zeros", False)):
+            A = torch.randn((n, n), generator=g, device=dev).half() if fill else torch.zeros((n, n), device=dev).half()
+            B = torch.randn((n, n), generator=g, device=dev).half() if fill else torch.zeros((n, n), device=dev).half()
+            C = torch.empty((n, n), device=dev, dtype=torch.float16)
+            for _ in range(10):
+                torch.matmul(A, B, out=C)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(20):
+                torch.matmul(A, B, out=C)
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / 20
+            res[name] = {"ms": round(ms, 3), "TFLOPS": round(2 * n ** 3 / ms / 1e9, 1)}
+        print(json.dumps({"mfma_calib_fp16_gemm_8192": res}))
         return
 
     def ev():
