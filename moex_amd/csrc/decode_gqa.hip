@@ -544,11 +544,20 @@ template <int NPR> constexpr int wsp_lds() { return wsp_ns<NPR>() * ring_stage<w
 static_assert(WS_NC * 16 * AHD * 4 <= wsp_lds<1>() && WS_NC * 16 * AHD * 4 <= wsp_lds<2>(), "the pair merge fits");
 static_assert(wsp_lds<1>() <= 160 * 1024 && wsp_lds<2>() <= 160 * 1024, "LDS");
 
-template <int NPR>
+// FR (one token group, T <= 2 NPR, fr.q set, skip flag clear): attn_decode's q/k front runs in the prologue, as
+// front_rows_kernel would, bit for bit. The consumers issue the reads of the group's 8 T query rows (a token's rows
+// on one or two consumers, which share its RoPE angles) and of the split's new cache rows, a barrier lets the
+// producers send the first chunks, and the consumers form the rows while those fly: the query rows into the last ring
+// stage (its first chunk is issued only at the first chunk barrier, after the query digits are taken from it) and to
+// qo from split 0, the
+// new rows to the cache. The new rows sit at the split's end, so a chunk that holds them is moved after the first
+// chunk barrier, which follows the stores; only a split whose new rows fall in its first NS - 1 chunks holds its
+// first chunks back until the rows are stored.
+template <int NPR, bool FR>
 __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wsp_kernel(const float* __restrict__ qo, moex_kv_cache kv,
                                                                          int H, const int* __restrict__ pos_d,
                                                                          int max_t, float* __restrict__ part, int T,
-                                                                         int ns) {
+                                                                         int ns, FrontArgs fr) {
     constexpr int CH = wsp_ch<NPR>(), NS = wsp_ns<NPR>(), KB = CH * AHD, STAGE = ring_stage<CH>();
     constexpr int TT = 2 * NPR, KPC = CH * NPR / WS_NC;  // tokens per workgroup, keys per consumer per chunk
     static_assert(KPC == 32, "one 32-key block per consumer and chunk");
@@ -566,8 +575,63 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wsp_kernel(const 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 4, m16 = lane & 15;
     const size_t rbase = (size_t)kvh * max_t;
 
+    const bool fused = FR && ngr == 1 && fr.q && !(fr.skip && *fr.skip);
+    const float* qtab = reinterpret_cast<const float*>(smem + (NS - 1) * STAGE);  // [token][head][256] when fused
+    if (fused) {
+        // this split's new cache rows: positions [nlo, hi)
+        const int nlo = max(lo, pos0), nk = max(0, hi - nlo);
+        const int cnew = nlo < lo + first ? 0 : 1 + (nlo - lo - first) / CH;  // the chunk of the first new row
+        const bool late = nk > 0 && cnew < NS - 1;  // ... among the first chunks: they wait for the stores
+        // consumer w takes token t = w / P, heads (w % P) 8 / P .. (P = 2 consumers a token for T <= 2, else 1), and
+        // the token's new cache row when it is this split's (w % P == 0): one set of RoPE angles for all its rows
+        constexpr int P = TT == 2 ? 2 : 1, HP = GQ / P;
+        const int t = wv / P, h0 = (wv % P) * HP;
+        const bool qrows = wv < WS_NC && t < T;
+        const bool krow = qrows && wv % P == 0 && pos0 + t >= nlo && pos0 + t < hi;
+        float4 qa[HP], ka, va;
+        uint2 wq, wk;
+        if (qrows) {
+#pragma unroll
+            for (int j = 0; j < HP; j++)
+                qa[j] = *reinterpret_cast<const float4*>(fr.q + (size_t)t * fr.ld + (kvh * GQ + h0 + j) * 2 * AHD + 4 * lane);
+            wq = *reinterpret_cast<const uint2*>(fr.qn + 4 * lane);
+            if (krow) {
+                const size_t o = (size_t)t * fr.ld + kvh * AHD + 4 * lane;
+                ka = *reinterpret_cast<const float4*>(fr.k + o);
+                va = *reinterpret_cast<const float4*>(fr.v + o);
+                wk = *reinterpret_cast<const uint2*>(fr.kn + 4 * lane);
+            }
+        }
+        asm volatile("s_barrier" ::: "memory");  // the consumers' row reads are issued
+        if (wv >= WS_NC) {
+            if (!late) ring_first<CH, NS>(smem, kv, rbase, wv - WS_NC, lane, lo, first, nch);
+        } else {
+            float* qt = reinterpret_cast<float*>(smem + (NS - 1) * STAGE);
+            if (qrows) {
+                const front::wave::Rope rp = front::wave::rope_angles(lane, pos0 + t, fr.rot, fr.theta);
+#pragma unroll
+                for (int j = 0; j < HP; j++) {
+                    const int h = h0 + j;
+                    float x[4] = {qa[j].x, qa[j].y, qa[j].z, qa[j].w};
+                    front::wave::norm_rope(x, wq, lane, rp, fr.rot, fr.eps);
+                    const float4 y = make_float4(x[0], x[1], x[2], x[3]);
+                    *reinterpret_cast<float4*>(qt + (t * GQ + h) * AHD + 4 * lane) = y;
+                    if (s == 0) *reinterpret_cast<float4*>(fr.qo + ((size_t)t * H + kvh * GQ + h) * AHD + 4 * lane) = y;
+                }
+                if (krow) {
+                    float x[4] = {ka.x, ka.y, ka.z, ka.w};
+                    const float vv[4] = {va.x, va.y, va.z, va.w};
+                    front::wave::norm_rope(x, wk, lane, rp, fr.rot, fr.eps);
+                    front::wave::append(x, vv, kv, rbase + pos0 + t, lane);
+                }
+            }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the new rows are in memory
+        }
+        front::sync<true>();
+        if (wv >= WS_NC && late) ring_first<CH, NS>(smem, kv, rbase, wv - WS_NC, lane, lo, first, nch);
+    }
     if (wv >= WS_NC) {
-        ring_producer<CH, NS>(smem, kv, rbase, wv - WS_NC, lane, lo, first, nch);
+        ring_producer<CH, NS>(smem, kv, rbase, wv - WS_NC, lane, lo, first, nch, fused);
     } else {
         const int pr = wv % NPR;                                        // token pair
         const bool live = 2 * pr < ntok;
@@ -579,7 +643,8 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wsp_kernel(const 
         int4_t_ qd[3][4];
         float qs;
         {
-            const float* qrow = qo + ((size_t)(tb + min(tl, ntok - 1)) * H + kvh * GQ + (m16 & 7)) * AHD + 16 * g;
+            const float* qrow = fused ? qtab + (min(tl, ntok - 1) * GQ + (m16 & 7)) * AHD + 16 * g
+                                      : qo + ((size_t)(tb + min(tl, ntok - 1)) * H + kvh * GQ + (m16 & 7)) * AHD + 16 * g;
             float4 qv4[16];
 #pragma unroll
             for (int ks = 0; ks < 4; ks++)
@@ -795,15 +860,22 @@ __global__ void __launch_bounds__(64 * (WS_NC + WS_NP), 1) gqa_wsp_kernel(const 
 
 template <int NPR>
 static void launch_wsp(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part,
-                       int T, int ns, hipStream_t st) {
+                       int T, int ns, hipStream_t st, const FrontArgs* fr) {
     static bool once = [] {
-        MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_wsp_kernel<NPR>),
+        MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_wsp_kernel<NPR, false>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, wsp_lds<NPR>()));
+        MOEX_CK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_wsp_kernel<NPR, true>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, wsp_lds<NPR>()));
         return true;
     }();
     (void)once;
-    hipLaunchKernelGGL(gqa_wsp_kernel<NPR>, dim3(KV * ns * ((T + 2 * NPR - 1) / (2 * NPR))),
-                       dim3(64 * (WS_NC + WS_NP)), wsp_lds<NPR>(), st, qo, kv, H, pos_d, max_t, part, T, ns);
+    const dim3 grid(KV * ns * ((T + 2 * NPR - 1) / (2 * NPR))), block(64 * (WS_NC + WS_NP));
+    if (fr && fr->q && T <= 2 * NPR)
+        hipLaunchKernelGGL((gqa_wsp_kernel<NPR, true>), grid, block, wsp_lds<NPR>(), st, qo, kv, H, pos_d, max_t, part, T,
+                           ns, *fr);
+    else
+        hipLaunchKernelGGL((gqa_wsp_kernel<NPR, false>), grid, block, wsp_lds<NPR>(), st, qo, kv, H, pos_d, max_t, part,
+                           T, ns, FrontArgs{});
 }
 
 // TurboQuant codes -> signed int8 centroid codes (kernels.cuh:1122-1170 tables, scaled by 127 / max centroid):
@@ -1322,8 +1394,8 @@ void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos
                 hipLaunchKernelGGL(gqa_ws1_kernel<false>, dim3(KV * ns), dim3(64 * (WS_NC + WS_NP)), W1_LDS, st, qo, kv, H,
                                    pos_d, max_t, part, ns, FrontArgs{});
         }
-        else if (T == 2) launch_wsp<1>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
-        else launch_wsp<2>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st);
+        else if (T == 2) launch_wsp<1>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st, fr);
+        else launch_wsp<2>(qo, kv, H, KV, pos_d, max_t, part, T, ns, st, fr);
     }
     MOEX_LAUNCHED();
 }

@@ -298,23 +298,14 @@ __device__ __forceinline__ float row_max(const float (&v)[4]) {
     return m;
 }
 
-// norm_rope on the lane's 4 dims (rot % 8 == 0: a RoPE partner is 4 dims per lane away, same slot); wb: the lane's 4
-// fp16 norm weights (w + 4 lane), loaded by the caller
-__device__ __forceinline__ void norm_rope(float (&x)[4], uint2 wb, int lane, int pos, int rot, float theta, float eps) {
+// The RoPE factors of the lane's 4 dims at one position: they depend on the position and the dim only, so the rows
+// of one token (every head, and its key row) share them
+struct Rope {
+    float cs[4], sn[4];
+};
+__device__ __forceinline__ Rope rope_angles(int lane, int pos, int rot, float theta) {
 #pragma clang fp contract(off)
-    float sq[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) sq[i] = x[i] * x[i];
-    const float r = rsqrtf(block_sum(sq) / AHD + eps);
-    const uint16_t wh[4] = {(uint16_t)(wb.x & 0xffffu), (uint16_t)(wb.x >> 16), (uint16_t)(wb.y & 0xffffu),
-                            (uint16_t)(wb.y >> 16)};
-#pragma unroll
-    for (int i = 0; i < 4; i++) x[i] = x[i] * r * (1.f + (float)__builtin_bit_cast(_Float16, wh[i]));
     const int h2 = rot / 2, d0 = 4 * lane;
-    const int partner = d0 < h2 ? lane + h2 / 4 : lane - h2 / 4;
-    float px[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) px[i] = __shfl(x[i], partner & 63);
     // the angles depend on j = d mod h2 only: lane t computes those of j = t and t + 64 (the same expression as the
     // 256-thread function), the rotating lanes take theirs by shuffle
     float ca = 1.f, sa = 0.f, cb = 1.f, sb = 0.f;
@@ -328,14 +319,53 @@ __device__ __forceinline__ void norm_rope(float (&x)[4], uint2 wb, int lane, int
         cb = cosf(ang);
         sb = sinf(ang);
     }
+    Rope rp;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int d = d0 + i, j = d < h2 ? d : d - h2;
         const float c0 = __shfl(ca, j & 63), c1 = __shfl(cb, j & 63);  // every lane takes part in every shuffle
         const float s0 = __shfl(sa, j & 63), s1 = __shfl(sb, j & 63);
-        const float cs = j < 64 ? c0 : c1, sn = j < 64 ? s0 : s1;
-        if (d < rot) x[i] = d < h2 ? x[i] * cs - px[i] * sn : x[i] * cs + px[i] * sn;
+        rp.cs[i] = j < 64 ? c0 : c1;
+        rp.sn[i] = j < 64 ? s0 : s1;
     }
+    return rp;
+}
+// norm_rope on the lane's 4 dims (rot % 8 == 0: a RoPE partner is 4 dims per lane away, same slot); wb: the lane's 4
+// fp16 norm weights (w + 4 lane), loaded by the caller. In two steps: the RMSNorm(1 + w) and the partner values,
+// then the rotation by rp = rope_angles of the row's position
+__device__ __forceinline__ void norm_partner(float (&x)[4], float (&px)[4], uint2 wb, int lane, int rot, float eps) {
+#pragma clang fp contract(off)
+    float sq[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) sq[i] = x[i] * x[i];
+    const float r = rsqrtf(block_sum(sq) / AHD + eps);
+    const uint16_t wh[4] = {(uint16_t)(wb.x & 0xffffu), (uint16_t)(wb.x >> 16), (uint16_t)(wb.y & 0xffffu),
+                            (uint16_t)(wb.y >> 16)};
+#pragma unroll
+    for (int i = 0; i < 4; i++) x[i] = x[i] * r * (1.f + (float)__builtin_bit_cast(_Float16, wh[i]));
+    const int h2 = rot / 2, d0 = 4 * lane;
+    const int partner = d0 < h2 ? lane + h2 / 4 : lane - h2 / 4;
+#pragma unroll
+    for (int i = 0; i < 4; i++) px[i] = __shfl(x[i], partner & 63);
+}
+__device__ __forceinline__ void rotate(float (&x)[4], const float (&px)[4], const Rope& rp, int lane, int rot) {
+#pragma clang fp contract(off)
+    const int h2 = rot / 2, d0 = 4 * lane;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int d = d0 + i;
+        if (d < rot) x[i] = d < h2 ? x[i] * rp.cs[i] - px[i] * rp.sn[i] : x[i] * rp.cs[i] + px[i] * rp.sn[i];
+    }
+}
+__device__ __forceinline__ void norm_rope(float (&x)[4], uint2 wb, int lane, const Rope& rp, int rot, float eps) {
+    float px[4];
+    norm_partner(x, px, wb, lane, rot, eps);
+    rotate(x, px, rp, lane, rot);
+}
+__device__ __forceinline__ void norm_rope(float (&x)[4], uint2 wb, int lane, int pos, int rot, float theta, float eps) {
+    float px[4];
+    norm_partner(x, px, wb, lane, rot, eps);
+    rotate(x, px, rope_angles(lane, pos, rot, theta), lane, rot);
 }
 __device__ __forceinline__ void norm_rope(float (&x)[4], const uint16_t* w, int lane, int pos, int rot, float theta,
                                           float eps) {

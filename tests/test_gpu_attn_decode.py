@@ -208,6 +208,58 @@ def test_fused_front_matches_three_launches(pos, ns, turbo):
     assert np.all(np.isfinite(ga)) and np.array_equal(ga, gb)
 
 
+def _crossing_pos(start, T, nsg):
+    """the first position from start whose window [pos, pos + T) straddles a split boundary of nsg splits"""
+    for pos in range(start, start + 100000):
+        L = -(-(pos + T) // nsg)
+        if any(pos < b < pos + T for b in range(L, pos + T, L)):
+            return pos
+    raise AssertionError("no crossing window")
+
+
+@pytest.mark.parametrize("T", [2, 3, 4])
+@pytest.mark.parametrize("case", ["p0", "cross_small", "p100", "cross_3000", "p20480", "end", "cross_12000"])
+def test_fused_front_window_matches_three_launches(T, case):
+    """attn_decode's int8 MTP step (T = 2..4, split-K) runs the q/k front and the appends inside the split kernel;
+    the same step as three launches (qk_norm_rope, the split kernel, attn_combine) must give the same qo, cache rows
+    and output, bit for bit. Cases: every row in a split's first chunks (pos 0), windows across a split boundary
+    (some of the new rows at the start of the next split, whose first chunks must wait for them), short and deep
+    caches."""
+    import torch
+    import moex_amd as M
+    ns = {"p0": 4, "cross_small": 2, "p100": 3, "cross_3000": 128, "p20480": 64, "end": 128, "cross_12000": 128}[case]
+    nsg = M.gqa_splits(T, KV, ns)
+    pos = {"p0": 0, "cross_small": None, "p100": 100, "cross_3000": None, "p20480": 20480, "end": 89996 - T,
+           "cross_12000": None}[case]
+    if pos is None:
+        pos = _crossing_pos({"cross_small": 1, "cross_3000": 3000, "cross_12000": 12000}[case], T, nsg)
+    max_t = max(pos + T + 8, 1024)
+    hc, (da, db) = _caches(M, torch, 0, max_t, 91)
+    rng = np.random.default_rng(92 + pos + T)
+    LQ = H * 2 * AHD + 2 * KV * AHD
+    qkv = dev(rng.standard_normal((T, LQ), dtype=np.float32))
+    qn = dev((0.1 * rng.standard_normal(AHD)).astype(np.float16).view(np.int16))
+    kn = dev((0.1 * rng.standard_normal(AHD)).astype(np.float16).view(np.int16))
+    part = torch.empty(T * H * ns * (AHD + 2), device="cuda")
+    qa, qb = torch.full((T, H, AHD), float("nan"), device="cuda"), torch.full((T, H, AHD), float("nan"), device="cuda")
+    oa, ob = torch.full((T, H, AHD), float("nan"), device="cuda"), torch.full((T, H, AHD), float("nan"), device="cuda")
+    pd = pos_tensor(pos)
+    M.attn_decode(qkv, qkv[:, H * 2 * AHD:], qkv[:, H * 2 * AHD + KV * AHD:], qn, kn, qa, da, oa, H, KV, pd, max_t,
+                  64, 1e7, 1e-6, T, LQ, None, part, ns)
+    M.qk_norm_rope(qkv, qkv[:, H * 2 * AHD:], qkv[:, H * 2 * AHD + KV * AHD:], qn, kn, qb, db, H, KV, pd, max_t,
+                   64, 1e7, 1e-6, LQ, T)
+    M.attn_gqa(qb, db, H, KV, pd, max_t, part, T, nsg)
+    M.attn_combine(part, qkv, ob, H, nsg, LQ, T)
+    torch.cuda.synchronize()
+    ca, cb = download(da), download(db)
+    for x, y, name in ((ca.k, cb.k, "k"), (ca.v, cb.v, "v"), (ca.ks, cb.ks, "ks"), (ca.vs, cb.vs, "vs")):
+        assert np.array_equal(x.view(np.uint8), y.view(np.uint8)), f"cache {name} differs"
+    ga, gb = oa.cpu().numpy(), ob.cpu().numpy()
+    report("fused front window vs three launches", T=T, pos=pos, ns=nsg, maxdiff=float(np.abs(ga - gb).max()))
+    assert np.array_equal(qa.cpu().numpy(), qb.cpu().numpy())
+    assert np.all(np.isfinite(ga)) and np.array_equal(ga, gb)
+
+
 @pytest.mark.parametrize("turbo", [0, 1])
 @pytest.mark.parametrize("T", [1, 2])
 def test_one_split_call_runs_split_k(turbo, T):
