@@ -127,30 +127,30 @@ def _caches(M, torch, turbo, max_t, seed, n=2):
     return download(cs[0]), cs
 
 
-@pytest.mark.parametrize("turbo", [0, 1])
-def test_skip_flag_fused_front(turbo):
-    """With g_skip set, attn_decode's T = 1 split-K step (whose split kernel runs the front and the append in its
-    prologue) appends nothing, leaves qo as it was and attends with that qo, as the reference's attention after a
-    skipped qk_norm_rope_k (kernels.cuh:1189) does: its output equals the split kernel + attn_combine on the same qo,
-    bit for bit (turbo: the partials rotated back, as the step runs them)."""
+@pytest.mark.parametrize("turbo,T", [(0, 1), (1, 1), (0, 2), (0, 4)])
+def test_skip_flag_fused_front(turbo, T):
+    """With g_skip set, attn_decode's split-K step (whose split kernel runs the front and the appends in its prologue:
+    T = 1, and int8 windows of up to 4) appends nothing, leaves qo as it was and attends with that qo, as the
+    reference's attention after a skipped qk_norm_rope_k (kernels.cuh:1189) does: its output equals the split kernel
+    + attn_combine on the same qo, bit for bit (turbo: the partials rotated back, as the step runs them)."""
     import torch
     import moex_amd as M
     pos, max_t = 3000, 3072
     hc, (dc,) = _caches(M, torch, turbo, max_t, 71, 1)
     rng = np.random.default_rng(72)
     LQ = H * 2 * AHD + 2 * KV * AHD
-    qkv = dev(rng.standard_normal((1, LQ), dtype=np.float32))
-    qo0 = rng.standard_normal((1, H, AHD), dtype=np.float32)
+    qkv = dev(rng.standard_normal((T, LQ), dtype=np.float32))
+    qo0 = rng.standard_normal((T, H, AHD), dtype=np.float32)
     qo = dev(qo0)
     qn = torch.zeros(AHD, dtype=torch.int16, device="cuda")
-    ns = M.decode_splits(pos + 1)
+    ns = M.decode_splits(pos + T)
     assert ns > 1
-    part = torch.empty(H * ns * (AHD + 2), device="cuda")
-    out = torch.full((1, H, AHD), float("nan"), device="cuda")
+    part = torch.empty(T * H * ns * (AHD + 2), device="cuda")
+    out = torch.full((T, H, AHD), float("nan"), device="cuda")
     M.set_skip(1)
     try:
         M.attn_decode(qkv, qkv[:, H * 2 * AHD:], qkv[:, H * 2 * AHD + KV * AHD:], qn, qn, qo, dc, out, H, KV,
-                      pos_tensor(pos), max_t, 64, 1e7, 1e-6, 1, LQ, None, part, ns)
+                      pos_tensor(pos), max_t, 64, 1e7, 1e-6, T, LQ, None, part, ns)
         torch.cuda.synchronize()
     finally:
         M.set_skip(0)
@@ -159,14 +159,14 @@ def test_skip_flag_fused_front(turbo):
     for a, b, name in ((after.k, hc.k, "k"), (after.v, hc.v, "v"), (after.ks, hc.ks, "ks"), (after.vs, hc.vs, "vs")):
         assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"cache {name} changed under the skip flag"
     assert np.array_equal(qo.cpu().numpy(), qo0), "qo changed under the skip flag"
-    nsg = M.gqa_splits(1, KV, ns, turbo)
-    part2 = torch.empty(H * ns * (AHD + 2), device="cuda")
-    out2 = torch.full((1, H, AHD), float("nan"), device="cuda")
-    (M.attn_gqa_out if turbo else M.attn_gqa)(qo, dc, H, KV, pos_tensor(pos), max_t, part2, 1, nsg)
-    M.attn_combine(part2, qkv, out2, H, nsg, LQ, 1)
+    nsg = M.gqa_splits(T, KV, ns, turbo)
+    part2 = torch.empty(T * H * ns * (AHD + 2), device="cuda")
+    out2 = torch.full((T, H, AHD), float("nan"), device="cuda")
+    (M.attn_gqa_out if turbo else M.attn_gqa)(qo, dc, H, KV, pos_tensor(pos), max_t, part2, T, nsg)
+    M.attn_combine(part2, qkv, out2, H, nsg, LQ, T)
     torch.cuda.synchronize()
     got, ref = out.cpu().numpy(), out2.cpu().numpy()
-    report("skip flag, fused front", turbo=turbo, ns=nsg, same=bool(np.array_equal(got, ref)))
+    report("skip flag, fused front", turbo=turbo, T=T, ns=nsg, same=bool(np.array_equal(got, ref)))
     assert np.all(np.isfinite(got)) and np.array_equal(got, ref)
 
 
