@@ -10,8 +10,10 @@ from tests.gpu_util import AHD, H, KV
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("turbo", [0, 1])
-def test_attn_decode_graph_replays(turbo):
+@pytest.mark.parametrize("turbo,T", [(0, 1), (1, 1), (0, 4)])
+def test_attn_decode_graph_replays(turbo, T):
+    """attn_decode steps (T = 1, and an int8 MTP window of 4: the front inside the split kernel) captured once and
+    replayed at four positions give the eager steps' outputs and cache rows, bit for bit."""
     import torch
     import moex_amd as M
     LQ = H * 2 * AHD + 2 * KV * AHD
@@ -37,16 +39,16 @@ def test_attn_decode_graph_replays(turbo):
 
     def step_args(qkv, qo, out, pos_d, part, c):
         return (qkv, qkv[:, H * 2 * AHD:], qkv[:, H * 2 * AHD + KV * AHD:], qn, kn, qo, c, out, H, KV, pos_d, ctx, 64,
-                1e7, 1e-6, 1, LQ)
+                1e7, 1e-6, T, LQ)
 
     # graph-side static buffers
-    qkv_g = torch.zeros((1, LQ), dtype=torch.float32, device="cuda")
-    qo_g = torch.empty((1, H, AHD), dtype=torch.float32, device="cuda")
-    out_g = torch.empty((1, H, AHD), dtype=torch.float32, device="cuda")
-    part_g = torch.empty(H * ns * (AHD + 2), dtype=torch.float32, device="cuda")
+    qkv_g = torch.zeros((T, LQ), dtype=torch.float32, device="cuda")
+    qo_g = torch.empty((T, H, AHD), dtype=torch.float32, device="cuda")
+    out_g = torch.empty((T, H, AHD), dtype=torch.float32, device="cuda")
+    part_g = torch.empty(T * H * ns * (AHD + 2), dtype=torch.float32, device="cuda")
     pos_g = torch.zeros(1, dtype=torch.int32, device="cuda")
     # eager-side buffers
-    qkv_e = torch.empty((1, LQ), dtype=torch.float32, device="cuda")
+    qkv_e = torch.empty((T, LQ), dtype=torch.float32, device="cuda")
     qo_e = torch.empty_like(qo_g)
     out_e = torch.empty_like(out_g)
     part_e = torch.empty_like(part_g)
@@ -62,8 +64,8 @@ def test_attn_decode_graph_replays(turbo):
     torch.cuda.synchronize()
 
     for i in range(4):
-        pos = base + i
-        row = torch.randn((1, LQ), generator=g, device="cuda")
+        pos = base + T * i
+        row = torch.randn((T, LQ), generator=g, device="cuda")
         # eager reference on ce
         qkv_e.copy_(row)
         M.set_int(pos_e, pos)
@@ -78,7 +80,7 @@ def test_attn_decode_graph_replays(turbo):
         assert np.all(np.isfinite(a)) and np.array_equal(a, b), f"replay {i}: max diff {np.abs(a - b).max()}"
     # every written row (context and the four appended ones) agrees byte for byte
     for name in ("k", "v", "ks", "vs"):
-        te, tg = getattr(ce, name)[:, :base + 4], getattr(cg, name)[:, :base + 4]
+        te, tg = getattr(ce, name)[:, :base + 4 * T], getattr(cg, name)[:, :base + 4 * T]
         assert torch.equal(te, tg), name
 
 
