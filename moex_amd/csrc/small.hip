@@ -8,6 +8,7 @@
 // reference's warp tree is reproduced exactly. The WHT's stage 32 is a shuffle too (dims d and d^32 share a
 // wavefront); only stage 64 crosses wavefronts and goes through LDS.
 #pragma clang fp contract(off)
+#include <cstdlib>
 #include <mutex>
 #include "front.hpp"
 
@@ -63,28 +64,48 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(
     }
 }
 
-// The same front on one wavefront per head row (front::wave, the same bits): rows r = token (H + KV) + head of the
-// chunk, four to a workgroup, no barrier. KV rows append (k normalized and rotated; v raw). Needs rot % 8 == 0.
+// The same front on wavefronts of RPW rows of one token each (front::wave, the same bits): a token's H + KV rows go
+// to ceil((H + KV) / RPW) wavefronts, four to a workgroup, no barrier. A wavefront issues all of its row reads first
+// and computes the token's RoPE angles once for its rows (powf, sinf and cosf of arguments up to the position: most
+// of a row's arithmetic). KV rows append (k normalized and rotated; v raw). Needs rot % 8 == 0.
+template <int RPW>
 __global__ void __launch_bounds__(256) front_rows_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const uint16_t* __restrict__ qn, const uint16_t* __restrict__ kn, float* __restrict__ qo, moex_kv_cache kv,
     int H, int KV, const int* __restrict__ pos_d, int max_t, int rot, float theta, float eps, int ld, int T) {
     if (g_skip) return;
-    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (r >= T * (H + KV)) return;
-    const int tok = r / (H + KV), hh = r - tok * (H + KV), pos = *pos_d + tok;
+    const int R = H + KV, wpt = (R + RPW - 1) / RPW;
+    const int w = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (w >= T * wpt) return;
+    const int tok = w / wpt, r0 = (w - tok * wpt) * RPW, pos = *pos_d + tok;
     q += (size_t)tok * ld; k += (size_t)tok * ld; v += (size_t)tok * ld;
-    const bool isq = hh < H;
-    const float4 x4 = *reinterpret_cast<const float4*>((isq ? q + hh * 2 * AHD : k + (hh - H) * AHD) + 4 * lane);
-    float x[4] = {x4.x, x4.y, x4.z, x4.w};
-    front::wave::norm_rope(x, isq ? qn : kn, lane, pos, rot, theta, eps);
-    if (isq) {
-        if (kv.turbo) front::wave::wht(x, 0, lane);  // the keys' rotation
-        *reinterpret_cast<float4*>(qo + ((size_t)tok * H + hh) * AHD + 4 * lane) = make_float4(x[0], x[1], x[2], x[3]);
-    } else {
-        const float4 v4 = *reinterpret_cast<const float4*>(v + (hh - H) * AHD + 4 * lane);
-        const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
-        front::wave::append(x, vv, kv, (size_t)(hh - H) * max_t + pos, lane);
+    float4 x4[RPW], v4[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+        const int hh = r0 + i;
+        if (hh < H) {
+            x4[i] = *reinterpret_cast<const float4*>(q + hh * 2 * AHD + 4 * lane);
+        } else if (hh < R) {
+            x4[i] = *reinterpret_cast<const float4*>(k + (hh - H) * AHD + 4 * lane);
+            v4[i] = *reinterpret_cast<const float4*>(v + (hh - H) * AHD + 4 * lane);
+        }
+    }
+    const uint2 wq = *reinterpret_cast<const uint2*>(qn + 4 * lane), wk = *reinterpret_cast<const uint2*>(kn + 4 * lane);
+    const front::wave::Rope rp = front::wave::rope_angles(lane, pos, rot, theta);
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+        const int hh = r0 + i;
+        if (hh >= R) break;
+        const bool isq = hh < H;
+        float x[4] = {x4[i].x, x4[i].y, x4[i].z, x4[i].w};
+        front::wave::norm_rope(x, isq ? wq : wk, lane, rp, rot, eps);
+        if (isq) {
+            if (kv.turbo) front::wave::wht(x, 0, lane);  // the keys' rotation
+            *reinterpret_cast<float4*>(qo + ((size_t)tok * H + hh) * AHD + 4 * lane) = make_float4(x[0], x[1], x[2], x[3]);
+        } else {
+            const float vv[4] = {v4[i].x, v4[i].y, v4[i].z, v4[i].w};
+            front::wave::append(x, vv, kv, (size_t)(hh - H) * max_t + pos, lane);
+        }
     }
 }
 // Quantize-append only, one wavefront per row (rows r = token KV + kv head)
@@ -373,10 +394,26 @@ void launch_qk_norm_rope(const float* q, const float* k, const float* v, const u
     // the 16-byte row loads and the wavefront layout need 4-float aligned rows
     const bool al = ld % 4 == 0 && ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)qo) % 16 == 0 &&
                     ((uintptr_t)qn | (uintptr_t)kn) % 8 == 0;
-    if (rot % 8 == 0 && al)
-        hipLaunchKernelGGL(front_rows_kernel, dim3((T * (H + KV) + 3) / 4), dim3(256), 0, st, q, k, v, qn, kn, qo, kv,
-                           H, KV, pos_d, max_t, rot, theta, eps, ld, T);
-    else
+    // rows per wavefront: 3 (a 2048-token chunk at 32768: int8 26.7-29.3 -> 20.1-22.0 us, turbo 33.4-34.4 -> 32.4;
+    // 6 and 9 no better, turbo slower at 6); MOEX_FRONT_RPW=1, 3, 6 or 9 for comparisons (read on every call)
+    int rpw = 3;
+    if (const char* e = std::getenv("MOEX_FRONT_RPW")) rpw = std::atoi(e);
+    const int waves = T * ((H + KV + rpw - 1) / std::max(rpw, 1));
+    const dim3 grid((waves + 3) / 4);
+    if (rot % 8 == 0 && al) {
+        if (rpw == 1)
+            hipLaunchKernelGGL(front_rows_kernel<1>, grid, dim3(256), 0, st, q, k, v, qn, kn, qo, kv, H, KV, pos_d, max_t,
+                               rot, theta, eps, ld, T);
+        else if (rpw == 9)
+            hipLaunchKernelGGL(front_rows_kernel<9>, grid, dim3(256), 0, st, q, k, v, qn, kn, qo, kv, H, KV, pos_d, max_t,
+                               rot, theta, eps, ld, T);
+        else if (rpw == 6)
+            hipLaunchKernelGGL(front_rows_kernel<6>, grid, dim3(256), 0, st, q, k, v, qn, kn, qo, kv, H, KV, pos_d, max_t,
+                               rot, theta, eps, ld, T);
+        else
+            hipLaunchKernelGGL(front_rows_kernel<3>, dim3((T * ((H + KV + 2) / 3) + 3) / 4), dim3(256), 0, st, q, k, v, qn,
+                               kn, qo, kv, H, KV, pos_d, max_t, rot, theta, eps, ld, T);
+    } else
         hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(H + KV, T), dim3(256), 0, st, q, k, v, qn, kn, qo, kv, H, KV,
                            pos_d, max_t, rot, theta, eps, ld);
     MOEX_LAUNCHED();

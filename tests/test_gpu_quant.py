@@ -161,3 +161,35 @@ def test_wavefront_kernels_match_block_kernels(turbo):
     for x, y in ((ca.k, cb.k), (ca.v, cb.v), (ca.ks, cb.ks), (ca.vs, cb.vs)):
         a, b = np.ascontiguousarray(x[:, rows]), np.ascontiguousarray(y[:, rows])
         assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
+
+
+@pytest.mark.parametrize("turbo,KV", [(0, 2), (1, 2), (0, 3)])
+def test_front_rows_per_wavefront(turbo, KV, monkeypatch):
+    """front_rows_kernel puts RPW rows of one token on a wavefront, which computes the token's RoPE angles once for
+    them (MOEX_FRONT_RPW): 1, 3, 6 and 9 rows per wavefront give the same qo and cache bytes (3 kv heads: 27 rows a
+    token, so the last wavefront of a token is partial)."""
+    import torch
+    import moex_amd as M
+    Hq = 8 * KV
+    T, pos0, max_t = 29, 5000, 5120
+    LQ = Hq * 2 * AHD + 2 * KV * AHD
+    rng = np.random.default_rng(93 + KV)
+    qkv = dev(rng.standard_normal((T, LQ), dtype=np.float32))
+    qn = dev((0.1 * rng.standard_normal(AHD)).astype(np.float16).view(np.int16))
+    kn = dev((0.1 * rng.standard_normal(AHD)).astype(np.float16).view(np.int16))
+    res = []
+    for rpw in ("1", "3", "6", "9"):
+        monkeypatch.setenv("MOEX_FRONT_RPW", rpw)
+        qo = torch.full((T, Hq, AHD), float("nan"), device="cuda")
+        c = M.DeviceKVCache(KV, max_t, turbo)
+        M.qk_norm_rope(qkv, qkv[:, Hq * 2 * AHD:], qkv[:, Hq * 2 * AHD + KV * AHD:], qn, kn, qo, c, Hq, KV,
+                       pos_tensor(pos0), max_t, 64, 1e7, 1e-6, LQ, T)
+        torch.cuda.synchronize()
+        hc = download(c)
+        res.append((qo.cpu().numpy(), [np.ascontiguousarray(x[:, pos0:pos0 + T]) for x in (hc.k, hc.v, hc.ks, hc.vs)]))
+    q0, c0 = res[0]
+    assert np.all(np.isfinite(q0))
+    for qx, cx in res[1:]:
+        assert np.array_equal(q0.view(np.uint32), qx.view(np.uint32))
+        for a, b in zip(c0, cx):
+            assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
