@@ -81,8 +81,8 @@ void moex_kv_free(moex_kv_cache kv);
  * ns > 1 -> split-K GQA decode + combine (part: T*H*ns*(256+2) floats); ns == 1 with T <= 2 and H/KV == 8 -> the
  * same split-K kernels with partials in the library's per-stream workspace (the per-head kernel of the reference
  * only under a first-time capture or when one split would do); otherwise the per-head kernel.
- * ns > 1, H/KV == 8, T == 1 (int8 or turbo) or int8 T <= 4: the front and the appends run inside the split kernel
- * (two launches in all), with qo, the cache rows and out bit-identical to the separate front's. */
+ * ns > 1, H/KV == 8, T <= 4 (int8 or turbo): the front and the appends run inside the split kernel (two launches in
+ * all), with qo, the cache rows and out bit-identical to the separate front's. */
 void moex_attn_decode(const float* q, const float* k, const float* v, const uint16_t* qn, const uint16_t* kn,
                       float* qo, moex_kv_cache kv, float* out, int H, int KV, const int* pos_d, int max_t,
                       int rot, float theta, float eps, int T, int ld, void* stream, float* part, int ns);

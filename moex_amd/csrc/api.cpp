@@ -292,9 +292,9 @@ void decode_step(const float* q, const float* k, const float* v, const uint16_t*
             ns = n2;
         }
     }
-    if (ns > 1 && G == GQ && (T == 1 || (T <= 4 && !kv.turbo))) {
-        // one token (int8 or turbo) or an int8 window of up to 4: the split kernel runs the q/k front in its prologue
-        // (one launch fewer per step); turbo: its partials rotated back, so the combine gates them and no turbo_out
+    if (ns > 1 && G == GQ && T <= 4) {
+        // up to 4 tokens (a decode step or an MTP window): the split kernel runs the q/k front in its prologue (one
+        // launch fewer per step); turbo: its partials rotated back, so the combine gates them and no turbo_out
         // follows
         const FrontArgs fr{q, k, v, qn, kn, qo, skip_flag(), rot, theta, eps, ld};
         ns = gqa_splits(T, KV, ns, kv.turbo != 0);

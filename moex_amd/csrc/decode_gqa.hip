@@ -1068,28 +1068,33 @@ __global__ void __launch_bounds__(64 * WT_NW, 1) gqa_wst_kernel(const float* __r
         else vm_wait<0>();
     };
 
-    // ---- the front (T = 1, fr.q set, skip flag clear), one wavefront per row (front::wave: the arithmetic of
-    // qk_norm_rope_kernel, no barrier): wavefront w forms query head w (RMSNorm, RoPE, the forward rotation) and keeps
-    // it for its query digits; in the split that holds pos0, wavefront 0 also forms the key row and appends the new
-    // row (TurboQuant), which leaves the queue (vmcnt) before a barrier that all transfers follow ----
+    // ---- the front (T <= 4, fr.q set, skip flag clear), one wavefront per row (front::wave: the arithmetic of
+    // front_rows_kernel, no barrier): wavefront w forms query head w of the workgroup's token (RMSNorm, RoPE, the
+    // forward rotation) and keeps it for its query digits; wavefronts 0 .. nr - 1 form the new key rows this token sees
+    // in this split, [na, hi), and append them (TurboQuant). The rows leave the queue (vmcnt) before a barrier that all
+    // transfers follow. Workgroups of later tokens in the same split append the same rows again, with the same bytes:
+    // every workgroup moves only rows it has written itself ----
     const bool fused = fr.q && !(fr.skip && *fr.skip);
-    const bool app = fused && hi == Tmax && hi > lo;
+    const int na = max(lo, pos0), nr = fused ? max(0, hi - na) : 0;  // nr <= tok + 1 <= 4 rows
+    const bool app = nr > 0;
     float qf4[4];
     if (fused) {
-        const float4 a = *reinterpret_cast<const float4*>(fr.q + (kvh * GQ + wv) * 2 * AHD + 4 * lane);
+        const float4 a =
+            *reinterpret_cast<const float4*>(fr.q + (size_t)tok * fr.ld + (kvh * GQ + wv) * 2 * AHD + 4 * lane);
         qf4[0] = a.x; qf4[1] = a.y; qf4[2] = a.z; qf4[3] = a.w;
-        front::wave::norm_rope(qf4, fr.qn, lane, pos0, fr.rot, fr.theta, fr.eps);
+        front::wave::norm_rope(qf4, fr.qn, lane, pos0 + tok, fr.rot, fr.theta, fr.eps);
         front::wave::wht(qf4, 0, lane);
         if (s == 0)
-            *reinterpret_cast<float4*>(fr.qo + (kvh * GQ + wv) * AHD + 4 * lane) =
+            *reinterpret_cast<float4*>(fr.qo + ((size_t)tok * H + kvh * GQ + wv) * AHD + 4 * lane) =
                 make_float4(qf4[0], qf4[1], qf4[2], qf4[3]);
-        if (app && wv == 0) {
-            const float4 k4 = *reinterpret_cast<const float4*>(fr.k + kvh * AHD + 4 * lane);
-            const float4 v4 = *reinterpret_cast<const float4*>(fr.v + kvh * AHD + 4 * lane);
+        if (wv < nr) {
+            const size_t o = (size_t)(na + wv - pos0) * fr.ld + kvh * AHD + 4 * lane;
+            const float4 k4 = *reinterpret_cast<const float4*>(fr.k + o);
+            const float4 v4 = *reinterpret_cast<const float4*>(fr.v + o);
             float x[4] = {k4.x, k4.y, k4.z, k4.w};
             const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
-            front::wave::norm_rope(x, fr.kn, lane, pos0, fr.rot, fr.theta, fr.eps);
-            front::wave::append(x, vv, kv, rbase + pos0, lane);
+            front::wave::norm_rope(x, fr.kn, lane, na + wv, fr.rot, fr.theta, fr.eps);
+            front::wave::append(x, vv, kv, rbase + na + wv, lane);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
     }
@@ -1376,7 +1381,7 @@ void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos
         }();
         (void)once;
         hipLaunchKernelGGL(gqa_wst_kernel, dim3(KV * ns * T), dim3(64 * WT_NW), WT_LDS, st, qo, kv, H, pos_d,
-                           max_t, part, T, ns, rot_out ? 1 : 0, fr && T == 1 ? *fr : FrontArgs{});
+                           max_t, part, T, ns, rot_out ? 1 : 0, fr && T <= 4 ? *fr : FrontArgs{});
     } else {
         if (T == 1) {
             static bool once = [] {

@@ -127,7 +127,7 @@ def _caches(M, torch, turbo, max_t, seed, n=2):
     return download(cs[0]), cs
 
 
-@pytest.mark.parametrize("turbo,T", [(0, 1), (1, 1), (0, 2), (0, 4)])
+@pytest.mark.parametrize("turbo,T", [(0, 1), (1, 1), (0, 2), (0, 4), (1, 3)])
 def test_skip_flag_fused_front(turbo, T):
     """With g_skip set, attn_decode's split-K step (whose split kernel runs the front and the appends in its prologue:
     T = 1, and int8 windows of up to 4) appends nothing, leaves qo as it was and attends with that qo, as the
@@ -209,18 +209,26 @@ def test_fused_front_matches_three_launches(pos, ns, turbo):
 
 
 def _crossing_pos(start, T, nsg):
-    """the first position from start whose window [pos, pos + T) straddles a split boundary of nsg splits"""
-    for pos in range(start, start + 100000):
+    """the first position from start whose window [pos, pos + T) straddles a split boundary of nsg splits (windows
+    only straddle one while the splits are shorter than about nsg + T keys; past that, the last one below start)"""
+    def crosses(pos):
         L = -(-(pos + T) // nsg)
-        if any(pos < b < pos + T for b in range(L, pos + T, L)):
+        return any(pos < b < pos + T for b in range(L, pos + T, L))
+    for pos in range(start, start + 20000):
+        if crosses(pos):
+            return pos
+    for pos in range(start, 0, -1):
+        if crosses(pos):
             return pos
     raise AssertionError("no crossing window")
 
 
+@pytest.mark.parametrize("turbo", [0, 1])
 @pytest.mark.parametrize("T", [2, 3, 4])
 @pytest.mark.parametrize("case", ["p0", "cross_small", "p100", "cross_3000", "p20480", "end", "cross_12000"])
-def test_fused_front_window_matches_three_launches(T, case):
-    """attn_decode's int8 MTP step (T = 2..4, split-K) runs the q/k front and the appends inside the split kernel;
+def test_fused_front_window_matches_three_launches(T, case, turbo):
+    """attn_decode's MTP step (T = 2..4, split-K; int8, and turbo with a workgroup per token) runs the q/k front and
+    the appends inside the split kernel;
     the same step as three launches (qk_norm_rope, the split kernel, attn_combine) must give the same qo, cache rows
     and output, bit for bit. Cases: every row in a split's first chunks (pos 0), windows across a split boundary
     (some of the new rows at the start of the next split, whose first chunks must wait for them), short and deep
@@ -228,13 +236,13 @@ def test_fused_front_window_matches_three_launches(T, case):
     import torch
     import moex_amd as M
     ns = {"p0": 4, "cross_small": 2, "p100": 3, "cross_3000": 128, "p20480": 64, "end": 128, "cross_12000": 128}[case]
-    nsg = M.gqa_splits(T, KV, ns)
+    nsg = M.gqa_splits(T, KV, ns, turbo)
     pos = {"p0": 0, "cross_small": None, "p100": 100, "cross_3000": None, "p20480": 20480, "end": 89996 - T,
            "cross_12000": None}[case]
     if pos is None:
         pos = _crossing_pos({"cross_small": 1, "cross_3000": 3000, "cross_12000": 12000}[case], T, nsg)
     max_t = max(pos + T + 8, 1024)
-    hc, (da, db) = _caches(M, torch, 0, max_t, 91)
+    hc, (da, db) = _caches(M, torch, turbo, max_t, 91)
     rng = np.random.default_rng(92 + pos + T)
     LQ = H * 2 * AHD + 2 * KV * AHD
     qkv = dev(rng.standard_normal((T, LQ), dtype=np.float32))
@@ -248,14 +256,14 @@ def test_fused_front_window_matches_three_launches(T, case):
                   64, 1e7, 1e-6, T, LQ, None, part, ns)
     M.qk_norm_rope(qkv, qkv[:, H * 2 * AHD:], qkv[:, H * 2 * AHD + KV * AHD:], qn, kn, qb, db, H, KV, pd, max_t,
                    64, 1e7, 1e-6, LQ, T)
-    M.attn_gqa(qb, db, H, KV, pd, max_t, part, T, nsg)
+    (M.attn_gqa_out if turbo else M.attn_gqa)(qb, db, H, KV, pd, max_t, part, T, nsg)
     M.attn_combine(part, qkv, ob, H, nsg, LQ, T)
     torch.cuda.synchronize()
     ca, cb = download(da), download(db)
     for x, y, name in ((ca.k, cb.k, "k"), (ca.v, cb.v, "v"), (ca.ks, cb.ks, "ks"), (ca.vs, cb.vs, "vs")):
         assert np.array_equal(x.view(np.uint8), y.view(np.uint8)), f"cache {name} differs"
     ga, gb = oa.cpu().numpy(), ob.cpu().numpy()
-    report("fused front window vs three launches", T=T, pos=pos, ns=nsg, maxdiff=float(np.abs(ga - gb).max()))
+    report("fused front window vs three launches", turbo=turbo, T=T, pos=pos, ns=nsg, maxdiff=float(np.abs(ga - gb).max()))
     assert np.array_equal(qa.cpu().numpy(), qb.cpu().numpy())
     assert np.all(np.isfinite(ga)) and np.array_equal(ga, gb)
 

@@ -10,7 +10,7 @@ from tests.gpu_util import AHD, H, KV
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("turbo,T", [(0, 1), (1, 1), (0, 4)])
+@pytest.mark.parametrize("turbo,T", [(0, 1), (1, 1), (0, 4), (1, 4)])
 def test_attn_decode_graph_replays(turbo, T):
     """attn_decode steps (T = 1, and an int8 MTP window of 4: the front inside the split kernel) captured once and
     replayed at four positions give the eager steps' outputs and cache rows, bit for bit."""
