@@ -268,7 +268,8 @@ int fa_grid(int KV, int T) {
 }  // namespace
 
 // Tile images: a workgroup widens 32-key tiles j = blockIdx.x, + gridDim.x, .. of one kv head (keys past pos0 + T
-// zeroed) into their images, with the staging wavefronts' code. The prefill kernel then copies images into LDS by DMA,
+// zeroed) into their images, with the staging wavefronts' code. The V^T part, which a thread writes as 16-byte pieces
+// of rows 320 bytes apart, goes through LDS and leaves in whole rows (1 KB runs a wavefront instruction). The prefill kernel then copies images into LDS by DMA,
 // so each tile is widened once instead of once per token tile. The grid is sized from the cache (the chunk's end is a
 // device value) but capped: a cache of 262 144 positions would otherwise launch 8 194 workgroups per kv head, most
 // of them for tiles past the chunk's end, and their dispatch alone took microseconds.
@@ -277,6 +278,7 @@ __global__ void __launch_bounds__(256) fa_image_kernel(moex_kv_cache kv, const i
                                                        int ntmax, unsigned char* __restrict__ img) {
     const int kvh = blockIdx.y, hi = *pos_d + T, tid = threadIdx.x;
     const size_t rbase = (size_t)kvh * max_t;
+    __shared__ __align__(16) unsigned char vl[VT_BYTES];  // the tile's V^T, written transposed, copied out in rows
     for (int j = blockIdx.x; j < ntmax && j * BK < hi; j += gridDim.x) {
         const int k0 = j * BK;
         unsigned char* t = img + ((size_t)kvh * ntmax + j) * TILE_BYTES;
@@ -287,13 +289,21 @@ __global__ void __launch_bounds__(256) fa_image_kernel(moex_kv_cache kv, const i
             load_k<TB, true>(sk, kv, rbase, k0, hi, tid);
             load_v<TB, true>(sv, kv, rbase, k0, hi, tid);
             store_k<TB, true>(sk, t, sc, sc + BK, k0, hi, tid);
-            store_v<TB, true>(sv, t + KT_BYTES, k0, hi, tid);
+            store_v<TB, true>(sv, vl, k0, hi, tid);
         } else {
             load_k<TB>(sk, kv, rbase, k0, hi, tid);
             load_v<TB>(sv, kv, rbase, k0, hi, tid);
             store_k<TB>(sk, t, sc, sc + BK, k0, hi, tid);
-            store_v<TB>(sv, t + KT_BYTES, k0, hi, tid);
+            store_v<TB>(sv, vl, k0, hi, tid);
         }
+        __syncthreads();
+        // the 1024 data slots of V^T (rows of 5 16-byte slots, the fifth padding): slot d = row d / 4, piece d % 4
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int d = tid + 256 * u, off = (d >> 2) * (VST * 2) + 16 * (d & 3);
+            *reinterpret_cast<uint4*>(t + KT_BYTES + off) = *reinterpret_cast<const uint4*>(vl + off);
+        }
+        __syncthreads();
     }
 }
 
