@@ -285,7 +285,32 @@ __global__ void __launch_bounds__(256) fa_image_kernel(moex_kv_cache kv, const i
         float* sc = reinterpret_cast<float*>(t + KT_BYTES + VT_BYTES);
         StageK sk;
         StageV sv;
-        if (k0 + BK <= hi) {
+        if (!TB) {
+            // int8 K rows by 16-byte slots: thread t takes slots t + 256 u (row s / 32, dims 8 (s % 32) ..), so a
+            // wavefront's loads read 2 whole rows and its stores write 2 whole rows of the image
+            uint2 kr[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int sl = tid + 256 * u, r = sl >> 5;
+                kr[u] = *reinterpret_cast<const uint2*>(kv.k + (rbase + min(k0 + r, hi - 1)) * AHD + 8 * (sl & 31));
+            }
+            const float ks = kv.ks[rbase + min(k0 + (tid & (BK - 1)), hi - 1)];
+            if (k0 + BK <= hi) load_v<TB, true>(sv, kv, rbase, k0, hi, tid);
+            else load_v<TB>(sv, kv, rbase, k0, hi, tid);
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int sl = tid + 256 * u, r = sl >> 5;
+                uint32_t h0, h1, h2, h3;
+                i8x4_to_h4(kr[u].x, h0, h1);
+                i8x4_to_h4(kr[u].y, h2, h3);
+                const bool ok = k0 + r < hi;
+                *reinterpret_cast<uint4*>(t + r * (KST * 2) + 16 * (sl & 31)) =
+                    ok ? make_uint4(h0, h1, h2, h3) : make_uint4(0u, 0u, 0u, 0u);
+            }
+            if (tid < BK) sc[tid] = k0 + tid < hi ? ks * SL2 : 0.f;
+            if (k0 + BK <= hi) store_v<TB, true>(sv, vl, k0, hi, tid);
+            else store_v<TB>(sv, vl, k0, hi, tid);
+        } else if (k0 + BK <= hi) {
             load_k<TB, true>(sk, kv, rbase, k0, hi, tid);
             load_v<TB, true>(sv, kv, rbase, k0, hi, tid);
             store_k<TB, true>(sk, t, sc, sc + BK, k0, hi, tid);
