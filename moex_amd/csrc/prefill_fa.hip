@@ -268,10 +268,11 @@ int fa_grid(int KV, int T) {
 }  // namespace
 
 // Tile images: a workgroup widens 32-key tiles j = blockIdx.x, + gridDim.x, .. of one kv head (keys past pos0 + T
-// zeroed) into their images, with the staging wavefronts' code. The V^T part, which a thread writes as 16-byte pieces
-// of rows 320 bytes apart, goes through LDS and leaves in whole rows (1 KB runs a wavefront instruction). The prefill kernel then copies images into LDS by DMA,
-// so each tile is widened once instead of once per token tile. The grid is sized from the cache (the chunk's end is a
-// device value) but capped: a cache of 262 144 positions would otherwise launch 8 194 workgroups per kv head, most
+// zeroed) into their images, with the staging wavefronts' arithmetic. The prefill kernel then copies images into LDS
+// by DMA, so each tile is widened once instead of once per token tile. The stores go out in whole rows: the V^T part,
+// which a staging thread holds as 16-byte pieces of rows 320 bytes apart, is assembled in LDS first, and int8 K rows
+// are taken by 16-byte slots (two rows a wavefront instruction). The grid is sized from the cache (the chunk's end is
+// a device value) but capped: a cache of 262 144 positions would otherwise launch 8 194 workgroups per kv head, most
 // of them for tiles past the chunk's end, and their dispatch alone took microseconds.
 template <bool TB>
 __global__ void __launch_bounds__(256) fa_image_kernel(moex_kv_cache kv, const int* __restrict__ pos_d, int T, int max_t,
