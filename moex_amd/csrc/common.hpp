@@ -104,8 +104,8 @@ void launch_set_skip(int v, hipStream_t st);
 int gqa_splits(int T, int KV, int ns, bool turbo);
 // rot_out (turbo caches): the partials come out rotated back to the output domain, for a gated combine with no
 // turbo_out after it
-// fr (int8, T = 1): the split kernel runs the q/k front itself (query rows, the new K/V row appended to the cache) and
-// writes qo; without it qo must hold the front's output already
+// fr (T <= 4, int8 or turbo): the split kernel runs the q/k front itself (query rows, the new K/V rows appended to the
+// cache) and writes qo; without it qo must hold the front's output already
 void launch_gqa(const float* qo, moex_kv_cache kv, int H, int KV, const int* pos_d, int max_t, float* part, int T,
                 int ns, hipStream_t st, bool rot_out = false, const FrontArgs* fr = nullptr);
 // this device's graph-fallback flag (g_skip, kernels.cuh:46), for kernels of other files; nullptr if unavailable
